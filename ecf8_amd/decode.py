@@ -1,0 +1,133 @@
+"""Device-side decode API over libecf8 (torch tensors in, torch tensors out).
+
+Tensors supply device memory and the stream; the work runs in the HIP
+kernels of libecf8.  Shapes and dtypes are checked on the host before every
+launch, and any failure raises ``ECF8Error`` -- there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ._lib import ECF8_MAX_LUTS, ECF8_TABLE_BYTES, ECF8Error, check, lib
+
+__all__ = ["build_table", "decode_into", "decode", "n_format_blocks", "validate_format", "ECF8Error"]
+
+
+def _stream_handle(device: torch.device, stream=None):
+    s = torch.cuda.current_stream(device) if stream is None else stream
+    return s.cuda_stream
+
+
+def n_format_blocks(n_bytes: int, threads_per_block: int = 512, bytes_per_thread: int = 8) -> int:
+    fb = threads_per_block * bytes_per_thread
+    return (int(n_bytes) + fb - 1) // fb
+
+
+def _n_luts(luts: torch.Tensor) -> int:
+    if luts.ndim == 2:
+        if luts.shape[1] != 256:
+            raise ECF8Error(f"luts must be [n_luts, 256], got {tuple(luts.shape)}")
+        return int(luts.shape[0])
+    if luts.numel() % 256:
+        raise ECF8Error("luts size is not a multiple of 256")
+    return luts.numel() // 256
+
+
+def _op_entries(op: torch.Tensor) -> int:
+    if op.dtype == torch.uint8:
+        if op.numel() % 8:
+            raise ECF8Error("output_positions byte view is not a multiple of 8")
+        return op.numel() // 8
+    if op.dtype in (torch.uint64, torch.int64):
+        return op.numel()
+    raise ECF8Error(f"output_positions must be u64 (or its u8 view), got {op.dtype}")
+
+
+def build_table(luts: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Derived multi-symbol decode table (u32[4096] as int32) for ``luts``."""
+    if not luts.is_cuda or luts.dtype != torch.uint8 or not luts.is_contiguous():
+        raise ECF8Error("luts must be a contiguous uint8 CUDA tensor")
+    n_luts = _n_luts(luts)
+    if not 2 <= n_luts <= ECF8_MAX_LUTS:
+        raise ECF8Error(f"n_luts={n_luts} outside [2, {ECF8_MAX_LUTS}]")
+    if out is None:
+        out = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32, device=luts.device)
+    elif out.numel() * out.element_size() < ECF8_TABLE_BYTES or out.device != luts.device:
+        raise ECF8Error("table buffer too small or on another device")
+    with torch.cuda.device(luts.device):
+        check(lib().ecf8_build_table(luts.data_ptr(), n_luts, out.data_ptr(),
+                                     _stream_handle(luts.device, stream)), "ecf8_build_table")
+    return out
+
+
+def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
+                packed_other_4bits: torch.Tensor, output_positions: torch.Tensor,
+                gaps: torch.Tensor, table: torch.Tensor | None = None,
+                threads_per_block: int = 512, bytes_per_thread: int = 8,
+                n_elements: int | None = None, stream=None) -> torch.Tensor:
+    """Decode one compressed block into ``out`` (uint8 / e4m3fn, >= n elements)."""
+    dev = encoded.device
+    tensors = {"luts": luts, "encoded": encoded, "packed_other_4bits": packed_other_4bits,
+               "output_positions": output_positions, "gaps": gaps, "out": out}
+    for name, t in tensors.items():
+        if not t.is_cuda or t.device != dev:
+            raise ECF8Error(f"{name} must be on {dev}")
+        if not t.is_contiguous():
+            raise ECF8Error(f"{name} must be contiguous")
+    for name in ("luts", "encoded", "packed_other_4bits", "gaps"):
+        if tensors[name].dtype != torch.uint8:
+            raise ECF8Error(f"{name} must be uint8, got {tensors[name].dtype}")
+    if out.dtype not in (torch.uint8, torch.float8_e4m3fn):
+        raise ECF8Error(f"out must be uint8 or float8_e4m3fn, got {out.dtype}")
+    n = packed_other_4bits.numel() * 2 if n_elements is None else int(n_elements)
+    if n > packed_other_4bits.numel() * 2 or n % 2:
+        raise ECF8Error("n_elements must be even and covered by packed_other_4bits")
+    if out.numel() < n:
+        raise ECF8Error(f"out holds {out.numel()} elements, {n} needed")
+    n_bytes = encoded.numel()
+    n_fb = n_format_blocks(n_bytes, threads_per_block, bytes_per_thread)
+    if n_fb and gaps.numel() != n_fb * threads_per_block // 2:
+        raise ECF8Error(f"gaps has {gaps.numel()} bytes, expected {n_fb * threads_per_block // 2}")
+    if n_fb and _op_entries(output_positions) != n_fb + 1:
+        raise ECF8Error(f"output_positions has {_op_entries(output_positions)} entries, "
+                        f"expected {n_fb + 1}")
+    n_luts = _n_luts(luts)
+    if table is None:
+        table = build_table(luts, stream=stream)
+    with torch.cuda.device(dev):
+        check(lib().ecf8_decode(luts.data_ptr(), encoded.data_ptr(),
+                                packed_other_4bits.data_ptr(), output_positions.data_ptr(),
+                                gaps.data_ptr(), out.data_ptr(), n_luts, n_bytes, n,
+                                table.data_ptr(), threads_per_block, bytes_per_thread,
+                                _stream_handle(dev, stream)), "ecf8_decode")
+    return out
+
+
+def decode(luts, encoded, packed_other_4bits, output_positions, gaps, table=None,
+           threads_per_block=512, bytes_per_thread=8, stream=None) -> torch.Tensor:
+    """Decode one compressed block into a new e4m3fn tensor."""
+    n = packed_other_4bits.numel() * 2
+    out = torch.empty(n, dtype=torch.float8_e4m3fn, device=encoded.device)
+    return decode_into(out, luts, encoded, packed_other_4bits, output_positions, gaps, table,
+                       threads_per_block, bytes_per_thread, stream=stream)
+
+
+def validate_format(luts, encoded_bytes: int, packed_other_4bits_bytes: int, output_positions,
+                    gaps_bytes: int, threads_per_block: int = 512, bytes_per_thread: int = 8):
+    """Host-side format check of one compressed block (libecf8
+    ecf8_validate_format); raises ECF8Error with the reason."""
+    import ctypes
+
+    luts_np = np.ascontiguousarray(torch.as_tensor(luts).cpu().numpy().reshape(-1), dtype=np.uint8)
+    op = torch.as_tensor(output_positions).cpu().contiguous()
+    op_np = np.ascontiguousarray(op.view(torch.uint8).numpy()).view(np.uint64)
+    msg = ctypes.create_string_buffer(256)
+    rc = lib().ecf8_validate_format(
+        luts_np.ctypes.data_as(ctypes.c_void_p), luts_np.size // 256, int(encoded_bytes),
+        int(packed_other_4bits_bytes), op_np.ctypes.data_as(ctypes.c_void_p), op_np.size,
+        int(gaps_bytes), 2 * int(packed_other_4bits_bytes), threads_per_block, bytes_per_thread,
+        msg, 256)
+    if rc != 0:
+        raise ECF8Error(f"invalid compressed block: {msg.value.decode()}")

@@ -1,0 +1,342 @@
+"""Drop-in runtime layer with the reference's names (dfloat/run/run.py).
+
+* ``_decode``          callable with the cp.RawKernel call form the reference
+                       uses (grid=, block=, shared_mem=, args=[...]);
+* ``TensorManager``    one grow-only e4m3fn decode buffer per device;
+* ``get_hook``         forward-pre-hook: decode the module's compressed block
+                       into the buffer and inject ``.weight`` views;
+* ``load_and_replace_tensors[_parallel]`` / ``_process_compressed_tensor``
+                       register compressed buffers + hooks from safetensors;
+* ``DFloatModel``      local-checkpoint loader (no hub download).
+
+Launches go on torch's current stream of the module's device, so decode and
+the consuming GEMM are ordered without any cross-runtime synchronisation.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+import re
+from sys import stderr
+from typing import Dict, Optional, Union
+
+import torch
+import torch.nn as nn
+
+from . import decode as _dev
+from ._lib import ECF8_TABLE_BYTES, ECF8Error, check, lib
+
+__all__ = [
+    "DFloatModel",
+    "_decode",
+    "get_dfloat_model_name_or_path",
+    "load_and_replace_tensors",
+    "load_and_replace_tensors_parallel",
+    "TensorManager",
+    "get_hook",
+]
+
+
+class _DecodeLauncher:
+    """Call-compatible stand-in for ``_decode = cp.RawKernel(decode.cu,
+    "decode")`` (dfloat/run/run.py:24-33).  ``args`` are the reference
+    kernel's: luts, encoded, packed_other_4bits, output_positions, gaps,
+    outputs (device addresses), n_luts, n_bytes, n_elements
+    (decode.cu:16-26).  The multi-symbol table for the given LUTs is rebuilt
+    into a per-device scratch table on every call (two launches on the
+    current stream); the hook path caches it per module instead."""
+
+    def __init__(self):
+        self._tables = {}
+
+    def _table(self, device_index: int) -> torch.Tensor:
+        t = self._tables.get(device_index)
+        if t is None:
+            t = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32,
+                            device=torch.device("cuda", device_index))
+            self._tables[device_index] = t
+        return t
+
+    def __call__(self, grid, block, args, shared_mem: int = 0, stream=None):
+        luts, encoded, packed, op, gaps, outputs, n_luts, n_bytes, n_elements = args
+        tpb = int(block[0] if isinstance(block, (tuple, list)) else block)
+        nblk = int(grid[0] if isinstance(grid, (tuple, list)) else grid)
+        bpt = 8
+        if nblk != _dev.n_format_blocks(n_bytes, tpb, bpt):
+            raise ECF8Error(f"grid {nblk} does not cover {n_bytes} bytes with {tpb} threads")
+        dev = torch.cuda.current_device()
+        table = self._table(dev)
+        s = (torch.cuda.current_stream(dev) if stream is None else stream).cuda_stream
+        L = lib()
+        check(L.ecf8_build_table(int(luts), int(n_luts), table.data_ptr(), s), "ecf8_build_table")
+        check(L.ecf8_decode(int(luts), int(encoded), int(packed), int(op), int(gaps), int(outputs),
+                            int(n_luts), int(n_bytes), int(n_elements), table.data_ptr(), tpb, bpt,
+                            s), "ecf8_decode")
+
+
+_decode = _DecodeLauncher()
+
+
+class TensorManager:
+    """One grow-only e4m3fn decode buffer per device, shared by every
+    compressed block on it (dfloat/run/run.py:36-81)."""
+
+    _tensors: Dict[torch.device, torch.Tensor] = {}
+
+    @staticmethod
+    def get_tensor(device, n_elements: int, dtype=torch.float8_e4m3fn) -> torch.Tensor:
+        if isinstance(device, str):
+            device = torch.device(device)
+        cur = TensorManager._tensors.get(device)
+        if cur is not None:
+            if cur.numel() >= n_elements:
+                return cur[:n_elements]
+            del TensorManager._tensors[device]
+            del cur
+            torch.cuda.empty_cache()
+        new = torch.empty(n_elements, dtype=dtype, device=device)
+        print(f"Allocated {n_elements} {dtype} on device {device}", file=stderr)
+        TensorManager._tensors[device] = new
+        return new
+
+    @staticmethod
+    def clear_device(device=None):
+        if device is None:
+            TensorManager._tensors.clear()
+        else:
+            if isinstance(device, str):
+                device = torch.device(device)
+            TensorManager._tensors.pop(device, None)
+        torch.cuda.empty_cache()
+
+
+def _module_table(module: nn.Module) -> torch.Tensor:
+    """Per-module multi-symbol table, built on first use on the module's
+    device and rebuilt if the LUT buffer moves."""
+    luts = module.luts
+    key = (luts.device, luts.data_ptr())
+    cached = module.__dict__.get("_ecf8_table")
+    if cached is None or cached[0] != key:
+        table = _dev.build_table(luts.contiguous())
+        module.__dict__["_ecf8_table"] = (key, table)
+        return table
+    return cached[1]
+
+
+def _inject(module: nn.Module, reconstructed: torch.Tensor) -> None:
+    """dfloat/run/run.py:121-153: a Linear/Embedding gets a 2-D view of the
+    whole buffer; any other module's ``weight_injection_modules`` get views
+    of ``tensor_split(reconstructed, split_positions)`` in order."""
+    if isinstance(module, nn.Linear):
+        module.weight = reconstructed.view(module.out_features, module.in_features)
+    elif isinstance(module, nn.Embedding):
+        module.weight = reconstructed.view(module.num_embeddings, module.embedding_dim)
+    else:
+        parts = torch.tensor_split(reconstructed, module.split_positions)
+        for sub, w in zip(module.weight_injection_modules, parts):
+            if isinstance(sub, nn.Embedding):
+                sub.weight = w.view(sub.num_embeddings, sub.embedding_dim)
+            elif isinstance(sub, nn.Module) and hasattr(sub, "out_features"):
+                sub.weight = w.view(sub.out_features, sub.in_features)
+            else:
+                raise ValueError(f"Unsupported module type: {type(sub)}")
+
+
+def get_hook(threads_per_block: int, bytes_per_thread: int):
+    """Forward-pre-hook factory (dfloat/run/run.py:84-155): decode the
+    module's compressed block on its device's current stream into the shared
+    TensorManager buffer, then inject the weight views."""
+
+    def decode_hook(module, _):
+        n_elements = module.packed_other_4bits.numel() * 2
+        device = module.encoded.device
+        reconstructed = TensorManager.get_tensor(device, n_elements)
+        _dev.decode_into(reconstructed, module.luts, module.encoded, module.packed_other_4bits,
+                         module.output_positions, module.gaps, table=_module_table(module),
+                         threads_per_block=threads_per_block, bytes_per_thread=bytes_per_thread)
+        _inject(module, reconstructed)
+
+    return decode_hook
+
+
+def _shared_mem_size(module, threads_per_block: int) -> int:
+    op = module.output_positions.view(torch.uint64).cpu().numpy().astype("int64")
+    per_block = op[1:] - op[:-1]
+    longest = int(per_block.max()) if per_block.size else 0
+    return threads_per_block * 4 + 4 + longest
+
+
+def _process_compressed_tensor(module, attr_name, tensor_value, tensor_name, pattern_dict,
+                               threads_per_block, bytes_per_thread):
+    """Register one compressed tensor of a block (dfloat/run/run.py:406-458):
+    ``split_positions`` becomes a list attribute, everything else a buffer;
+    ``encoded`` also installs the decode hook and removes the dense weights
+    the block replaces; ``output_positions`` also records shared_mem_size."""
+    if attr_name == "split_positions":
+        module.split_positions = tensor_value.tolist()
+    else:
+        module.register_buffer(attr_name, tensor_value)
+    if attr_name == "encoded":
+        module.register_forward_pre_hook(get_hook(threads_per_block, bytes_per_thread))
+        module_path = ".".join(tensor_name.split(".")[:-1])
+        for pattern, attr_names in pattern_dict.items():
+            if not re.fullmatch(pattern, module_path):
+                continue
+            if isinstance(module, (nn.Embedding, nn.Linear)):
+                tmp = module.weight
+                delattr(module, "weight")
+                del tmp
+            else:
+                module.weight_injection_modules = []
+                for attr_path in attr_names:
+                    target = module
+                    for p in attr_path.split("."):
+                        target = getattr(target, p)
+                    if not hasattr(target, "weight"):
+                        raise ValueError(f"Weight not found for {attr_path}")
+                    tmp = target.weight
+                    delattr(target, "weight")
+                    del tmp
+                    module.weight_injection_modules.append(target)
+            break
+    elif attr_name == "output_positions":
+        module.shared_mem_size = _shared_mem_size(module, threads_per_block)
+
+
+def _process_file(model, path, pattern_dict, tpb, bpt, state_names, params, bufs, cache):
+    from safetensors.torch import load_file
+
+    loaded = load_file(path)
+    for name, value in loaded.items():
+        if name in state_names:
+            target = params.get(name)
+            if target is None:
+                target = bufs[name]
+            if target.shape == value.shape:
+                target.data = value
+            else:
+                print(f"Shape mismatch for {name}: model {target.shape} vs loaded {value.shape}",
+                      file=stderr)
+            continue
+        parts = name.split(".")
+        mpath = ".".join(parts[:-1])
+        module = cache.get(mpath)
+        if module is None:
+            module = model
+            for p in parts[:-1]:
+                if not hasattr(module, p):
+                    print(f"Cannot find module path for {name}", file=stderr)
+                    module = None
+                    break
+                module = getattr(module, p)
+            if module is None:
+                continue
+            cache[mpath] = module
+        _process_compressed_tensor(module, parts[-1], value, name, pattern_dict, tpb, bpt)
+    return len(loaded)
+
+
+def validate_compressed_modules(model, threads_per_block: int = 512, bytes_per_thread: int = 8):
+    """Run the host format validator over every hooked module (buffers must
+    still be reachable); raises ECF8Error on the first malformed block."""
+    count = 0
+    for name, m in model.named_modules():
+        if all(hasattr(m, a) for a in ("luts", "encoded", "packed_other_4bits",
+                                        "output_positions", "gaps")):
+            try:
+                _dev.validate_format(m.luts, m.encoded.numel(), m.packed_other_4bits.numel(),
+                                     m.output_positions, m.gaps.numel(), threads_per_block,
+                                     bytes_per_thread)
+            except ECF8Error as e:
+                raise ECF8Error(f"{name}: {e}") from None
+            count += 1
+    return count
+
+
+def load_and_replace_tensors(model, directory_path, dfloat_config):
+    """Sequential loader (dfloat/run/run.py:158-275)."""
+    tpb = dfloat_config["threads_per_block"]
+    bpt = dfloat_config["bytes_per_thread"]
+    pattern_dict = dfloat_config["pattern_dict"]["fp8"]
+    files = sorted(f for f in os.listdir(directory_path) if f.endswith(".safetensors"))
+    state_names = set(model.state_dict().keys())
+    params = dict(model.named_parameters())
+    bufs = dict(model.named_buffers())
+    cache = {}
+    for f in files:
+        _process_file(model, os.path.join(directory_path, f), pattern_dict, tpb, bpt, state_names,
+                      params, bufs, cache)
+    validate_compressed_modules(model, tpb, bpt)
+    return model
+
+
+def load_and_replace_tensors_parallel(model, directory_path, dfloat_config):
+    """Thread-pooled loader over the safetensors files
+    (dfloat/run/run.py:278-403).  Unlike the reference, a failing file
+    raises instead of being counted as 0 tensors."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    tpb = dfloat_config["threads_per_block"]
+    bpt = dfloat_config["bytes_per_thread"]
+    pattern_dict = dfloat_config["pattern_dict"]["fp8"]
+    files = sorted(f for f in os.listdir(directory_path) if f.endswith(".safetensors"))
+    state_names = set(model.state_dict().keys())
+    params = dict(model.named_parameters())
+    bufs = dict(model.named_buffers())
+    cache = {}
+    workers = max(1, min(8, len(files), os.cpu_count() or 4))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        futs = [ex.submit(_process_file, model, os.path.join(directory_path, f), pattern_dict,
+                          tpb, bpt, state_names, params, bufs, cache) for f in files]
+        total = sum(f.result() for f in futs)
+    print(f"Processed {total} tensors from {len(files)} files", file=stderr)
+    validate_compressed_modules(model, tpb, bpt)
+    return model
+
+
+def get_dfloat_model_name_or_path(repo_id: str, dfloat_dir: str = "../dfloat-models"):
+    """Local directory and hub id of a compressed model
+    (dfloat/run/run.py:473-480)."""
+    parts = repo_id.split("/")
+    parts[0] = "DFloat11"
+    dfloat_model_id = "/".join(parts) + "-DF6.5"
+    dfloat_repo_id = os.path.join(dfloat_dir, "models--" + "--".join(parts) + "-DF6.5")
+    return dfloat_repo_id, dfloat_model_id
+
+
+class DFloatModel:
+    """Compressed causal LM from local directories (dfloat/run/run.py:483-566).
+
+    ``dfloat_repo_id`` must be a local directory holding config.json with a
+    ``dfloat_config`` entry, pattern_dict.json and the compressed
+    safetensors; ``model_name_or_path`` a local directory of the original FP8
+    model.  Nothing is downloaded.
+    """
+
+    @classmethod
+    def from_pretrained(cls, dfloat_repo_id: str, dfloat_model_id: str, model_name_or_path: str,
+                        device: Optional[str] = None, device_map: str = "auto",
+                        max_memory: Optional[Dict[Union[int, str], Union[int, str]]] = None,
+                        trust_remote_code: bool = True, **kwargs):
+        from transformers import AutoConfig, AutoModelForCausalLM
+
+        if not os.path.isdir(dfloat_repo_id):
+            raise FileNotFoundError(f"{dfloat_repo_id} is not a local directory "
+                                    f"(hub download of {dfloat_model_id} is not supported)")
+        model = AutoModelForCausalLM.from_pretrained(
+            model_name_or_path, trust_remote_code=trust_remote_code,
+            dtype=kwargs.get("torch_dtype", torch.bfloat16),
+            attn_implementation=kwargs.get("attn_implementation"), low_cpu_mem_usage=True)
+        model.eval()
+        config = AutoConfig.from_pretrained(dfloat_repo_id)
+        dfloat_config = dict(getattr(config, "dfloat_config"))
+        with open(os.path.join(dfloat_repo_id, "pattern_dict.json")) as f:
+            dfloat_config["pattern_dict"] = json.load(f)
+        load_and_replace_tensors_parallel(model, dfloat_repo_id, dfloat_config)
+        if device:
+            model = model.to(device)
+        elif device_map == "auto":
+            model = model.to("cuda")
+        return model

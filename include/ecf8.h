@@ -1,0 +1,118 @@
+/*
+ * ecf8.h -- C ABI of libecf8.so, the MI355X (gfx950) ECF8 decode engine.
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device addresses
+ * (e.g. torch tensor data_ptr()); `stream` is a hipStream_t passed as void*
+ * (NULL = the null stream).  Every call returns an ECF8_* status; device
+ * calls are asynchronous on `stream` and allocate nothing.
+ *
+ * Reference interfaces each entry point replaces are cited as
+ * file:line of zeyuyang8/ecf8.
+ */
+#ifndef ECF8_H
+#define ECF8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ECF8_OK 0
+#define ECF8_ERR_INVALID_ARG 1       /* null pointer, negative size, odd n     */
+#define ECF8_ERR_UNSUPPORTED 2       /* format geometry the kernels do not run */
+#define ECF8_ERR_MISALIGNED 3        /* device buffer alignment not met        */
+#define ECF8_ERR_FORMAT 4            /* compressed block fails validation      */
+#define ECF8_ERR_HIP 5               /* HIP runtime error (launch, device)     */
+#define ECF8_ERR_CAPACITY 6          /* caller buffer too small                */
+
+/* Bytes of the derived decode table (u32[4096]) built by ecf8_build_table. */
+#define ECF8_TABLE_BYTES 16384
+/* Largest LUT stack the format allows: 1 first-level row, at most 16
+ * second-level rows (pointer values 240..255, dfloat/run/decode.cu:87),
+ * 1 length row. */
+#define ECF8_MAX_LUTS 18
+
+const char *ecf8_version(void);
+const char *ecf8_status_string(int status);
+
+/* ---------------------------------------------------------------- device */
+
+/*
+ * Build the derived multi-symbol decode table from a block's on-disk LUTs.
+ * No reference counterpart: the reference walks the LUTs per symbol
+ * (dfloat/run/decode.cu:86-91); this table is computed once per compressed
+ * block (at load time, like shared_mem_size in dfloat/run/run.py:453-458) and
+ * decodes up to four symbols per lookup with exactly the reference's rule.
+ *   luts   device u8[n_luts*256]      table  device u32[4096] (output)
+ */
+int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *stream);
+
+/*
+ * Decode one compressed block into FP8 e4m3fn bytes.
+ * Replaces the CUDA kernel `decode` (dfloat/run/decode.cu:15-26) as launched
+ * by decode_hook (dfloat/run/run.py:97-119) and validate_cuda_decoding_fp8
+ * (scripts/compress.py:86-124).  Arguments keep the reference's meaning:
+ *   luts               device u8[n_luts*256]   (run.py:109)
+ *   encoded            device u8[n_bytes]      (run.py:110), 8-byte aligned
+ *   packed_other_4bits device u8[n_elements/2] (run.py:111), 8-byte aligned
+ *   output_positions   device u64[n_fb+1]      (run.py:112)
+ *   gaps               device u8[n_fb*threads_per_block/2] (run.py:113)
+ *   outputs            device u8[n_elements]   (run.py:114), 16-byte aligned
+ *   table              device u32[4096] from ecf8_build_table for these luts
+ * where n_fb = ceil(n_bytes / (threads_per_block*bytes_per_thread)).
+ * Geometry: bytes_per_thread must be 8 (the reference kernel hard-codes it,
+ * decode.cu:5); threads_per_block one of 128, 256, 512, 1024.
+ * Outputs outside [0, n_elements) are never written.
+ */
+int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *packed_other_4bits,
+                const uint64_t *output_positions, const uint8_t *gaps, uint8_t *outputs,
+                int n_luts, int64_t n_bytes, int64_t n_elements, const uint32_t *table,
+                int threads_per_block, int bytes_per_thread, void *stream);
+
+/* ------------------------------------------------------------------ host */
+
+/*
+ * Sizes of the encoder outputs for `n` exponents under the given code
+ * lengths (code_bits[s] = length of symbol s, 0 = absent): encoded bytes,
+ * packed gap bytes and output_positions entries.  Host memory.
+ */
+int ecf8_encoded_sizes(const uint8_t *exponents, int64_t n, const uint8_t *code_bits,
+                       int bytes_per_thread, int threads_per_block,
+                       int64_t *n_bytes, int64_t *gaps_bytes, int64_t *n_output_positions);
+
+/*
+ * Bitstream encoder.  Replaces _encode_exponents_for_cuda
+ * (dfloat/utils.py:373-499) and encode_exponents_for_cuda (:502-530):
+ * MSB-first Huffman codes, 4-bit per-chunk gaps (even chunk in the high
+ * nibble), per-format-block output positions closed by n, final byte padded
+ * with the leading bits of the EOF code.  code_bits/code_vals are indexed by
+ * symbol 0..15; eof_bits/eof_value is the EOF pseudo-symbol's code.
+ * Host memory; capacities from ecf8_encoded_sizes.
+ */
+int ecf8_encode_exponents(const uint8_t *exponents, int64_t n, const uint8_t *code_bits,
+                          const uint32_t *code_vals, int eof_bits, uint32_t eof_value,
+                          int bytes_per_thread, int threads_per_block,
+                          uint8_t *encoded, int64_t encoded_capacity,
+                          uint8_t *gaps, int64_t gaps_capacity,
+                          uint64_t *output_positions, int64_t output_positions_capacity);
+
+/*
+ * Format validator for one compressed block (host memory).  No reference
+ * counterpart (the reference validates nothing before launch); it checks the
+ * invariants the decode rule relies on: LUT stack shape and pointers
+ * (utils.py:270-370), n_luts <= 18, code lengths 1..16, gaps/output_positions
+ * sizes (utils.py:463-478), monotone output positions ending at n_elements,
+ * n_elements == 2 * packed bytes.  On failure writes a message to msg.
+ */
+int ecf8_validate_format(const uint8_t *luts, int n_luts, int64_t n_bytes,
+                         int64_t packed_bytes, const uint64_t *output_positions,
+                         int64_t n_output_positions, int64_t gaps_bytes, int64_t n_elements,
+                         int threads_per_block, int bytes_per_thread, char *msg, size_t msg_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ECF8_H */

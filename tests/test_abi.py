@@ -1,0 +1,92 @@
+"""The C-ABI library loads, binds torch's HIP runtime, exports every function
+include/ecf8.h declares, and rejects bad arguments before touching the GPU.
+CPU only: no call here reaches a HIP API."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "ecf8.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ecf8_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    from ecf8_amd._lib import EXPORTED
+
+    assert _declared_functions() == sorted(EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    from ecf8_amd._lib import lib
+
+    L = lib()
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    assert L.ecf8_version().decode().startswith("ecf8_amd")
+
+
+def test_single_hip_runtime_mapped():
+    import torch  # noqa: F401
+
+    from ecf8_amd._lib import lib
+
+    lib()
+    maps = open("/proc/self/maps").read()
+    runtimes = set(re.findall(r"(/\S*libamdhip64\S*)", maps))
+    assert len(runtimes) == 1, runtimes
+
+
+def test_status_strings():
+    from ecf8_amd._lib import lib
+
+    L = lib()
+    assert L.ecf8_status_string(0) == b"ok"
+    assert L.ecf8_status_string(3) == b"misaligned device buffer"
+
+
+def _decode_call(**kw):
+    from ecf8_amd._lib import lib
+
+    args = dict(luts=0x1000, encoded=0x2000, packed=0x3000, op=0x4000, gaps=0x5000, out=0x6000,
+                n_luts=3, n_bytes=100, n=64, table=0x7000, tpb=512, bpt=8)
+    args.update(kw)
+    return lib().ecf8_decode(args["luts"], args["encoded"], args["packed"], args["op"],
+                             args["gaps"], args["out"], args["n_luts"], args["n_bytes"], args["n"],
+                             args["table"], args["tpb"], args["bpt"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(bpt=4), 2),           # geometry the reference kernel does not have
+    (dict(tpb=300), 2),
+    (dict(n=63), 1),            # odd element count
+    (dict(n_bytes=-1), 1),
+    (dict(n_luts=1), 4),
+    (dict(n_luts=19), 4),
+    (dict(out=0x6001), 3),      # 16-byte output alignment
+    (dict(encoded=0x2004), 3),  # 8-byte bitstream alignment
+    (dict(packed=0x3002), 3),
+    (dict(gaps=0), 1),
+])
+def test_decode_rejects_before_launch(kw, status):
+    assert _decode_call(**kw) == status
+
+
+def test_decode_of_empty_block_is_a_no_op():
+    assert _decode_call(n_bytes=0, n=0) == 0
+
+
+def test_build_table_rejects_bad_lut_count():
+    from ecf8_amd._lib import lib
+
+    assert lib().ecf8_build_table(ctypes.c_void_p(0x1000), 19, ctypes.c_void_p(0x2000), None) == 4
+    assert lib().ecf8_build_table(None, 3, ctypes.c_void_p(0x2000), None) == 1

@@ -1,0 +1,295 @@
+"""GPU parity of the HIP decoder: bit-exact against the original FP8 bytes
+(the reference's own check, scripts/compress.py:126), the CPU oracle's
+decode (oracle/, restating dfloat/run/decode.cu) and the golden vectors."""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import codec as oc
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+CASES = sorted(json.load(open(os.path.join(GOLDEN, "index.json"))))
+KEYS = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _dev_block(block, dev):
+    out = {}
+    for k in KEYS:
+        v = block[k]
+        t = torch.from_numpy(np.ascontiguousarray(v)) if isinstance(v, np.ndarray) else v
+        out[k] = t.contiguous().to(dev)
+    return out
+
+
+def _gpu_decode(block, dev, tpb=512, n_elements=None, out=None):
+    from ecf8_amd.decode import decode, decode_into
+
+    d = _dev_block(block, dev)
+    if out is None and n_elements is None:
+        r = decode(d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
+                   d["gaps"], threads_per_block=tpb)
+    else:
+        r = decode_into(out, d["luts"], d["encoded"], d["packed_other_4bits"],
+                        d["output_positions"], d["gaps"], threads_per_block=tpb,
+                        n_elements=n_elements)
+    torch.cuda.synchronize()
+    return r.view(torch.uint8).cpu().numpy()
+
+
+def _compress(flat_u8: np.ndarray, tpb=512):
+    from ecf8_amd.compress import compress_flat
+
+    flat = torch.from_numpy(np.ascontiguousarray(flat_u8)).view(torch.float8_e4m3fn)
+    res = compress_flat(flat, 8, tpb)
+    return {k: res[k] for k in KEYS}
+
+
+# ------------------------------------------------------------------ table
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_table_entries_follow_the_lut_rule(name, cuda_device):
+    from ecf8_amd.decode import build_table
+
+    _say(f"table {name}")
+    g = dict(np.load(os.path.join(GOLDEN, f"{name}.npz")))
+    luts = g["luts"]
+    table = build_table(torch.from_numpy(luts).to(cuda_device)).cpu().numpy().view(np.uint32)
+    rng = np.random.default_rng(0)
+    for w in range(4096):
+        e = int(table[w])
+        total = e >> 28
+        mask = (e >> 16) & 0xFFF
+        n = bin(mask).count("1")
+        if total == 0:
+            assert e == 0
+            continue
+        for _ in range(3):
+            bits = (w << 20) | int(rng.integers(0, 1 << 20))  # window + any continuation
+            off = 0
+            for k in range(n):
+                assert mask >> off & 1
+                sym, ln = oc.lut_decode_one(luts, (bits >> (16 - off)) & 0xFFFF)
+                assert sym == (e >> (4 * k)) & 0xF and ln > 0
+                off += ln
+            assert off == total <= 12
+
+
+# ----------------------------------------------------------------- golden
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_golden_blocks_decode_bit_exact(name, cuda_device):
+    _say(f"golden {name}")
+    g = dict(np.load(os.path.join(GOLDEN, f"{name}.npz")))
+    got = _gpu_decode(g, cuda_device, tpb=int(g["threads_per_block"]))
+    assert np.array_equal(got, g["flat"])
+
+
+# ------------------------------------------------------------ distributions
+
+
+def _random_block(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 60000)) * 2
+    kind = seed % 5
+    if kind == 0:
+        k = int(rng.integers(1, 17))
+        syms = rng.choice(16, k, replace=False)
+        p = rng.pareto(0.5 + rng.random() * 2, k) + 1e-3
+        exps = rng.choice(syms, n, p=p / p.sum()).astype(np.uint8)
+    elif kind == 1:  # geometric: long codes, 1-bit codes
+        exps = np.minimum(rng.geometric(0.5 + 0.45 * rng.random(), n) - 1, 15).astype(np.uint8)
+    elif kind == 2:
+        exps = np.full(n, int(rng.integers(0, 16)), np.uint8)
+    elif kind == 3:
+        exps = rng.integers(0, 16, n, dtype=np.uint8)
+    else:
+        w = rng.normal(0, 0.02, n).astype(np.float32)
+        w = w / (np.abs(w).max() / 448.0)
+        return torch.from_numpy(w).to(torch.float8_e4m3fn).view(torch.uint8).numpy().copy()
+    other = rng.integers(0, 16, n, dtype=np.uint8)
+    return (((other & 8) << 4) | (exps << 3) | (other & 7)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_blocks_bit_exact_vs_original_and_oracle(seed, cuda_device, oracle_native):
+    flat = _random_block(seed)
+    tpb = (128, 256, 512, 1024)[seed % 4]
+    _say(f"random seed={seed} n={flat.size} tpb={tpb}")
+    block = _compress(flat, tpb)
+    got = _gpu_decode(block, cuda_device, tpb=tpb)
+    want = oracle_native.decode(block["luts"].numpy(), block["encoded"].numpy(),
+                                block["packed_other_4bits"].numpy(),
+                                block["output_positions"].numpy(), block["gaps"].numpy(),
+                                threads_per_block=tpb)
+    assert np.array_equal(want, flat)
+    assert np.array_equal(got, flat)
+
+
+def test_config1_4096x4096_bit_exact(cuda_device, oracle_native):
+    from ecf8_amd.synth import synthetic_fp8
+
+    _say("config1 4096x4096")
+    w, _ = synthetic_fp8(4096, 4096, 0.02, seed=0)
+    flat = w.reshape(-1).view(torch.uint8).numpy()
+    block = _compress(flat)
+    got = _gpu_decode(block, cuda_device)
+    assert np.array_equal(got, flat)
+    want = oracle_native.decode(*(block[k].numpy() for k in KEYS), threads=8)
+    assert np.array_equal(want, got)
+
+
+def test_config2_qwen3_layer_bit_exact(cuda_device):
+    from ecf8_amd.synth import flat_block, qwen3_8b_layer
+
+    _say("config2 qwen3-8b layer")
+    flat, _ = flat_block(qwen3_8b_layer(seed=0))
+    flat_u8 = flat.view(torch.uint8).numpy()
+    block = _compress(flat_u8)
+    got = _gpu_decode(block, cuda_device)
+    assert got.size == 192_937_984
+    assert np.array_equal(got, flat_u8)
+
+
+# ---------------------------------------------------------------- edge cases
+
+
+def test_outputs_past_n_elements_are_untouched(cuda_device):
+    flat = _random_block(4)
+    block = _compress(flat)
+    out = torch.full((flat.size + 64,), 0xAB, dtype=torch.uint8, device=cuda_device)
+    got = _gpu_decode(block, cuda_device, n_elements=flat.size, out=out)
+    assert np.array_equal(got[: flat.size], flat)
+    assert (got[flat.size:] == 0xAB).all()
+
+
+def test_shorter_n_elements_clamps_like_the_reference(cuda_device):
+    flat = _random_block(9)
+    block = _compress(flat)
+    out = torch.full((flat.size,), 0xCD, dtype=torch.uint8, device=cuda_device)
+    n = (flat.size // 3) & ~1
+    got = _gpu_decode(block, cuda_device, n_elements=n, out=out)
+    assert np.array_equal(got[:n], flat[:n])
+    assert (got[n:] == 0xCD).all()
+
+
+def test_misaligned_output_is_rejected(cuda_device):
+    from ecf8_amd.decode import ECF8Error, decode_into
+
+    flat = _random_block(3)
+    d = _dev_block(_compress(flat), cuda_device)
+    buf = torch.empty(flat.size + 16, dtype=torch.uint8, device=cuda_device)
+    with pytest.raises(ECF8Error):
+        decode_into(buf[1:1 + flat.size], d["luts"], d["encoded"], d["packed_other_4bits"],
+                    d["output_positions"], d["gaps"])
+
+
+def test_decode_on_a_side_stream(cuda_device):
+    from ecf8_amd.decode import decode_into
+
+    flat = _random_block(14)
+    d = _dev_block(_compress(flat), cuda_device)
+    out = torch.empty(flat.size, dtype=torch.uint8, device=cuda_device)
+    s = torch.cuda.Stream(device=cuda_device)
+    s.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(s):
+        decode_into(out, d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
+                    d["gaps"])
+    s.synchronize()
+    assert np.array_equal(out.cpu().numpy(), flat)
+
+
+# ------------------------------------------------------- drop-in call forms
+
+
+def test_reference_call_form_of_decode(cuda_device):
+    """_decode(grid=, block=, shared_mem=, args=[...]) exactly as
+    scripts/compress.py:109-124 calls the CUDA kernel."""
+    from ecf8_amd.run import _decode
+
+    flat = _random_block(20)
+    d = _dev_block(_compress(flat), cuda_device)
+    n_bytes = d["encoded"].numel()
+    op = d["output_positions"].view(torch.uint64).cpu().numpy().astype(np.int64)
+    shared = 512 * 4 + 4 + int((op[1:] - op[:-1]).max())
+    out = torch.empty(flat.size, dtype=torch.float8_e4m3fn, device=cuda_device)
+    _decode(grid=(int(np.ceil(n_bytes / (512 * 8))),), block=(512,), shared_mem=shared,
+            args=[d["luts"].data_ptr(), d["encoded"].data_ptr(), d["packed_other_4bits"].data_ptr(),
+                  d["output_positions"].data_ptr(), d["gaps"].data_ptr(), out.data_ptr(),
+                  d["luts"].shape[0], n_bytes, flat.size])
+    torch.cuda.synchronize()
+    assert np.array_equal(out.view(torch.uint8).cpu().numpy(), flat)
+
+
+def test_validate_cuda_decoding_fp8_api(cuda_device):
+    from ecf8_amd.compress import compress_flat, validate_cuda_decoding_fp8
+
+    flat = torch.from_numpy(_random_block(4)).view(torch.float8_e4m3fn)
+    res = compress_flat(flat)
+    validate_cuda_decoding_fp8({"threads_per_block": 512, "bytes_per_thread": 8}, res, cuda_device)
+
+
+class _Block(nn.Module):
+    def __init__(self, shapes):
+        super().__init__()
+        self.attn = nn.Module()
+        self.mlp = nn.Module()
+        for path, (o, i) in shapes.items():
+            parent, name = path.split(".")
+            setattr(getattr(self, parent), name, nn.Linear(i, o, bias=False))
+
+    def forward(self, x):
+        return x
+
+
+def test_forward_pre_hook_injects_bit_exact_weights(cuda_device):
+    """Block-level hook flow: flatten name-sorted linears, compress, register
+    buffers + hook the way the loader does (run.py:406-458), forward, and
+    compare every injected .weight with the original FP8 tensor."""
+    from ecf8_amd.compress import compress_flat
+    from ecf8_amd.run import TensorManager, _process_compressed_tensor
+    from ecf8_amd.synth import synthetic_fp8
+    from ecf8_amd.utils import flatten_block_of_weights
+
+    shapes = {"attn.q": (256, 128), "attn.k": (128, 128), "mlp.up": (384, 128)}
+    blk = _Block(shapes)
+    orig = {}
+    for i, (path, (o, inp)) in enumerate(sorted(shapes.items())):
+        w, _ = synthetic_fp8(o, inp, 0.02, seed=i)
+        lin = blk.get_submodule(path)
+        lin.weight = nn.Parameter(w, requires_grad=False)
+        orig[path] = w.view(torch.uint8).clone()
+    layers = {p: blk.get_submodule(p) for p in sorted(shapes)}
+    flat, split = flatten_block_of_weights(layers)
+    res = compress_flat(flat)
+    pattern = {r"block": sorted(shapes)}
+    for key in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps"):
+        _process_compressed_tensor(blk, key, res[key], f"block.{key}", pattern, 512, 8)
+    _process_compressed_tensor(blk, "split_positions", split, "block.split_positions", pattern,
+                               512, 8)
+    for path in shapes:
+        assert "weight" not in blk.get_submodule(path)._parameters
+    blk.to(cuda_device)
+    TensorManager.clear_device()
+    blk(torch.zeros(1, device=cuda_device))
+    torch.cuda.synchronize()
+    for path in shapes:
+        w = blk.get_submodule(path).weight
+        assert w.dtype == torch.float8_e4m3fn and tuple(w.shape) == shapes[path]
+        assert torch.equal(w.view(torch.uint8).cpu(), orig[path])
