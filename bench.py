@@ -1,0 +1,227 @@
+"""ECF8 decode benchmark on one MI355X.
+
+Workload: one Qwen3-8B-shaped decoder layer's seven FP8 e4m3fn linears
+(q/k/v/o/gate/up/down, 192,937,984 elements), synthetic N(0, sigma) weights
+block-quantized per 128x128 tile, compressed as ONE block exactly as the
+reference compresses a `model.layers.N` block.  A step is one decode of the
+whole layer (one kernel launch) from HBM-resident compressed tensors into an
+FP8 buffer.  Inputs/outputs rotate over several copies so the 256 MB
+Infinity Cache cannot serve a step from the previous one.
+
+Prints ONE JSON line: decode GB/s of algorithmic bytes
+(compressed bytes read + FP8 bytes written), the roofline of the decode
+kernel against the 8 TB/s HBM peak, and the CPU decode baseline (the C
+restatement of the decode rule in oracle/) timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0
+REPO = os.path.dirname(os.path.abspath(__file__))
+
+
+def algorithmic_bytes(n_elements: int, n_bytes: int, n_luts: int, tpb: int = 512, bpt: int = 8):
+    """Bytes a decode must move: encoded + sign/mantissa nibbles + gaps +
+    output positions + LUTs read, FP8 bytes written."""
+    n_fb = -(-n_bytes // (tpb * bpt))
+    reads = n_bytes + n_elements // 2 + n_fb * tpb // 2 + 8 * (n_fb + 1) + 256 * n_luts
+    return reads + n_elements, reads, n_elements
+
+
+def _traffic_from_profile():
+    """HBM bytes per launch from the committed rocprofv3 counter summary, if
+    present (line `traffic_bytes_per_launch: <int>`)."""
+    path = os.path.join(REPO, "profiles", "decode_qwen3_layer_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", open(path).read())
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(block, n_elements, alg_bytes, repeats=3):
+    """The oracle's C decoder (single-threaded per format-block range, ranges
+    spread over every host core) on the same compressed layer."""
+    import numpy as np
+
+    from oracle import native
+
+    threads = os.cpu_count() or 1
+    args = [block[k].numpy() for k in ("luts", "encoded", "packed_other_4bits",
+                                        "output_positions", "gaps")]
+    out = np.empty(n_elements, np.uint8)
+    native.decode(*args, threads=threads, out=out)  # warm-up (page-in)
+    best = float("inf")
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        native.decode(*args, threads=threads, out=out)
+        best = min(best, time.perf_counter() - t0)
+    return {
+        "value": round(alg_bytes / best / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"whole layer ({n_elements} elements), best of {repeats} decodes, "
+                  f"C restatement of dfloat/run/decode.cu over {threads} threads",
+    }
+
+
+def copy_calibration(steps, warmup):
+    """A plain device-to-device copy of known size (1 GiB read + 1 GiB
+    written per launch): the reference point for scaling the HBM counters
+    and the practical bandwidth ceiling of a streaming kernel."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "ms_per_copy": ms,
+                      "GBps_read_plus_write": round(2 * n / ms / 1e6, 1)}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--copies", type=int, default=4, help="rotated input/output sets")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", choices=("decode", "copy"), default="decode",
+                    help="copy: time a plain 1 GiB device copy (HBM counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path has no multi-GPU component)", file=sys.stderr)
+        sys.exit(2)
+    if args.mode == "copy":
+        return copy_calibration(args.steps, args.warmup)
+
+    import torch
+
+    from ecf8_amd._lib import lib
+    from ecf8_amd.compress import compress_flat
+    from ecf8_amd.decode import build_table, decode_into, largest_block
+    from ecf8_amd.synth import flat_block, qwen3_8b_layer
+
+    dev = torch.device("cuda", 0)
+    t0 = time.time()
+    flat, _ = flat_block(qwen3_8b_layer(seed=args.seed))
+    block = compress_flat(flat)
+    n = flat.numel()
+    print(f"[bench] compressed layer: {n} elements -> {block['encoded'].numel()} bitstream bytes "
+          f"in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    n_luts = block["luts"].shape[0]
+    alg, alg_r, alg_w = algorithmic_bytes(n, block["encoded"].numel(), n_luts)
+
+    keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
+    max_block = largest_block(block["output_positions"])
+    sets = []
+    for _ in range(args.copies):
+        d = {k: block[k].contiguous().to(dev) for k in keys}
+        d["table"] = build_table(d["luts"])
+        d["out"] = torch.empty(n, dtype=torch.float8_e4m3fn, device=dev)
+        sets.append(d)
+    torch.cuda.synchronize()
+
+    # first decode of every set through the checked API, then straight C-ABI
+    # calls with the same arguments so host overhead cannot starve the queue
+    for d in sets:
+        decode_into(d["out"], d["luts"], d["encoded"], d["packed_other_4bits"],
+                    d["output_positions"], d["gaps"], table=d["table"],
+                    max_block_elements=max_block)
+    L = lib()
+    hstream = torch.cuda.current_stream(dev).cuda_stream
+    calls = [(d["luts"].data_ptr(), d["encoded"].data_ptr(), d["packed_other_4bits"].data_ptr(),
+              d["output_positions"].data_ptr(), d["gaps"].data_ptr(), d["out"].data_ptr(), n_luts,
+              d["encoded"].numel(), n, max_block, d["table"].data_ptr(), 512, 8, hstream)
+             for d in sets]
+
+    def step(i):
+        rc = L.ecf8_decode(*calls[i % len(calls)])
+        if rc:
+            raise RuntimeError(f"ecf8_decode failed with status {rc}")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ok = torch.equal(sets[0]["out"].view(torch.uint8).cpu(), flat.view(torch.uint8))
+    if not ok:
+        print("[bench] decoded layer differs from the original FP8 bytes", file=sys.stderr)
+        sys.exit(1)
+
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    per_launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    total_ms = starts[0].elapsed_time(ends[-1])
+    ms_per_step = total_ms / args.steps
+    avg_launch_ms = sum(per_launch_ms) / len(per_launch_ms)
+    gbps = alg / (ms_per_step * 1e-3) / 1e9
+    kernel_gbps = alg / (avg_launch_ms * 1e-3) / 1e9
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(block, n, alg)
+    line = {
+        "metric": "ECF8 decode GB/s + % HBM roofline; e2e tokens/s, Qwen3-8B-shape bs16",
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3-8b-layer-decode",
+            "elements": n,
+            "linears": "q,k,v,o,gate,up,down (one compressed block)",
+            "bitstream_bytes": block["encoded"].numel(),
+            "algorithmic_bytes": alg,
+            "rotated_copies": args.copies,
+            "threads_per_block": 512,
+            "bytes_per_thread": 8,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(kernel_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic_from_profile(),
+        },
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 4),
+        "bit_exact": ok,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -14,20 +14,23 @@
 // v = L0[W >> 8]; if v >= 240 then v = L[256 - v][W & 0xFF]; length =
 // Llen[v]; the output byte is (o & 8) << 4 | v << 3 | (o & 7).
 //
-// MI355X design (one workgroup per format-block at a time, persistent grid):
-//   1. each lane loads its 8-byte chunk + 2 look-ahead bytes (coalesced
-//      dwordx2 per lane) and decodes the codes it owns through a 4096-entry
-//      multi-symbol table in LDS (up to 4 symbols per lookup, derived once per
-//      compressed block by build_table_kernel); the exponents are packed as
-//      nibbles into a lane-private LDS run;
-//   2. the per-lane symbol counts are prefix-summed (wave64 shuffle scan +
+// MI355X design (one workgroup per format-block at a time, persistent grid,
+// the next block's bitstream prefetched while the current one decodes):
+//   1. each lane takes one chunk (one 128-bit load: chunk + look-ahead) and
+//      decodes the codes it owns through a 4096-entry multi-symbol table in
+//      LDS (up to 4 symbols per lookup, derived once per compressed block by
+//      build_table_kernel); exponents are ORed as nibbles into a lane-private
+//      LDS run (ds_or_b32, no per-symbol bookkeeping branches);
+//   2. the per-chunk symbol counts are prefix-summed (wave64 DPP scan +
 //      per-wave totals in LDS), giving each lane its output offset;
-//   3. each lane ORs its nibble run into a dense LDS staging array at that
-//      offset (ds_or_b32, so runs sharing a dword need no ordering);
-//   4. the staging array is swept in 16-element segments: 8 exponent
-//      nibbles + 8 bytes of sign/mantissa nibbles become 16 FP8 bytes with
-//      bitfield inserts and byte permutes, stored as one 128-bit store
-//      (byte stores only on the two partial segments at the block edges).
+//   3. each lane ORs its nibble run into a dense LDS staging buffer at that
+//      offset (double-buffered across blocks, sized from the largest block
+//      of the tensor like the reference's shared_mem_size);
+//   4. the staging buffer is swept in 16-element segments: 8 exponent
+//      nibbles + 8 bytes of sign/mantissa nibbles (prefetched at block
+//      start) become 16 FP8 bytes with bitfield inserts and byte permutes,
+//      stored as one 128-bit store (byte stores only on the two partial
+//      segments at the block edges).
 // All work is integer VALU/LDS; the HBM traffic is the compressed bytes read
 // once and the FP8 bytes written once.
 
@@ -121,85 +124,245 @@ __device__ __forceinline__ uint2 merge8(uint32_t e, uint32_t o) {
   return r;
 }
 
+// Inclusive prefix sum over a wave64 with DPP row shifts and row
+// broadcasts (six VALU ops, no LDS round trip).
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+
+typedef uint32_t u32x3_a8 __attribute__((ext_vector_type(3), aligned(8)));
+
+// A chunk as fetched: 12 raw bytes starting at the chunk (little-endian
+// dwords; 8 chunk bytes + 2 look-ahead + 2 unused) and the byte holding its
+// gap nibble.  Fetching never waits; the bytes are interpreted a whole decode
+// phase later, when the load has long completed.
+struct RawChunk {
+  u32x3_a8 v;
+  uint32_t gap_byte;
+};
+
+// One chunk's bits: the 8 chunk bytes big-endian in `hi`, the two
+// look-ahead bytes in `la`, and the chunk's gap.
+struct Chunk {
+  uint64_t hi;
+  uint32_t la;
+  uint32_t gap;
+};
+
+// Unconditional 96-bit load of chunk g's bytes.  Near the end of the stream
+// the address is clamped (8-aligned) so the load stays in bounds; such lanes
+// are re-read byte-wise in finish_chunk.  Requires n_bytes >= 16.
+__device__ __forceinline__ RawChunk fetch_chunk(const uint8_t *__restrict__ encoded,
+                                                int64_t last16, const uint8_t *__restrict__ gaps,
+                                                int64_t g) {
+  RawChunk r;
+  const int64_t b0 = g * kChunkBytes;
+  r.v = *reinterpret_cast<const u32x3_a8 *>(encoded + (b0 < last16 ? b0 : last16));
+  r.gap_byte = gaps[g >> 1];
+  return r;
+}
+
+__device__ __forceinline__ Chunk finish_chunk(const RawChunk &r, const uint8_t *__restrict__ encoded,
+                                              int64_t n_bytes, int64_t g) {
+  Chunk c;
+  const int64_t b0 = g * kChunkBytes;
+  if (b0 + 16 <= n_bytes) {
+    c.hi = __builtin_bswap64(((uint64_t)r.v.y << 32) | r.v.x);
+    c.la = ((r.v.z & 0xFFu) << 8) | ((r.v.z >> 8) & 0xFFu);
+  } else {  // stream tail: bytes past n_bytes read as zero
+    uint64_t hi = 0;
+    uint32_t la = 0;
+    for (int i = 0; i < kChunkBytes; ++i) {
+      const int64_t j = b0 + i;
+      hi = (hi << 8) | (j < n_bytes ? encoded[j] : 0u);
+    }
+    for (int i = kChunkBytes; i < kChunkBytes + 2; ++i) {
+      const int64_t j = b0 + i;
+      la = (la << 8) | (j < n_bytes ? encoded[j] : 0u);
+    }
+    c.hi = hi;
+    c.la = la;
+  }
+  c.gap = (g & 1) ? (r.gap_byte & 0xFu) : (r.gap_byte >> 4);
+  return c;
+}
+
+// The 8 sign/mantissa bytes of the 16 outputs at the 16-aligned gpos, read
+// byte-wise with bounds checks (stream edges only).
+__device__ __forceinline__ uint2 load_nibbles_checked(const uint8_t *__restrict__ packed,
+                                                      int64_t n_elements, int64_t gpos) {
+  uint32_t t[2] = {0u, 0u};
+  for (int i = 0; i < 8; ++i) {
+    const int64_t q = (gpos >> 1) + i;
+    const uint32_t b = (q >= 0 && q < (n_elements >> 1)) ? packed[q] : 0u;
+    t[i >> 2] |= b << (8 * (i & 3));
+  }
+  return make_uint2(t[0], t[1]);
+}
+
+__device__ __forceinline__ bool nibbles_in_bounds(int64_t gpos, int64_t n_elements) {
+  return gpos >= 0 && gpos + 16 <= n_elements;
+}
+
+// Unconditional 64-bit load for the segment at gpos, clamped in bounds
+// (requires n_elements >= 16); out-of-range segments are re-read checked.
+__device__ __forceinline__ uint2 fetch_nibbles(const uint8_t *__restrict__ packed,
+                                               int64_t last8, int64_t gpos) {
+  int64_t q = gpos >> 1;
+  q = q < 0 ? 0 : (q > last8 ? last8 : q);
+  return *reinterpret_cast<const uint2 *>(packed + q);
+}
+
+// Dwords of one staging buffer holding `cap` symbols from a 16-aligned base
+// (<= 15 leading nibbles), rounded to 16 bytes.
+__host__ __device__ constexpr int stage_dwords(int cap) { return ((((cap + 30) >> 4) * 2) + 3) & ~3; }
+
+constexpr int kPrivSlots = kPrivDwords + 1;  // + spill dword of the last 64-bit OR
+
 template <int kThreads>
 __global__ __launch_bounds__(kThreads) void decode_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
     const uint8_t *__restrict__ encoded, int64_t n_bytes, const uint8_t *__restrict__ packed,
     const uint64_t *__restrict__ op, const uint8_t *__restrict__ gaps,
-    uint8_t *__restrict__ out, int64_t n_elements, int64_t n_fb) {
+    uint8_t *__restrict__ out, int64_t n_elements, int64_t n_fb, int stage_cap) {
   constexpr int kWaves = kThreads / 64;
-  constexpr int kMaxSyms = kThreads * kChunkBits;     // symbols a format-block can own
-  constexpr int kStageDwords = kMaxSyms / 8 + 4;      // + alignment slack
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_stage[];  // 2 x stage_dw
   __shared__ uint32_t s_table[kTableSize];
   __shared__ uint8_t s_luts[ECF8_MAX_LUTS * 256];
-  __shared__ uint32_t s_priv[kPrivDwords * kThreads];  // [dword][lane]
-  __shared__ __attribute__((aligned(16))) uint32_t s_stage[kStageDwords];
+  __shared__ uint32_t s_priv[kPrivSlots * kThreads];  // [slot][lane] nibble runs
   __shared__ int s_wave_sum[kWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int stage_dw = stage_dwords(stage_cap);
+  uint32_t *const priv = s_priv + tid;  // slot k at priv[k * kThreads]
 
   for (int i = tid; i < kTableSize; i += kThreads) s_table[i] = table[i];
   const int lut_bytes = n_luts * 256;
   for (int i = tid; i < ECF8_MAX_LUTS * 256; i += kThreads) s_luts[i] = i < lut_bytes ? luts[i] : 0;
-  __syncthreads();
   const int len_row = (n_luts - 1) * 256;
   const uint32_t max_row = (uint32_t)(n_luts - 2);
 
-  for (int64_t fb = blockIdx.x; fb < n_fb; fb += gridDim.x) {
-    // ---- 1. load this lane's chunk (big-endian) and decode the codes it owns
-    const int64_t g = fb * kThreads + tid;
-    const int64_t byte0 = g * kChunkBytes;
-    uint64_t hi;
-    uint32_t la;
-    if (byte0 + kChunkBytes + 2 <= n_bytes) {
-      const uint2 d = *reinterpret_cast<const uint2 *>(encoded + byte0);
-      const uint16_t l = *reinterpret_cast<const uint16_t *>(encoded + byte0 + kChunkBytes);
-      hi = __builtin_bswap64(((uint64_t)d.y << 32) | d.x);
-      la = __builtin_bswap16(l);
-    } else {  // stream tail: bytes past n_bytes read as zero
-      hi = 0;
-      la = 0;
-      for (int i = 0; i < kChunkBytes; ++i) {
-        const int64_t j = byte0 + i;
-        hi = (hi << 8) | (j < n_bytes ? encoded[j] : 0u);
-      }
-      for (int i = kChunkBytes; i < kChunkBytes + 2; ++i) {
-        const int64_t j = byte0 + i;
-        la = (la << 8) | (j < n_bytes ? encoded[j] : 0u);
-      }
+  int64_t fb = blockIdx.x;
+  if (fb >= n_fb) return;  // uniform per workgroup, before any barrier
+  // tensors shorter than one vector load take the checked byte paths only
+  const bool big_stream = n_bytes >= 16;
+  const bool big_out = n_elements >= 16;
+  const int64_t last16 = (n_bytes - 16) & ~(int64_t)7;  // last 8-aligned 16-byte window
+  const int64_t last8 = ((n_elements >> 1) - 8) & ~(int64_t)7;
+  Chunk cur;
+  {
+    RawChunk r;
+    if (big_stream) r = fetch_chunk(encoded, last16, gaps, fb * kThreads + tid);
+    else r.gap_byte = gaps[(fb * kThreads + tid) >> 1];
+    cur = finish_chunk(r, encoded, n_bytes, fb * kThreads + tid);
+  }
+  uint64_t op_lo = op[fb], op_hi = op[fb + 1];
+  __syncthreads();
+
+  int buf_sel = 0;
+  for (; fb < n_fb; fb += gridDim.x, buf_sel ^= 1) {
+    uint32_t *const stage = s_stage + buf_sel * stage_dw;
+    const int64_t fb_next = fb + gridDim.x;
+    const bool has_next = fb_next < n_fb;
+
+    // ---- this block's output range; prefetch its sign/mantissa bytes
+    const int64_t start = (int64_t)op_lo;
+    int64_t end = (int64_t)op_hi;
+    if (end > n_elements) end = n_elements;
+    const int64_t base = start & ~(int64_t)15;
+    int64_t total = end - start;
+    if (total < 0 || start < 0) total = 0;  // malformed positions write nothing
+    if (total > stage_cap) total = stage_cap;
+    const int lead = (int)(start - base);
+    const int stage_nib = total > 0 ? lead + (int)total : 0;
+    const int seg_dw = ((stage_nib + 15) >> 4) * 2;
+    const int nseg = seg_dw >> 1;
+    // segments past nseg re-read the last one (no extra HBM traffic)
+    const int last_seg = nseg > 0 ? nseg - 1 : 0;
+    uint2 pre0 = make_uint2(0, 0), pre1 = make_uint2(0, 0);
+    if (big_out) {
+      pre0 = fetch_nibbles(packed, last8, base + 16 * (int64_t)min(tid, last_seg));
+      pre1 = fetch_nibbles(packed, last8, base + 16 * (int64_t)min(tid + kThreads, last_seg));
     }
-    const uint32_t gbyte = gaps[g >> 1];
-    const int gap = (g & 1) ? (gbyte & 0xF) : (gbyte >> 4);
 
-    int p = gap;               // bit offset of the next code inside the chunk
-    uint64_t buf = hi << gap;  // next code left-aligned
-    uint64_t acc = 0;          // pending exponent nibbles, first in bits 0..3
-    int accbits = 0, cnt = 0, j = 0;
+    // ---- prefetch the next block's chunk and positions with vector loads
+    // (left unset past the last block: the loop ends before they are read)
+    RawChunk nxt_raw;
+    uint64_t nop = 0;
+    if (has_next) {
+      if (big_stream) nxt_raw = fetch_chunk(encoded, last16, gaps, fb_next * kThreads + tid);
+      else nxt_raw.gap_byte = gaps[(fb_next * kThreads + tid) >> 1];
+      nop = op[fb_next + (lane & 1)];
+    }
 
-    auto step = [&](bool tail) {
-      uint32_t e = s_table[(uint32_t)(buf >> 52)];
-      uint32_t len = entry_len(e);
-      uint32_t syms = e & 0xFFFFu;
-      uint32_t mask = entry_mask(e);
-      if (len == 0) {  // code longer than 12 bits: one symbol, two-level LUT
+    // ---- 1. decode the codes this lane's chunk owns into its nibble run
+#pragma unroll
+    for (int k = 0; k < kPrivSlots; ++k) priv[k * kThreads] = 0u;
+    const int zero4 = (seg_dw + 3) >> 2;
+    for (int i = tid; i < zero4; i += kThreads)
+      reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
+
+    int p = (int)cur.gap;
+    uint64_t buf = cur.hi << cur.gap;
+    int cnt = 0;
+    auto emit = [&](uint32_t syms, uint32_t n) {
+      const uint64_t v = (uint64_t)syms << ((cnt & 7) * 4);
+      uint32_t *q = priv + (cnt >> 3) * kThreads;
+      atomicOr(q, (uint32_t)v);
+      atomicOr(q + kThreads, (uint32_t)(v >> 32));
+      cnt += n;
+    };
+    // symbols starting before bit 48: all fit the 64-bit window with 16
+    // bits to spare, and every symbol of a table entry starts before 60
+    while (p < 48) {
+      const uint32_t e = s_table[(uint32_t)(buf >> 52)];
+      uint32_t len = entry_len(e), syms = e & 0xFFFFu, n = __builtin_popcount(e & 0x0FFF0000u);
+      if (len == 0) {  // code longer than 12 bits: one symbol via the two-level LUT
         const uint32_t w16 = (uint32_t)(buf >> 48);
         uint32_t v = s_luts[w16 >> 8];
         if (v >= 240) {
-          uint32_t row = 256 - v;
-          row = row < max_row ? row : max_row;
+          const uint32_t row = min(256 - v, max_row);
           v = s_luts[row * 256 + (w16 & 0xFF)];
         }
         len = s_luts[len_row + v];
-        syms = v & 0xF;
-        mask = 1;
-        if (len == 0) {  // malformed LUT: stop this chunk
+        if (len == 0) {  // code-less LUT entry (EOF pad bits): chunk ends
           p = kChunkBits;
-          return;
+          break;
         }
+        syms = v & 0xF;
+        n = 1;
       }
-      if (tail) {  // keep only symbols that start inside this chunk
+      emit(syms, n);
+      p += len;
+      buf <<= len;
+    }
+    // symbols starting in [48, 64): window rebuilt from chunk bits 32..79;
+    // table symbols starting at or after bit 64 belong to the next chunk
+    if (p < kChunkBits) {
+      buf = ((cur.hi << 32) | ((uint64_t)cur.la << 16)) << (p - 32);
+      while (p < kChunkBits) {
+        const uint32_t e = s_table[(uint32_t)(buf >> 52)];
+        uint32_t len = entry_len(e), syms = e & 0xFFFFu, mask = entry_mask(e);
+        if (len == 0) {
+          const uint32_t w16 = (uint32_t)(buf >> 48);
+          uint32_t v = s_luts[w16 >> 8];
+          if (v >= 240) {
+            const uint32_t row = min(256 - v, max_row);
+            v = s_luts[row * 256 + (w16 & 0xFF)];
+          }
+          len = s_luts[len_row + v];
+          if (len == 0) break;
+          syms = v & 0xF;
+          mask = 1;
+        }
         const int rem = kChunkBits - p;
         if (rem < kWinBits) {
           const uint32_t m2 = mask & ((1u << rem) - 1);
@@ -208,55 +371,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
             len = rem;
           }
         }
+        emit(syms, __builtin_popcount(mask));
+        p += len;
+        buf <<= len;
       }
-      const uint32_t n = __builtin_popcount(mask);
-      syms &= (1u << (4 * n)) - 1;
-      acc |= (uint64_t)syms << accbits;
-      accbits += 4 * n;
-      cnt += n;
-      if (accbits >= 32) {
-        if (j < kPrivDwords) s_priv[j * kThreads + tid] = (uint32_t)acc;
-        ++j;
-        acc >>= 32;
-        accbits -= 32;
-      }
-      p += len;
-      buf <<= len;
-    };
-
-    while (p < 32) step(false);
-    if (p < kChunkBits) {
-      buf = ((hi << 32) | ((uint64_t)la << 16)) << (p - 32);
-      while (p < kChunkBits) step(true);
     }
-    if (accbits > 0 && j < kPrivDwords) s_priv[j * kThreads + tid] = (uint32_t)acc;
 
     // ---- 2. block-wide exclusive prefix of the per-chunk symbol counts
-    int incl = cnt;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int t = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += t;
-    }
+    const int incl = wave_inclusive_scan(cnt);
     if (lane == 63) s_wave_sum[wave] = incl;
-
-    const int64_t start = (int64_t)op[fb];
-    int64_t end = (int64_t)op[fb + 1];
-    if (end > n_elements) end = n_elements;
-    const int64_t base = start & ~(int64_t)15;  // 16-element aligned sweep origin
-    int64_t total = end - start;
-    if (total < 0 || start < 0) total = 0;  // malformed positions write nothing
-    if (total > kMaxSyms) total = kMaxSyms;
-    const int lead = (int)(start - base);
-    const int stage_nib = total > 0 ? lead + (int)total : 0;
-    const int stage_dw = ((stage_nib + 15) >> 4) * 2;
-    for (int i = tid; i < stage_dw; i += kThreads) s_stage[i] = 0;
     __syncthreads();
-
     int excl = incl - cnt;
-    for (int w = 0; w < wave; ++w) excl += s_wave_sum[w];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      if (w < wave) excl += s_wave_sum[w];
 
-    // ---- 3. OR this lane's nibble run into the staging array
+    // ---- 3. OR this lane's nibble run into the staging buffer
     int c = cnt;
     if ((int64_t)excl + c > total) c = (int)(total - excl);
     if (c > 0) {
@@ -265,34 +395,37 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
       const int d0 = nib0 >> 3;
       const int ndw = (c + 7) >> 3;
       uint32_t carry = 0;
-      for (int k = 0; k < ndw; ++k) {
-        uint32_t v = s_priv[k * kThreads + tid];
-        if (k == ndw - 1 && (c & 7)) v &= (1u << (4 * (c & 7))) - 1;
-        atomicOr(&s_stage[d0 + k], (v << sh) | carry);
-        carry = sh ? (v >> (32 - sh)) : 0u;
+#pragma unroll
+      for (int k = 0; k < kPrivDwords; ++k) {
+        if (k < ndw) {
+          uint32_t v = priv[k * kThreads];
+          if (k == ndw - 1 && (c & 7)) v &= (1u << (4 * (c & 7))) - 1;
+          atomicOr(&stage[d0 + k], (v << sh) | carry);
+          carry = sh ? (v >> (32 - sh)) : 0u;
+        }
       }
-      if (carry) atomicOr(&s_stage[d0 + ndw], carry);
+      if (carry) atomicOr(&stage[d0 + ndw], carry);
     }
     __syncthreads();
 
+    // the next block's chunk, fetched a whole decode phase ago
+    if (has_next) {
+      cur = finish_chunk(nxt_raw, encoded, n_bytes, fb_next * kThreads + tid);
+      const uint32_t lo0 = __builtin_amdgcn_readlane((uint32_t)nop, 0);
+      const uint32_t lo1 = __builtin_amdgcn_readlane((uint32_t)(nop >> 32), 0);
+      const uint32_t hi0 = __builtin_amdgcn_readlane((uint32_t)nop, 1);
+      const uint32_t hi1 = __builtin_amdgcn_readlane((uint32_t)(nop >> 32), 1);
+      op_lo = ((uint64_t)lo1 << 32) | lo0;
+      op_hi = ((uint64_t)hi1 << 32) | hi0;
+    }
+
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
-    const int nseg = stage_dw >> 1;
-    for (int s = tid; s < nseg; s += kThreads) {
-      const uint2 ev = reinterpret_cast<const uint2 *>(s_stage)[s];
+    for (int s = tid, k = 0; s < nseg; s += kThreads, ++k) {
+      const uint2 ev = reinterpret_cast<const uint2 *>(stage)[s];
       const int64_t gpos = base + 16 * (int64_t)s;
-      uint2 ov;
-      if (gpos + 16 <= n_elements) {
-        ov = *reinterpret_cast<const uint2 *>(packed + (gpos >> 1));
-      } else {
-        uint32_t t[2] = {0u, 0u};
-        for (int i = 0; i < 8; ++i) {
-          const int64_t q = (gpos >> 1) + i;
-          const uint32_t b = q < (n_elements >> 1) ? packed[q] : 0u;
-          t[i >> 2] |= b << (8 * (i & 3));
-        }
-        ov.x = t[0];
-        ov.y = t[1];
-      }
+      uint2 ov = k == 0 ? pre0 : pre1;
+      if (k > 1 || !big_out || !nibbles_in_bounds(gpos, n_elements))
+        ov = load_nibbles_checked(packed, n_elements, gpos);
       const uint2 lo = merge8(ev.x, ov.x);
       const uint2 hi8 = merge8(ev.y, ov.y);
       if (gpos >= start && gpos + 16 <= end) {
@@ -305,14 +438,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
         }
       }
     }
-    __syncthreads();
+    // the next iteration writes the other staging buffer; its barrier after
+    // the scan orders this sweep before any reuse of this one
   }
 }
 
 struct LaunchCache {
   int device = -1;
   int cus = 0;
-  int per_cu[4] = {0, 0, 0, 0};  // occupancy for 128, 256, 512, 1024 threads
+  int occ_cap[4] = {-1, -1, -1, -1};  // stage_cap the occupancy below was computed for
+  int occ[4] = {0, 0, 0, 0};          // per slot: 128, 256, 512, 1024 threads
+  bool attr_set[4] = {false, false, false, false};
 };
 constexpr int kMaxDevices = 64;
 LaunchCache g_cache[kMaxDevices];
@@ -320,7 +456,13 @@ LaunchCache g_cache[kMaxDevices];
 template <int kThreads>
 int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
                   int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
-                  uint8_t *out, int64_t n_elements, int64_t n_fb, hipStream_t stream, int slot) {
+                  uint8_t *out, int64_t n_elements, int64_t n_fb, int64_t max_block_elements,
+                  hipStream_t stream, int slot) {
+  constexpr int kMaxSyms = kThreads * kChunkBits;
+  int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms) ? kMaxSyms
+                                                                        : (int)max_block_elements;
+  if (cap < 16) cap = 16;
+  const size_t dyn = 2 * sizeof(uint32_t) * (size_t)stage_dwords(cap);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return ECF8_ERR_HIP;
   LaunchCache &c = g_cache[dev];
@@ -329,18 +471,26 @@ int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const 
       return ECF8_ERR_HIP;
     c.device = dev;
   }
-  if (c.per_cu[slot] == 0) {
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel<kThreads>, kThreads, 0) !=
-        hipSuccess)
+  if (!c.attr_set[slot]) {
+    const size_t max_dyn = 2 * sizeof(uint32_t) * (size_t)stage_dwords(kMaxSyms);
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<kThreads>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dyn) != hipSuccess)
       return ECF8_ERR_HIP;
-    c.per_cu[slot] = occ > 0 ? occ : 1;
+    c.attr_set[slot] = true;
   }
-  int64_t grid = (int64_t)c.cus * c.per_cu[slot];
+  if (c.occ_cap[slot] != cap) {
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel<kThreads>, kThreads,
+                                                     dyn) != hipSuccess)
+      return ECF8_ERR_HIP;
+    c.occ[slot] = occ > 0 ? occ : 1;
+    c.occ_cap[slot] = cap;
+  }
+  int64_t grid = (int64_t)c.cus * c.occ[slot];
   if (grid > n_fb) grid = n_fb;
-  hipLaunchKernelGGL(decode_kernel<kThreads>, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL(decode_kernel<kThreads>, dim3((unsigned)grid), dim3(kThreads), dyn, stream,
                      luts, n_luts, table, encoded, n_bytes, packed, op, gaps, out, n_elements,
-                     n_fb);
+                     n_fb, cap);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
@@ -357,8 +507,8 @@ extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table
 extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
                            const uint8_t *packed_other_4bits, const uint64_t *output_positions,
                            const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
-                           int64_t n_elements, const uint32_t *table, int threads_per_block,
-                           int bytes_per_thread, void *stream) {
+                           int64_t n_elements, int64_t max_block_elements, const uint32_t *table,
+                           int threads_per_block, int bytes_per_thread, void *stream) {
   if (n_bytes < 0 || n_elements < 0 || (n_elements & 1)) return ECF8_ERR_INVALID_ARG;
   if (bytes_per_thread != kChunkBytes) return ECF8_ERR_UNSUPPORTED;
   if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
@@ -378,15 +528,15 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   switch (threads_per_block) {
     case 128:
       return launch_decode<128>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, s, 0);
+                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 0);
     case 256:
       return launch_decode<256>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, s, 1);
+                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 1);
     case 512:
       return launch_decode<512>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, s, 2);
+                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 2);
     default:
       return launch_decode<1024>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                 output_positions, gaps, outputs, n_elements, n_fb, s, 3);
+                                 output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 3);
   }
 }

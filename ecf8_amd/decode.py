@@ -12,7 +12,8 @@ import torch
 
 from ._lib import ECF8_MAX_LUTS, ECF8_TABLE_BYTES, ECF8Error, check, lib
 
-__all__ = ["build_table", "decode_into", "decode", "n_format_blocks", "validate_format", "ECF8Error"]
+__all__ = ["build_table", "decode_into", "decode", "n_format_blocks", "largest_block",
+           "validate_format", "ECF8Error"]
 
 
 def _stream_handle(device: torch.device, stream=None):
@@ -45,6 +46,17 @@ def _op_entries(op: torch.Tensor) -> int:
     raise ECF8Error(f"output_positions must be u64 (or its u8 view), got {op.dtype}")
 
 
+def largest_block(output_positions) -> int:
+    """Largest output_positions[b+1] - output_positions[b] of a block (the
+    quantity the reference turns into shared_mem_size, run.py:453-458).
+    Reads the positions on the host; call once per block, not per decode."""
+    op = torch.as_tensor(output_positions).detach().contiguous()
+    if op.dtype != torch.uint8:
+        op = op.view(torch.uint8)
+    op = op.cpu().numpy().view(np.uint64).astype(np.int64)
+    return int((op[1:] - op[:-1]).max()) if op.size > 1 else 0
+
+
 def build_table(luts: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Derived multi-symbol decode table (u32[4096] as int32) for ``luts``."""
     if not luts.is_cuda or luts.dtype != torch.uint8 or not luts.is_contiguous():
@@ -66,8 +78,13 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
                 packed_other_4bits: torch.Tensor, output_positions: torch.Tensor,
                 gaps: torch.Tensor, table: torch.Tensor | None = None,
                 threads_per_block: int = 512, bytes_per_thread: int = 8,
-                n_elements: int | None = None, stream=None) -> torch.Tensor:
-    """Decode one compressed block into ``out`` (uint8 / e4m3fn, >= n elements)."""
+                n_elements: int | None = None, max_block_elements: int = 0,
+                stream=None) -> torch.Tensor:
+    """Decode one compressed block into ``out`` (uint8 / e4m3fn, >= n elements).
+
+    ``max_block_elements`` (see largest_block()) sizes the kernel's LDS
+    staging; 0 assumes the worst case, which is always correct but lowers
+    occupancy."""
     dev = encoded.device
     tensors = {"luts": luts, "encoded": encoded, "packed_other_4bits": packed_other_4bits,
                "output_positions": output_positions, "gaps": gaps, "out": out}
@@ -100,18 +117,24 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
         check(lib().ecf8_decode(luts.data_ptr(), encoded.data_ptr(),
                                 packed_other_4bits.data_ptr(), output_positions.data_ptr(),
                                 gaps.data_ptr(), out.data_ptr(), n_luts, n_bytes, n,
-                                table.data_ptr(), threads_per_block, bytes_per_thread,
+                                int(max_block_elements), table.data_ptr(), threads_per_block,
+                                bytes_per_thread,
                                 _stream_handle(dev, stream)), "ecf8_decode")
     return out
 
 
 def decode(luts, encoded, packed_other_4bits, output_positions, gaps, table=None,
-           threads_per_block=512, bytes_per_thread=8, stream=None) -> torch.Tensor:
-    """Decode one compressed block into a new e4m3fn tensor."""
+           threads_per_block=512, bytes_per_thread=8, max_block_elements=None,
+           stream=None) -> torch.Tensor:
+    """Decode one compressed block into a new e4m3fn tensor (computes
+    max_block_elements from the positions when not given)."""
     n = packed_other_4bits.numel() * 2
     out = torch.empty(n, dtype=torch.float8_e4m3fn, device=encoded.device)
+    if max_block_elements is None:
+        max_block_elements = largest_block(output_positions)
     return decode_into(out, luts, encoded, packed_other_4bits, output_positions, gaps, table,
-                       threads_per_block, bytes_per_thread, stream=stream)
+                       threads_per_block, bytes_per_thread,
+                       max_block_elements=max_block_elements, stream=stream)
 
 
 def validate_format(luts, encoded_bytes: int, packed_other_4bits_bytes: int, output_positions,

@@ -62,6 +62,8 @@ class _DecodeLauncher:
     def __call__(self, grid, block, args, shared_mem: int = 0, stream=None):
         luts, encoded, packed, op, gaps, outputs, n_luts, n_bytes, n_elements = args
         tpb = int(block[0] if isinstance(block, (tuple, list)) else block)
+        # the reference's shared_mem = tpb*4 + 4 + largest block (run.py:268-270)
+        max_block = max(0, int(shared_mem) - tpb * 4 - 4)
         nblk = int(grid[0] if isinstance(grid, (tuple, list)) else grid)
         bpt = 8
         if nblk != _dev.n_format_blocks(n_bytes, tpb, bpt):
@@ -72,8 +74,8 @@ class _DecodeLauncher:
         L = lib()
         check(L.ecf8_build_table(int(luts), int(n_luts), table.data_ptr(), s), "ecf8_build_table")
         check(L.ecf8_decode(int(luts), int(encoded), int(packed), int(op), int(gaps), int(outputs),
-                            int(n_luts), int(n_bytes), int(n_elements), table.data_ptr(), tpb, bpt,
-                            s), "ecf8_decode")
+                            int(n_luts), int(n_bytes), int(n_elements), max_block,
+                            table.data_ptr(), tpb, bpt, s), "ecf8_decode")
 
 
 _decode = _DecodeLauncher()
@@ -112,17 +114,23 @@ class TensorManager:
         torch.cuda.empty_cache()
 
 
-def _module_table(module: nn.Module) -> torch.Tensor:
-    """Per-module multi-symbol table, built on first use on the module's
-    device and rebuilt if the LUT buffer moves."""
+def _module_state(module: nn.Module):
+    """Per-module decode state, derived once on the module's device and
+    rebuilt if the buffers move: the multi-symbol table and the largest
+    format-block (the quantity behind the reference's shared_mem_size)."""
     luts = module.luts
-    key = (luts.device, luts.data_ptr())
-    cached = module.__dict__.get("_ecf8_table")
+    key = (luts.device, luts.data_ptr(), module.output_positions.data_ptr())
+    cached = module.__dict__.get("_ecf8_state")
     if cached is None or cached[0] != key:
         table = _dev.build_table(luts.contiguous())
-        module.__dict__["_ecf8_table"] = (key, table)
-        return table
-    return cached[1]
+        tpb = module.__dict__.get("_ecf8_tpb", 512)
+        if hasattr(module, "shared_mem_size"):
+            max_block = max(0, int(module.shared_mem_size) - tpb * 4 - 4)
+        else:
+            max_block = _dev.largest_block(module.output_positions)
+        cached = (key, table, max_block)
+        module.__dict__["_ecf8_state"] = cached
+    return cached[1], cached[2]
 
 
 def _inject(module: nn.Module, reconstructed: torch.Tensor) -> None:
@@ -153,9 +161,12 @@ def get_hook(threads_per_block: int, bytes_per_thread: int):
         n_elements = module.packed_other_4bits.numel() * 2
         device = module.encoded.device
         reconstructed = TensorManager.get_tensor(device, n_elements)
+        module.__dict__["_ecf8_tpb"] = threads_per_block
+        table, max_block = _module_state(module)
         _dev.decode_into(reconstructed, module.luts, module.encoded, module.packed_other_4bits,
-                         module.output_positions, module.gaps, table=_module_table(module),
-                         threads_per_block=threads_per_block, bytes_per_thread=bytes_per_thread)
+                         module.output_positions, module.gaps, table=table,
+                         threads_per_block=threads_per_block, bytes_per_thread=bytes_per_thread,
+                         max_block_elements=max_block)
         _inject(module, reconstructed)
 
     return decode_hook

@@ -61,6 +61,12 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  *   gaps               device u8[n_fb*threads_per_block/2] (run.py:113)
  *   outputs            device u8[n_elements]   (run.py:114), 16-byte aligned
  *   table              device u32[4096] from ecf8_build_table for these luts
+ *   max_block_elements largest output_positions[b+1] - output_positions[b]
+ *                      (the reference derives shared_mem_size from it,
+ *                      dfloat/run/run.py:453-458); sizes the kernel's LDS
+ *                      staging.  0 = unknown (worst case is assumed).  A
+ *                      value below the true maximum leaves the excess
+ *                      elements of such blocks unwritten.
  * where n_fb = ceil(n_bytes / (threads_per_block*bytes_per_thread)).
  * Geometry: bytes_per_thread must be 8 (the reference kernel hard-codes it,
  * decode.cu:5); threads_per_block one of 128, 256, 512, 1024.
@@ -68,8 +74,9 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  */
 int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *packed_other_4bits,
                 const uint64_t *output_positions, const uint8_t *gaps, uint8_t *outputs,
-                int n_luts, int64_t n_bytes, int64_t n_elements, const uint32_t *table,
-                int threads_per_block, int bytes_per_thread, void *stream);
+                int n_luts, int64_t n_bytes, int64_t n_elements, int64_t max_block_elements,
+                const uint32_t *table, int threads_per_block, int bytes_per_thread,
+                void *stream);
 
 /* ------------------------------------------------------------------ host */
 
