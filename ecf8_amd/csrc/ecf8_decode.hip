@@ -46,7 +46,6 @@ constexpr int kTableSize = 1 << kWinBits;    // 4096 entries, u32 each
 constexpr int kMaxSymsPerEntry = 4;
 constexpr int kChunkBytes = 8;               // bytes_per_thread of the format
 constexpr int kChunkBits = 8 * kChunkBytes;
-constexpr int kPrivDwords = kChunkBits / 8;  // <= 64 nibbles per chunk
 
 // Table entry layout:
 //   bits  0..15  up to 4 exponents, first decoded in bits 0..3
@@ -136,54 +135,60 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
   return x;
 }
 
+// ---------------------------------------------------------------------------
+// Decoder: one workgroup of T threads per format-block of T chunks at a time
+// (persistent grid; the next block's bitstream is fetched while the current
+// one decodes), one chunk per lane.  Index arithmetic is 32-bit (the
+// format's positions are < 2^31).
+// ---------------------------------------------------------------------------
+
 typedef uint32_t u32x3_a8 __attribute__((ext_vector_type(3), aligned(8)));
 
-// A chunk as fetched: 12 raw bytes starting at the chunk (little-endian
-// dwords; 8 chunk bytes + 2 look-ahead + 2 unused) and the byte holding its
-// gap nibble.  Fetching never waits; the bytes are interpreted a whole decode
-// phase later, when the load has long completed.
+// A chunk as fetched: 12 raw bytes from the chunk start (8 chunk bytes, 2
+// look-ahead bytes, 2 unused; little-endian dwords) and the byte holding its
+// gap nibble.  Fetching never waits; the bytes are interpreted a whole
+// decode phase later.
 struct RawChunk {
   u32x3_a8 v;
   uint32_t gap_byte;
 };
 
-// One chunk's bits: the 8 chunk bytes big-endian in `hi`, the two
-// look-ahead bytes in `la`, and the chunk's gap.
+// The chunk as a big-endian bit string (hi), its two look-ahead bytes (la)
+// and its gap.
 struct Chunk {
   uint64_t hi;
   uint32_t la;
   uint32_t gap;
 };
 
-// Unconditional 96-bit load of chunk g's bytes.  Near the end of the stream
-// the address is clamped (8-aligned) so the load stays in bounds; such lanes
-// are re-read byte-wise in finish_chunk.  Requires n_bytes >= 16.
-__device__ __forceinline__ RawChunk fetch_chunk(const uint8_t *__restrict__ encoded,
-                                                int64_t last16, const uint8_t *__restrict__ gaps,
-                                                int64_t g) {
+// Unconditional 96-bit load of chunk g, the address clamped to the last
+// full 12-byte window so it stays in bounds; lanes near the stream end are
+// re-read byte-wise in finish_chunk.
+__device__ __forceinline__ RawChunk fetch_chunk(const uint8_t *__restrict__ encoded, uint32_t last12,
+                                                const uint8_t *__restrict__ gaps, uint32_t g) {
   RawChunk r;
-  const int64_t b0 = g * kChunkBytes;
-  r.v = *reinterpret_cast<const u32x3_a8 *>(encoded + (b0 < last16 ? b0 : last16));
+  const uint32_t b = g * kChunkBytes;
+  r.v = *reinterpret_cast<const u32x3_a8 *>(encoded + (b < last12 ? b : last12));
   r.gap_byte = gaps[g >> 1];
   return r;
 }
 
 __device__ __forceinline__ Chunk finish_chunk(const RawChunk &r, const uint8_t *__restrict__ encoded,
-                                              int64_t n_bytes, int64_t g) {
+                                              uint32_t n_bytes, uint32_t g, bool vector_ok) {
   Chunk c;
-  const int64_t b0 = g * kChunkBytes;
-  if (b0 + 16 <= n_bytes) {
+  const uint32_t b = g * kChunkBytes;
+  if (vector_ok && b + 12 <= n_bytes) {
     c.hi = __builtin_bswap64(((uint64_t)r.v.y << 32) | r.v.x);
     c.la = ((r.v.z & 0xFFu) << 8) | ((r.v.z >> 8) & 0xFFu);
   } else {  // stream tail: bytes past n_bytes read as zero
     uint64_t hi = 0;
     uint32_t la = 0;
     for (int i = 0; i < kChunkBytes; ++i) {
-      const int64_t j = b0 + i;
+      const uint32_t j = b + i;
       hi = (hi << 8) | (j < n_bytes ? encoded[j] : 0u);
     }
     for (int i = kChunkBytes; i < kChunkBytes + 2; ++i) {
-      const int64_t j = b0 + i;
+      const uint32_t j = b + i;
       la = (la << 8) | (j < n_bytes ? encoded[j] : 0u);
     }
     c.hi = hi;
@@ -193,187 +198,219 @@ __device__ __forceinline__ Chunk finish_chunk(const RawChunk &r, const uint8_t *
   return c;
 }
 
+// Bits [p, p+16) of the 80-bit string hi:la (chunk + look-ahead), p < 64.
+__device__ __forceinline__ uint32_t window16(uint64_t hi, uint32_t la, int p) {
+  const uint64_t w = p < 48 ? (hi << p) : (((hi << 32) | ((uint64_t)la << 16)) << (p - 32));
+  return (uint32_t)(w >> 48);
+}
+
 // The 8 sign/mantissa bytes of the 16 outputs at the 16-aligned gpos, read
-// byte-wise with bounds checks (stream edges only).
+// byte-wise with bounds checks.
 __device__ __forceinline__ uint2 load_nibbles_checked(const uint8_t *__restrict__ packed,
-                                                      int64_t n_elements, int64_t gpos) {
+                                                      uint32_t n_elements, uint32_t gpos) {
   uint32_t t[2] = {0u, 0u};
   for (int i = 0; i < 8; ++i) {
-    const int64_t q = (gpos >> 1) + i;
-    const uint32_t b = (q >= 0 && q < (n_elements >> 1)) ? packed[q] : 0u;
+    const uint32_t q = (gpos >> 1) + i;
+    const uint32_t b = q < (n_elements >> 1) ? packed[q] : 0u;
     t[i >> 2] |= b << (8 * (i & 3));
   }
   return make_uint2(t[0], t[1]);
 }
 
-__device__ __forceinline__ bool nibbles_in_bounds(int64_t gpos, int64_t n_elements) {
-  return gpos >= 0 && gpos + 16 <= n_elements;
-}
-
-// Unconditional 64-bit load for the segment at gpos, clamped in bounds
-// (requires n_elements >= 16); out-of-range segments are re-read checked.
-__device__ __forceinline__ uint2 fetch_nibbles(const uint8_t *__restrict__ packed,
-                                               int64_t last8, int64_t gpos) {
-  int64_t q = gpos >> 1;
-  q = q < 0 ? 0 : (q > last8 ? last8 : q);
-  return *reinterpret_cast<const uint2 *>(packed + q);
-}
-
 // Dwords of one staging buffer holding `cap` symbols from a 16-aligned base
 // (<= 15 leading nibbles), rounded to 16 bytes.
-__host__ __device__ constexpr int stage_dwords(int cap) { return ((((cap + 30) >> 4) * 2) + 3) & ~3; }
+__host__ __device__ constexpr int stage_dwords(int cap) {
+  return ((((cap + 30) >> 4) * 2) + 3) & ~3;
+}
 
-constexpr int kPrivSlots = kPrivDwords + 1;  // + spill dword of the last 64-bit OR
+constexpr int kRunSlots = kChunkBits / 8 + 1;  // nibble run dwords + spill of the last OR
+constexpr int kZeroEntry = kTableSize;          // all-zero table entry: a lookup that does nothing
 
-template <int kThreads>
+// kChecked: tensors too small for the clamped vector loads (fewer than 12
+// bitstream bytes or 16 elements) use byte-wise loads throughout.
+template <int kThreads, bool kChecked>
 __global__ __launch_bounds__(kThreads) void decode_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
-    const uint8_t *__restrict__ encoded, int64_t n_bytes, const uint8_t *__restrict__ packed,
+    const uint8_t *__restrict__ encoded, uint32_t n_bytes, const uint8_t *__restrict__ packed,
     const uint64_t *__restrict__ op, const uint8_t *__restrict__ gaps,
-    uint8_t *__restrict__ out, int64_t n_elements, int64_t n_fb, int stage_cap) {
+    uint8_t *__restrict__ out, uint32_t n_elements, int n_fb, int stage_cap) {
   constexpr int kWaves = kThreads / 64;
   extern __shared__ __attribute__((aligned(16))) uint32_t s_stage[];  // 2 x stage_dw
-  __shared__ uint32_t s_table[kTableSize];
+  __shared__ uint32_t s_table[kTableSize + 1];
   __shared__ uint8_t s_luts[ECF8_MAX_LUTS * 256];
-  __shared__ uint32_t s_priv[kPrivSlots * kThreads];  // [slot][lane] nibble runs
+  __shared__ uint32_t s_run[kRunSlots * kThreads];  // [slot][lane] nibble runs
   __shared__ int s_wave_sum[kWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int stage_dw = stage_dwords(stage_cap);
-  uint32_t *const priv = s_priv + tid;  // slot k at priv[k * kThreads]
+  uint32_t *const run = s_run + tid;  // slot k at run[k * kThreads]
 
-  for (int i = tid; i < kTableSize; i += kThreads) s_table[i] = table[i];
+  for (int i = tid; i <= kTableSize; i += kThreads) s_table[i] = i < kTableSize ? table[i] : 0u;
   const int lut_bytes = n_luts * 256;
   for (int i = tid; i < ECF8_MAX_LUTS * 256; i += kThreads) s_luts[i] = i < lut_bytes ? luts[i] : 0;
   const int len_row = (n_luts - 1) * 256;
   const uint32_t max_row = (uint32_t)(n_luts - 2);
 
-  int64_t fb = blockIdx.x;
+  int fb = blockIdx.x;
   if (fb >= n_fb) return;  // uniform per workgroup, before any barrier
-  // tensors shorter than one vector load take the checked byte paths only
-  const bool big_stream = n_bytes >= 16;
-  const bool big_out = n_elements >= 16;
-  const int64_t last16 = (n_bytes - 16) & ~(int64_t)7;  // last 8-aligned 16-byte window
-  const int64_t last8 = ((n_elements >> 1) - 8) & ~(int64_t)7;
-  Chunk cur;
-  {
+  const uint32_t last12 = kChecked ? 0u : ((n_bytes - 12) & ~7u);
+  const uint32_t last8 = kChecked ? 0u : (((n_elements >> 1) - 8) & ~7u);
+
+  auto fetch = [&](int fb_) {
+    const uint32_t g = (uint32_t)fb_ * kThreads + tid;
     RawChunk r;
-    if (big_stream) r = fetch_chunk(encoded, last16, gaps, fb * kThreads + tid);
-    else r.gap_byte = gaps[(fb * kThreads + tid) >> 1];
-    cur = finish_chunk(r, encoded, n_bytes, fb * kThreads + tid);
+    if (kChecked) {
+      r.v = u32x3_a8{0u, 0u, 0u};
+      r.gap_byte = gaps[g >> 1];
+    } else {
+      r = fetch_chunk(encoded, last12, gaps, g);
+    }
+    return r;
+  };
+  Chunk cur = finish_chunk(fetch(fb), encoded, n_bytes, (uint32_t)fb * kThreads + tid, !kChecked);
+  // this block's output range [op_lo, op_hi), wave-uniform.  Positions are
+  // always read (readlane waits on the vector load) before the block's
+  // stores are issued: the memory counter also counts stores, so a later
+  // wait would drain them too.
+  uint32_t op_lo, op_hi;
+  {
+    const uint64_t opv = op[fb + (lane & 1)];
+    op_lo = __builtin_amdgcn_readlane((uint32_t)opv, 0);
+    op_hi = __builtin_amdgcn_readlane((uint32_t)opv, 1);
   }
-  uint64_t op_lo = op[fb], op_hi = op[fb + 1];
   __syncthreads();
 
-  int buf_sel = 0;
-  for (; fb < n_fb; fb += gridDim.x, buf_sel ^= 1) {
+  for (int buf_sel = 0;; buf_sel ^= 1) {
     uint32_t *const stage = s_stage + buf_sel * stage_dw;
-    const int64_t fb_next = fb + gridDim.x;
-    const bool has_next = fb_next < n_fb;
+    const int fb_next = fb + (int)gridDim.x;
+    // prefetch target: the next block, or this one again after the last (in
+    // bounds, discarded) so no load or wait depends on a branch
+    const int fb_pf = fb_next < n_fb ? fb_next : fb;
 
     // ---- this block's output range; prefetch its sign/mantissa bytes
-    const int64_t start = (int64_t)op_lo;
-    int64_t end = (int64_t)op_hi;
+    const uint32_t start = op_lo;
+    uint32_t end = op_hi;
     if (end > n_elements) end = n_elements;
-    const int64_t base = start & ~(int64_t)15;
-    int64_t total = end - start;
-    if (total < 0 || start < 0) total = 0;  // malformed positions write nothing
+    int total = (int)end - (int)start;
+    if (total < 0 || start > n_elements) total = 0;  // malformed positions write nothing
     if (total > stage_cap) total = stage_cap;
+    const uint32_t base = start & ~15u;  // 16-element aligned sweep origin
     const int lead = (int)(start - base);
-    const int stage_nib = total > 0 ? lead + (int)total : 0;
+    const int stage_nib = total > 0 ? lead + total : 0;
     const int seg_dw = ((stage_nib + 15) >> 4) * 2;
     const int nseg = seg_dw >> 1;
-    // segments past nseg re-read the last one (no extra HBM traffic)
-    const int last_seg = nseg > 0 ? nseg - 1 : 0;
     uint2 pre0 = make_uint2(0, 0), pre1 = make_uint2(0, 0);
-    if (big_out) {
-      pre0 = fetch_nibbles(packed, last8, base + 16 * (int64_t)min(tid, last_seg));
-      pre1 = fetch_nibbles(packed, last8, base + 16 * (int64_t)min(tid + kThreads, last_seg));
+    if (!kChecked) {
+      // segments past nseg re-read the last one (no extra HBM traffic)
+      const int last_seg = nseg > 0 ? nseg - 1 : 0;
+      uint32_t q0 = (base >> 1) + 8u * (uint32_t)min(tid, last_seg);
+      uint32_t q1 = (base >> 1) + 8u * (uint32_t)min(tid + kThreads, last_seg);
+      pre0 = *reinterpret_cast<const uint2 *>(packed + (q0 < last8 ? q0 : last8));
+      pre1 = *reinterpret_cast<const uint2 *>(packed + (q1 < last8 ? q1 : last8));
     }
 
-    // ---- prefetch the next block's chunk and positions with vector loads
-    // (left unset past the last block: the loop ends before they are read)
-    RawChunk nxt_raw;
-    uint64_t nop = 0;
-    if (has_next) {
-      if (big_stream) nxt_raw = fetch_chunk(encoded, last16, gaps, fb_next * kThreads + tid);
-      else nxt_raw.gap_byte = gaps[(fb_next * kThreads + tid) >> 1];
-      nop = op[fb_next + (lane & 1)];
-    }
+    // ---- prefetch the next block's chunk and positions (vector loads, so
+    // the LDS waits of the decode below never wait on them)
+    const RawChunk nxt_raw = fetch(fb_pf);
+    const uint64_t nopv = op[fb_pf + (lane & 1)];
 
     // ---- 1. decode the codes this lane's chunk owns into its nibble run
 #pragma unroll
-    for (int k = 0; k < kPrivSlots; ++k) priv[k * kThreads] = 0u;
+    for (int k = 0; k < kRunSlots; ++k) run[k * kThreads] = 0u;
     const int zero4 = (seg_dw + 3) >> 2;
     for (int i = tid; i < zero4; i += kThreads)
       reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
 
-    int p = (int)cur.gap;
-    uint64_t buf = cur.hi << cur.gap;
-    int cnt = 0;
-    auto emit = [&](uint32_t syms, uint32_t n) {
-      const uint64_t v = (uint64_t)syms << ((cnt & 7) * 4);
-      uint32_t *q = priv + (cnt >> 3) * kThreads;
+    int p = (int)cur.gap;              // bit offset of the next code in the chunk
+    uint64_t buf = cur.hi << cur.gap;  // the bits from p on, left-aligned
+    int cnt = 0;                       // exponents in the run
+    // OR an entry's exponents (its unused nibbles are zero) at nibble cnt of
+    // the run; nibbles past the counted ones are masked off by the copy
+    auto emit = [&](uint32_t e, uint32_t n) {
+      const uint64_t v = (uint64_t)(e & 0xFFFFu) << ((cnt & 7) * 4);
+      uint32_t *q = run + (cnt >> 3) * kThreads;
       atomicOr(q, (uint32_t)v);
       atomicOr(q + kThreads, (uint32_t)(v >> 32));
-      cnt += n;
+      cnt += (int)n;
     };
-    // symbols starting before bit 48: all fit the 64-bit window with 16
-    // bits to spare, and every symbol of a table entry starts before 60
-    while (p < 48) {
-      const uint32_t e = s_table[(uint32_t)(buf >> 52)];
-      uint32_t len = entry_len(e), syms = e & 0xFFFFu, n = __builtin_popcount(e & 0x0FFF0000u);
-      if (len == 0) {  // code longer than 12 bits: one symbol via the two-level LUT
-        const uint32_t w16 = (uint32_t)(buf >> 48);
-        uint32_t v = s_luts[w16 >> 8];
-        if (v >= 240) {
-          const uint32_t row = min(256 - v, max_row);
-          v = s_luts[row * 256 + (w16 & 0xFF)];
-        }
-        len = s_luts[len_row + v];
-        if (len == 0) {  // code-less LUT entry (EOF pad bits): chunk ends
-          p = kChunkBits;
-          break;
-        }
-        syms = v & 0xF;
-        n = 1;
-      }
-      emit(syms, n);
-      p += len;
+    // A lookup at a code longer than the 12-bit window reads an all-zero
+    // entry: the lane emits nothing and stays in place ("parked") until the
+    // exact path below.  Codes starting before bit 53 have 12 valid window
+    // bits and all their entry's symbols end inside the chunk.  Every lane
+    // starts below bit 16 and a lookup spans at most 12 bits, so the first
+    // four lookups need no predicate.
+    uint32_t e = 1;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      e = s_table[(uint32_t)(buf >> 52)];
+      const uint32_t len = entry_len(e);
+      emit(e, __builtin_popcount(entry_mask(e)));
+      p += (int)len;
       buf <<= len;
     }
-    // symbols starting in [48, 64): window rebuilt from chunk bits 32..79;
-    // table symbols starting at or after bit 64 belong to the next chunk
-    if (p < kChunkBits) {
-      buf = ((cur.hi << 32) | ((uint64_t)cur.la << 16)) << (p - 32);
-      while (p < kChunkBits) {
-        const uint32_t e = s_table[(uint32_t)(buf >> 52)];
-        uint32_t len = entry_len(e), syms = e & 0xFFFFu, mask = entry_mask(e);
-        if (len == 0) {
-          const uint32_t w16 = (uint32_t)(buf >> 48);
-          uint32_t v = s_luts[w16 >> 8];
-          if (v >= 240) {
-            const uint32_t row = min(256 - v, max_row);
-            v = s_luts[row * 256 + (w16 & 0xFF)];
+    // then while any lane of the wave is active; inactive lanes read the
+    // zero entry, which changes nothing
+    bool act = e != 0 && p < 53;
+    while (__builtin_amdgcn_ballot_w64(act)) {
+      e = s_table[act ? (uint32_t)(buf >> 52) : (uint32_t)kZeroEntry];
+      const uint32_t len = entry_len(e);
+      emit(e, __builtin_popcount(entry_mask(e)));
+      p += (int)len;
+      buf <<= len;
+      act = act && e != 0 && p < 53;
+    }
+    // codes starting in [53, 64) (lanes that did not park): window rebuilt
+    // from chunk bits 32..79; entry symbols starting at or after bit 64
+    // belong to the next chunk
+    act = p >= 53 && p < kChunkBits;
+    if (__builtin_amdgcn_ballot_w64(act)) {
+      buf = ((cur.hi << 32) | ((uint64_t)cur.la << 16)) << ((p - 32) & 63);
+      while (__builtin_amdgcn_ballot_w64(act)) {
+        e = s_table[act ? (uint32_t)(buf >> 52) : (uint32_t)kZeroEntry];
+        uint32_t len = entry_len(e);
+        const uint32_t rem = (uint32_t)(kChunkBits - p) & 31u;  // 1..11 when active
+        const uint32_t mask = entry_mask(e);
+        const uint32_t kept = mask & ((1u << rem) - 1);
+        emit(e, __builtin_popcount(kept));
+        len = kept != mask ? rem : len;  // the lane ends at bit 64
+        p += (int)len;
+        buf <<= (len & 63);
+        act = act && e != 0 && p < kChunkBits;
+      }
+    }
+    // parked lanes (a code longer than 12 bits, rare): the exact rule,
+    // through the table where it decides and the two-level LUT where not
+    if (__builtin_amdgcn_ballot_w64(p < kChunkBits)) {
+      if (p < kChunkBits) {
+        int q = p;
+        while (q < kChunkBits) {
+          const uint32_t w16 = window16(cur.hi, cur.la, q);
+          uint32_t f = s_table[w16 >> 4];
+          uint32_t len = entry_len(f), mask = entry_mask(f);
+          if (len == 0) {
+            uint32_t v = s_luts[w16 >> 8];
+            if (v >= 240) {
+              const uint32_t row = min(256 - v, max_row);
+              v = s_luts[row * 256 + (w16 & 0xFF)];
+            }
+            len = s_luts[len_row + v];
+            if (len == 0) break;  // code-less entry: only the EOF pad bits reach it
+            f = v & 0xF;
+            mask = 1;
           }
-          len = s_luts[len_row + v];
-          if (len == 0) break;
-          syms = v & 0xF;
-          mask = 1;
-        }
-        const int rem = kChunkBits - p;
-        if (rem < kWinBits) {
-          const uint32_t m2 = mask & ((1u << rem) - 1);
-          if (m2 != mask) {
-            mask = m2;
-            len = rem;
+          const int rem = kChunkBits - q;
+          if (rem < kWinBits) {
+            const uint32_t kept = mask & ((1u << rem) - 1);
+            if (kept != mask) {
+              mask = kept;
+              len = rem;
+            }
           }
+          emit(f, __builtin_popcount(mask));
+          q += (int)len;
         }
-        emit(syms, __builtin_popcount(mask));
-        p += len;
-        buf <<= len;
       }
     }
 
@@ -388,43 +425,37 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 
     // ---- 3. OR this lane's nibble run into the staging buffer
     int c = cnt;
-    if ((int64_t)excl + c > total) c = (int)(total - excl);
+    if (excl + c > total) c = total - excl;
     if (c > 0) {
       const int nib0 = lead + excl;
-      const int sh = (nib0 & 7) * 4;
-      const int d0 = nib0 >> 3;
+      const uint32_t sh = (uint32_t)(nib0 & 7) * 4;
+      uint32_t *const dst = stage + (nib0 >> 3);
       const int ndw = (c + 7) >> 3;
+      const uint32_t last_mask = (c & 7) ? (1u << (4 * (c & 7))) - 1 : 0xFFFFFFFFu;
       uint32_t carry = 0;
-#pragma unroll
-      for (int k = 0; k < kPrivDwords; ++k) {
-        if (k < ndw) {
-          uint32_t v = priv[k * kThreads];
-          if (k == ndw - 1 && (c & 7)) v &= (1u << (4 * (c & 7))) - 1;
-          atomicOr(&stage[d0 + k], (v << sh) | carry);
-          carry = sh ? (v >> (32 - sh)) : 0u;
-        }
+      for (int k = 0; k < ndw; ++k) {
+        uint32_t v = run[k * kThreads];
+        v &= k == ndw - 1 ? last_mask : 0xFFFFFFFFu;
+        const uint64_t w = (uint64_t)v << sh;
+        atomicOr(dst + k, (uint32_t)w | carry);
+        carry = (uint32_t)(w >> 32);
       }
-      if (carry) atomicOr(&stage[d0 + ndw], carry);
+      if (carry) atomicOr(dst + ndw, carry);
     }
     __syncthreads();
 
-    // the next block's chunk, fetched a whole decode phase ago
-    if (has_next) {
-      cur = finish_chunk(nxt_raw, encoded, n_bytes, fb_next * kThreads + tid);
-      const uint32_t lo0 = __builtin_amdgcn_readlane((uint32_t)nop, 0);
-      const uint32_t lo1 = __builtin_amdgcn_readlane((uint32_t)(nop >> 32), 0);
-      const uint32_t hi0 = __builtin_amdgcn_readlane((uint32_t)nop, 1);
-      const uint32_t hi1 = __builtin_amdgcn_readlane((uint32_t)(nop >> 32), 1);
-      op_lo = ((uint64_t)lo1 << 32) | lo0;
-      op_hi = ((uint64_t)hi1 << 32) | hi0;
-    }
+    // the next block's chunk and positions, fetched a whole decode phase ago
+    const Chunk nxt = finish_chunk(nxt_raw, encoded, n_bytes, (uint32_t)fb_pf * kThreads + tid,
+                                   !kChecked);
+    const uint32_t nop_lo = __builtin_amdgcn_readlane((uint32_t)nopv, 0);
+    const uint32_t nop_hi = __builtin_amdgcn_readlane((uint32_t)nopv, 1);
 
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
     for (int s = tid, k = 0; s < nseg; s += kThreads, ++k) {
       const uint2 ev = reinterpret_cast<const uint2 *>(stage)[s];
-      const int64_t gpos = base + 16 * (int64_t)s;
+      const uint32_t gpos = base + 16u * (uint32_t)s;
       uint2 ov = k == 0 ? pre0 : pre1;
-      if (k > 1 || !big_out || !nibbles_in_bounds(gpos, n_elements))
+      if (kChecked || k > 1 || gpos + 16 > n_elements)
         ov = load_nibbles_checked(packed, n_elements, gpos);
       const uint2 lo = merge8(ev.x, ov.x);
       const uint2 hi8 = merge8(ev.y, ov.y);
@@ -433,36 +464,39 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
       } else {
         const uint32_t words[4] = {lo.x, lo.y, hi8.x, hi8.y};
         for (int i = 0; i < 16; ++i) {
-          const int64_t q = gpos + i;
+          const uint32_t q = gpos + i;
           if (q >= start && q < end) out[q] = (uint8_t)(words[i >> 2] >> (8 * (i & 3)));
         }
       }
     }
     // the next iteration writes the other staging buffer; its barrier after
     // the scan orders this sweep before any reuse of this one
+    if (fb_next >= n_fb) break;
+    fb = fb_next;
+    cur = nxt;
+    op_lo = nop_lo;
+    op_hi = nop_hi;
   }
 }
 
 struct LaunchCache {
   int device = -1;
   int cus = 0;
-  int occ_cap[4] = {-1, -1, -1, -1};  // stage_cap the occupancy below was computed for
-  int occ[4] = {0, 0, 0, 0};          // per slot: 128, 256, 512, 1024 threads
-  bool attr_set[4] = {false, false, false, false};
+  int occ_cap[8] = {-1, -1, -1, -1, -1, -1, -1, -1};  // stage_cap of occ below
+  int occ[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // per (threads slot, checked) variant
+  bool attr_set[8] = {false, false, false, false, false, false, false, false};
 };
 constexpr int kMaxDevices = 64;
 LaunchCache g_cache[kMaxDevices];
 
-template <int kThreads>
-int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
-                  int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
-                  uint8_t *out, int64_t n_elements, int64_t n_fb, int64_t max_block_elements,
-                  hipStream_t stream, int slot) {
+template <int kThreads, bool kChecked>
+int launch_variant(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
+                   int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
+                   uint8_t *out, int64_t n_elements, int64_t n_fb, int cap, hipStream_t stream,
+                   int slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
-  int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms) ? kMaxSyms
-                                                                        : (int)max_block_elements;
-  if (cap < 16) cap = 16;
   const size_t dyn = 2 * sizeof(uint32_t) * (size_t)stage_dwords(cap);
+  auto kernel = decode_kernel<kThreads, kChecked>;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return ECF8_ERR_HIP;
   LaunchCache &c = g_cache[dev];
@@ -473,25 +507,41 @@ int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const 
   }
   if (!c.attr_set[slot]) {
     const size_t max_dyn = 2 * sizeof(uint32_t) * (size_t)stage_dwords(kMaxSyms);
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(decode_kernel<kThreads>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dyn) != hipSuccess)
       return ECF8_ERR_HIP;
     c.attr_set[slot] = true;
   }
   if (c.occ_cap[slot] != cap) {
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel<kThreads>, kThreads,
-                                                     dyn) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, dyn) != hipSuccess)
       return ECF8_ERR_HIP;
     c.occ[slot] = occ > 0 ? occ : 1;
     c.occ_cap[slot] = cap;
   }
   int64_t grid = (int64_t)c.cus * c.occ[slot];
   if (grid > n_fb) grid = n_fb;
-  hipLaunchKernelGGL(decode_kernel<kThreads>, dim3((unsigned)grid), dim3(kThreads), dyn, stream,
-                     luts, n_luts, table, encoded, n_bytes, packed, op, gaps, out, n_elements,
-                     n_fb, cap);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, stream, luts, n_luts,
+                     table, encoded, (uint32_t)n_bytes, packed, op, gaps, out,
+                     (uint32_t)n_elements, (int)n_fb, cap);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
+template <int kThreads>
+int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
+                  int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
+                  uint8_t *out, int64_t n_elements, int64_t n_fb, int64_t max_block_elements,
+                  hipStream_t stream, int slot) {
+  constexpr int kMaxSyms = kThreads * kChunkBits;
+  int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms) ? kMaxSyms
+                                                                        : (int)max_block_elements;
+  if (cap < 16) cap = 16;
+  // the clamped vector loads need 12 bitstream bytes and 8 nibble bytes
+  if (n_bytes < 12 || n_elements < 16)
+    return launch_variant<kThreads, true>(luts, n_luts, table, encoded, n_bytes, packed, op, gaps,
+                                          out, n_elements, n_fb, cap, stream, 2 * slot + 1);
+  return launch_variant<kThreads, false>(luts, n_luts, table, encoded, n_bytes, packed, op, gaps,
+                                         out, n_elements, n_fb, cap, stream, 2 * slot);
 }
 
 }  // namespace
@@ -510,6 +560,9 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
                            int64_t n_elements, int64_t max_block_elements, const uint32_t *table,
                            int threads_per_block, int bytes_per_thread, void *stream) {
   if (n_bytes < 0 || n_elements < 0 || (n_elements & 1)) return ECF8_ERR_INVALID_ARG;
+  // the reference's positions are 32-bit (decode.cu:23-25, 151); so is this
+  // kernel's index arithmetic
+  if (n_bytes > INT32_MAX - 64 || n_elements > INT32_MAX - 64) return ECF8_ERR_UNSUPPORTED;
   if (bytes_per_thread != kChunkBytes) return ECF8_ERR_UNSUPPORTED;
   if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
   const int64_t fb_bytes = (int64_t)threads_per_block * bytes_per_thread;
@@ -521,7 +574,7 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   if (!luts || !encoded || !output_positions || !gaps || !table ||
       (n_elements > 0 && (!packed_other_4bits || !outputs)))
     return ECF8_ERR_INVALID_ARG;
-  if (((uintptr_t)encoded & 7) || ((uintptr_t)packed_other_4bits & 7) ||
+  if (((uintptr_t)encoded & 15) || ((uintptr_t)packed_other_4bits & 7) ||
       ((uintptr_t)outputs & 15) || ((uintptr_t)table & 3) || ((uintptr_t)output_positions & 7))
     return ECF8_ERR_MISALIGNED;
   hipStream_t s = (hipStream_t)stream;

@@ -55,7 +55,7 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  * by decode_hook (dfloat/run/run.py:97-119) and validate_cuda_decoding_fp8
  * (scripts/compress.py:86-124).  Arguments keep the reference's meaning:
  *   luts               device u8[n_luts*256]   (run.py:109)
- *   encoded            device u8[n_bytes]      (run.py:110), 8-byte aligned
+ *   encoded            device u8[n_bytes]      (run.py:110), 16-byte aligned
  *   packed_other_4bits device u8[n_elements/2] (run.py:111), 8-byte aligned
  *   output_positions   device u64[n_fb+1]      (run.py:112)
  *   gaps               device u8[n_fb*threads_per_block/2] (run.py:113)
@@ -70,7 +70,9 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  * where n_fb = ceil(n_bytes / (threads_per_block*bytes_per_thread)).
  * Geometry: bytes_per_thread must be 8 (the reference kernel hard-codes it,
  * decode.cu:5); threads_per_block one of 128, 256, 512, 1024.
- * Outputs outside [0, n_elements) are never written.
+ * Outputs outside [0, n_elements) are never written.  n_bytes and n_elements
+ * must stay below 2^31 - 64 (the reference's positions are 32-bit,
+ * decode.cu:23-25).
  */
 int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *packed_other_4bits,
                 const uint64_t *output_positions, const uint8_t *gaps, uint8_t *outputs,

@@ -73,7 +73,8 @@ def _decode_call(**kw):
     (dict(n_luts=1), 4),
     (dict(n_luts=19), 4),
     (dict(out=0x6001), 3),      # 16-byte output alignment
-    (dict(encoded=0x2004), 3),  # 8-byte bitstream alignment
+    (dict(encoded=0x2008), 3),  # 16-byte bitstream alignment
+    (dict(n_bytes=2**31), 2),   # positions are 32-bit, as in the reference
     (dict(packed=0x3002), 3),
     (dict(gaps=0), 1),
 ])
