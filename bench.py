@@ -117,7 +117,7 @@ def main():
 
     from ecf8_amd._lib import lib
     from ecf8_amd.compress import compress_flat
-    from ecf8_amd.decode import build_table, decode_into, largest_block
+    from ecf8_amd.decode import build_table, decode_into, largest_block, min_code_bits
     from ecf8_amd.synth import flat_block, qwen3_8b_layer
 
     dev = torch.device("cuda", 0)
@@ -132,6 +132,7 @@ def main():
 
     keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
     max_block = largest_block(block["output_positions"])
+    min_bits = min_code_bits(block["luts"])
     sets = []
     for _ in range(args.copies):
         d = {k: block[k].contiguous().to(dev) for k in keys}
@@ -145,13 +146,13 @@ def main():
     for d in sets:
         decode_into(d["out"], d["luts"], d["encoded"], d["packed_other_4bits"],
                     d["output_positions"], d["gaps"], table=d["table"],
-                    max_block_elements=max_block)
+                    max_block_elements=max_block, min_code_bits=min_bits)
     L = lib()
     hstream = torch.cuda.current_stream(dev).cuda_stream
     calls = [(d["luts"].data_ptr(), d["encoded"].data_ptr(), d["packed_other_4bits"].data_ptr(),
               d["output_positions"].data_ptr(), d["gaps"].data_ptr(), d["out"].data_ptr(), n_luts,
-              d["encoded"].numel(), n, max_block, d["table"].data_ptr(), 512, 8, hstream)
-             for d in sets]
+              d["encoded"].numel(), n, max_block, min_bits, d["table"].data_ptr(), 512, 8,
+              hstream) for d in sets]
 
     def step(i):
         rc = L.ecf8_decode(*calls[i % len(calls)])
@@ -166,21 +167,23 @@ def main():
         print("[bench] decoded layer differs from the original FP8 bytes", file=sys.stderr)
         sys.exit(1)
 
+    # One event pair around the K back-to-back launches on the launch stream:
+    # a step is exactly one decode kernel, so the average launch duration is
+    # the timed span over K (events between launches would add their own gaps).
     stream = torch.cuda.current_stream(dev)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
+    start.record(stream)
     for i in range(args.steps):
-        starts[i].record(stream)
         step(i)
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
-    per_launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    total_ms = starts[0].elapsed_time(ends[-1])
+    total_ms = start.elapsed_time(end)
     ms_per_step = total_ms / args.steps
-    avg_launch_ms = sum(per_launch_ms) / len(per_launch_ms)
+    avg_launch_ms = ms_per_step
     gbps = alg / (ms_per_step * 1e-3) / 1e9
     kernel_gbps = alg / (avg_launch_ms * 1e-3) / 1e9
 

@@ -223,33 +223,40 @@ __host__ __device__ constexpr int stage_dwords(int cap) {
   return ((((cap + 30) >> 4) * 2) + 3) & ~3;
 }
 
-constexpr int kRunSlots = kChunkBits / 8 + 1;  // nibble run dwords + spill of the last OR
+// Dwords of a lane's nibble run: room for every symbol a chunk can own when
+// no code is shorter than min_bits, plus the spill dword of the last 64-bit OR.
+__host__ __device__ constexpr int run_slots_for(int min_bits) {
+  return ((kChunkBits + min_bits - 1) / min_bits + 7) / 8 + 1;
+}
 constexpr int kZeroEntry = kTableSize;          // all-zero table entry: a lookup that does nothing
 
 // kChecked: tensors too small for the clamped vector loads (fewer than 12
 // bitstream bytes or 16 elements) use byte-wise loads throughout.
+//
+// SGPRs are capped at 80: measured on MI355X, at 99 SGPRs only 7 waves of
+// 8 per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
+// the cap causes go to VGPR lanes.
 template <int kThreads, bool kChecked>
-__global__ __launch_bounds__(kThreads) void decode_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void decode_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
     const uint8_t *__restrict__ encoded, uint32_t n_bytes, const uint8_t *__restrict__ packed,
     const uint64_t *__restrict__ op, const uint8_t *__restrict__ gaps,
-    uint8_t *__restrict__ out, uint32_t n_elements, int n_fb, int stage_cap) {
+    uint8_t *__restrict__ out, uint32_t n_elements, int n_fb, int stage_cap, int run_slots) {
   constexpr int kWaves = kThreads / 64;
-  extern __shared__ __attribute__((aligned(16))) uint32_t s_stage[];  // 2 x stage_dw
+  // dynamic LDS: [run_slots][kThreads] nibble runs, then 2 staging buffers
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
   __shared__ uint32_t s_table[kTableSize + 1];
-  __shared__ uint8_t s_luts[ECF8_MAX_LUTS * 256];
-  __shared__ uint32_t s_run[kRunSlots * kThreads];  // [slot][lane] nibble runs
   __shared__ int s_wave_sum[kWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int stage_dw = stage_dwords(stage_cap);
-  uint32_t *const run = s_run + tid;  // slot k at run[k * kThreads]
+  uint32_t *const s_stage = s_dyn + run_slots * kThreads;
+  uint32_t *const run = s_dyn + tid;  // slot k at run[k * kThreads]
+  const int max_slot = run_slots - 2;  // last slot a 64-bit OR may start in
 
   for (int i = tid; i <= kTableSize; i += kThreads) s_table[i] = i < kTableSize ? table[i] : 0u;
-  const int lut_bytes = n_luts * 256;
-  for (int i = tid; i < ECF8_MAX_LUTS * 256; i += kThreads) s_luts[i] = i < lut_bytes ? luts[i] : 0;
   const int len_row = (n_luts - 1) * 256;
   const uint32_t max_row = (uint32_t)(n_luts - 2);
 
@@ -270,15 +277,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     return r;
   };
   Chunk cur = finish_chunk(fetch(fb), encoded, n_bytes, (uint32_t)fb * kThreads + tid, !kChecked);
+  // Positions are below 2^31 (checked on the host), so only the low dword of
+  // each little-endian u64 is loaded: a dead high half would be reused as a
+  // temporary and force an early wait on every load in flight.
+  const uint32_t *const op32 = reinterpret_cast<const uint32_t *>(op);
   // this block's output range [op_lo, op_hi), wave-uniform.  Positions are
   // always read (readlane waits on the vector load) before the block's
   // stores are issued: the memory counter also counts stores, so a later
   // wait would drain them too.
   uint32_t op_lo, op_hi;
   {
-    const uint64_t opv = op[fb + (lane & 1)];
-    op_lo = __builtin_amdgcn_readlane((uint32_t)opv, 0);
-    op_hi = __builtin_amdgcn_readlane((uint32_t)opv, 1);
+    const uint32_t opv = op32[2 * (fb + (lane & 1))];
+    op_lo = __builtin_amdgcn_readlane(opv, 0);
+    op_hi = __builtin_amdgcn_readlane(opv, 1);
   }
   __syncthreads();
 
@@ -314,11 +325,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     // ---- prefetch the next block's chunk and positions (vector loads, so
     // the LDS waits of the decode below never wait on them)
     const RawChunk nxt_raw = fetch(fb_pf);
-    const uint64_t nopv = op[fb_pf + (lane & 1)];
+    const uint32_t nopv = op32[2 * (fb_pf + (lane & 1))];
 
     // ---- 1. decode the codes this lane's chunk owns into its nibble run
-#pragma unroll
-    for (int k = 0; k < kRunSlots; ++k) run[k * kThreads] = 0u;
+    for (int k = 0; k < run_slots; ++k) run[k * kThreads] = 0u;
     const int zero4 = (seg_dw + 3) >> 2;
     for (int i = tid; i < zero4; i += kThreads)
       reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
@@ -330,7 +340,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     // the run; nibbles past the counted ones are masked off by the copy
     auto emit = [&](uint32_t e, uint32_t n) {
       const uint64_t v = (uint64_t)(e & 0xFFFFu) << ((cnt & 7) * 4);
-      uint32_t *q = run + (cnt >> 3) * kThreads;
+      // runs are sized for the block's shortest code; the clamp only keeps
+      // LDS accesses in bounds for inputs that break that bound
+      uint32_t *q = run + min(cnt >> 3, max_slot) * kThreads;
       atomicOr(q, (uint32_t)v);
       atomicOr(q + kThreads, (uint32_t)(v >> 32));
       cnt += (int)n;
@@ -390,12 +402,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
           uint32_t f = s_table[w16 >> 4];
           uint32_t len = entry_len(f), mask = entry_mask(f);
           if (len == 0) {
-            uint32_t v = s_luts[w16 >> 8];
+            uint32_t v = luts[w16 >> 8];
             if (v >= 240) {
               const uint32_t row = min(256 - v, max_row);
-              v = s_luts[row * 256 + (w16 & 0xFF)];
+              v = luts[row * 256 + (w16 & 0xFF)];
             }
-            len = s_luts[len_row + v];
+            len = luts[len_row + v];
             if (len == 0) break;  // code-less entry: only the EOF pad bits reach it
             f = v & 0xF;
             mask = 1;
@@ -430,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
       const int nib0 = lead + excl;
       const uint32_t sh = (uint32_t)(nib0 & 7) * 4;
       uint32_t *const dst = stage + (nib0 >> 3);
-      const int ndw = (c + 7) >> 3;
+      const int ndw = min((c + 7) >> 3, run_slots - 1);
       const uint32_t last_mask = (c & 7) ? (1u << (4 * (c & 7))) - 1 : 0xFFFFFFFFu;
       uint32_t carry = 0;
       for (int k = 0; k < ndw; ++k) {
@@ -447,8 +459,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     // the next block's chunk and positions, fetched a whole decode phase ago
     const Chunk nxt = finish_chunk(nxt_raw, encoded, n_bytes, (uint32_t)fb_pf * kThreads + tid,
                                    !kChecked);
-    const uint32_t nop_lo = __builtin_amdgcn_readlane((uint32_t)nopv, 0);
-    const uint32_t nop_hi = __builtin_amdgcn_readlane((uint32_t)nopv, 1);
+    const uint32_t nop_lo = __builtin_amdgcn_readlane(nopv, 0);
+    const uint32_t nop_hi = __builtin_amdgcn_readlane(nopv, 1);
 
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
     for (int s = tid, k = 0; s < nseg; s += kThreads, ++k) {
@@ -482,8 +494,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 struct LaunchCache {
   int device = -1;
   int cus = 0;
-  int occ_cap[8] = {-1, -1, -1, -1, -1, -1, -1, -1};  // stage_cap of occ below
-  int occ[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // per (threads slot, checked) variant
+  size_t occ_dyn[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // dynamic LDS of occ below
+  int occ[8] = {0, 0, 0, 0, 0, 0, 0, 0};         // per (threads slot, checked) variant
   bool attr_set[8] = {false, false, false, false, false, false, false, false};
 };
 constexpr int kMaxDevices = 64;
@@ -492,10 +504,11 @@ LaunchCache g_cache[kMaxDevices];
 template <int kThreads, bool kChecked>
 int launch_variant(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
                    int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
-                   uint8_t *out, int64_t n_elements, int64_t n_fb, int cap, hipStream_t stream,
-                   int slot) {
+                   uint8_t *out, int64_t n_elements, int64_t n_fb, int cap, int run_slots,
+                   hipStream_t stream, int slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
-  const size_t dyn = 2 * sizeof(uint32_t) * (size_t)stage_dwords(cap);
+  const size_t dyn =
+      sizeof(uint32_t) * ((size_t)run_slots * kThreads + 2 * (size_t)stage_dwords(cap));
   auto kernel = decode_kernel<kThreads, kChecked>;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return ECF8_ERR_HIP;
@@ -506,24 +519,25 @@ int launch_variant(const uint8_t *luts, int n_luts, const uint32_t *table, const
     c.device = dev;
   }
   if (!c.attr_set[slot]) {
-    const size_t max_dyn = 2 * sizeof(uint32_t) * (size_t)stage_dwords(kMaxSyms);
+    const size_t max_dyn = sizeof(uint32_t) * ((size_t)run_slots_for(1) * kThreads +
+                                               2 * (size_t)stage_dwords(kMaxSyms));
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dyn) != hipSuccess)
       return ECF8_ERR_HIP;
     c.attr_set[slot] = true;
   }
-  if (c.occ_cap[slot] != cap) {
+  if (c.occ_dyn[slot] != dyn) {
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, dyn) != hipSuccess)
       return ECF8_ERR_HIP;
     c.occ[slot] = occ > 0 ? occ : 1;
-    c.occ_cap[slot] = cap;
+    c.occ_dyn[slot] = dyn;
   }
   int64_t grid = (int64_t)c.cus * c.occ[slot];
   if (grid > n_fb) grid = n_fb;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, stream, luts, n_luts,
                      table, encoded, (uint32_t)n_bytes, packed, op, gaps, out,
-                     (uint32_t)n_elements, (int)n_fb, cap);
+                     (uint32_t)n_elements, (int)n_fb, cap, run_slots);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
@@ -531,17 +545,19 @@ template <int kThreads>
 int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
                   int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
                   uint8_t *out, int64_t n_elements, int64_t n_fb, int64_t max_block_elements,
-                  hipStream_t stream, int slot) {
+                  int min_code_bits, hipStream_t stream, int slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms) ? kMaxSyms
                                                                         : (int)max_block_elements;
   if (cap < 16) cap = 16;
+  const int run_slots = run_slots_for(min_code_bits >= 1 && min_code_bits <= 16 ? min_code_bits : 1);
   // the clamped vector loads need 12 bitstream bytes and 8 nibble bytes
   if (n_bytes < 12 || n_elements < 16)
     return launch_variant<kThreads, true>(luts, n_luts, table, encoded, n_bytes, packed, op, gaps,
-                                          out, n_elements, n_fb, cap, stream, 2 * slot + 1);
+                                          out, n_elements, n_fb, cap, run_slots, stream,
+                                          2 * slot + 1);
   return launch_variant<kThreads, false>(luts, n_luts, table, encoded, n_bytes, packed, op, gaps,
-                                         out, n_elements, n_fb, cap, stream, 2 * slot);
+                                         out, n_elements, n_fb, cap, run_slots, stream, 2 * slot);
 }
 
 }  // namespace
@@ -557,8 +573,9 @@ extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table
 extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
                            const uint8_t *packed_other_4bits, const uint64_t *output_positions,
                            const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
-                           int64_t n_elements, int64_t max_block_elements, const uint32_t *table,
-                           int threads_per_block, int bytes_per_thread, void *stream) {
+                           int64_t n_elements, int64_t max_block_elements, int min_code_bits,
+                           const uint32_t *table, int threads_per_block, int bytes_per_thread,
+                           void *stream) {
   if (n_bytes < 0 || n_elements < 0 || (n_elements & 1)) return ECF8_ERR_INVALID_ARG;
   // the reference's positions are 32-bit (decode.cu:23-25, 151); so is this
   // kernel's index arithmetic
@@ -581,15 +598,19 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   switch (threads_per_block) {
     case 128:
       return launch_decode<128>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 0);
+                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
+                                min_code_bits, s, 0);
     case 256:
       return launch_decode<256>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 1);
+                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
+                                min_code_bits, s, 1);
     case 512:
       return launch_decode<512>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 2);
+                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
+                                min_code_bits, s, 2);
     default:
       return launch_decode<1024>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                 output_positions, gaps, outputs, n_elements, n_fb, max_block_elements, s, 3);
+                                 output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
+                                min_code_bits, s, 3);
   }
 }

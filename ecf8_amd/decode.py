@@ -12,7 +12,7 @@ import torch
 
 from ._lib import ECF8_MAX_LUTS, ECF8_TABLE_BYTES, ECF8Error, check, lib
 
-__all__ = ["build_table", "decode_into", "decode", "n_format_blocks", "largest_block",
+__all__ = ["build_table", "decode_into", "decode", "n_format_blocks", "largest_block", "min_code_bits",
            "validate_format", "ECF8Error"]
 
 
@@ -57,6 +57,15 @@ def largest_block(output_positions) -> int:
     return int((op[1:] - op[:-1]).max()) if op.size > 1 else 0
 
 
+def min_code_bits(luts) -> int:
+    """Shortest nonzero code length in a LUT stack's length row (its last
+    row); 0 if the row is empty.  Reads the LUTs on the host: call once per
+    block, not per decode."""
+    row = torch.as_tensor(luts).detach().reshape(-1, 256)[-1].cpu().numpy()
+    nz = row[row > 0]
+    return int(nz.min()) if nz.size else 0
+
+
 def build_table(luts: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Derived multi-symbol decode table (u32[4096] as int32) for ``luts``."""
     if not luts.is_cuda or luts.dtype != torch.uint8 or not luts.is_contiguous():
@@ -79,12 +88,12 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
                 gaps: torch.Tensor, table: torch.Tensor | None = None,
                 threads_per_block: int = 512, bytes_per_thread: int = 8,
                 n_elements: int | None = None, max_block_elements: int = 0,
-                stream=None) -> torch.Tensor:
+                min_code_bits: int = 0, stream=None) -> torch.Tensor:
     """Decode one compressed block into ``out`` (uint8 / e4m3fn, >= n elements).
 
-    ``max_block_elements`` (see largest_block()) sizes the kernel's LDS
-    staging; 0 assumes the worst case, which is always correct but lowers
-    occupancy."""
+    ``max_block_elements`` (see largest_block()) and ``min_code_bits`` (see
+    min_code_bits()) size the kernel's LDS; 0 assumes the worst case, which
+    is always correct but lowers occupancy."""
     dev = encoded.device
     tensors = {"luts": luts, "encoded": encoded, "packed_other_4bits": packed_other_4bits,
                "output_positions": output_positions, "gaps": gaps, "out": out}
@@ -117,7 +126,8 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
         check(lib().ecf8_decode(luts.data_ptr(), encoded.data_ptr(),
                                 packed_other_4bits.data_ptr(), output_positions.data_ptr(),
                                 gaps.data_ptr(), out.data_ptr(), n_luts, n_bytes, n,
-                                int(max_block_elements), table.data_ptr(), threads_per_block,
+                                int(max_block_elements), int(min_code_bits), table.data_ptr(),
+                                threads_per_block,
                                 bytes_per_thread,
                                 _stream_handle(dev, stream)), "ecf8_decode")
     return out
@@ -125,16 +135,19 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
 
 def decode(luts, encoded, packed_other_4bits, output_positions, gaps, table=None,
            threads_per_block=512, bytes_per_thread=8, max_block_elements=None,
-           stream=None) -> torch.Tensor:
-    """Decode one compressed block into a new e4m3fn tensor (computes
-    max_block_elements from the positions when not given)."""
+           min_code_bits=None, stream=None) -> torch.Tensor:
+    """Decode one compressed block into a new e4m3fn tensor (derives
+    max_block_elements and min_code_bits on the host when not given)."""
     n = packed_other_4bits.numel() * 2
     out = torch.empty(n, dtype=torch.float8_e4m3fn, device=encoded.device)
     if max_block_elements is None:
         max_block_elements = largest_block(output_positions)
+    if min_code_bits is None:
+        min_code_bits = globals()["min_code_bits"](luts)
     return decode_into(out, luts, encoded, packed_other_4bits, output_positions, gaps, table,
                        threads_per_block, bytes_per_thread,
-                       max_block_elements=max_block_elements, stream=stream)
+                       max_block_elements=max_block_elements, min_code_bits=min_code_bits,
+                       stream=stream)
 
 
 def validate_format(luts, encoded_bytes: int, packed_other_4bits_bytes: int, output_positions,

@@ -74,7 +74,7 @@ class _DecodeLauncher:
         L = lib()
         check(L.ecf8_build_table(int(luts), int(n_luts), table.data_ptr(), s), "ecf8_build_table")
         check(L.ecf8_decode(int(luts), int(encoded), int(packed), int(op), int(gaps), int(outputs),
-                            int(n_luts), int(n_bytes), int(n_elements), max_block,
+                            int(n_luts), int(n_bytes), int(n_elements), max_block, 0,
                             table.data_ptr(), tpb, bpt, s), "ecf8_decode")
 
 
@@ -117,7 +117,8 @@ class TensorManager:
 def _module_state(module: nn.Module):
     """Per-module decode state, derived once on the module's device and
     rebuilt if the buffers move: the multi-symbol table and the largest
-    format-block (the quantity behind the reference's shared_mem_size)."""
+    format-block (the quantity behind the reference's shared_mem_size) and
+    the shortest code length, which size the kernel's LDS."""
     luts = module.luts
     key = (luts.device, luts.data_ptr(), module.output_positions.data_ptr())
     cached = module.__dict__.get("_ecf8_state")
@@ -128,9 +129,9 @@ def _module_state(module: nn.Module):
             max_block = max(0, int(module.shared_mem_size) - tpb * 4 - 4)
         else:
             max_block = _dev.largest_block(module.output_positions)
-        cached = (key, table, max_block)
+        cached = (key, table, max_block, _dev.min_code_bits(luts))
         module.__dict__["_ecf8_state"] = cached
-    return cached[1], cached[2]
+    return cached[1], cached[2], cached[3]
 
 
 def _inject(module: nn.Module, reconstructed: torch.Tensor) -> None:
@@ -162,11 +163,11 @@ def get_hook(threads_per_block: int, bytes_per_thread: int):
         device = module.encoded.device
         reconstructed = TensorManager.get_tensor(device, n_elements)
         module.__dict__["_ecf8_tpb"] = threads_per_block
-        table, max_block = _module_state(module)
+        table, max_block, min_bits = _module_state(module)
         _dev.decode_into(reconstructed, module.luts, module.encoded, module.packed_other_4bits,
                          module.output_positions, module.gaps, table=table,
                          threads_per_block=threads_per_block, bytes_per_thread=bytes_per_thread,
-                         max_block_elements=max_block)
+                         max_block_elements=max_block, min_code_bits=min_bits)
         _inject(module, reconstructed)
 
     return decode_hook

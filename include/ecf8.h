@@ -67,6 +67,11 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  *                      staging.  0 = unknown (worst case is assumed).  A
  *                      value below the true maximum leaves the excess
  *                      elements of such blocks unwritten.
+ *   min_code_bits      shortest nonzero code length in the LUTs' length row
+ *                      (ecf8 length row = last LUT row); sizes the per-lane
+ *                      LDS run.  0 = unknown (1 bit assumed).  A value above
+ *                      the true minimum can leave outputs wrong, never
+ *                      touches memory out of bounds.
  * where n_fb = ceil(n_bytes / (threads_per_block*bytes_per_thread)).
  * Geometry: bytes_per_thread must be 8 (the reference kernel hard-codes it,
  * decode.cu:5); threads_per_block one of 128, 256, 512, 1024.
@@ -77,8 +82,8 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
 int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *packed_other_4bits,
                 const uint64_t *output_positions, const uint8_t *gaps, uint8_t *outputs,
                 int n_luts, int64_t n_bytes, int64_t n_elements, int64_t max_block_elements,
-                const uint32_t *table, int threads_per_block, int bytes_per_thread,
-                void *stream);
+                int min_code_bits, const uint32_t *table, int threads_per_block,
+                int bytes_per_thread, void *stream);
 
 /* ------------------------------------------------------------------ host */
 

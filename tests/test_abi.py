@@ -62,7 +62,7 @@ def _decode_call(**kw):
     args.update(kw)
     return lib().ecf8_decode(args["luts"], args["encoded"], args["packed"], args["op"],
                              args["gaps"], args["out"], args["n_luts"], args["n_bytes"], args["n"],
-                             0, args["table"], args["tpb"], args["bpt"], None)
+                             0, 0, args["table"], args["tpb"], args["bpt"], None)
 
 
 @pytest.mark.parametrize("kw,status", [
