@@ -47,12 +47,13 @@ def _traffic_from_profile():
 
 def cpu_baseline(block, n_elements, alg_bytes, repeats=3):
     """The oracle's C decoder (single-threaded per format-block range, ranges
-    spread over every host core) on the same compressed layer."""
+    spread over up to 16 host cores) on the same compressed layer."""
     import numpy as np
 
     from oracle import native
 
-    threads = os.cpu_count() or 1
+    # the host share of one GPU is 16 cores; never spread wider than that
+    threads = min(os.cpu_count() or 1, 16)
     args = [block[k].numpy() for k in ("luts", "encoded", "packed_other_4bits",
                                         "output_positions", "gaps")]
     out = np.empty(n_elements, np.uint8)

@@ -62,11 +62,18 @@ __host__ __device__ constexpr uint32_t entry_mask(uint32_t e) { return (e >> 16)
 // only while the reference rule's result provably does not depend on the
 // bits after the window (every LUT entry the unknown bits could select holds
 // the same value), so the table reproduces the rule exactly for any LUT
-// stack, well-formed or not.
+// stack, well-formed or not.  The LUT stack (at most 18 x 256 bytes) is
+// staged in LDS first: the constancy checks read up to 128 entries per step.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void build_table_kernel(const uint8_t *__restrict__ luts,
+__global__ __launch_bounds__(256) void build_table_kernel(const uint8_t *__restrict__ g_luts,
                                                           int n_luts,
                                                           uint32_t *__restrict__ table) {
+  __shared__ uint32_t s_lut_words[ECF8_MAX_LUTS * 64];
+  const int n_words = n_luts * 64;
+  for (int i = threadIdx.x; i < n_words; i += blockDim.x)
+    s_lut_words[i] = reinterpret_cast<const uint32_t *>(g_luts)[i];
+  __syncthreads();
+  const uint8_t *const luts = reinterpret_cast<const uint8_t *>(s_lut_words);
   const int w = blockIdx.x * blockDim.x + threadIdx.x;
   if (w >= kTableSize) return;
   const uint8_t *len_row = luts + 256 * (n_luts - 1);
@@ -565,6 +572,7 @@ int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const 
 extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *stream) {
   if (!luts || !table) return ECF8_ERR_INVALID_ARG;
   if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
+  if (((uintptr_t)luts & 3) || ((uintptr_t)table & 3)) return ECF8_ERR_MISALIGNED;
   hipLaunchKernelGGL(build_table_kernel, dim3(kTableSize / 256), dim3(256), 0,
                      (hipStream_t)stream, luts, n_luts, table);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;

@@ -45,7 +45,8 @@ const char *ecf8_status_string(int status);
  * (dfloat/run/decode.cu:86-91); this table is computed once per compressed
  * block (at load time, like shared_mem_size in dfloat/run/run.py:453-458) and
  * decodes up to four symbols per lookup with exactly the reference's rule.
- *   luts   device u8[n_luts*256]      table  device u32[4096] (output)
+ *   luts   device u8[n_luts*256], 4-byte aligned
+ *   table  device u32[4096] (output), 4-byte aligned
  */
 int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *stream);
 

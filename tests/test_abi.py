@@ -91,3 +91,4 @@ def test_build_table_rejects_bad_lut_count():
 
     assert lib().ecf8_build_table(ctypes.c_void_p(0x1000), 19, ctypes.c_void_p(0x2000), None) == 4
     assert lib().ecf8_build_table(None, 3, ctypes.c_void_p(0x2000), None) == 1
+    assert lib().ecf8_build_table(ctypes.c_void_p(0x1001), 3, ctypes.c_void_p(0x2000), None) == 3

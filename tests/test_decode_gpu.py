@@ -215,6 +215,45 @@ def test_decode_on_a_side_stream(cuda_device):
     assert np.array_equal(out.cpu().numpy(), flat)
 
 
+@pytest.mark.parametrize("seed", [1, 6, 11])  # geometric exponents: 1-bit codes
+def test_min_code_bits_unknown_equals_derived(seed, cuda_device):
+    from ecf8_amd.decode import decode, min_code_bits
+
+    _say(f"min_code_bits seed {seed}")
+    from ecf8_amd.compress import compress_flat
+
+    flat = _random_block(seed)
+    res = compress_flat(torch.from_numpy(flat).view(torch.float8_e4m3fn))
+    shortest = min(bits for sym, (bits, _) in res["table"].items() if isinstance(sym, int))
+    assert min_code_bits(res["luts"]) == shortest
+    d = _dev_block({k: res[k] for k in KEYS}, cuda_device)
+    for bits in (0, None):
+        got = decode(d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
+                     d["gaps"], min_code_bits=bits)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.view(torch.uint8).cpu().numpy(), flat)
+
+
+def test_min_code_bits_above_the_truth_stays_in_bounds(cuda_device):
+    """A min_code_bits larger than the block's shortest code sizes the LDS
+    runs too small; the kernel clamps its run indexes, so outputs may be
+    wrong but nothing outside [0, n) is written."""
+    from ecf8_amd.decode import decode_into
+
+    g = dict(np.load(os.path.join(GOLDEN, "single_exponent.npz")))  # 1-bit codes
+    n = int(g["flat"].size)
+    d = _dev_block(g, cuda_device)
+    out = torch.full((n + 256,), 0x5A, dtype=torch.uint8, device=cuda_device)
+    decode_into(out[:n], d["luts"], d["encoded"], d["packed_other_4bits"],
+                d["output_positions"], d["gaps"], min_code_bits=16)
+    torch.cuda.synchronize()
+    assert (out[n:].cpu().numpy() == 0x5A).all()
+    decode_into(out[:n], d["luts"], d["encoded"], d["packed_other_4bits"],
+                d["output_positions"], d["gaps"], min_code_bits=1)
+    torch.cuda.synchronize()
+    assert np.array_equal(out[:n].cpu().numpy(), g["flat"])
+
+
 # ------------------------------------------------------- drop-in call forms
 
 
