@@ -152,8 +152,8 @@ def main():
     hstream = torch.cuda.current_stream(dev).cuda_stream
     calls = [(d["luts"].data_ptr(), d["encoded"].data_ptr(), d["packed_other_4bits"].data_ptr(),
               d["output_positions"].data_ptr(), d["gaps"].data_ptr(), d["out"].data_ptr(), n_luts,
-              d["encoded"].numel(), n, max_block, min_bits, d["table"].data_ptr(), 512, 8,
-              hstream) for d in sets]
+              d["encoded"].numel(), n, max_block, min_bits, d["table"].data.data_ptr(),
+              d["table"].kind, 512, 8, hstream) for d in sets]
 
     def step(i):
         rc = L.ecf8_decode(*calls[i % len(calls)])

@@ -16,8 +16,11 @@ import torch  # noqa: F401  (must be loaded before libecf8.so)
 from .build import LIB_PATH
 
 ECF8_OK = 0
-ECF8_TABLE_BYTES = 16384
+ECF8_TABLE_BYTES = 24608
 ECF8_MAX_LUTS = 18
+ECF8_TABLE_ANY = -1
+ECF8_TABLE_MULTI = 0
+ECF8_TABLE_DFA = 1
 
 
 class ECF8Error(RuntimeError):
@@ -30,9 +33,10 @@ _vp, _i64, _i32, _u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_
 _SIGNATURES = {
     "ecf8_version": ([], ctypes.c_char_p),
     "ecf8_status_string": ([_i32], ctypes.c_char_p),
-    "ecf8_build_table": ([_vp, _i32, _vp, _vp], _i32),
+    "ecf8_build_table_host": ([_vp, _i32, _i32, _vp, _vp], _i32),
+    "ecf8_build_table": ([_vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "ecf8_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _i32, _i32,
-                     _vp], _i32),
+                     _i32, _vp], _i32),
     "ecf8_encoded_sizes": ([_vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "ecf8_encode_exponents": (
         [_vp, _i64, _vp, _vp, _i32, _u32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _i64],

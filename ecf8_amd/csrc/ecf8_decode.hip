@@ -14,18 +14,22 @@
 // v = L0[W >> 8]; if v >= 240 then v = L[256 - v][W & 0xFF]; length =
 // Llen[v]; the output byte is (o & 8) << 4 | v << 3 | (o & 7).
 //
-// MI355X design (one workgroup per format-block at a time, persistent grid,
-// the next block's bitstream prefetched while the current one decodes):
-//   1. each lane takes one chunk (one 128-bit load: chunk + look-ahead) and
-//      decodes the codes it owns through a 4096-entry multi-symbol table in
-//      LDS (up to 4 symbols per lookup, derived once per compressed block by
-//      build_table_kernel); exponents are ORed as nibbles into a lane-private
-//      LDS run (ds_or_b32, no per-symbol bookkeeping branches);
+// MI355X design: a persistent grid, one workgroup per format-block at a
+// time and one chunk per lane; the next block's bitstream and positions are
+// fetched a whole block ahead.  Per block:
+//   1. each lane decodes the codes its chunk owns through a table derived
+//      once per compressed block (ecf8_tables.cpp), held in LDS:
+//        DFA   kernel: a byte automaton, exactly 8 lookups per chunk plus
+//              one (rarely two) for the code in flight at the chunk's end;
+//              no data-dependent loop, the entries stay in registers;
+//        MULTI kernel: 12-bit windows, up to 4 symbols per lookup, a
+//              predicated loop, exponents ORed into a lane-private LDS run
+//              (any LUT stack, e.g. one with a 1-bit code);
 //   2. the per-chunk symbol counts are prefix-summed (wave64 DPP scan +
 //      per-wave totals in LDS), giving each lane its output offset;
-//   3. each lane ORs its nibble run into a dense LDS staging buffer at that
-//      offset (double-buffered across blocks, sized from the largest block
-//      of the tensor like the reference's shared_mem_size);
+//   3. each lane ORs its exponent nibbles into a dense LDS staging buffer at
+//      that offset (double-buffered across blocks, sized from the largest
+//      block of the tensor like the reference's shared_mem_size);
 //   4. the staging buffer is swept in 16-element segments: 8 exponent
 //      nibbles + 8 bytes of sign/mantissa nibbles (prefetched at block
 //      start) become 16 FP8 bytes with bitfield inserts and byte permutes,
@@ -37,79 +41,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "ecf8.h"
+#include "ecf8_layout.h"
 
 namespace {
 
-constexpr int kWinBits = 12;                 // multi-symbol table index width
-constexpr int kTableSize = 1 << kWinBits;    // 4096 entries, u32 each
-constexpr int kMaxSymsPerEntry = 4;
-constexpr int kChunkBytes = 8;               // bytes_per_thread of the format
-constexpr int kChunkBits = 8 * kChunkBytes;
-
-// Table entry layout:
-//   bits  0..15  up to 4 exponents, first decoded in bits 0..3
-//   bits 16..27  start mask: bit j set iff one of those symbols starts at
-//                window offset j (so popcount = number of symbols)
-//   bits 28..31  total code length of those symbols (0 = no symbol fully
-//                determined by the 12 window bits; decode one symbol with
-//                the two-level LUT instead)
-__host__ __device__ constexpr uint32_t entry_len(uint32_t e) { return e >> 28; }
-__host__ __device__ constexpr uint32_t entry_mask(uint32_t e) { return (e >> 16) & 0xFFFu; }
-
-// ---------------------------------------------------------------------------
-// Table builder: one thread per 12-bit window value.  Symbols are accepted
-// only while the reference rule's result provably does not depend on the
-// bits after the window (every LUT entry the unknown bits could select holds
-// the same value), so the table reproduces the rule exactly for any LUT
-// stack, well-formed or not.  The LUT stack (at most 18 x 256 bytes) is
-// staged in LDS first: the constancy checks read up to 128 entries per step.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void build_table_kernel(const uint8_t *__restrict__ g_luts,
-                                                          int n_luts,
-                                                          uint32_t *__restrict__ table) {
-  __shared__ uint32_t s_lut_words[ECF8_MAX_LUTS * 64];
-  const int n_words = n_luts * 64;
-  for (int i = threadIdx.x; i < n_words; i += blockDim.x)
-    s_lut_words[i] = reinterpret_cast<const uint32_t *>(g_luts)[i];
-  __syncthreads();
-  const uint8_t *const luts = reinterpret_cast<const uint8_t *>(s_lut_words);
-  const int w = blockIdx.x * blockDim.x + threadIdx.x;
-  if (w >= kTableSize) return;
-  const uint8_t *len_row = luts + 256 * (n_luts - 1);
-  uint32_t syms = 0, mask = 0;
-  int n = 0, off = 0;
-  while (n < kMaxSymsPerEntry && off < kWinBits) {
-    const int known = kWinBits - off;  // window bits from this symbol's start
-    // first level: the 8 bits at the symbol start
-    const int kb = known < 8 ? known : 8;
-    const int idx = ((w >> (known - kb)) & ((1 << kb) - 1)) << (8 - kb);
-    const int span = 1 << (8 - kb);
-    int v = luts[idx];
-    bool fixed = true;
-    for (int x = 1; x < span; ++x) fixed &= luts[idx + x] == v;
-    if (!fixed) break;
-    if (v >= 240) {
-      const int row = 256 - v;
-      if (row > n_luts - 2) break;
-      const int known2 = known - 8;  // bits of the second byte inside the window
-      const int kb2 = known2 <= 0 ? 0 : (known2 < 8 ? known2 : 8);
-      const int idx2 = kb2 ? ((w >> (known2 - kb2)) & ((1 << kb2) - 1)) << (8 - kb2) : 0;
-      const int span2 = 1 << (8 - kb2);
-      const uint8_t *r = luts + 256 * row;
-      v = r[idx2];
-      for (int x = 1; x < span2; ++x) fixed &= r[idx2 + x] == v;
-      if (!fixed) break;
-    }
-    const int len = len_row[v];
-    if (len == 0 || len > known || v > 15) break;
-    syms |= (uint32_t)v << (4 * n);
-    mask |= 1u << off;
-    ++n;
-    off += len;
-  }
-  table[w] = n ? (syms | (mask << 16) | ((uint32_t)off << 28)) : 0u;
-}
+using namespace ecf8;
 
 __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
   return (a & m) | (b & ~m);
@@ -142,13 +81,6 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
   return x;
 }
 
-// ---------------------------------------------------------------------------
-// Decoder: one workgroup of T threads per format-block of T chunks at a time
-// (persistent grid; the next block's bitstream is fetched while the current
-// one decodes), one chunk per lane.  Index arithmetic is 32-bit (the
-// format's positions are < 2^31).
-// ---------------------------------------------------------------------------
-
 typedef uint32_t u32x3_a8 __attribute__((ext_vector_type(3), aligned(8)));
 
 // A chunk as fetched: 12 raw bytes from the chunk start (8 chunk bytes, 2
@@ -160,17 +92,9 @@ struct RawChunk {
   uint32_t gap_byte;
 };
 
-// The chunk as a big-endian bit string (hi), its two look-ahead bytes (la)
-// and its gap.
-struct Chunk {
-  uint64_t hi;
-  uint32_t la;
-  uint32_t gap;
-};
-
 // Unconditional 96-bit load of chunk g, the address clamped to the last
 // full 12-byte window so it stays in bounds; lanes near the stream end are
-// re-read byte-wise in finish_chunk.
+// re-read byte-wise when the chunk is finished.
 __device__ __forceinline__ RawChunk fetch_chunk(const uint8_t *__restrict__ encoded, uint32_t last12,
                                                 const uint8_t *__restrict__ gaps, uint32_t g) {
   RawChunk r;
@@ -180,35 +104,22 @@ __device__ __forceinline__ RawChunk fetch_chunk(const uint8_t *__restrict__ enco
   return r;
 }
 
-__device__ __forceinline__ Chunk finish_chunk(const RawChunk &r, const uint8_t *__restrict__ encoded,
-                                              uint32_t n_bytes, uint32_t g, bool vector_ok) {
-  Chunk c;
-  const uint32_t b = g * kChunkBytes;
-  if (vector_ok && b + 12 <= n_bytes) {
-    c.hi = __builtin_bswap64(((uint64_t)r.v.y << 32) | r.v.x);
-    c.la = ((r.v.z & 0xFFu) << 8) | ((r.v.z >> 8) & 0xFFu);
-  } else {  // stream tail: bytes past n_bytes read as zero
-    uint64_t hi = 0;
-    uint32_t la = 0;
-    for (int i = 0; i < kChunkBytes; ++i) {
-      const uint32_t j = b + i;
-      hi = (hi << 8) | (j < n_bytes ? encoded[j] : 0u);
-    }
-    for (int i = kChunkBytes; i < kChunkBytes + 2; ++i) {
-      const uint32_t j = b + i;
-      la = (la << 8) | (j < n_bytes ? encoded[j] : 0u);
-    }
-    c.hi = hi;
-    c.la = la;
-  }
-  c.gap = (g & 1) ? (r.gap_byte & 0xFu) : (r.gap_byte >> 4);
-  return c;
+__device__ __forceinline__ uint32_t gap_of(uint32_t gap_byte, uint32_t g) {
+  return (g & 1) ? (gap_byte & 0xFu) : (gap_byte >> 4);
 }
 
-// Bits [p, p+16) of the 80-bit string hi:la (chunk + look-ahead), p < 64.
-__device__ __forceinline__ uint32_t window16(uint64_t hi, uint32_t la, int p) {
-  const uint64_t w = p < 48 ? (hi << p) : (((hi << 32) | ((uint64_t)la << 16)) << (p - 32));
-  return (uint32_t)(w >> 48);
+// The chunk's 10 bytes as little-endian dwords (byte k of the chunk in bits
+// 8(k%4).. of dword k/4), bytes past n_bytes read as zero.
+__device__ __forceinline__ uint3 chunk_bytes(const RawChunk &r, const uint8_t *__restrict__ encoded,
+                                             uint32_t n_bytes, uint32_t g, bool vector_ok) {
+  const uint32_t b = g * kChunkBytes;
+  if (vector_ok && b + 12 <= n_bytes) return make_uint3(r.v.x, r.v.y, r.v.z);
+  uint32_t d[3] = {0u, 0u, 0u};
+  for (int i = 0; i < kChunkBytes + 2; ++i) {
+    const uint32_t j = b + i;
+    d[i >> 2] |= (j < n_bytes ? (uint32_t)encoded[j] : 0u) << (8 * (i & 3));
+  }
+  return make_uint3(d[0], d[1], d[2]);
 }
 
 // The 8 sign/mantissa bytes of the 16 outputs at the 16-aligned gpos, read
@@ -230,21 +141,324 @@ __host__ __device__ constexpr int stage_dwords(int cap) {
   return ((((cap + 30) >> 4) * 2) + 3) & ~3;
 }
 
+// A format-block's output range and its staging geometry (wave-uniform).
+struct BlockRange {
+  uint32_t start, end;  // outputs [start, end) are written
+  uint32_t base;        // 16-element aligned sweep origin
+  int lead;             // start - base
+  int seg_dw;           // staging dwords in use (whole 16-element segments)
+  int nseg;             // 16-element segments to sweep
+};
+
+__device__ __forceinline__ BlockRange block_range(uint32_t op_lo, uint32_t op_hi,
+                                                  uint32_t n_elements, int stage_cap) {
+  BlockRange r;
+  r.start = op_lo;
+  const uint32_t end = op_hi < n_elements ? op_hi : n_elements;
+  int total = (int)end - (int)op_lo;
+  if (total < 0 || op_lo > n_elements) total = 0;  // malformed positions write nothing
+  if (total > stage_cap) total = stage_cap;         // an understated largest block
+  r.end = op_lo + (uint32_t)total;
+  r.base = op_lo & ~15u;
+  r.lead = (int)(op_lo - r.base);
+  const int stage_nib = total > 0 ? r.lead + total : 0;
+  r.seg_dw = ((stage_nib + 15) >> 4) * 2;
+  r.nseg = r.seg_dw >> 1;
+  return r;
+}
+
+// Sign/mantissa bytes of this lane's first two segments, loaded at block
+// start so they arrive during the decode (segments past nseg re-read the
+// last one: no extra HBM traffic).
+__device__ __forceinline__ void prefetch_nibbles(const BlockRange &br, const uint8_t *packed,
+                                                 uint32_t last8, int tid, int threads, uint2 &pre0,
+                                                 uint2 &pre1) {
+  const int last_seg = br.nseg > 0 ? br.nseg - 1 : 0;
+  const uint32_t q0 = (br.base >> 1) + 8u * (uint32_t)min(tid, last_seg);
+  const uint32_t q1 = (br.base >> 1) + 8u * (uint32_t)min(tid + threads, last_seg);
+  pre0 = *reinterpret_cast<const uint2 *>(packed + (q0 < last8 ? q0 : last8));
+  pre1 = *reinterpret_cast<const uint2 *>(packed + (q1 < last8 ? q1 : last8));
+}
+
+// Step 4: merge the staged exponents with the sign/mantissa nibbles and
+// store the block's FP8 bytes.
+template <int kThreads, bool kChecked>
+__device__ __forceinline__ void write_block(const uint32_t *stage, const BlockRange &br,
+                                            uint2 pre0, uint2 pre1,
+                                            const uint8_t *__restrict__ packed,
+                                            uint32_t n_elements, uint8_t *__restrict__ out,
+                                            int tid) {
+  for (int s = tid, k = 0; s < br.nseg; s += kThreads, ++k) {
+    const uint2 ev = reinterpret_cast<const uint2 *>(stage)[s];
+    const uint32_t gpos = br.base + 16u * (uint32_t)s;
+    uint2 ov = k == 0 ? pre0 : pre1;
+    if (kChecked || k > 1 || gpos + 16 > n_elements)
+      ov = load_nibbles_checked(packed, n_elements, gpos);
+    const uint2 lo = merge8(ev.x, ov.x);
+    const uint2 hi8 = merge8(ev.y, ov.y);
+    if (gpos >= br.start && gpos + 16 <= br.end) {
+      *reinterpret_cast<uint4 *>(out + gpos) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
+    } else {
+      const uint32_t words[4] = {lo.x, lo.y, hi8.x, hi8.y};
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t q = gpos + i;
+        if (q >= br.start && q < br.end) out[q] = (uint8_t)(words[i >> 2] >> (8 * (i & 3)));
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// DFA kernel (tables of kind ECF8_TABLE_DFA)
+// ===========================================================================
+
+// The reference rule (decode.cu:85-112) over one chunk, symbol by symbol,
+// from its gap: f(v) for each symbol starting before bit 64; a code-less
+// LUT entry ends the chunk.  LUT reads go to global memory (rare path).
+template <class F>
+__device__ __forceinline__ void exact_walk(const uint3 &d, uint32_t gap,
+                                           const uint8_t *__restrict__ luts, int n_luts, F &&f) {
+  const uint64_t hi = __builtin_bswap64(((uint64_t)d.y << 32) | d.x);
+  const uint32_t la = ((d.z & 0xFFu) << 8) | ((d.z >> 8) & 0xFFu);
+  const uint32_t len_row = (uint32_t)(n_luts - 1) * 256;
+  const uint32_t max_row = (uint32_t)(n_luts - 2);
+  for (int q = (int)gap; q < kChunkBits;) {
+    const uint64_t w = q < 48 ? (hi << q) : (((hi << 32) | ((uint64_t)la << 16)) << (q - 32));
+    const uint32_t w16 = (uint32_t)(w >> 48);
+    uint32_t v = luts[w16 >> 8];
+    if (v >= 240) v = luts[min(256 - v, max_row) * 256 + (w16 & 0xFF)];
+    const uint32_t len = luts[len_row + v];
+    if (len == 0) break;
+    f(v & 0xFu);
+    q += (int)len;
+  }
+}
+
+// The entry at byte offset `off` of the automaton in LDS.
+__device__ __forceinline__ uint32_t dfa_at(const uint32_t *s_dfa, uint32_t off) {
+  return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(s_dfa) + off);
+}
+
+// kChecked: tensors too small for the clamped vector loads (fewer than 12
+// bitstream bytes or 16 elements) use byte-wise loads throughout.
+//
+// SGPRs are capped at 80: measured on MI355X, above that fewer than 8 waves
+// per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
+// the cap causes go to VGPR lanes.
+template <int kThreads, bool kChecked>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void decode_dfa_kernel(
+    const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
+    const uint8_t *__restrict__ encoded, uint32_t n_bytes,
+    const uint8_t *__restrict__ packed, const uint64_t *__restrict__ op,
+    const uint8_t *__restrict__ gaps, uint8_t *__restrict__ out, uint32_t n_elements, int n_fb,
+    int stage_cap) {
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ int s_wave_sum[kWaves];
+  // dynamic LDS: 2 staging buffers, each followed by spill dwords that take
+  // the ORs of positions past the buffer (malformed or understated input)
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int stage_dw = stage_dwords(stage_cap);
+  const int stage_stride = stage_dw + 4;
+
+  // a row number outside the automaton (only a corrupt table has one) is
+  // replaced by the exact row, so every lookup stays inside s_dfa
+  for (int i = tid; i < kDfaEntries; i += kThreads) {
+    uint32_t e = table[i];
+    if ((e & kDfaRowMask) >= ((uint32_t)kDfaRows << 10))
+      e = (e & ~kDfaRowMask) | ((uint32_t)kDfaExactRow << 10);
+    s_dfa[i] = e;
+  }
+
+  int fb = blockIdx.x;
+  if (fb >= n_fb) return;  // uniform per workgroup, before any barrier
+  const uint32_t last12 = kChecked ? 0u : ((n_bytes - 12) & ~7u);
+  const uint32_t last8 = kChecked ? 0u : (((n_elements >> 1) - 8) & ~7u);
+
+  auto fetch = [&](int fb_) {
+    const uint32_t g = (uint32_t)fb_ * kThreads + tid;
+    RawChunk r;
+    if (kChecked) {
+      r.v = u32x3_a8{0u, 0u, 0u};
+      r.gap_byte = gaps[g >> 1];
+    } else {
+      r = fetch_chunk(encoded, last12, gaps, g);
+    }
+    return r;
+  };
+  uint32_t g_cur = (uint32_t)fb * kThreads + tid;
+  const RawChunk raw0 = fetch(fb);
+  uint3 cur = chunk_bytes(raw0, encoded, n_bytes, g_cur, !kChecked);
+  uint32_t gap = gap_of(raw0.gap_byte, g_cur);
+  // Positions are below 2^31 (checked on the host), so only the low dword of
+  // each little-endian u64 is loaded: a dead high half would be reused as a
+  // temporary and force an early wait on every load in flight.
+  const uint32_t *const op32 = reinterpret_cast<const uint32_t *>(op);
+  // this block's output range, wave-uniform.  Positions are always read
+  // (readlane waits on the vector load) before the block's stores are
+  // issued: the memory counter also counts stores, so a later wait would
+  // drain them too.
+  uint32_t op_lo, op_hi;
+  {
+    const uint32_t opv = op32[2 * (fb + (lane & 1))];
+    op_lo = __builtin_amdgcn_readlane(opv, 0);
+    op_hi = __builtin_amdgcn_readlane(opv, 1);
+  }
+  __syncthreads();
+
+  for (int buf_sel = 0;; buf_sel ^= 1) {
+    uint32_t *const stage = s_dyn + buf_sel * stage_stride;
+    const int fb_next = fb + (int)gridDim.x;
+    // prefetch target: the next block, or this one again after the last (in
+    // bounds, discarded) so no load or wait depends on a branch
+    const int fb_pf = fb_next < n_fb ? fb_next : fb;
+
+    const BlockRange br = block_range(op_lo, op_hi, n_elements, stage_cap);
+    uint2 pre0 = make_uint2(0, 0), pre1 = make_uint2(0, 0);
+    if (!kChecked) prefetch_nibbles(br, packed, last8, tid, kThreads, pre0, pre1);
+    // the next block's chunk and positions (vector loads, so the LDS waits
+    // below never wait on them)
+    const RawChunk nxt_raw = fetch(fb_pf);
+    const uint32_t nopv = op32[2 * (fb_pf + (lane & 1))];
+
+    for (int i = tid; i < ((br.seg_dw + 3) >> 2); i += kThreads)
+      reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
+
+    // ---- 1. the byte automaton over this lane's chunk.  The first code
+    // starts at bit `gap`: inside byte 0 (start from the skip-`gap` row) or
+    // inside byte 1 (byte 0 is skipped whole, then `gap - 8` bits).
+    const uint32_t a0 = gap < 8 ? ((gap << 10) | ((cur.x << 2) & 0x3FCu))
+                                : (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
+    const uint32_t e0 = dfa_at(s_dfa, a0);
+    const uint32_t e1 = dfa_at(s_dfa, (e0 & kDfaRowMask) | ((cur.x >> 6) & 0x3FCu));
+    const uint32_t e2 = dfa_at(s_dfa, (e1 & kDfaRowMask) | ((cur.x >> 14) & 0x3FCu));
+    const uint32_t e3 = dfa_at(s_dfa, (e2 & kDfaRowMask) | ((cur.x >> 22) & 0x3FCu));
+    const uint32_t e4 = dfa_at(s_dfa, (e3 & kDfaRowMask) | ((cur.y << 2) & 0x3FCu));
+    const uint32_t e5 = dfa_at(s_dfa, (e4 & kDfaRowMask) | ((cur.y >> 6) & 0x3FCu));
+    const uint32_t e6 = dfa_at(s_dfa, (e5 & kDfaRowMask) | ((cur.y >> 14) & 0x3FCu));
+    const uint32_t e7 = dfa_at(s_dfa, (e6 & kDfaRowMask) | ((cur.y >> 22) & 0x3FCu));
+    // A code still open at bit 64 started in this chunk, so it is owned
+    // here: its symbol is the first one completed in the look-ahead bytes
+    // (codes are at most 16 bits, so it ends in byte 8 or 9).
+    const uint32_t row7 = e7 & kDfaRowMask;
+    const bool open = row7 >= ((uint32_t)kDfaFirstPendingRow << 10);
+    uint32_t e8 = dfa_at(s_dfa, row7 | ((cur.z << 2) & 0x3FCu));
+    if (__builtin_amdgcn_ballot_w64(open && (e8 & 7u) == 0)) {
+      const uint32_t e9 = dfa_at(s_dfa, (e8 & kDfaRowMask) | ((cur.z >> 6) & 0x3FCu));
+      if ((e8 & 7u) == 0) e8 = e9;
+    }
+    const uint32_t et = open ? ((e8 & 0xF0000u) | 1u) : 0u;
+    int cnt = (int)((e0 & 7u) + (e1 & 7u) + (e2 & 7u) + (e3 & 7u) + (e4 & 7u) + (e5 & 7u) +
+                    (e6 & 7u) + (e7 & 7u) + (et & 7u));
+    // lanes in the exact row (the stream's final padding) count their chunk
+    // with the reference rule instead
+    const bool exact = row7 == ((uint32_t)kDfaExactRow << 10);
+    const bool any_exact = __builtin_amdgcn_ballot_w64(exact) != 0;
+    if (any_exact && exact) {
+      int n = 0;
+      exact_walk(cur, gap, luts, n_luts, [&](uint32_t) { ++n; });
+      cnt = n;
+    }
+
+    // ---- 2. block-wide exclusive prefix of the per-chunk symbol counts
+    const int incl = wave_inclusive_scan(cnt);
+    if (lane == 63) s_wave_sum[wave] = incl;
+    __syncthreads();
+    int excl = incl - cnt;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      if (w < wave) excl += s_wave_sum[w];
+
+    // ---- 3. OR the exponents into the staging buffer at their positions,
+    // two automaton entries (at most 8 symbols, 32 bits) per 64-bit OR.
+    // Symbols past the block's count (only the stream's last chunk decodes
+    // any: padding) land past the block's outputs and are never stored;
+    // positions past the buffer go to its spill dwords.
+    uint32_t pos4 = (uint32_t)(br.lead + excl) << 2;  // bit offset in the buffer
+    const uint32_t spill = (uint32_t)stage_dw;
+    auto put = [&](uint32_t syms, uint32_t n4) {
+      const uint64_t v = (uint64_t)syms << (pos4 & 31u);
+      uint32_t *const q = stage + min(pos4 >> 5, spill);
+      atomicOr(q, (uint32_t)v);
+      atomicOr(q + 1, (uint32_t)(v >> 32));
+      pos4 += n4;
+    };
+    auto put2 = [&](uint32_t ea, uint32_t eb) {
+      const uint32_t na4 = (ea & 7u) << 2;
+      put(((eb >> 16) << na4) | (ea >> 16), na4 + ((eb & 7u) << 2));
+    };
+    if (!any_exact || !exact) {
+      put2(e0, e1);
+      put2(e2, e3);
+      put2(e4, e5);
+      put2(e6, e7);
+      put(et >> 16, 0u);
+    } else {
+      exact_walk(cur, gap, luts, n_luts, [&](uint32_t v) { put(v, 4u); });
+    }
+    __syncthreads();
+
+    // the next block's chunk and positions, fetched a whole decode phase ago
+    g_cur = (uint32_t)fb_pf * kThreads + tid;
+    const uint3 nxt = chunk_bytes(nxt_raw, encoded, n_bytes, g_cur, !kChecked);
+    const uint32_t nxt_gap = gap_of(nxt_raw.gap_byte, g_cur);
+    const uint32_t nop_lo = __builtin_amdgcn_readlane(nopv, 0);
+    const uint32_t nop_hi = __builtin_amdgcn_readlane(nopv, 1);
+
+    // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
+    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, tid);
+    // the next iteration writes the other staging buffer; its barrier after
+    // the scan orders this sweep before any reuse of this one
+    if (fb_next >= n_fb) break;
+    fb = fb_next;
+    cur = nxt;
+    gap = nxt_gap;
+    op_lo = nop_lo;
+    op_hi = nop_hi;
+  }
+}
+
+// ===========================================================================
+// MULTI kernel (tables of kind ECF8_TABLE_MULTI)
+// ===========================================================================
+
+// The chunk as a big-endian bit string (hi), its two look-ahead bytes (la)
+// and its gap.
+struct Chunk {
+  uint64_t hi;
+  uint32_t la;
+  uint32_t gap;
+};
+
+__device__ __forceinline__ Chunk finish_chunk(const RawChunk &r, const uint8_t *__restrict__ encoded,
+                                              uint32_t n_bytes, uint32_t g, bool vector_ok) {
+  const uint3 d = chunk_bytes(r, encoded, n_bytes, g, vector_ok);
+  Chunk c;
+  c.hi = __builtin_bswap64(((uint64_t)d.y << 32) | d.x);
+  c.la = ((d.z & 0xFFu) << 8) | ((d.z >> 8) & 0xFFu);
+  c.gap = gap_of(r.gap_byte, g);
+  return c;
+}
+
+// Bits [p, p+16) of the 80-bit string hi:la (chunk + look-ahead), p < 64.
+__device__ __forceinline__ uint32_t window16(uint64_t hi, uint32_t la, int p) {
+  const uint64_t w = p < 48 ? (hi << p) : (((hi << 32) | ((uint64_t)la << 16)) << (p - 32));
+  return (uint32_t)(w >> 48);
+}
+
 // Dwords of a lane's nibble run: room for every symbol a chunk can own when
 // no code is shorter than min_bits, plus the spill dword of the last 64-bit OR.
 __host__ __device__ constexpr int run_slots_for(int min_bits) {
   return ((kChunkBits + min_bits - 1) / min_bits + 7) / 8 + 1;
 }
-constexpr int kZeroEntry = kTableSize;          // all-zero table entry: a lookup that does nothing
+constexpr int kZeroEntry = kMultiEntries;  // all-zero table entry: a lookup that does nothing
 
-// kChecked: tensors too small for the clamped vector loads (fewer than 12
-// bitstream bytes or 16 elements) use byte-wise loads throughout.
-//
-// SGPRs are capped at 80: measured on MI355X, at 99 SGPRs only 7 waves of
-// 8 per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
-// the cap causes go to VGPR lanes.
 template <int kThreads, bool kChecked>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void decode_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void decode_multi_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
     const uint8_t *__restrict__ encoded, uint32_t n_bytes, const uint8_t *__restrict__ packed,
     const uint64_t *__restrict__ op, const uint8_t *__restrict__ gaps,
@@ -252,7 +466,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   constexpr int kWaves = kThreads / 64;
   // dynamic LDS: [run_slots][kThreads] nibble runs, then 2 staging buffers
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
-  __shared__ uint32_t s_table[kTableSize + 1];
+  __shared__ uint32_t s_table[kMultiEntries + 1];
   __shared__ int s_wave_sum[kWaves];
 
   const int tid = threadIdx.x;
@@ -263,7 +477,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   uint32_t *const run = s_dyn + tid;  // slot k at run[k * kThreads]
   const int max_slot = run_slots - 2;  // last slot a 64-bit OR may start in
 
-  for (int i = tid; i <= kTableSize; i += kThreads) s_table[i] = i < kTableSize ? table[i] : 0u;
+  for (int i = tid; i <= kMultiEntries; i += kThreads)
+    s_table[i] = i < kMultiEntries ? table[i] : 0u;
   const int len_row = (n_luts - 1) * 256;
   const uint32_t max_row = (uint32_t)(n_luts - 2);
 
@@ -284,14 +499,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     return r;
   };
   Chunk cur = finish_chunk(fetch(fb), encoded, n_bytes, (uint32_t)fb * kThreads + tid, !kChecked);
-  // Positions are below 2^31 (checked on the host), so only the low dword of
-  // each little-endian u64 is loaded: a dead high half would be reused as a
-  // temporary and force an early wait on every load in flight.
   const uint32_t *const op32 = reinterpret_cast<const uint32_t *>(op);
-  // this block's output range [op_lo, op_hi), wave-uniform.  Positions are
-  // always read (readlane waits on the vector load) before the block's
-  // stores are issued: the memory counter also counts stores, so a later
-  // wait would drain them too.
   uint32_t op_lo, op_hi;
   {
     const uint32_t opv = op32[2 * (fb + (lane & 1))];
@@ -303,41 +511,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   for (int buf_sel = 0;; buf_sel ^= 1) {
     uint32_t *const stage = s_stage + buf_sel * stage_dw;
     const int fb_next = fb + (int)gridDim.x;
-    // prefetch target: the next block, or this one again after the last (in
-    // bounds, discarded) so no load or wait depends on a branch
     const int fb_pf = fb_next < n_fb ? fb_next : fb;
 
-    // ---- this block's output range; prefetch its sign/mantissa bytes
-    const uint32_t start = op_lo;
-    uint32_t end = op_hi;
-    if (end > n_elements) end = n_elements;
-    int total = (int)end - (int)start;
-    if (total < 0 || start > n_elements) total = 0;  // malformed positions write nothing
-    if (total > stage_cap) total = stage_cap;
-    const uint32_t base = start & ~15u;  // 16-element aligned sweep origin
-    const int lead = (int)(start - base);
-    const int stage_nib = total > 0 ? lead + total : 0;
-    const int seg_dw = ((stage_nib + 15) >> 4) * 2;
-    const int nseg = seg_dw >> 1;
+    const BlockRange br = block_range(op_lo, op_hi, n_elements, stage_cap);
+    const int total = (int)(br.end - br.start);
     uint2 pre0 = make_uint2(0, 0), pre1 = make_uint2(0, 0);
-    if (!kChecked) {
-      // segments past nseg re-read the last one (no extra HBM traffic)
-      const int last_seg = nseg > 0 ? nseg - 1 : 0;
-      uint32_t q0 = (base >> 1) + 8u * (uint32_t)min(tid, last_seg);
-      uint32_t q1 = (base >> 1) + 8u * (uint32_t)min(tid + kThreads, last_seg);
-      pre0 = *reinterpret_cast<const uint2 *>(packed + (q0 < last8 ? q0 : last8));
-      pre1 = *reinterpret_cast<const uint2 *>(packed + (q1 < last8 ? q1 : last8));
-    }
-
-    // ---- prefetch the next block's chunk and positions (vector loads, so
-    // the LDS waits of the decode below never wait on them)
+    if (!kChecked) prefetch_nibbles(br, packed, last8, tid, kThreads, pre0, pre1);
     const RawChunk nxt_raw = fetch(fb_pf);
     const uint32_t nopv = op32[2 * (fb_pf + (lane & 1))];
 
     // ---- 1. decode the codes this lane's chunk owns into its nibble run
     for (int k = 0; k < run_slots; ++k) run[k * kThreads] = 0u;
-    const int zero4 = (seg_dw + 3) >> 2;
-    for (int i = tid; i < zero4; i += kThreads)
+    for (int i = tid; i < ((br.seg_dw + 3) >> 2); i += kThreads)
       reinterpret_cast<uint4 *>(stage)[i] = make_uint4(0, 0, 0, 0);
 
     int p = (int)cur.gap;              // bit offset of the next code in the chunk
@@ -370,15 +555,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
       buf <<= len;
     }
     // then while any lane of the wave is active; inactive lanes read the
-    // zero entry, which changes nothing
-    bool act = e != 0 && p < 53;
+    // zero entry, which changes nothing.  A lane stops at an entry of length
+    // 0 whatever its other bits (a corrupt table cannot stall the loop).
+    bool act = entry_len(e) != 0 && p < 53;
     while (__builtin_amdgcn_ballot_w64(act)) {
       e = s_table[act ? (uint32_t)(buf >> 52) : (uint32_t)kZeroEntry];
       const uint32_t len = entry_len(e);
       emit(e, __builtin_popcount(entry_mask(e)));
       p += (int)len;
       buf <<= len;
-      act = act && e != 0 && p < 53;
+      act = act && len != 0 && p < 53;
     }
     // codes starting in [53, 64) (lanes that did not park): window rebuilt
     // from chunk bits 32..79; entry symbols starting at or after bit 64
@@ -396,7 +582,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
         len = kept != mask ? rem : len;  // the lane ends at bit 64
         p += (int)len;
         buf <<= (len & 63);
-        act = act && e != 0 && p < kChunkBits;
+        act = act && len != 0 && p < kChunkBits;
       }
     }
     // parked lanes (a code longer than 12 bits, rare): the exact rule,
@@ -446,7 +632,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     int c = cnt;
     if (excl + c > total) c = total - excl;
     if (c > 0) {
-      const int nib0 = lead + excl;
+      const int nib0 = br.lead + excl;
       const uint32_t sh = (uint32_t)(nib0 & 7) * 4;
       uint32_t *const dst = stage + (nib0 >> 3);
       const int ndw = min((c + 7) >> 3, run_slots - 1);
@@ -463,33 +649,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     }
     __syncthreads();
 
-    // the next block's chunk and positions, fetched a whole decode phase ago
     const Chunk nxt = finish_chunk(nxt_raw, encoded, n_bytes, (uint32_t)fb_pf * kThreads + tid,
                                    !kChecked);
     const uint32_t nop_lo = __builtin_amdgcn_readlane(nopv, 0);
     const uint32_t nop_hi = __builtin_amdgcn_readlane(nopv, 1);
 
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
-    for (int s = tid, k = 0; s < nseg; s += kThreads, ++k) {
-      const uint2 ev = reinterpret_cast<const uint2 *>(stage)[s];
-      const uint32_t gpos = base + 16u * (uint32_t)s;
-      uint2 ov = k == 0 ? pre0 : pre1;
-      if (kChecked || k > 1 || gpos + 16 > n_elements)
-        ov = load_nibbles_checked(packed, n_elements, gpos);
-      const uint2 lo = merge8(ev.x, ov.x);
-      const uint2 hi8 = merge8(ev.y, ov.y);
-      if (gpos >= start && gpos + 16 <= end) {
-        *reinterpret_cast<uint4 *>(out + gpos) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
-      } else {
-        const uint32_t words[4] = {lo.x, lo.y, hi8.x, hi8.y};
-        for (int i = 0; i < 16; ++i) {
-          const uint32_t q = gpos + i;
-          if (q >= start && q < end) out[q] = (uint8_t)(words[i >> 2] >> (8 * (i & 3)));
-        }
-      }
-    }
-    // the next iteration writes the other staging buffer; its barrier after
-    // the scan orders this sweep before any reuse of this one
+    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, tid);
     if (fb_next >= n_fb) break;
     fb = fb_next;
     cur = nxt;
@@ -498,25 +664,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   }
 }
 
+// ===========================================================================
+// Launchers
+// ===========================================================================
+
+// Per device: CU count, and per kernel variant the occupancy at the last
+// dynamic LDS size it was launched with.
+constexpr int kVariants = 16;  // {DFA, MULTI} x 4 block sizes x {unchecked, checked}
 struct LaunchCache {
   int device = -1;
   int cus = 0;
-  size_t occ_dyn[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // dynamic LDS of occ below
-  int occ[8] = {0, 0, 0, 0, 0, 0, 0, 0};         // per (threads slot, checked) variant
-  bool attr_set[8] = {false, false, false, false, false, false, false, false};
+  size_t occ_dyn[kVariants] = {};
+  int occ[kVariants] = {};
+  bool attr_set[kVariants] = {};
 };
 constexpr int kMaxDevices = 64;
 LaunchCache g_cache[kMaxDevices];
 
-template <int kThreads, bool kChecked>
-int launch_variant(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
-                   int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
-                   uint8_t *out, int64_t n_elements, int64_t n_fb, int cap, int run_slots,
-                   hipStream_t stream, int slot) {
-  constexpr int kMaxSyms = kThreads * kChunkBits;
-  const size_t dyn =
-      sizeof(uint32_t) * ((size_t)run_slots * kThreads + 2 * (size_t)stage_dwords(cap));
-  auto kernel = decode_kernel<kThreads, kChecked>;
+// Grid size for `kernel` (persistent: resident workgroups per CU x CUs).
+int persistent_grid(const void *kernel, int threads, size_t dyn, size_t max_dyn, int slot,
+                    int64_t n_fb, int *grid) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return ECF8_ERR_HIP;
   LaunchCache &c = g_cache[dev];
@@ -526,70 +693,128 @@ int launch_variant(const uint8_t *luts, int n_luts, const uint32_t *table, const
     c.device = dev;
   }
   if (!c.attr_set[slot]) {
-    const size_t max_dyn = sizeof(uint32_t) * ((size_t)run_slots_for(1) * kThreads +
-                                               2 * (size_t)stage_dwords(kMaxSyms));
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dyn) != hipSuccess)
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dyn) !=
+        hipSuccess)
       return ECF8_ERR_HIP;
     c.attr_set[slot] = true;
   }
-  if (c.occ_dyn[slot] != dyn) {
+  if (c.occ_dyn[slot] != dyn || c.occ[slot] == 0) {
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, dyn) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, dyn) != hipSuccess)
       return ECF8_ERR_HIP;
     c.occ[slot] = occ > 0 ? occ : 1;
     c.occ_dyn[slot] = dyn;
   }
-  int64_t grid = (int64_t)c.cus * c.occ[slot];
-  if (grid > n_fb) grid = n_fb;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, stream, luts, n_luts,
-                     table, encoded, (uint32_t)n_bytes, packed, op, gaps, out,
-                     (uint32_t)n_elements, (int)n_fb, cap, run_slots);
+  const int64_t g = (int64_t)c.cus * c.occ[slot];
+  *grid = (int)(g < n_fb ? g : n_fb);
+  return ECF8_OK;
+}
+
+struct DecodeArgs {
+  const uint8_t *luts;
+  int n_luts;
+  const uint32_t *table;
+  const uint8_t *encoded;
+  int64_t n_bytes;
+  const uint8_t *packed;
+  const uint64_t *op;
+  const uint8_t *gaps;
+  uint8_t *out;
+  int64_t n_elements;
+  int64_t n_fb;
+  int cap;
+  int min_code_bits;
+  hipStream_t stream;
+};
+
+template <int kThreads, bool kChecked>
+int launch_dfa(const DecodeArgs &a, int slot) {
+  constexpr int kMaxSyms = kThreads * kChunkBits;
+  const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(a.cap) + 4);
+  const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + 4);
+  auto kernel = decode_dfa_kernel<kThreads, kChecked>;
+  int grid = 0;
+  const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
+                                 slot, a.n_fb, &grid);
+  if (rc != ECF8_OK) return rc;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, a.stream, a.luts,
+                     a.n_luts, a.table, a.encoded, (uint32_t)a.n_bytes, a.packed, a.op, a.gaps,
+                     a.out, (uint32_t)a.n_elements, (int)a.n_fb, a.cap);
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
+template <int kThreads, bool kChecked>
+int launch_multi(const DecodeArgs &a, int slot) {
+  constexpr int kMaxSyms = kThreads * kChunkBits;
+  const int mb = a.min_code_bits >= 1 && a.min_code_bits <= 16 ? a.min_code_bits : 1;
+  const int run_slots = run_slots_for(mb);
+  const size_t dyn =
+      sizeof(uint32_t) * ((size_t)run_slots * kThreads + 2 * (size_t)stage_dwords(a.cap));
+  const size_t max_dyn = sizeof(uint32_t) * ((size_t)run_slots_for(1) * kThreads +
+                                             2 * (size_t)stage_dwords(kMaxSyms));
+  auto kernel = decode_multi_kernel<kThreads, kChecked>;
+  int grid = 0;
+  const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
+                                 slot, a.n_fb, &grid);
+  if (rc != ECF8_OK) return rc;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, a.stream, a.luts,
+                     a.n_luts, a.table, a.encoded, (uint32_t)a.n_bytes, a.packed, a.op, a.gaps,
+                     a.out, (uint32_t)a.n_elements, (int)a.n_fb, a.cap, run_slots);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
 template <int kThreads>
-int launch_decode(const uint8_t *luts, int n_luts, const uint32_t *table, const uint8_t *encoded,
-                  int64_t n_bytes, const uint8_t *packed, const uint64_t *op, const uint8_t *gaps,
-                  uint8_t *out, int64_t n_elements, int64_t n_fb, int64_t max_block_elements,
-                  int min_code_bits, hipStream_t stream, int slot) {
+int launch_decode(DecodeArgs a, int64_t max_block_elements, bool dfa, int tpb_slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
-  int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms) ? kMaxSyms
-                                                                        : (int)max_block_elements;
-  if (cap < 16) cap = 16;
-  const int run_slots = run_slots_for(min_code_bits >= 1 && min_code_bits <= 16 ? min_code_bits : 1);
+  const int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms)
+                      ? kMaxSyms
+                      : (int)max_block_elements;
+  a.cap = cap < 16 ? 16 : cap;
   // the clamped vector loads need 12 bitstream bytes and 8 nibble bytes
-  if (n_bytes < 12 || n_elements < 16)
-    return launch_variant<kThreads, true>(luts, n_luts, table, encoded, n_bytes, packed, op, gaps,
-                                          out, n_elements, n_fb, cap, run_slots, stream,
-                                          2 * slot + 1);
-  return launch_variant<kThreads, false>(luts, n_luts, table, encoded, n_bytes, packed, op, gaps,
-                                         out, n_elements, n_fb, cap, run_slots, stream, 2 * slot);
+  const bool checked = a.n_bytes < 12 || a.n_elements < 16;
+  const int slot = (dfa ? 0 : 8) + 2 * tpb_slot + (checked ? 1 : 0);
+  if (dfa)
+    return checked ? launch_dfa<kThreads, true>(a, slot) : launch_dfa<kThreads, false>(a, slot);
+  return checked ? launch_multi<kThreads, true>(a, slot) : launch_multi<kThreads, false>(a, slot);
 }
 
 }  // namespace
 
-extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *stream) {
+extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, uint32_t *table,
+                                int *table_kind, void *stream) {
   if (!luts || !table) return ECF8_ERR_INVALID_ARG;
   if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
   if (((uintptr_t)luts & 3) || ((uintptr_t)table & 3)) return ECF8_ERR_MISALIGNED;
-  hipLaunchKernelGGL(build_table_kernel, dim3(kTableSize / 256), dim3(256), 0,
-                     (hipStream_t)stream, luts, n_luts, table);
-  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<uint8_t> h_luts((size_t)n_luts * 256);
+  std::vector<uint32_t> h_table(ECF8_TABLE_BYTES / 4);
+  if (hipMemcpyAsync(h_luts.data(), luts, h_luts.size(), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return ECF8_ERR_HIP;
+  int kind = 0;
+  const int rc = ecf8_build_table_host(h_luts.data(), n_luts, want_kind, h_table.data(), &kind);
+  if (rc != ECF8_OK) return rc;
+  if (hipMemcpyAsync(table, h_table.data(), ECF8_TABLE_BYTES, hipMemcpyHostToDevice, s) !=
+          hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return ECF8_ERR_HIP;
+  if (table_kind) *table_kind = kind;
+  return ECF8_OK;
 }
 
 extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
                            const uint8_t *packed_other_4bits, const uint64_t *output_positions,
                            const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
                            int64_t n_elements, int64_t max_block_elements, int min_code_bits,
-                           const uint32_t *table, int threads_per_block, int bytes_per_thread,
-                           void *stream) {
+                           const uint32_t *table, int table_kind, int threads_per_block,
+                           int bytes_per_thread, void *stream) {
   if (n_bytes < 0 || n_elements < 0 || (n_elements & 1)) return ECF8_ERR_INVALID_ARG;
   // the reference's positions are 32-bit (decode.cu:23-25, 151); so is this
   // kernel's index arithmetic
   if (n_bytes > INT32_MAX - 64 || n_elements > INT32_MAX - 64) return ECF8_ERR_UNSUPPORTED;
   if (bytes_per_thread != kChunkBytes) return ECF8_ERR_UNSUPPORTED;
   if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
+  if (table_kind != ECF8_TABLE_MULTI && table_kind != ECF8_TABLE_DFA) return ECF8_ERR_INVALID_ARG;
   const int64_t fb_bytes = (int64_t)threads_per_block * bytes_per_thread;
   if (threads_per_block != 128 && threads_per_block != 256 && threads_per_block != 512 &&
       threads_per_block != 1024)
@@ -602,23 +827,18 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   if (((uintptr_t)encoded & 15) || ((uintptr_t)packed_other_4bits & 7) ||
       ((uintptr_t)outputs & 15) || ((uintptr_t)table & 3) || ((uintptr_t)output_positions & 7))
     return ECF8_ERR_MISALIGNED;
-  hipStream_t s = (hipStream_t)stream;
+  DecodeArgs a{luts,      n_luts, table,      encoded, n_bytes, packed_other_4bits,
+               output_positions, gaps, outputs, n_elements, n_fb, 0,
+               min_code_bits, (hipStream_t)stream};
+  const bool dfa = table_kind == ECF8_TABLE_DFA;
   switch (threads_per_block) {
     case 128:
-      return launch_decode<128>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
-                                min_code_bits, s, 0);
+      return launch_decode<128>(a, max_block_elements, dfa, 0);
     case 256:
-      return launch_decode<256>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
-                                min_code_bits, s, 1);
+      return launch_decode<256>(a, max_block_elements, dfa, 1);
     case 512:
-      return launch_decode<512>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
-                                min_code_bits, s, 2);
+      return launch_decode<512>(a, max_block_elements, dfa, 2);
     default:
-      return launch_decode<1024>(luts, n_luts, table, encoded, n_bytes, packed_other_4bits,
-                                 output_positions, gaps, outputs, n_elements, n_fb, max_block_elements,
-                                min_code_bits, s, 3);
+      return launch_decode<1024>(a, max_block_elements, dfa, 3);
   }
 }

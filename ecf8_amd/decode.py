@@ -7,13 +7,26 @@ launch, and any failure raises ``ECF8Error`` -- there is no CPU fallback.
 
 from __future__ import annotations
 
+import ctypes
+from typing import NamedTuple
+
 import numpy as np
 import torch
 
-from ._lib import ECF8_MAX_LUTS, ECF8_TABLE_BYTES, ECF8Error, check, lib
+from ._lib import (ECF8_MAX_LUTS, ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8_TABLE_DFA,
+                   ECF8_TABLE_MULTI, ECF8Error, check, lib)
 
-__all__ = ["build_table", "decode_into", "decode", "n_format_blocks", "largest_block", "min_code_bits",
-           "validate_format", "ECF8Error"]
+__all__ = ["DecodeTable", "build_table", "build_table_host", "decode_into", "decode",
+           "n_format_blocks", "largest_block", "min_code_bits", "validate_format", "ECF8Error",
+           "ECF8_TABLE_ANY", "ECF8_TABLE_MULTI", "ECF8_TABLE_DFA"]
+
+
+class DecodeTable(NamedTuple):
+    """A derived decode table on the device and its kind (ECF8_TABLE_DFA or
+    ECF8_TABLE_MULTI); the kind selects the decode kernel."""
+
+    data: torch.Tensor
+    kind: int
 
 
 def _stream_handle(device: torch.device, stream=None):
@@ -66,21 +79,41 @@ def min_code_bits(luts) -> int:
     return int(nz.min()) if nz.size else 0
 
 
-def build_table(luts: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-    """Derived multi-symbol decode table (u32[4096] as int32) for ``luts``."""
+def build_table_host(luts, kind: int = ECF8_TABLE_ANY):
+    """Derived decode table for a LUT stack, built on the host: (u32 numpy
+    array of ECF8_TABLE_BYTES, kind).  ``kind`` ECF8_TABLE_ANY picks the byte
+    automaton when the LUTs allow it, else the multi-symbol table."""
+    lut = np.ascontiguousarray(torch.as_tensor(luts).detach().cpu().numpy(), dtype=np.uint8)
+    if lut.size % 256:
+        raise ECF8Error("luts size is not a multiple of 256")
+    n_luts = lut.size // 256
+    table = np.zeros(ECF8_TABLE_BYTES // 4, np.uint32)
+    got = ctypes.c_int(-1)
+    check(lib().ecf8_build_table_host(lut.ctypes.data_as(ctypes.c_void_p), n_luts, int(kind),
+                                      table.ctypes.data_as(ctypes.c_void_p), ctypes.byref(got)),
+          "ecf8_build_table_host")
+    return table, got.value
+
+
+def build_table(luts: torch.Tensor, out: torch.Tensor | None = None, stream=None,
+                kind: int = ECF8_TABLE_ANY) -> DecodeTable:
+    """Derived decode table for ``luts`` (a CUDA tensor), built on the host
+    and copied to ``luts``' device (into ``out`` if given).  Synchronizes:
+    call once per compressed block, at load time."""
     if not luts.is_cuda or luts.dtype != torch.uint8 or not luts.is_contiguous():
         raise ECF8Error("luts must be a contiguous uint8 CUDA tensor")
     n_luts = _n_luts(luts)
     if not 2 <= n_luts <= ECF8_MAX_LUTS:
         raise ECF8Error(f"n_luts={n_luts} outside [2, {ECF8_MAX_LUTS}]")
+    table, got = build_table_host(luts, kind)
+    host = torch.from_numpy(table.view(np.int32))
     if out is None:
-        out = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32, device=luts.device)
-    elif out.numel() * out.element_size() < ECF8_TABLE_BYTES or out.device != luts.device:
-        raise ECF8Error("table buffer too small or on another device")
-    with torch.cuda.device(luts.device):
-        check(lib().ecf8_build_table(luts.data_ptr(), n_luts, out.data_ptr(),
-                                     _stream_handle(luts.device, stream)), "ecf8_build_table")
-    return out
+        out = host.to(luts.device)
+    else:
+        if out.numel() * out.element_size() < ECF8_TABLE_BYTES or out.device != luts.device:
+            raise ECF8Error("table buffer too small or on another device")
+        out.view(torch.int32)[: host.numel()].copy_(host)
+    return DecodeTable(out, got)
 
 
 def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
@@ -122,13 +155,16 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
     n_luts = _n_luts(luts)
     if table is None:
         table = build_table(luts, stream=stream)
+    elif not isinstance(table, DecodeTable):
+        raise ECF8Error("table must be the DecodeTable returned by build_table")
+    if table.data.device != dev:
+        raise ECF8Error(f"table must be on {dev}")
     with torch.cuda.device(dev):
         check(lib().ecf8_decode(luts.data_ptr(), encoded.data_ptr(),
                                 packed_other_4bits.data_ptr(), output_positions.data_ptr(),
                                 gaps.data_ptr(), out.data_ptr(), n_luts, n_bytes, n,
-                                int(max_block_elements), int(min_code_bits), table.data_ptr(),
-                                threads_per_block,
-                                bytes_per_thread,
+                                int(max_block_elements), int(min_code_bits), table.data.data_ptr(),
+                                int(table.kind), threads_per_block, bytes_per_thread,
                                 _stream_handle(dev, stream)), "ecf8_decode")
     return out
 
@@ -154,8 +190,6 @@ def validate_format(luts, encoded_bytes: int, packed_other_4bits_bytes: int, out
                     gaps_bytes: int, threads_per_block: int = 512, bytes_per_thread: int = 8):
     """Host-side format check of one compressed block (libecf8
     ecf8_validate_format); raises ECF8Error with the reason."""
-    import ctypes
-
     luts_np = np.ascontiguousarray(torch.as_tensor(luts).cpu().numpy().reshape(-1), dtype=np.uint8)
     op = torch.as_tensor(output_positions).cpu().contiguous()
     op_np = np.ascontiguousarray(op.view(torch.uint8).numpy()).view(np.uint64)

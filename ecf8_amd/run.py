@@ -15,6 +15,7 @@ the consuming GEMM are ordered without any cross-runtime synchronisation.
 
 from __future__ import annotations
 
+import ctypes
 import json
 import math
 import os
@@ -26,7 +27,7 @@ import torch
 import torch.nn as nn
 
 from . import decode as _dev
-from ._lib import ECF8_TABLE_BYTES, ECF8Error, check, lib
+from ._lib import ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8Error, check, lib
 
 __all__ = [
     "DFloatModel",
@@ -44,9 +45,10 @@ class _DecodeLauncher:
     "decode")`` (dfloat/run/run.py:24-33).  ``args`` are the reference
     kernel's: luts, encoded, packed_other_4bits, output_positions, gaps,
     outputs (device addresses), n_luts, n_bytes, n_elements
-    (decode.cu:16-26).  The multi-symbol table for the given LUTs is rebuilt
-    into a per-device scratch table on every call (two launches on the
-    current stream); the hook path caches it per module instead."""
+    (decode.cu:16-26).  The derived table for the given LUTs is rebuilt into
+    a per-device scratch table on every call (the LUTs are read back to the
+    host, which synchronizes the stream); the hook path caches it per module
+    instead."""
 
     def __init__(self):
         self._tables = {}
@@ -72,10 +74,12 @@ class _DecodeLauncher:
         table = self._table(dev)
         s = (torch.cuda.current_stream(dev) if stream is None else stream).cuda_stream
         L = lib()
-        check(L.ecf8_build_table(int(luts), int(n_luts), table.data_ptr(), s), "ecf8_build_table")
+        kind = ctypes.c_int(-1)
+        check(L.ecf8_build_table(int(luts), int(n_luts), ECF8_TABLE_ANY, table.data_ptr(),
+                                 ctypes.byref(kind), s), "ecf8_build_table")
         check(L.ecf8_decode(int(luts), int(encoded), int(packed), int(op), int(gaps), int(outputs),
                             int(n_luts), int(n_bytes), int(n_elements), max_block, 0,
-                            table.data_ptr(), tpb, bpt, s), "ecf8_decode")
+                            table.data_ptr(), kind.value, tpb, bpt, s), "ecf8_decode")
 
 
 _decode = _DecodeLauncher()
@@ -116,7 +120,7 @@ class TensorManager:
 
 def _module_state(module: nn.Module):
     """Per-module decode state, derived once on the module's device and
-    rebuilt if the buffers move: the multi-symbol table and the largest
+    rebuilt if the buffers move: the derived decode table, the largest
     format-block (the quantity behind the reference's shared_mem_size) and
     the shortest code length, which size the kernel's LDS."""
     luts = module.luts

@@ -27,8 +27,13 @@ extern "C" {
 #define ECF8_ERR_HIP 5               /* HIP runtime error (launch, device)     */
 #define ECF8_ERR_CAPACITY 6          /* caller buffer too small                */
 
-/* Bytes of the derived decode table (u32[4096]) built by ecf8_build_table. */
-#define ECF8_TABLE_BYTES 16384
+/* Bytes of a derived decode table buffer (either kind). */
+#define ECF8_TABLE_BYTES 24608
+/* Kinds of derived decode table. */
+#define ECF8_TABLE_ANY (-1)   /* builder's choice: DFA when the LUTs allow it */
+#define ECF8_TABLE_MULTI 0    /* 12-bit multi-symbol table; any LUT stack      */
+#define ECF8_TABLE_DFA 1      /* byte automaton; prefix-code LUTs with <= 15
+                                 pending prefixes and <= 4 codes per byte     */
 /* Largest LUT stack the format allows: 1 first-level row, at most 16
  * second-level rows (pointer values 240..255, dfloat/run/decode.cu:87),
  * 1 length row. */
@@ -40,15 +45,30 @@ const char *ecf8_status_string(int status);
 /* ---------------------------------------------------------------- device */
 
 /*
- * Build the derived multi-symbol decode table from a block's on-disk LUTs.
+ * Build the derived decode table from a block's on-disk LUTs.
  * No reference counterpart: the reference walks the LUTs per symbol
- * (dfloat/run/decode.cu:86-91); this table is computed once per compressed
+ * (dfloat/run/decode.cu:86-91); the table is computed once per compressed
  * block (at load time, like shared_mem_size in dfloat/run/run.py:453-458) and
- * decodes up to four symbols per lookup with exactly the reference's rule.
- *   luts   device u8[n_luts*256], 4-byte aligned
- *   table  device u32[4096] (output), 4-byte aligned
+ * reproduces the reference's rule exactly.  Two kinds:
+ *   ECF8_TABLE_DFA    a byte automaton (8-9 lookups per 8-byte chunk);
+ *                     requires LUTs forming a prefix code with at most 15
+ *                     pending prefixes and at most 4 codes ending in any
+ *                     byte (every code >= 2 bits)
+ *   ECF8_TABLE_MULTI  12-bit windows, up to 4 symbols per lookup; any LUTs
+ * want_kind ECF8_TABLE_ANY picks DFA when possible; asking for DFA when it
+ * is not possible returns ECF8_ERR_FORMAT.  *table_kind receives the kind
+ * built; pass it to ecf8_decode.
+ *
+ * ecf8_build_table_host: luts and table in host memory
+ *   (table: ECF8_TABLE_BYTES).
+ * ecf8_build_table: luts (4-byte aligned) and table (ECF8_TABLE_BYTES,
+ *   4-byte aligned) in device memory; copies the LUTs to the host and the
+ *   table back on `stream`, and synchronizes `stream`.
  */
-int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *stream);
+int ecf8_build_table_host(const uint8_t *luts, int n_luts, int want_kind, uint32_t *table,
+                          int *table_kind);
+int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, uint32_t *table,
+                     int *table_kind, void *stream);
 
 /*
  * Decode one compressed block into FP8 e4m3fn bytes.
@@ -61,7 +81,8 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  *   output_positions   device u64[n_fb+1]      (run.py:112)
  *   gaps               device u8[n_fb*threads_per_block/2] (run.py:113)
  *   outputs            device u8[n_elements]   (run.py:114), 16-byte aligned
- *   table              device u32[4096] from ecf8_build_table for these luts
+ *   table, table_kind  the derived table ecf8_build_table built for these
+ *                      luts, and its kind
  *   max_block_elements largest output_positions[b+1] - output_positions[b]
  *                      (the reference derives shared_mem_size from it,
  *                      dfloat/run/run.py:453-458); sizes the kernel's LDS
@@ -70,9 +91,10 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
  *                      elements of such blocks unwritten.
  *   min_code_bits      shortest nonzero code length in the LUTs' length row
  *                      (ecf8 length row = last LUT row); sizes the per-lane
- *                      LDS run.  0 = unknown (1 bit assumed).  A value above
- *                      the true minimum can leave outputs wrong, never
- *                      touches memory out of bounds.
+ *                      LDS run of the ECF8_TABLE_MULTI kernel.  0 = unknown
+ *                      (1 bit assumed).  A value above the true minimum can
+ *                      leave outputs wrong, never touches memory out of
+ *                      bounds.
  * where n_fb = ceil(n_bytes / (threads_per_block*bytes_per_thread)).
  * Geometry: bytes_per_thread must be 8 (the reference kernel hard-codes it,
  * decode.cu:5); threads_per_block one of 128, 256, 512, 1024.
@@ -83,8 +105,8 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, uint32_t *table, void *str
 int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *packed_other_4bits,
                 const uint64_t *output_positions, const uint8_t *gaps, uint8_t *outputs,
                 int n_luts, int64_t n_bytes, int64_t n_elements, int64_t max_block_elements,
-                int min_code_bits, const uint32_t *table, int threads_per_block,
-                int bytes_per_thread, void *stream);
+                int min_code_bits, const uint32_t *table, int table_kind,
+                int threads_per_block, int bytes_per_thread, void *stream);
 
 /* ------------------------------------------------------------------ host */
 

@@ -58,11 +58,11 @@ def _decode_call(**kw):
     from ecf8_amd._lib import lib
 
     args = dict(luts=0x1000, encoded=0x2000, packed=0x3000, op=0x4000, gaps=0x5000, out=0x6000,
-                n_luts=3, n_bytes=100, n=64, table=0x7000, tpb=512, bpt=8)
+                n_luts=3, n_bytes=100, n=64, table=0x7000, kind=1, tpb=512, bpt=8)
     args.update(kw)
     return lib().ecf8_decode(args["luts"], args["encoded"], args["packed"], args["op"],
                              args["gaps"], args["out"], args["n_luts"], args["n_bytes"], args["n"],
-                             0, 0, args["table"], args["tpb"], args["bpt"], None)
+                             0, 0, args["table"], args["kind"], args["tpb"], args["bpt"], None)
 
 
 @pytest.mark.parametrize("kw,status", [
@@ -77,6 +77,8 @@ def _decode_call(**kw):
     (dict(n_bytes=2**31), 2),   # positions are 32-bit, as in the reference
     (dict(packed=0x3002), 3),
     (dict(gaps=0), 1),
+    (dict(kind=2), 1),          # unknown table kind
+    (dict(kind=-1), 1),
 ])
 def test_decode_rejects_before_launch(kw, status):
     assert _decode_call(**kw) == status
@@ -89,6 +91,10 @@ def test_decode_of_empty_block_is_a_no_op():
 def test_build_table_rejects_bad_lut_count():
     from ecf8_amd._lib import lib
 
-    assert lib().ecf8_build_table(ctypes.c_void_p(0x1000), 19, ctypes.c_void_p(0x2000), None) == 4
-    assert lib().ecf8_build_table(None, 3, ctypes.c_void_p(0x2000), None) == 1
-    assert lib().ecf8_build_table(ctypes.c_void_p(0x1001), 3, ctypes.c_void_p(0x2000), None) == 3
+    kind = ctypes.c_int()
+    assert lib().ecf8_build_table(ctypes.c_void_p(0x1000), 19, -1, ctypes.c_void_p(0x2000),
+                                  ctypes.byref(kind), None) == 4
+    assert lib().ecf8_build_table(None, 3, -1, ctypes.c_void_p(0x2000), ctypes.byref(kind),
+                                  None) == 1
+    assert lib().ecf8_build_table(ctypes.c_void_p(0x1001), 3, -1, ctypes.c_void_p(0x2000),
+                                  ctypes.byref(kind), None) == 3

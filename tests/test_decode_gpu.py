@@ -36,16 +36,35 @@ def _dev_block(block, dev):
     return out
 
 
-def _gpu_decode(block, dev, tpb=512, n_elements=None, out=None):
+ANY, MULTI, DFA = -1, 0, 1
+
+
+def _table_for(d, kind):
+    """Device table of the requested kind; None when the automaton cannot
+    represent these LUTs (then only the multi-symbol kernel applies)."""
+    from ecf8_amd.decode import ECF8Error, build_table
+
+    try:
+        return build_table(d["luts"], kind=kind)
+    except ECF8Error:
+        if kind == DFA:
+            return None
+        raise
+
+
+def _gpu_decode(block, dev, tpb=512, n_elements=None, out=None, kind=ANY):
     from ecf8_amd.decode import decode, decode_into
 
     d = _dev_block(block, dev)
+    table = _table_for(d, kind)
+    if table is None:
+        pytest.skip("LUTs with a 1-bit code: no automaton table")
     if out is None and n_elements is None:
         r = decode(d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
-                   d["gaps"], threads_per_block=tpb)
+                   d["gaps"], table=table, threads_per_block=tpb)
     else:
         r = decode_into(out, d["luts"], d["encoded"], d["packed_other_4bits"],
-                        d["output_positions"], d["gaps"], threads_per_block=tpb,
+                        d["output_positions"], d["gaps"], table=table, threads_per_block=tpb,
                         n_elements=n_elements)
     torch.cuda.synchronize()
     return r.view(torch.uint8).cpu().numpy()
@@ -59,45 +78,15 @@ def _compress(flat_u8: np.ndarray, tpb=512):
     return {k: res[k] for k in KEYS}
 
 
-# ------------------------------------------------------------------ table
-
-
-@pytest.mark.parametrize("name", CASES)
-def test_table_entries_follow_the_lut_rule(name, cuda_device):
-    from ecf8_amd.decode import build_table
-
-    _say(f"table {name}")
-    g = dict(np.load(os.path.join(GOLDEN, f"{name}.npz")))
-    luts = g["luts"]
-    table = build_table(torch.from_numpy(luts).to(cuda_device)).cpu().numpy().view(np.uint32)
-    rng = np.random.default_rng(0)
-    for w in range(4096):
-        e = int(table[w])
-        total = e >> 28
-        mask = (e >> 16) & 0xFFF
-        n = bin(mask).count("1")
-        if total == 0:
-            assert e == 0
-            continue
-        for _ in range(3):
-            bits = (w << 20) | int(rng.integers(0, 1 << 20))  # window + any continuation
-            off = 0
-            for k in range(n):
-                assert mask >> off & 1
-                sym, ln = oc.lut_decode_one(luts, (bits >> (16 - off)) & 0xFFFF)
-                assert sym == (e >> (4 * k)) & 0xF and ln > 0
-                off += ln
-            assert off == total <= 12
-
-
 # ----------------------------------------------------------------- golden
 
 
+@pytest.mark.parametrize("kind", [MULTI, DFA])
 @pytest.mark.parametrize("name", CASES)
-def test_golden_blocks_decode_bit_exact(name, cuda_device):
-    _say(f"golden {name}")
+def test_golden_blocks_decode_bit_exact(name, kind, cuda_device):
+    _say(f"golden {name} kind={kind}")
     g = dict(np.load(os.path.join(GOLDEN, f"{name}.npz")))
-    got = _gpu_decode(g, cuda_device, tpb=int(g["threads_per_block"]))
+    got = _gpu_decode(g, cuda_device, tpb=int(g["threads_per_block"]), kind=kind)
     assert np.array_equal(got, g["flat"])
 
 
@@ -127,13 +116,14 @@ def _random_block(seed):
     return (((other & 8) << 4) | (exps << 3) | (other & 7)).astype(np.uint8)
 
 
+@pytest.mark.parametrize("kind", [MULTI, DFA])
 @pytest.mark.parametrize("seed", range(40))
-def test_random_blocks_bit_exact_vs_original_and_oracle(seed, cuda_device, oracle_native):
+def test_random_blocks_bit_exact_vs_original_and_oracle(seed, kind, cuda_device, oracle_native):
     flat = _random_block(seed)
     tpb = (128, 256, 512, 1024)[seed % 4]
-    _say(f"random seed={seed} n={flat.size} tpb={tpb}")
+    _say(f"random seed={seed} n={flat.size} tpb={tpb} kind={kind}")
     block = _compress(flat, tpb)
-    got = _gpu_decode(block, cuda_device, tpb=tpb)
+    got = _gpu_decode(block, cuda_device, tpb=tpb, kind=kind)
     want = oracle_native.decode(block["luts"].numpy(), block["encoded"].numpy(),
                                 block["packed_other_4bits"].numpy(),
                                 block["output_positions"].numpy(), block["gaps"].numpy(),
@@ -142,49 +132,79 @@ def test_random_blocks_bit_exact_vs_original_and_oracle(seed, cuda_device, oracl
     assert np.array_equal(got, flat)
 
 
-def test_config1_4096x4096_bit_exact(cuda_device, oracle_native):
+@pytest.mark.parametrize("kind", [MULTI, DFA])
+def test_config1_4096x4096_bit_exact(kind, cuda_device, oracle_native):
     from ecf8_amd.synth import synthetic_fp8
 
-    _say("config1 4096x4096")
+    _say(f"config1 4096x4096 kind={kind}")
     w, _ = synthetic_fp8(4096, 4096, 0.02, seed=0)
     flat = w.reshape(-1).view(torch.uint8).numpy()
     block = _compress(flat)
-    got = _gpu_decode(block, cuda_device)
+    got = _gpu_decode(block, cuda_device, kind=kind)
     assert np.array_equal(got, flat)
     want = oracle_native.decode(*(block[k].numpy() for k in KEYS), threads=8)
     assert np.array_equal(want, got)
 
 
 def test_config2_qwen3_layer_bit_exact(cuda_device):
+    from ecf8_amd.decode import build_table
     from ecf8_amd.synth import flat_block, qwen3_8b_layer
 
     _say("config2 qwen3-8b layer")
     flat, _ = flat_block(qwen3_8b_layer(seed=0))
     flat_u8 = flat.view(torch.uint8).numpy()
     block = _compress(flat_u8)
-    got = _gpu_decode(block, cuda_device)
-    assert got.size == 192_937_984
-    assert np.array_equal(got, flat_u8)
+    d = _dev_block(block, cuda_device)
+    assert build_table(d["luts"]).kind == DFA  # the automaton runs this workload
+    for kind in (DFA, MULTI):
+        _say(f"config2 kind={kind}")
+        got = _gpu_decode(block, cuda_device, kind=kind)
+        assert got.size == 192_937_984
+        assert np.array_equal(got, flat_u8)
+
+
+def test_dfa_exact_path_is_bit_exact(cuda_device):
+    """Chunks whose automaton walk reaches the exact row are decoded with the
+    LUT rule itself.  Valid streams only get there in their final padding,
+    so here a copy of the automaton sends every chunk whose first byte is
+    odd there; the output must not change."""
+    from ecf8_amd.decode import DecodeTable, build_table_host, decode
+
+    flat = _random_block(24)
+    block = _compress(flat)
+    d = _dev_block(block, cuda_device)
+    table, kind = build_table_host(block["luts"], DFA)
+    assert kind == DFA
+    for r in range(8):  # root and skip rows: the first byte of every chunk
+        for b in range(1, 256, 2):
+            table[r * 256 + b] = 8 << 10
+    t = DecodeTable(torch.from_numpy(table.view(np.int32)).to(cuda_device), DFA)
+    got = decode(d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
+                 d["gaps"], table=t)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.view(torch.uint8).cpu().numpy(), flat)
 
 
 # ---------------------------------------------------------------- edge cases
 
 
-def test_outputs_past_n_elements_are_untouched(cuda_device):
+@pytest.mark.parametrize("kind", [MULTI, DFA])
+def test_outputs_past_n_elements_are_untouched(kind, cuda_device):
     flat = _random_block(4)
     block = _compress(flat)
     out = torch.full((flat.size + 64,), 0xAB, dtype=torch.uint8, device=cuda_device)
-    got = _gpu_decode(block, cuda_device, n_elements=flat.size, out=out)
+    got = _gpu_decode(block, cuda_device, n_elements=flat.size, out=out, kind=kind)
     assert np.array_equal(got[: flat.size], flat)
     assert (got[flat.size:] == 0xAB).all()
 
 
-def test_shorter_n_elements_clamps_like_the_reference(cuda_device):
+@pytest.mark.parametrize("kind", [MULTI, DFA])
+def test_shorter_n_elements_clamps_like_the_reference(kind, cuda_device):
     flat = _random_block(9)
     block = _compress(flat)
     out = torch.full((flat.size,), 0xCD, dtype=torch.uint8, device=cuda_device)
     n = (flat.size // 3) & ~1
-    got = _gpu_decode(block, cuda_device, n_elements=n, out=out)
+    got = _gpu_decode(block, cuda_device, n_elements=n, out=out, kind=kind)
     assert np.array_equal(got[:n], flat[:n])
     assert (got[n:] == 0xCD).all()
 
@@ -227,9 +247,10 @@ def test_min_code_bits_unknown_equals_derived(seed, cuda_device):
     shortest = min(bits for sym, (bits, _) in res["table"].items() if isinstance(sym, int))
     assert min_code_bits(res["luts"]) == shortest
     d = _dev_block({k: res[k] for k in KEYS}, cuda_device)
+    table = _table_for(d, MULTI)  # min_code_bits sizes the multi kernel's runs
     for bits in (0, None):
         got = decode(d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
-                     d["gaps"], min_code_bits=bits)
+                     d["gaps"], table=table, min_code_bits=bits)
         torch.cuda.synchronize()
         assert np.array_equal(got.view(torch.uint8).cpu().numpy(), flat)
 
@@ -244,12 +265,13 @@ def test_min_code_bits_above_the_truth_stays_in_bounds(cuda_device):
     n = int(g["flat"].size)
     d = _dev_block(g, cuda_device)
     out = torch.full((n + 256,), 0x5A, dtype=torch.uint8, device=cuda_device)
+    table = _table_for(d, MULTI)
     decode_into(out[:n], d["luts"], d["encoded"], d["packed_other_4bits"],
-                d["output_positions"], d["gaps"], min_code_bits=16)
+                d["output_positions"], d["gaps"], table=table, min_code_bits=16)
     torch.cuda.synchronize()
     assert (out[n:].cpu().numpy() == 0x5A).all()
     decode_into(out[:n], d["luts"], d["encoded"], d["packed_other_4bits"],
-                d["output_positions"], d["gaps"], min_code_bits=1)
+                d["output_positions"], d["gaps"], table=table, min_code_bits=1)
     torch.cuda.synchronize()
     assert np.array_equal(out[:n].cpu().numpy(), g["flat"])
 
