@@ -81,6 +81,20 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
   return x;
 }
 
+// Sum of the totals of the waves before this one (s_wave_sum[w] = total of
+// wave w): lanes 0..kWaves-1 load one total each, a DPP prefix inside the
+// first row adds them up, and this wave's entry is read back.
+template <int kWaves>
+__device__ __forceinline__ int waves_before(const int *s_wave_sum, int lane, int wave) {
+  const int own = lane < kWaves ? s_wave_sum[lane] : 0;
+  int t = own;
+  if (kWaves > 1) t += __builtin_amdgcn_update_dpp(0, t, 0x111, 0xF, 0xF, true);  // row_shr:1
+  if (kWaves > 2) t += __builtin_amdgcn_update_dpp(0, t, 0x112, 0xF, 0xF, true);  // row_shr:2
+  if (kWaves > 4) t += __builtin_amdgcn_update_dpp(0, t, 0x114, 0xF, 0xF, true);  // row_shr:4
+  if (kWaves > 8) t += __builtin_amdgcn_update_dpp(0, t, 0x118, 0xF, 0xF, true);  // row_shr:8
+  return __builtin_amdgcn_readlane(t - own, __builtin_amdgcn_readfirstlane(wave));
+}
+
 typedef uint32_t u32x3_a8 __attribute__((ext_vector_type(3), aligned(8)));
 
 // A chunk as fetched: 12 raw bytes from the chunk start (8 chunk bytes, 2
@@ -180,14 +194,21 @@ __device__ __forceinline__ void prefetch_nibbles(const BlockRange &br, const uin
   pre1 = *reinterpret_cast<const uint2 *>(packed + (q1 < last8 ? q1 : last8));
 }
 
+// LDS slots for the two edge segments of a block (first and last, which it
+// shares with its neighbours): 16 merged bytes, then gpos, start, end.
+constexpr int kEdgeSlotDwords = 8;
+constexpr int kEdgeDwords = 2 * kEdgeSlotDwords;
+
 // Step 4: merge the staged exponents with the sign/mantissa nibbles and
-// store the block's FP8 bytes.
+// store the block's FP8 bytes: whole segments as one 128-bit store each;
+// the edge segments are parked in s_edge and stored byte-wise by
+// flush_edges after the next barrier, spread over lanes.
 template <int kThreads, bool kChecked>
 __device__ __forceinline__ void write_block(const uint32_t *stage, const BlockRange &br,
                                             uint2 pre0, uint2 pre1,
                                             const uint8_t *__restrict__ packed,
                                             uint32_t n_elements, uint8_t *__restrict__ out,
-                                            int tid) {
+                                            uint32_t *s_edge, int tid) {
   for (int s = tid, k = 0; s < br.nseg; s += kThreads, ++k) {
     const uint2 ev = reinterpret_cast<const uint2 *>(stage)[s];
     const uint32_t gpos = br.base + 16u * (uint32_t)s;
@@ -198,12 +219,32 @@ __device__ __forceinline__ void write_block(const uint32_t *stage, const BlockRa
     const uint2 hi8 = merge8(ev.y, ov.y);
     if (gpos >= br.start && gpos + 16 <= br.end) {
       *reinterpret_cast<uint4 *>(out + gpos) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
-    } else {
-      const uint32_t words[4] = {lo.x, lo.y, hi8.x, hi8.y};
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t q = gpos + i;
-        if (q >= br.start && q < br.end) out[q] = (uint8_t)(words[i >> 2] >> (8 * (i & 3)));
-      }
+    } else {  // only the first and the last segment can be partial
+      uint32_t *const e = s_edge + (s == 0 ? 0 : kEdgeSlotDwords);
+      *reinterpret_cast<uint4 *>(e) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
+      e[4] = gpos;
+      e[5] = br.start;
+      e[6] = br.end;
+    }
+  }
+}
+
+// Store the in-range bytes of the edge segments parked by the last
+// write_block (lanes 0..31 of the workgroup, one byte each), then mark the
+// slots empty.  Called between a barrier that follows that write_block and
+// the barrier before the next one.
+__device__ __forceinline__ void flush_edges(uint32_t *s_edge, uint8_t *__restrict__ out,
+                                            int tid) {
+  if (tid < 32) {
+    uint32_t *const e = s_edge + (tid >> 4) * kEdgeSlotDwords;
+    const uint32_t i = (uint32_t)tid & 15u;
+    const uint32_t q = e[4] + i;
+    const uint32_t b = (e[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    const bool in_range = q >= e[5] && q < e[6];
+    if (in_range) out[q] = (uint8_t)b;
+    if (i == 0) {
+      e[5] = 0u;
+      e[6] = 0u;
     }
   }
 }
@@ -246,7 +287,7 @@ __device__ __forceinline__ uint32_t dfa_at(const uint32_t *s_dfa, uint32_t off) 
 // per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
 // the cap causes go to VGPR lanes.
 template <int kThreads, bool kChecked>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void decode_dfa_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
     const uint8_t *__restrict__ encoded, uint32_t n_bytes,
     const uint8_t *__restrict__ packed, const uint64_t *__restrict__ op,
@@ -255,6 +296,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   constexpr int kWaves = kThreads / 64;
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ int s_wave_sum[kWaves];
+  __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
   // dynamic LDS: 2 staging buffers, each followed by spill dwords that take
   // the ORs of positions past the buffer (malformed or understated input)
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
@@ -273,6 +315,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
       e = (e & ~kDfaRowMask) | ((uint32_t)kDfaExactRow << 10);
     s_dfa[i] = e;
   }
+  if (tid < kEdgeDwords) s_edge[tid] = 0u;
 
   int fb = blockIdx.x;
   if (fb >= n_fb) return;  // uniform per workgroup, before any barrier
@@ -347,13 +390,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     const uint32_t row7 = e7 & kDfaRowMask;
     const bool open = row7 >= ((uint32_t)kDfaFirstPendingRow << 10);
     uint32_t e8 = dfa_at(s_dfa, row7 | ((cur.z << 2) & 0x3FCu));
-    if (__builtin_amdgcn_ballot_w64(open && (e8 & 7u) == 0)) {
+    if (__builtin_amdgcn_ballot_w64(open && (e8 & 0xFFu) == 0)) {
       const uint32_t e9 = dfa_at(s_dfa, (e8 & kDfaRowMask) | ((cur.z >> 6) & 0x3FCu));
-      if ((e8 & 7u) == 0) e8 = e9;
+      if ((e8 & 0xFFu) == 0) e8 = e9;
     }
-    const uint32_t et = open ? ((e8 & 0xF0000u) | 1u) : 0u;
-    int cnt = (int)((e0 & 7u) + (e1 & 7u) + (e2 & 7u) + (e3 & 7u) + (e4 & 7u) + (e5 & 7u) +
-                    (e6 & 7u) + (e7 & 7u) + (et & 7u));
+    const uint32_t et = open ? ((e8 & 0xF0000u) | 4u) : 0u;
+    // symbol counts are kept x4: the width of the chunk's nibbles in bits
+    int cnt4 = (int)((e0 & 0xFFu) + (e1 & 0xFFu) + (e2 & 0xFFu) + (e3 & 0xFFu) + (e4 & 0xFFu) +
+                     (e5 & 0xFFu) + (e6 & 0xFFu) + (e7 & 0xFFu) + (et & 0xFFu));
     // lanes in the exact row (the stream's final padding) count their chunk
     // with the reference rule instead
     const bool exact = row7 == ((uint32_t)kDfaExactRow << 10);
@@ -361,24 +405,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     if (any_exact && exact) {
       int n = 0;
       exact_walk(cur, gap, luts, n_luts, [&](uint32_t) { ++n; });
-      cnt = n;
+      cnt4 = 4 * n;
     }
 
     // ---- 2. block-wide exclusive prefix of the per-chunk symbol counts
-    const int incl = wave_inclusive_scan(cnt);
+    const int incl = wave_inclusive_scan(cnt4);
     if (lane == 63) s_wave_sum[wave] = incl;
     __syncthreads();
-    int excl = incl - cnt;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      if (w < wave) excl += s_wave_sum[w];
+    const int excl4 = incl - cnt4 + waves_before<kWaves>(s_wave_sum, lane, wave);
+    // the previous block's edge segments (parked before the barrier above)
+    flush_edges(s_edge, out, tid);
 
     // ---- 3. OR the exponents into the staging buffer at their positions,
     // two automaton entries (at most 8 symbols, 32 bits) per 64-bit OR.
     // Symbols past the block's count (only the stream's last chunk decodes
     // any: padding) land past the block's outputs and are never stored;
     // positions past the buffer go to its spill dwords.
-    uint32_t pos4 = (uint32_t)(br.lead + excl) << 2;  // bit offset in the buffer
+    uint32_t pos4 = ((uint32_t)br.lead << 2) + (uint32_t)excl4;  // bit offset in the buffer
     const uint32_t spill = (uint32_t)stage_dw;
     auto put = [&](uint32_t syms, uint32_t n4) {
       const uint64_t v = (uint64_t)syms << (pos4 & 31u);
@@ -388,8 +431,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
       pos4 += n4;
     };
     auto put2 = [&](uint32_t ea, uint32_t eb) {
-      const uint32_t na4 = (ea & 7u) << 2;
-      put(((eb >> 16) << na4) | (ea >> 16), na4 + ((eb & 7u) << 2));
+      const uint32_t na4 = ea & 0xFFu;
+      put(((eb >> 16) << na4) | (ea >> 16), na4 + (eb & 0xFFu));
     };
     if (!any_exact || !exact) {
       put2(e0, e1);
@@ -410,7 +453,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     const uint32_t nop_hi = __builtin_amdgcn_readlane(nopv, 1);
 
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
-    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, tid);
+    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, s_edge, tid);
     // the next iteration writes the other staging buffer; its barrier after
     // the scan orders this sweep before any reuse of this one
     if (fb_next >= n_fb) break;
@@ -420,6 +463,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     op_lo = nop_lo;
     op_hi = nop_hi;
   }
+  __syncthreads();
+  flush_edges(s_edge, out, tid);
 }
 
 // ===========================================================================
@@ -468,6 +513,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
   __shared__ uint32_t s_table[kMultiEntries + 1];
   __shared__ int s_wave_sum[kWaves];
+  __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -479,6 +525,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
 
   for (int i = tid; i <= kMultiEntries; i += kThreads)
     s_table[i] = i < kMultiEntries ? table[i] : 0u;
+  if (tid < kEdgeDwords) s_edge[tid] = 0u;
   const int len_row = (n_luts - 1) * 256;
   const uint32_t max_row = (uint32_t)(n_luts - 2);
 
@@ -623,10 +670,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     const int incl = wave_inclusive_scan(cnt);
     if (lane == 63) s_wave_sum[wave] = incl;
     __syncthreads();
-    int excl = incl - cnt;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      if (w < wave) excl += s_wave_sum[w];
+    const int excl = incl - cnt + waves_before<kWaves>(s_wave_sum, lane, wave);
+    flush_edges(s_edge, out, tid);
 
     // ---- 3. OR this lane's nibble run into the staging buffer
     int c = cnt;
@@ -655,13 +700,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     const uint32_t nop_hi = __builtin_amdgcn_readlane(nopv, 1);
 
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
-    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, tid);
+    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, s_edge, tid);
     if (fb_next >= n_fb) break;
     fb = fb_next;
     cur = nxt;
     op_lo = nop_lo;
     op_hi = nop_hi;
   }
+  __syncthreads();
+  flush_edges(s_edge, out, tid);
 }
 
 // ===========================================================================

@@ -51,7 +51,9 @@ ECF8_HD constexpr uint32_t entry_mask(uint32_t e) { return (e >> 16) & 0xFFFu; }
 // followed by 8 "skip a whole byte" entries (index 24*256 + r) that move to
 // row r without decoding, for chunks whose first code starts in byte 1.
 // Entry layout:
-//   bits  0..2   number of symbols completed in this byte (0..4)
+//   bits  0..7   4 x the number of symbols completed in this byte (0..16:
+//                their width in bits of packed nibbles; a whole byte, so it
+//                can be added without a mask)
 //   bits 10..14  next row (so entry & kDfaRowMask = next row * 1024 = the
 //                byte offset of that row in the table)
 //   bits 16..31  the completed symbols' exponents, first in bits 16..19;

@@ -167,7 +167,7 @@ class DfaBuilder {
       pos += l;
     }
     if (next < 0) return false;
-    *entry = (uint32_t)count | ((uint32_t)next << 10) | (syms << 16);
+    *entry = (uint32_t)(4 * count) | ((uint32_t)next << 10) | (syms << 16);
     return true;
   }
 

@@ -51,12 +51,14 @@ def _dfa_chunk_symbols(table, enc, gaps, g):
         return None  # the kernel decodes this chunk with the LUT rule itself
     is_open = row7 >= FIRST_PENDING_ROW << 10
     e8 = int(table[(row7 | (b[8] << 2)) >> 2])
-    if is_open and (e8 & 7) == 0:
+    if is_open and (e8 & 0xFF) == 0:
         e8 = int(table[((e8 & ROW_MASK) | (b[9] << 2)) >> 2])
     syms = []
     for e in entries:
-        syms += [(e >> (16 + 4 * i)) & 0xF for i in range(e & 7)]
-        assert e >> (16 + 4 * (e & 7)) == 0  # unused nibbles are zero
+        n = (e & 0xFF) >> 2
+        assert e & 0xFF == 4 * n
+        syms += [(e >> (16 + 4 * i)) & 0xF for i in range(n)]
+        assert e >> (16 + 4 * n) == 0  # unused nibbles are zero
     if is_open:
         syms.append((e8 >> 16) & 0xF)
     return syms
@@ -172,8 +174,8 @@ def test_dfa_rows_stay_inside_the_table():
     table, _ = _table(_golden("synth_128x256")["luts"], ECF8_TABLE_DFA)
     used = table[: SKIP_BYTE + 8]
     assert ((used & ROW_MASK) >> 10).max() < 24
-    assert (used & 7).max() <= 4
-    assert ((used >> 3) & 0x7F).max() == 0 and ((used >> 15) & 1).max() == 0
+    assert (used & 0xFF).max() <= 16 and ((used & 0xFF) % 4).max() == 0
+    assert ((used >> 8) & 3).max() == 0 and ((used >> 15) & 1).max() == 0
 
 
 def test_corrupt_luts_never_crash_the_builder():
