@@ -96,6 +96,7 @@ __device__ __forceinline__ int waves_before(const int *s_wave_sum, int lane, int
 }
 
 typedef uint32_t u32x3_a8 __attribute__((ext_vector_type(3), aligned(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // A chunk as fetched: 12 raw bytes from the chunk start (8 chunk bytes, 2
 // look-ahead bytes, 2 unused; little-endian dwords) and the byte holding its
@@ -218,7 +219,10 @@ __device__ __forceinline__ void write_block(const uint32_t *stage, const BlockRa
     const uint2 lo = merge8(ev.x, ov.x);
     const uint2 hi8 = merge8(ev.y, ov.y);
     if (gpos >= br.start && gpos + 16 <= br.end) {
-      *reinterpret_cast<uint4 *>(out + gpos) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
+      // streaming (non-temporal) store: the output is written once and read
+      // by the next kernel from HBM, so it should not displace cached input
+      const u32x4 w = {lo.x, lo.y, hi8.x, hi8.y};
+      __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(out + gpos));
     } else {  // only the first and the last segment can be partial
       uint32_t *const e = s_edge + (s == 0 ? 0 : kEdgeSlotDwords);
       *reinterpret_cast<uint4 *>(e) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
