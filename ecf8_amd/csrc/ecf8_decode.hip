@@ -257,12 +257,22 @@ __device__ __forceinline__ void flush_edges(uint32_t *s_edge, uint8_t *__restric
 // DFA kernel (tables of kind ECF8_TABLE_DFA)
 // ===========================================================================
 
+// Symbols one lane stages at most: 8 automaton entries of <= 4 plus the code
+// open at bit 64 (an exact-path chunk is capped at the same number), i.e.
+// 132 bits; the spill dwords after each staging buffer hold that much past
+// a start clamped to the buffer's end.
+constexpr int kMaxLaneSyms = 8 * kDfaMaxSyms + 1;
+constexpr int kSpillDwords = 8;
+
 // The reference rule (decode.cu:85-112) over one chunk, symbol by symbol,
 // from its gap: f(v) for each symbol starting before bit 64; a code-less
 // LUT entry ends the chunk.  LUT reads go to global memory (rare path).
 template <class F>
 __device__ __forceinline__ void exact_walk(const uint3 &d, uint32_t gap,
                                            const uint8_t *__restrict__ luts, int n_luts, F &&f) {
+  // a chunk of codes >= 2 bits owns at most 32; the cap bounds what a
+  // corrupt table's exact row could make the staging ORs reach
+  int left = kMaxLaneSyms;
   const uint64_t hi = __builtin_bswap64(((uint64_t)d.y << 32) | d.x);
   const uint32_t la = ((d.z & 0xFFu) << 8) | ((d.z >> 8) & 0xFFu);
   const uint32_t len_row = (uint32_t)(n_luts - 1) * 256;
@@ -273,11 +283,12 @@ __device__ __forceinline__ void exact_walk(const uint3 &d, uint32_t gap,
     uint32_t v = luts[w16 >> 8];
     if (v >= 240) v = luts[min(256 - v, max_row) * 256 + (w16 & 0xFF)];
     const uint32_t len = luts[len_row + v];
-    if (len == 0) break;
+    if (len == 0 || left-- == 0) break;
     f(v & 0xFu);
     q += (int)len;
   }
 }
+
 
 // The entry at byte offset `off` of the automaton in LDS.
 __device__ __forceinline__ uint32_t dfa_at(const uint32_t *s_dfa, uint32_t off) {
@@ -301,23 +312,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ int s_wave_sum[kWaves];
   __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
-  // dynamic LDS: 2 staging buffers, each followed by spill dwords that take
-  // the ORs of positions past the buffer (malformed or understated input)
+  // dynamic LDS: 2 staging buffers, each followed by kSpillDwords spill
+  // dwords that take the ORs of positions past the buffer
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int stage_dw = stage_dwords(stage_cap);
-  const int stage_stride = stage_dw + 4;
+  const int stage_stride = stage_dw + kSpillDwords;
 
-  // a row number outside the automaton (only a corrupt table has one) is
-  // replaced by the exact row, so every lookup stays inside s_dfa
+  // Fields a well-formed table never holds (only a corrupt or mismatched
+  // one) are forced into range as the table is loaded: a row outside the
+  // automaton becomes the exact row and a count above 4 symbols becomes 4,
+  // so every lookup stays inside s_dfa and every OR inside the staging
+  // buffer's spill dwords.
   for (int i = tid; i < kDfaEntries; i += kThreads) {
     uint32_t e = table[i];
     if ((e & kDfaRowMask) >= ((uint32_t)kDfaRows << 10))
       e = (e & ~kDfaRowMask) | ((uint32_t)kDfaExactRow << 10);
-    s_dfa[i] = e;
+    const uint32_t n4 = min(e & 0xFCu, 4u * kDfaMaxSyms);
+    s_dfa[i] = (e & 0xFFFF7C00u) | n4;
   }
   if (tid < kEdgeDwords) s_edge[tid] = 0u;
 
@@ -425,11 +440,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     // Symbols past the block's count (only the stream's last chunk decodes
     // any: padding) land past the block's outputs and are never stored;
     // positions past the buffer go to its spill dwords.
-    uint32_t pos4 = ((uint32_t)br.lead << 2) + (uint32_t)excl4;  // bit offset in the buffer
-    const uint32_t spill = (uint32_t)stage_dw;
+    // A lane's ORs reach at most 33 symbols (132 bits) past its start, so a
+    // start clamped to the buffer's end keeps every OR inside the buffer's
+    // 8 spill dwords (reached only by positions past the block's count).
+    uint32_t pos4 = min(((uint32_t)br.lead << 2) + (uint32_t)excl4, (uint32_t)stage_dw << 5);
     auto put = [&](uint32_t syms, uint32_t n4) {
       const uint64_t v = (uint64_t)syms << (pos4 & 31u);
-      uint32_t *const q = stage + min(pos4 >> 5, spill);
+      uint32_t *const q = stage + (pos4 >> 5);
       atomicOr(q, (uint32_t)v);
       atomicOr(q + 1, (uint32_t)(v >> 32));
       pos4 += n4;
@@ -444,7 +461,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
       put2(e4, e5);
       put2(e6, e7);
       put(et >> 16, 0u);
-    } else {
+    } else {  // at most 32 codes of >= 2 bits start in the chunk
       exact_walk(cur, gap, luts, n_luts, [&](uint32_t v) { put(v, 4u); });
     }
     __syncthreads();
@@ -781,8 +798,8 @@ struct DecodeArgs {
 template <int kThreads, bool kChecked>
 int launch_dfa(const DecodeArgs &a, int slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
-  const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(a.cap) + 4);
-  const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + 4);
+  const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(a.cap) + kSpillDwords);
+  const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
   auto kernel = decode_dfa_kernel<kThreads, kChecked>;
   int grid = 0;
   const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,

@@ -163,6 +163,28 @@ def test_config2_qwen3_layer_bit_exact(cuda_device):
         assert np.array_equal(got, flat_u8)
 
 
+@pytest.mark.parametrize("kind", [MULTI, DFA])
+def test_corrupt_table_stays_inside_the_output(kind, cuda_device):
+    """A table of random bits (a corrupt buffer, or one of the other kind)
+    decodes garbage, but the kernels force its fields into range: nothing is
+    written outside [0, n) and the launch completes."""
+    from ecf8_amd.decode import DecodeTable, decode_into
+
+    flat = _random_block(24)
+    block = _compress(flat)
+    d = _dev_block(block, cuda_device)
+    rng = np.random.default_rng(5 + kind)
+    junk = rng.integers(0, 2**32, 24608 // 4, dtype=np.uint64).astype(np.uint32)
+    n = flat.size
+    for table in (junk, _table_for(d, 1 - kind).data.cpu().numpy().view(np.uint32)):
+        t = DecodeTable(torch.from_numpy(table.view(np.int32)).to(cuda_device), kind)
+        out = torch.full((n + 512,), 0x77, dtype=torch.uint8, device=cuda_device)
+        decode_into(out[:n], d["luts"], d["encoded"], d["packed_other_4bits"],
+                    d["output_positions"], d["gaps"], table=t)
+        torch.cuda.synchronize()
+        assert (out[n:].cpu().numpy() == 0x77).all()
+
+
 def test_dfa_exact_path_is_bit_exact(cuda_device):
     """Chunks whose automaton walk reaches the exact row are decoded with the
     LUT rule itself.  Valid streams only get there in their final padding,
