@@ -124,3 +124,75 @@ def validate_cuda_decoding_fp8(result, tensors, device) -> None:
 
 
 validate_gpu_decoding_fp8 = validate_cuda_decoding_fp8
+
+
+def fp8_layers_by_block(model, fp8_regex) -> dict:
+    """{block name: {layer name: module}} of the FP8 layers to compress
+    (scripts/compress.py:515-536): with a list of block regexes, every FP8
+    Linear under each matching block; with a dict {regex: layer paths}, the
+    selected layers of each matching block."""
+    from .utils import (find_layers_by_data_type_and_layer_type, find_layers_by_selection,
+                        locate_block_by_regex)
+
+    out = {}
+    if isinstance(fp8_regex, dict):
+        for regex, selected in fp8_regex.items():
+            for name, block in locate_block_by_regex(model, regex).items():
+                out[name] = find_layers_by_selection(block, selected, name=name)
+    else:
+        for name, block in locate_block_by_regex(model, "|".join(fp8_regex)).items():
+            out[name] = find_layers_by_data_type_and_layer_type(
+                block, target_dtype=torch.float8_e4m3fn, layers=(torch.nn.Linear,), name=name)
+    return {k: v for k, v in out.items() if v}
+
+
+def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 512,
+                   bytes_per_thread: int = 8, bf16_regex=(), validate_device=None) -> dict:
+    """Compress every FP8 block of a local model and save it the way
+    scripts/compress.py:490-680 does for a model without a hub config: each
+    block's layers are removed and its compressed tensors registered as
+    buffers on the block module (:583-612); the state dict goes to
+    ``model.safetensors`` and the regexes to ``pattern_dict.json``
+    ({"fp8": {regex: layer names}, "bf16": {...}}, :634-680); the format
+    parameters to ``dfloat_config.json``.  Blocks are compressed one after
+    another (the reference's --sequential path).  Returns the pattern dict."""
+    import operator
+
+    from safetensors.torch import load_file, save_file
+
+    os.makedirs(save_path, exist_ok=True)
+    regexes = list(fp8_regex.keys()) if isinstance(fp8_regex, dict) else list(fp8_regex)
+    regex_dict = {r: None for r in regexes}
+    info = {"save_path": save_path, "model_fp8_regex": regexes,
+            "bytes_per_thread": bytes_per_thread, "threads_per_block": threads_per_block}
+    for block_name, layers in fp8_layers_by_block(model, fp8_regex).items():
+        result = process_fp8_block((block_name, layers), info)
+        tensors = load_file(result["block_save_path"])
+        if validate_device is not None:
+            validate_cuda_decoding_fp8(result, tensors, validate_device)
+        block = operator.attrgetter(block_name)(model)
+        for layer_name in result["layers_to_delete"]:
+            if layer_name == block_name:
+                delattr(block, "weight")
+            else:
+                parent_name, attr = layer_name.rsplit(".", 1)
+                delattr(operator.attrgetter(parent_name)(model), attr)
+        for key in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
+                    "split_positions"):
+            block.register_buffer(key, tensors[key])
+        matched = result["matched_regex"]
+        if matched:
+            if regex_dict[matched] is None:
+                regex_dict[matched] = result["layer_names"]
+            elif regex_dict[matched] != result["layer_names"]:
+                raise ValueError(f"{block_name}: layers {result['layer_names']} differ from "
+                                 f"{regex_dict[matched]} of the other blocks of {matched}")
+    state = {k: v.contiguous() for k, v in model.state_dict().items()}
+    save_file(state, os.path.join(save_path, "model.safetensors"))
+    pattern_dict = {"fp8": regex_dict, "bf16": {r: [] for r in bf16_regex}}
+    with open(os.path.join(save_path, "pattern_dict.json"), "w") as f:
+        json.dump(pattern_dict, f, indent=4)
+    with open(os.path.join(save_path, "dfloat_config.json"), "w") as f:
+        json.dump({"version": PACKAGE_FORMAT_VERSION, "threads_per_block": threads_per_block,
+                   "bytes_per_thread": bytes_per_thread}, f, indent=4)
+    return pattern_dict

@@ -35,6 +35,7 @@ __all__ = [
     "get_dfloat_model_name_or_path",
     "load_and_replace_tensors",
     "load_and_replace_tensors_parallel",
+    "load_compressed_model",
     "TensorManager",
     "get_hook",
 ]
@@ -310,6 +311,25 @@ def load_and_replace_tensors_parallel(model, directory_path, dfloat_config):
     print(f"Processed {total} tensors from {len(files)} files", file=stderr)
     validate_compressed_modules(model, tpb, bpt)
     return model
+
+
+def load_compressed_model(model, dfloat_dir: str, parallel: bool = False):
+    """Load a compressed checkpoint directory into ``model`` (an instance of
+    the original architecture): dfloat_config.json (or config.json's
+    ``dfloat_config``) and pattern_dict.json as DFloatDiffSynthModelFP8 and
+    DFloatModel read them (dfloat/run/run.py:510-522, 569-729), then the
+    loader registers every block's buffers and decode hook."""
+    cfg_path = os.path.join(dfloat_dir, "dfloat_config.json")
+    if os.path.exists(cfg_path):
+        with open(cfg_path) as f:
+            dfloat_config = json.load(f)
+    else:
+        with open(os.path.join(dfloat_dir, "config.json")) as f:
+            dfloat_config = dict(json.load(f)["dfloat_config"])
+    with open(os.path.join(dfloat_dir, "pattern_dict.json")) as f:
+        dfloat_config["pattern_dict"] = json.load(f)
+    loader = load_and_replace_tensors_parallel if parallel else load_and_replace_tensors
+    return loader(model, dfloat_dir, dfloat_config)
 
 
 def get_dfloat_model_name_or_path(repo_id: str, dfloat_dir: str = "../dfloat-models"):
