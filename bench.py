@@ -1,12 +1,17 @@
 """ECF8 decode benchmark on one MI355X.
 
-Workload: one Qwen3-8B-shaped decoder layer's seven FP8 e4m3fn linears
-(q/k/v/o/gate/up/down, 192,937,984 elements), synthetic N(0, sigma) weights
-block-quantized per 128x128 tile, compressed as ONE block exactly as the
-reference compresses a `model.layers.N` block.  A step is one decode of the
-whole layer (one kernel launch) from HBM-resident compressed tensors into an
-FP8 buffer.  Inputs/outputs rotate over several copies so the 256 MB
-Infinity Cache cannot serve a step from the previous one.
+Default workload (--workload qwen3-8b-layer): one Qwen3-8B-shaped decoder
+layer's seven FP8 e4m3fn linears (q/k/v/o/gate/up/down, 192,937,984
+elements), synthetic N(0, sigma) weights block-quantized per 128x128 tile,
+compressed as ONE block exactly as the reference compresses a
+`model.layers.N` block.  A step is one decode of the whole layer (one kernel
+launch) from HBM-resident compressed tensors into an FP8 buffer.
+Inputs/outputs rotate over several copies so the 256 MB Infinity Cache
+cannot serve a step from the previous one.
+
+--workload qwen3-moe-layer: one Qwen3-30B-A3B-shaped MoE layer, the
+attention block plus 128 expert blocks each compressed on its own, decoded
+by ONE batched launch (ecf8_decode_batched) per step.
 
 Prints ONE JSON line: decode GB/s of algorithmic bytes
 (compressed bytes read + FP8 bytes written), the roofline of the decode
@@ -35,10 +40,10 @@ def algorithmic_bytes(n_elements: int, n_bytes: int, n_luts: int, tpb: int = 512
     return reads + n_elements, reads, n_elements
 
 
-def _traffic_from_profile():
-    """HBM bytes per launch from the committed rocprofv3 counter summary, if
-    present (line `traffic_bytes_per_launch: <int>`)."""
-    path = os.path.join(REPO, "profiles", "decode_qwen3_layer_pmc.md")
+def _traffic_from_profile(name):
+    """HBM bytes per launch from the committed rocprofv3 counter summary
+    profiles/<name>, if present (line `traffic_bytes_per_launch: <int>`)."""
+    path = os.path.join(REPO, "profiles", name)
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", open(path).read())
@@ -96,6 +101,122 @@ def copy_calibration(steps, warmup):
                       "GBps_read_plus_write": round(2 * n / ms / 1e6, 1)}), flush=True)
 
 
+def _qwen3_layer_workload(args, dev):
+    """One Qwen3-8B-shaped layer as one compressed block: returns the
+    per-copy C-ABI calls, a verifier and the figures for the JSON line."""
+    import torch
+
+    from ecf8_amd._lib import lib
+    from ecf8_amd.compress import compress_flat
+    from ecf8_amd.decode import build_table, decode_into, largest_block, min_code_bits
+    from ecf8_amd.synth import flat_block, qwen3_8b_layer
+
+    t0 = time.time()
+    flat, _ = flat_block(qwen3_8b_layer(seed=args.seed))
+    block = compress_flat(flat)
+    n = flat.numel()
+    print(f"[bench] compressed layer: {n} elements -> {block['encoded'].numel()} bitstream bytes "
+          f"in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    n_luts = block["luts"].shape[0]
+    alg, _, _ = algorithmic_bytes(n, block["encoded"].numel(), n_luts)
+    keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
+    max_block = largest_block(block["output_positions"])
+    min_bits = min_code_bits(block["luts"])
+    sets = []
+    for _ in range(args.copies):
+        d = {k: block[k].contiguous().to(dev) for k in keys}
+        d["table"] = build_table(d["luts"])
+        d["out"] = torch.empty(n, dtype=torch.float8_e4m3fn, device=dev)
+        sets.append(d)
+    torch.cuda.synchronize()
+    # first decode of every set through the checked API, then straight C-ABI
+    # calls with the same arguments so host overhead cannot starve the queue
+    for d in sets:
+        decode_into(d["out"], d["luts"], d["encoded"], d["packed_other_4bits"],
+                    d["output_positions"], d["gaps"], table=d["table"],
+                    max_block_elements=max_block, min_code_bits=min_bits)
+    L = lib()
+    hstream = torch.cuda.current_stream(dev).cuda_stream
+    calls = [(L.ecf8_decode, (d["luts"].data_ptr(), d["encoded"].data_ptr(),
+                              d["packed_other_4bits"].data_ptr(), d["output_positions"].data_ptr(),
+                              d["gaps"].data_ptr(), d["out"].data_ptr(), n_luts,
+                              d["encoded"].numel(), n, max_block, min_bits,
+                              d["table"].data.data_ptr(), d["table"].kind, 512, 8, hstream))
+             for d in sets]
+
+    def verify():
+        return torch.equal(sets[0]["out"].view(torch.uint8).cpu(), flat.view(torch.uint8))
+
+    config = {
+        "workload": "qwen3-8b-layer-decode",
+        "elements": n,
+        "linears": "q,k,v,o,gate,up,down (one compressed block)",
+        "bitstream_bytes": block["encoded"].numel(),
+        "algorithmic_bytes": alg,
+        "rotated_copies": args.copies,
+        "threads_per_block": 512,
+        "bytes_per_thread": 8,
+        "table_kind": "dfa" if sets[0]["table"].kind == 1 else "multi",
+    }
+    return calls, verify, alg, n, config, (block, n)
+
+
+def _qwen3_moe_layer_workload(args, dev):
+    """One Qwen3-30B-A3B-shaped MoE layer: the attention block and all 128
+    expert blocks (each compressed on its own, as the reference's qwen3moe
+    patterns cut them), decoded by one batched launch."""
+    import torch
+
+    from ecf8_amd._lib import lib
+    from ecf8_amd.compress import compress_flat
+    from ecf8_amd.decode import build_table, prepare_batch
+    from ecf8_amd.synth import QWEN3_MOE_ATTN, QWEN3_MOE_EXPERT, flat_block, synthetic_block
+
+    t0 = time.time()
+    flats = [flat_block(synthetic_block(QWEN3_MOE_ATTN, args.seed))[0]]
+    flats += [flat_block(synthetic_block(QWEN3_MOE_EXPERT, args.seed + 1 + e))[0]
+              for e in range(128)]
+    comp = [compress_flat(f) for f in flats]
+    n = sum(f.numel() for f in flats)
+    alg = sum(algorithmic_bytes(f.numel(), c["encoded"].numel(), c["luts"].shape[0])[0]
+              for f, c in zip(flats, comp))
+    print(f"[bench] compressed moe layer: {len(flats)} blocks, {n} elements in "
+          f"{time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
+    plans, first_outs = [], None
+    copies = max(1, min(args.copies, 2))
+    for _ in range(copies):
+        blocks = [{k: c[k].contiguous().to(dev) for k in keys} for c in comp]
+        tables = [build_table(b["luts"]) for b in blocks]
+        outs = [torch.empty(f.numel(), dtype=torch.float8_e4m3fn, device=dev) for f in flats]
+        first_outs = outs if first_outs is None else first_outs
+        plans.append(prepare_batch(blocks, outs, tables))
+    torch.cuda.synchronize()
+    assert all(not p.singles for p in plans)
+    L = lib()
+    hstream = torch.cuda.current_stream(dev).cuda_stream
+    calls = [(L.ecf8_decode_batched, (p.descs.data_ptr(), p.count, p.n_tasks, p.blocks_per_task,
+                                      p.cap, 512, hstream)) for p in plans]
+
+    def verify():
+        return all(torch.equal(o.view(torch.uint8).cpu(), f.view(torch.uint8))
+                   for o, f in zip(first_outs, flats))
+
+    config = {
+        "workload": "qwen3-moe-layer-decode",
+        "elements": n,
+        "blocks": len(flats),
+        "linears": "attention q,k,v,o + 128 experts x gate,up,down (one block each)",
+        "algorithmic_bytes": alg,
+        "rotated_copies": copies,
+        "blocks_per_task": plans[0].blocks_per_task,
+        "tasks": plans[0].n_tasks,
+        "threads_per_block": 512,
+        "bytes_per_thread": 8,
+    }
+    return calls, verify, alg, n, config, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +225,9 @@ def main():
     ap.add_argument("--copies", type=int, default=4, help="rotated input/output sets")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer"),
+                    default="qwen3-8b-layer",
+                    help="qwen3-moe-layer: attention + 128 experts in one batched launch")
     ap.add_argument("--mode", choices=("decode", "copy"), default="decode",
                     help="copy: time a plain 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -116,56 +240,24 @@ def main():
 
     import torch
 
-    from ecf8_amd._lib import lib
-    from ecf8_amd.compress import compress_flat
-    from ecf8_amd.decode import build_table, decode_into, largest_block, min_code_bits
-    from ecf8_amd.synth import flat_block, qwen3_8b_layer
-
     dev = torch.device("cuda", 0)
-    t0 = time.time()
-    flat, _ = flat_block(qwen3_8b_layer(seed=args.seed))
-    block = compress_flat(flat)
-    n = flat.numel()
-    print(f"[bench] compressed layer: {n} elements -> {block['encoded'].numel()} bitstream bytes "
-          f"in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    n_luts = block["luts"].shape[0]
-    alg, alg_r, alg_w = algorithmic_bytes(n, block["encoded"].numel(), n_luts)
-
-    keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
-    max_block = largest_block(block["output_positions"])
-    min_bits = min_code_bits(block["luts"])
-    sets = []
-    for _ in range(args.copies):
-        d = {k: block[k].contiguous().to(dev) for k in keys}
-        d["table"] = build_table(d["luts"])
-        d["out"] = torch.empty(n, dtype=torch.float8_e4m3fn, device=dev)
-        sets.append(d)
-    torch.cuda.synchronize()
-
-    # first decode of every set through the checked API, then straight C-ABI
-    # calls with the same arguments so host overhead cannot starve the queue
-    for d in sets:
-        decode_into(d["out"], d["luts"], d["encoded"], d["packed_other_4bits"],
-                    d["output_positions"], d["gaps"], table=d["table"],
-                    max_block_elements=max_block, min_code_bits=min_bits)
-    L = lib()
-    hstream = torch.cuda.current_stream(dev).cuda_stream
-    calls = [(d["luts"].data_ptr(), d["encoded"].data_ptr(), d["packed_other_4bits"].data_ptr(),
-              d["output_positions"].data_ptr(), d["gaps"].data_ptr(), d["out"].data_ptr(), n_luts,
-              d["encoded"].numel(), n, max_block, min_bits, d["table"].data.data_ptr(),
-              d["table"].kind, 512, 8, hstream) for d in sets]
+    setup = _qwen3_layer_workload if args.workload == "qwen3-8b-layer" else _qwen3_moe_layer_workload
+    calls, verify, alg, n, config, cpu_case = setup(args, dev)
+    pmc_profile = ("decode_qwen3_layer_pmc.md" if args.workload == "qwen3-8b-layer"
+                   else "decode_qwen3_moe_layer_pmc.md")
 
     def step(i):
-        rc = L.ecf8_decode(*calls[i % len(calls)])
+        fn, cargs = calls[i % len(calls)]
+        rc = fn(*cargs)
         if rc:
-            raise RuntimeError(f"ecf8_decode failed with status {rc}")
+            raise RuntimeError(f"decode failed with status {rc}")
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    ok = torch.equal(sets[0]["out"].view(torch.uint8).cpu(), flat.view(torch.uint8))
+    ok = verify()
     if not ok:
-        print("[bench] decoded layer differs from the original FP8 bytes", file=sys.stderr)
+        print("[bench] decoded weights differ from the original FP8 bytes", file=sys.stderr)
         sys.exit(1)
 
     # One event pair around the K back-to-back launches on the launch stream:
@@ -188,7 +280,9 @@ def main():
     gbps = alg / (ms_per_step * 1e-3) / 1e9
     kernel_gbps = alg / (avg_launch_ms * 1e-3) / 1e9
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(block, n, alg)
+    cpu = None
+    if not args.no_cpu_baseline and cpu_case is not None:
+        cpu = cpu_baseline(cpu_case[0], cpu_case[1], alg)
     line = {
         "metric": "ECF8 decode GB/s + % HBM roofline; e2e tokens/s, Qwen3-8B-shape bs16",
         "value": round(gbps, 1),
@@ -202,23 +296,14 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic",
-        "config": {
-            "workload": "qwen3-8b-layer-decode",
-            "elements": n,
-            "linears": "q,k,v,o,gate,up,down (one compressed block)",
-            "bitstream_bytes": block["encoded"].numel(),
-            "algorithmic_bytes": alg,
-            "rotated_copies": args.copies,
-            "threads_per_block": 512,
-            "bytes_per_thread": 8,
-        },
+        "config": config,
         "roofline": {
             "bound": "hbm",
             "achieved": round(kernel_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": _traffic_from_profile(),
+            "traffic": _traffic_from_profile(pmc_profile),
         },
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 4),

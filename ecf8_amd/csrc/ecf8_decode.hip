@@ -295,38 +295,27 @@ __device__ __forceinline__ uint32_t dfa_at(const uint32_t *s_dfa, uint32_t off) 
   return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(s_dfa) + off);
 }
 
-// kChecked: tensors too small for the clamped vector loads (fewer than 12
-// bitstream bytes or 16 elements) use byte-wise loads throughout.
-//
-// SGPRs are capped at 80: measured on MI355X, above that fewer than 8 waves
-// per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
-// the cap causes go to VGPR lanes.
-template <int kThreads, bool kChecked>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_kernel(
-    const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
-    const uint8_t *__restrict__ encoded, uint32_t n_bytes,
-    const uint8_t *__restrict__ packed, const uint64_t *__restrict__ op,
-    const uint8_t *__restrict__ gaps, uint8_t *__restrict__ out, uint32_t n_elements, int n_fb,
-    int stage_cap) {
-  constexpr int kWaves = kThreads / 64;
-  __shared__ uint32_t s_dfa[kDfaEntries];
-  __shared__ int s_wave_sum[kWaves];
-  __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
-  // dynamic LDS: 2 staging buffers, each followed by kSpillDwords spill
-  // dwords that take the ORs of positions past the buffer
-  extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
+// One compressed block's device buffers.
+struct BlockArgs {
+  const uint8_t *luts;
+  int n_luts;
+  const uint8_t *encoded;
+  uint32_t n_bytes;
+  const uint8_t *packed;
+  const uint32_t *op32;  // output_positions as little-endian dword pairs
+  const uint8_t *gaps;
+  uint8_t *out;
+  uint32_t n_elements;
+};
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int stage_dw = stage_dwords(stage_cap);
-  const int stage_stride = stage_dw + kSpillDwords;
-
-  // Fields a well-formed table never holds (only a corrupt or mismatched
-  // one) are forced into range as the table is loaded: a row outside the
-  // automaton becomes the exact row and a count above 4 symbols becomes 4,
-  // so every lookup stays inside s_dfa and every OR inside the staging
-  // buffer's spill dwords.
+// Load a table into the workgroup's LDS automaton.  Fields a well-formed
+// table never holds (only a corrupt or mismatched one) are forced into range:
+// a row outside the automaton becomes the exact row and a count above 4
+// symbols becomes 4, so every lookup stays inside s_dfa and every OR inside
+// the staging buffer's spill dwords.
+template <int kThreads>
+__device__ __forceinline__ void load_dfa(uint32_t *s_dfa, const uint32_t *__restrict__ table,
+                                         int tid) {
   for (int i = tid; i < kDfaEntries; i += kThreads) {
     uint32_t e = table[i];
     if ((e & kDfaRowMask) >= ((uint32_t)kDfaRows << 10))
@@ -334,10 +323,35 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     const uint32_t n4 = min(e & 0xFCu, 4u * kDfaMaxSyms);
     s_dfa[i] = (e & 0xFFFF7C00u) | n4;
   }
-  if (tid < kEdgeDwords) s_edge[tid] = 0u;
+}
 
-  int fb = blockIdx.x;
-  if (fb >= n_fb) return;  // uniform per workgroup, before any barrier
+// Decode format-blocks fb, fb + fb_step, ... below fb_end (fb < fb_end) of
+// one tensor whose table is in s_dfa (loaded before the first barrier here).
+// s_edge's slots must be empty on entry; they are empty again on return, and
+// every wave has passed a final barrier.
+//
+// kChecked: tensors too small for the clamped vector loads (fewer than 12
+// bitstream bytes or 16 elements) use byte-wise loads throughout.
+template <int kThreads, bool kChecked>
+__device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s_dfa,
+                                           int *s_wave_sum, uint32_t *s_edge, uint32_t *s_dyn,
+                                           int stage_cap, int fb, int fb_step, int fb_end) {
+  constexpr int kWaves = kThreads / 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int stage_dw = stage_dwords(stage_cap);
+  const int stage_stride = stage_dw + kSpillDwords;
+  const uint8_t *const luts = a.luts;
+  const int n_luts = a.n_luts;
+  const uint8_t *const encoded = a.encoded;
+  const uint32_t n_bytes = a.n_bytes;
+  const uint8_t *const packed = a.packed;
+  const uint32_t *const op32 = a.op32;
+  const uint8_t *const gaps = a.gaps;
+  uint8_t *const out = a.out;
+  const uint32_t n_elements = a.n_elements;
+
   const uint32_t last12 = kChecked ? 0u : ((n_bytes - 12) & ~7u);
   const uint32_t last8 = kChecked ? 0u : (((n_elements >> 1) - 8) & ~7u);
 
@@ -356,14 +370,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   const RawChunk raw0 = fetch(fb);
   uint3 cur = chunk_bytes(raw0, encoded, n_bytes, g_cur, !kChecked);
   uint32_t gap = gap_of(raw0.gap_byte, g_cur);
-  // Positions are below 2^31 (checked on the host), so only the low dword of
-  // each little-endian u64 is loaded: a dead high half would be reused as a
-  // temporary and force an early wait on every load in flight.
-  const uint32_t *const op32 = reinterpret_cast<const uint32_t *>(op);
-  // this block's output range, wave-uniform.  Positions are always read
-  // (readlane waits on the vector load) before the block's stores are
-  // issued: the memory counter also counts stores, so a later wait would
-  // drain them too.
+  // This block's output range, wave-uniform.  Positions are below 2^31
+  // (checked on the host), so only the low dword of each little-endian u64
+  // is loaded: a dead high half would be reused as a temporary and force an
+  // early wait on every load in flight.  Positions are always read (readlane
+  // waits on the vector load) before the block's stores are issued: the
+  // memory counter also counts stores, so a later wait would drain them too.
   uint32_t op_lo, op_hi;
   {
     const uint32_t opv = op32[2 * (fb + (lane & 1))];
@@ -374,10 +386,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
 
   for (int buf_sel = 0;; buf_sel ^= 1) {
     uint32_t *const stage = s_dyn + buf_sel * stage_stride;
-    const int fb_next = fb + (int)gridDim.x;
+    const int fb_next = fb + fb_step;
     // prefetch target: the next block, or this one again after the last (in
     // bounds, discarded) so no load or wait depends on a branch
-    const int fb_pf = fb_next < n_fb ? fb_next : fb;
+    const int fb_pf = fb_next < fb_end ? fb_next : fb;
 
     const BlockRange br = block_range(op_lo, op_hi, n_elements, stage_cap);
     uint2 pre0 = make_uint2(0, 0), pre1 = make_uint2(0, 0);
@@ -477,7 +489,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, s_edge, tid);
     // the next iteration writes the other staging buffer; its barrier after
     // the scan orders this sweep before any reuse of this one
-    if (fb_next >= n_fb) break;
+    if (fb_next >= fb_end) break;
     fb = fb_next;
     cur = nxt;
     gap = nxt_gap;
@@ -486,6 +498,86 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   }
   __syncthreads();
   flush_edges(s_edge, out, tid);
+}
+
+// One tensor: the persistent grid strides over its format-blocks.
+//
+// SGPRs are capped at 80: measured on MI355X, above that fewer than 8 waves
+// per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
+// the cap causes go to VGPR lanes.
+template <int kThreads, bool kChecked>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_kernel(
+    const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
+    const uint8_t *__restrict__ encoded, uint32_t n_bytes,
+    const uint8_t *__restrict__ packed, const uint64_t *__restrict__ op,
+    const uint8_t *__restrict__ gaps, uint8_t *__restrict__ out, uint32_t n_elements, int n_fb,
+    int stage_cap) {
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ int s_wave_sum[kWaves];
+  __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
+  // dynamic LDS: 2 staging buffers, each followed by kSpillDwords spill
+  // dwords that take the ORs of positions past the buffer
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
+
+  const int tid = threadIdx.x;
+  load_dfa<kThreads>(s_dfa, table, tid);
+  if (tid < kEdgeDwords) s_edge[tid] = 0u;
+  if ((int)blockIdx.x >= n_fb) return;  // uniform per workgroup, before any barrier
+  const BlockArgs a{luts, n_luts, encoded, n_bytes, packed,
+                    reinterpret_cast<const uint32_t *>(op), gaps, out, n_elements};
+  dfa_blocks<kThreads, kChecked>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap,
+                                 (int)blockIdx.x, (int)gridDim.x, n_fb);
+}
+
+// Many tensors in one launch (e.g. the routed experts of an MoE layer): the
+// work is split into tasks of up to `blocks_per_task` format-blocks of one
+// tensor; desc[d].task_begin is the first task of tensor d.  Each workgroup
+// takes tasks blockIdx.x, + gridDim.x, ..., loading the task's table before
+// decoding it.
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_batched_kernel(
+    const ecf8_block_desc *__restrict__ descs, int count, int n_tasks, int blocks_per_task,
+    int stage_cap) {
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ int s_wave_sum[kWaves];
+  __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
+
+  const int tid = threadIdx.x;
+  if (tid < kEdgeDwords) s_edge[tid] = 0u;
+  constexpr uint32_t kBlockBytes = (uint32_t)kThreads * kChunkBytes;
+  for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
+    // the tensor of this task: the last descriptor whose first task is <= it
+    int lo = 0, hi = count - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (descs[mid].task_begin <= task) lo = mid;
+      else hi = mid - 1;
+    }
+    const ecf8_block_desc &d = descs[lo];
+    // uniform; blocks too small for the clamped vector loads (fewer than 12
+    // bitstream bytes or 16 elements) or too large for 32-bit positions are
+    // not batched, nor is a task outside its block (malformed task_begin)
+    if (d.n_bytes < 12 || d.n_elements < 16 || d.n_bytes > INT32_MAX - 64 ||
+        d.n_elements > INT32_MAX - 64 || task < d.task_begin)
+      continue;
+    const uint32_t n_bytes = (uint32_t)d.n_bytes;
+    const int n_fb = (int)((n_bytes + kBlockBytes - 1) / kBlockBytes);
+    // the block's n_tasks tasks interleave its format-blocks (task r takes
+    // r, r + n_tasks, ...), so the workgroups running them at the same time
+    // sweep the block's bytes in order, as the one-block kernel does
+    const int tasks = (n_fb + blocks_per_task - 1) / blocks_per_task;
+    const int fb0 = task - d.task_begin;
+    if (fb0 >= tasks) continue;
+    // the previous task ended with a barrier: no wave still reads s_dfa
+    load_dfa<kThreads>(s_dfa, d.table, tid);
+    const BlockArgs a{d.luts, d.n_luts, d.encoded, n_bytes, d.packed_other_4bits,
+                      reinterpret_cast<const uint32_t *>(d.output_positions), d.gaps,
+                      d.outputs, (uint32_t)d.n_elements};
+    dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, fb0, tasks, n_fb);
+  }
 }
 
 // ===========================================================================
@@ -738,7 +830,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
 
 // Per device: CU count, and per kernel variant the occupancy at the last
 // dynamic LDS size it was launched with.
-constexpr int kVariants = 16;  // {DFA, MULTI} x 4 block sizes x {unchecked, checked}
+// {DFA, MULTI} x 4 block sizes x {unchecked, checked}, then batched DFA x 4
+constexpr int kVariants = 20;
 struct LaunchCache {
   int device = -1;
   int cus = 0;
@@ -846,7 +939,50 @@ int launch_decode(DecodeArgs a, int64_t max_block_elements, bool dfa, int tpb_sl
   return checked ? launch_multi<kThreads, true>(a, slot) : launch_multi<kThreads, false>(a, slot);
 }
 
+template <int kThreads>
+int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int blocks_per_task,
+                       int cap, hipStream_t stream, int slot) {
+  constexpr int kMaxSyms = kThreads * kChunkBits;
+  const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(cap) + kSpillDwords);
+  const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
+  auto kernel = decode_dfa_batched_kernel<kThreads>;
+  int grid = 0;
+  const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
+                                 slot, n_tasks, &grid);
+  if (rc != ECF8_OK) return rc;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, stream, descs, count,
+                     n_tasks, blocks_per_task, cap);
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
 }  // namespace
+
+extern "C" int ecf8_decode_batched(const ecf8_block_desc *descs, int count, int n_tasks,
+                                   int blocks_per_task, int64_t max_block_elements,
+                                   int threads_per_block, void *stream) {
+  if (count < 0 || n_tasks < 0 || blocks_per_task < 1) return ECF8_ERR_INVALID_ARG;
+  if (count == 0 || n_tasks == 0) return ECF8_OK;
+  if (!descs) return ECF8_ERR_INVALID_ARG;
+  if ((uintptr_t)descs & 7) return ECF8_ERR_MISALIGNED;
+  if (threads_per_block != 128 && threads_per_block != 256 && threads_per_block != 512 &&
+      threads_per_block != 1024)
+    return ECF8_ERR_UNSUPPORTED;
+  const int64_t max_syms = (int64_t)threads_per_block * kChunkBits;
+  int cap = (max_block_elements <= 0 || max_block_elements > max_syms) ? (int)max_syms
+                                                                        : (int)max_block_elements;
+  if (cap < 16) cap = 16;
+  hipStream_t s = (hipStream_t)stream;
+  switch (threads_per_block) {
+    case 128:
+      return launch_dfa_batched<128>(descs, count, n_tasks, blocks_per_task, cap, s, 16);
+    case 256:
+      return launch_dfa_batched<256>(descs, count, n_tasks, blocks_per_task, cap, s, 17);
+    case 512:
+      return launch_dfa_batched<512>(descs, count, n_tasks, blocks_per_task, cap, s, 18);
+    default:
+      return launch_dfa_batched<1024>(descs, count, n_tasks, blocks_per_task, cap, s, 19);
+  }
+}
 
 extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, uint32_t *table,
                                 int *table_kind, void *stream) {

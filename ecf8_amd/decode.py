@@ -17,6 +17,7 @@ from ._lib import (ECF8_MAX_LUTS, ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8_TABLE_D
                    ECF8_TABLE_MULTI, ECF8Error, check, lib)
 
 __all__ = ["DecodeTable", "build_table", "build_table_host", "decode_into", "decode",
+           "decode_batched", "prepare_batch", "BatchPlan",
            "n_format_blocks", "largest_block", "min_code_bits", "validate_format", "ECF8Error",
            "ECF8_TABLE_ANY", "ECF8_TABLE_MULTI", "ECF8_TABLE_DFA"]
 
@@ -167,6 +168,127 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
                                 int(table.kind), threads_per_block, bytes_per_thread,
                                 _stream_handle(dev, stream)), "ecf8_decode")
     return out
+
+
+# ecf8_block_desc (include/ecf8.h): 7 device pointers, n_bytes, n_elements,
+# n_luts, task_begin
+BLOCK_DESC_DTYPE = np.dtype([
+    ("luts", "<u8"), ("encoded", "<u8"), ("packed_other_4bits", "<u8"),
+    ("output_positions", "<u8"), ("gaps", "<u8"), ("outputs", "<u8"), ("table", "<u8"),
+    ("n_bytes", "<i8"), ("n_elements", "<i8"), ("n_luts", "<i4"), ("task_begin", "<i4")])
+assert BLOCK_DESC_DTYPE.itemsize == 80
+
+
+class BatchPlan:
+    """Device descriptors for one batched decode (ecf8_decode_batched),
+    built once by prepare_batch and replayed by decode_batched: the tensors
+    they point to must stay alive and in place while the plan is used."""
+
+    def __init__(self, descs, count, n_tasks, blocks_per_task, cap, threads_per_block,
+                 singles, keep):
+        self.descs = descs            # u8 device tensor of ecf8_block_desc
+        self.count = count
+        self.n_tasks = n_tasks
+        self.blocks_per_task = blocks_per_task
+        self.cap = cap
+        self.threads_per_block = threads_per_block
+        self.singles = singles        # decode_into argument tuples of unbatched blocks
+        self._keep = keep             # the referenced tensors
+
+
+def prepare_batch(blocks, outs, tables, threads_per_block: int = 512, bytes_per_thread: int = 8,
+                  blocks_per_task: int | None = None, max_block_elements=None) -> BatchPlan:
+    """Plan a batched decode of many compressed blocks on one device (e.g.
+    the experts of an MoE layer): checks every block as decode_into does,
+    uploads the descriptors once, and picks blocks_per_task so that the work
+    splits into about four tasks per resident workgroup.
+
+    ``blocks``: dicts with the block tensors (``luts``, ``encoded``,
+    ``packed_other_4bits``, ``output_positions``, ``gaps``); ``outs``: one
+    output tensor per block; ``tables``: one DecodeTable per block.  Blocks
+    whose table is not an automaton, or that are too small for the batched
+    kernel, are decoded one by one with decode_into.  ``max_block_elements``
+    bounds every block's largest format-block (None: read on the host)."""
+    if not (len(blocks) == len(outs) == len(tables)):
+        raise ECF8Error("blocks, outs and tables differ in length")
+    keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
+    dev, rows, singles, largest = None, [], [], 0
+    for b, out, t in zip(blocks, outs, tables):
+        enc = b["encoded"]
+        n = b["packed_other_4bits"].numel() * 2
+        dev = enc.device if dev is None else dev
+        if not isinstance(t, DecodeTable):
+            raise ECF8Error("tables must be DecodeTables returned by build_table")
+        if (t.kind != ECF8_TABLE_DFA or enc.numel() < 12 or n < 16 or bytes_per_thread != 8):
+            singles.append(((out, *(b[k] for k in keys)), t))
+            continue
+        _check_block(out, b, t, n, threads_per_block, bytes_per_thread, dev)
+        rows.append((b["luts"].data_ptr(), enc.data_ptr(), b["packed_other_4bits"].data_ptr(),
+                     b["output_positions"].data_ptr(), b["gaps"].data_ptr(), out.data_ptr(),
+                     t.data.data_ptr(), enc.numel(), n, _n_luts(b["luts"]), 0))
+        if max_block_elements is None:
+            largest = max(largest, largest_block(b["output_positions"]))
+    descs = np.zeros(len(rows), BLOCK_DESC_DTYPE)
+    for i, r in enumerate(rows):
+        descs[i] = r
+    n_fb = -(-descs["n_bytes"] // (threads_per_block * bytes_per_thread))
+    if blocks_per_task is None:
+        slots = 4 * _resident_workgroups(dev) if rows else 1
+        blocks_per_task = int(min(64, max(2, -(-int(n_fb.sum()) // slots))))
+    if blocks_per_task < 1:
+        raise ECF8Error("blocks_per_task must be >= 1")
+    n_task = -(-n_fb // blocks_per_task)
+    if rows:
+        descs["task_begin"] = np.concatenate([[0], np.cumsum(n_task)[:-1]])
+    d_descs = torch.from_numpy(descs.view(np.uint8).copy()).to(dev) if rows else None
+    cap = int(max_block_elements) if max_block_elements is not None else largest
+    return BatchPlan(d_descs, len(rows), int(n_task.sum()), blocks_per_task, cap,
+                     threads_per_block, singles, (list(blocks), list(outs), list(tables)))
+
+
+def _resident_workgroups(dev) -> int:
+    """CUs x 4: the 512-lane automaton kernel keeps 4 workgroups per CU."""
+    return torch.cuda.get_device_properties(dev).multi_processor_count * 4
+
+
+def decode_batched(plan, outs=None, tables=None, stream=None, **kwargs):
+    """Run a BatchPlan (one launch plus the unbatched blocks).  For
+    convenience, ``decode_batched(blocks, outs, tables, ...)`` prepares the
+    plan first (prepare_batch's keyword arguments apply)."""
+    if not isinstance(plan, BatchPlan):
+        plan = prepare_batch(plan, outs, tables, **kwargs)
+    for args, t in plan.singles:
+        decode_into(*args, table=t, threads_per_block=plan.threads_per_block, stream=stream)
+    if plan.count:
+        dev = plan.descs.device
+        with torch.cuda.device(dev):
+            check(lib().ecf8_decode_batched(plan.descs.data_ptr(), plan.count, plan.n_tasks,
+                                            plan.blocks_per_task, plan.cap,
+                                            plan.threads_per_block, _stream_handle(dev, stream)),
+                  "ecf8_decode_batched")
+    return plan
+
+
+def _check_block(out, b, t, n, threads_per_block, bytes_per_thread, dev):
+    for name in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps"):
+        v = b[name]
+        if not v.is_cuda or v.device != dev or not v.is_contiguous():
+            raise ECF8Error(f"{name} must be a contiguous tensor on {dev}")
+    if not out.is_cuda or out.device != dev or out.numel() < n or out.dtype not in (
+            torch.uint8, torch.float8_e4m3fn):
+        raise ECF8Error("out must be a uint8/e4m3fn tensor on the blocks' device holding n")
+    if t.data.device != dev:
+        raise ECF8Error(f"table must be on {dev}")
+    n_fb = n_format_blocks(b["encoded"].numel(), threads_per_block, bytes_per_thread)
+    if b["gaps"].numel() != n_fb * threads_per_block // 2:
+        raise ECF8Error("gaps size does not match the bitstream")
+    if _op_entries(b["output_positions"]) != n_fb + 1:
+        raise ECF8Error("output_positions size does not match the bitstream")
+    if (b["encoded"].data_ptr() & 15 or b["packed_other_4bits"].data_ptr() & 7
+            or out.data_ptr() & 15 or t.data.data_ptr() & 3 or b["output_positions"].data_ptr() & 7):
+        raise ECF8Error("misaligned device buffer")
+    if b["encoded"].numel() > 2**31 - 65 or n > 2**31 - 65:
+        raise ECF8Error("block too large for 32-bit positions")
 
 
 def decode(luts, encoded, packed_other_4bits, output_positions, gaps, table=None,

@@ -27,6 +27,39 @@ QWEN3_8B_LAYER = {
 }
 
 
+# FLUX.1-dev-shaped DiT blocks (hidden 3072, MLP 12288, 24 heads x 128):
+# the FP8 linears of one double-stream and one single-stream block.
+FLUX_DOUBLE_BLOCK = {
+    "attn.a_to_out": (3072, 3072, 0.02),
+    "attn.a_to_qkv": (9216, 3072, 0.02),
+    "attn.b_to_out": (3072, 3072, 0.02),
+    "attn.b_to_qkv": (9216, 3072, 0.02),
+    "ff_a.0": (12288, 3072, 0.02),
+    "ff_a.2": (3072, 12288, 0.02),
+    "ff_b.0": (12288, 3072, 0.02),
+    "ff_b.2": (3072, 12288, 0.02),
+}
+FLUX_SINGLE_BLOCK = {
+    "norm.linear": (9216, 3072, 0.02),
+    "proj_out": (3072, 15360, 0.02),
+    "to_qkv_mlp": (21504, 3072, 0.02),
+}
+
+# Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128 experts of intermediate
+# 768, 32 query / 4 KV heads x 128): one expert block and the attention block.
+QWEN3_MOE_EXPERT = {
+    "down_proj": (2048, 768, 0.02),
+    "gate_proj": (768, 2048, 0.02),
+    "up_proj": (768, 2048, 0.02),
+}
+QWEN3_MOE_ATTN = {
+    "k_proj": (512, 2048, 0.02),
+    "o_proj": (2048, 4096, 0.01),
+    "q_proj": (4096, 2048, 0.02),
+    "v_proj": (512, 2048, 0.02),
+}
+
+
 def quantize_fp8_blockwise(w: torch.Tensor, block: int = BLOCK):
     """fp32 [out, in] -> (e4m3fn [out, in], weight_scale_inv fp32 [out/b, in/b])."""
     rows, cols = w.shape
@@ -49,11 +82,17 @@ def synthetic_fp8(rows: int, cols: int, sigma: float = 0.02, seed: int = 0,
     return quantize_fp8_blockwise(w)
 
 
-def qwen3_8b_layer(seed: int = 0):
-    """{name: (fp8 weight, scale_inv)} for one Qwen3-8B-shaped layer, drawn
-    from one generator seeded with ``seed`` in name-sorted order."""
+def synthetic_block(shapes: dict, seed: int = 0):
+    """{name: (fp8 weight, scale_inv)} for a block of linears given as
+    {name: (out, in, sigma)}, drawn from one generator seeded with ``seed``
+    in name-sorted order."""
     g = torch.Generator().manual_seed(seed)
-    return {name: synthetic_fp8(o, i, s, generator=g) for name, (o, i, s) in QWEN3_8B_LAYER.items()}
+    return {name: synthetic_fp8(o, i, s, generator=g) for name, (o, i, s) in sorted(shapes.items())}
+
+
+def qwen3_8b_layer(seed: int = 0):
+    """{name: (fp8 weight, scale_inv)} for one Qwen3-8B-shaped layer."""
+    return synthetic_block(QWEN3_8B_LAYER, seed)
 
 
 def flat_block(weights: dict) -> tuple[torch.Tensor, list[int]]:

@@ -108,6 +108,43 @@ int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *pack
                 int min_code_bits, const uint32_t *table, int table_kind,
                 int threads_per_block, int bytes_per_thread, void *stream);
 
+/*
+ * One compressed block of a batched decode.  The array of descriptors lives
+ * in device memory; every field keeps its ecf8_decode meaning and
+ * requirements (bytes_per_thread 8; `table` must be an ECF8_TABLE_DFA table
+ * built for `luts`); blocks with fewer than 12 bitstream bytes or 16
+ * elements are skipped (decode those with ecf8_decode).  task_begin is the
+ * index of the block's first task:
+ * task_begin[0] = 0 and task_begin[d+1] = task_begin[d] +
+ * ceil(ceil(n_bytes[d] / (threads_per_block * 8)) / blocks_per_task).
+ */
+typedef struct ecf8_block_desc {
+  const uint8_t *luts;
+  const uint8_t *encoded;
+  const uint8_t *packed_other_4bits;
+  const uint64_t *output_positions;
+  const uint8_t *gaps;
+  uint8_t *outputs;
+  const uint32_t *table;
+  int64_t n_bytes;
+  int64_t n_elements;
+  int32_t n_luts;
+  int32_t task_begin;
+} ecf8_block_desc; /* 80 bytes */
+
+/*
+ * Decode many compressed blocks in one launch: the routed experts of an MoE
+ * layer, or every block of a model.  No reference counterpart: the reference
+ * launches `decode` once per block from each module's hook
+ * (dfloat/run/run.py:97-119, per expert under the qwen3moe pattern of
+ * dfloat/const.py:15-21).  The work is cut into tasks of up to
+ * blocks_per_task format-blocks of one block (a block's tasks interleave
+ * its format-blocks); n_tasks is the total.  max_block_elements bounds every block's largest format-block (0 =
+ * unknown).  descs: device memory, 8-byte aligned.  Asynchronous on stream.
+ */
+int ecf8_decode_batched(const ecf8_block_desc *descs, int count, int n_tasks, int blocks_per_task,
+                        int64_t max_block_elements, int threads_per_block, void *stream);
+
 /* ------------------------------------------------------------------ host */
 
 /*

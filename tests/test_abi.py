@@ -98,3 +98,32 @@ def test_build_table_rejects_bad_lut_count():
                                   None) == 1
     assert lib().ecf8_build_table(ctypes.c_void_p(0x1001), 3, -1, ctypes.c_void_p(0x2000),
                                   ctypes.byref(kind), None) == 3
+
+
+@pytest.mark.parametrize("args,status", [
+    ((0x1000, -1, 1, 16, 0, 512), 1),      # negative count
+    ((0x1000, 1, 1, 0, 0, 512), 1),        # blocks_per_task < 1
+    ((0x1000, 1, 1, 16, 0, 300), 2),       # block size the kernels do not run
+    ((0x1004, 1, 1, 16, 0, 512), 3),       # descriptors not 8-byte aligned
+    ((None, 1, 1, 16, 0, 512), 1),
+    ((None, 0, 0, 16, 0, 512), 0),         # nothing to do
+])
+def test_batched_decode_rejects_before_launch(args, status):
+    from ecf8_amd._lib import lib
+
+    assert lib().ecf8_decode_batched(*args, None) == status
+
+
+def test_block_descriptor_layout_matches_the_header():
+    import numpy as np
+
+    from ecf8_amd.decode import BLOCK_DESC_DTYPE
+
+    text = open(HEADER).read()
+    struct = text[text.index("typedef struct ecf8_block_desc"):text.index("} ecf8_block_desc;")]
+    fields = re.findall(r"\b(\w+);", struct)
+    assert fields == list(BLOCK_DESC_DTYPE.names)
+    assert BLOCK_DESC_DTYPE.itemsize == 80 and "80 bytes" in text
+    assert [BLOCK_DESC_DTYPE.fields[f][1] for f in fields] == [0, 8, 16, 24, 32, 40, 48, 56, 64,
+                                                               72, 76]
+    assert np.dtype("<i4").itemsize == 4

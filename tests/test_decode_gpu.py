@@ -185,6 +185,35 @@ def test_corrupt_table_stays_inside_the_output(kind, cuda_device):
         assert (out[n:].cpu().numpy() == 0x77).all()
 
 
+def _config_blocks():
+    from ecf8_amd import synth
+
+    return [
+        ("qwen3-8b-layer-seed7", synth.QWEN3_8B_LAYER, 7),        # full-model layers
+        ("flux-double-block", synth.FLUX_DOUBLE_BLOCK, 1),        # DiT
+        ("flux-single-block", synth.FLUX_SINGLE_BLOCK, 2),
+        ("qwen3-moe-attention", synth.QWEN3_MOE_ATTN, 3),         # MoE
+        ("qwen3-moe-expert", synth.QWEN3_MOE_EXPERT, 4),
+    ]
+
+
+@pytest.mark.parametrize("name,shapes,seed", _config_blocks(), ids=[c[0] for c in _config_blocks()])
+def test_config_blocks_bit_exact(name, shapes, seed, cuda_device):
+    """One compressed block of each model family's shapes (the blocks the
+    reference's pattern dicts cut: a decoder layer, a DiT double/single
+    block, an MoE attention block and one expert) decodes bit-exactly."""
+    from ecf8_amd.decode import build_table
+    from ecf8_amd.synth import flat_block, synthetic_block
+
+    _say(f"config block {name}")
+    flat, _ = flat_block(synthetic_block(shapes, seed))
+    flat_u8 = flat.view(torch.uint8).numpy()
+    block = _compress(flat_u8)
+    assert build_table(_dev_block(block, cuda_device)["luts"]).kind == DFA
+    got = _gpu_decode(block, cuda_device)
+    assert np.array_equal(got, flat_u8)
+
+
 def test_dfa_exact_path_is_bit_exact(cuda_device):
     """Chunks whose automaton walk reaches the exact row are decoded with the
     LUT rule itself.  Valid streams only get there in their final padding,
@@ -376,3 +405,48 @@ def test_forward_pre_hook_injects_bit_exact_weights(cuda_device):
         w = blk.get_submodule(path).weight
         assert w.dtype == torch.float8_e4m3fn and tuple(w.shape) == shapes[path]
         assert torch.equal(w.view(torch.uint8).cpu(), orig[path])
+
+
+# ---------------------------------------------------------- batched launch
+
+
+def _batched_case(blocks_flat, cuda_device, blocks_per_task):
+    from ecf8_amd.decode import build_table, decode_batched
+
+    blocks, bufs, tables = [], [], []
+    for flat in blocks_flat:
+        d = _dev_block(_compress(flat), cuda_device)
+        blocks.append(d)
+        tables.append(build_table(d["luts"]))
+        bufs.append(torch.full((flat.size + 32,), 0x3C, dtype=torch.uint8, device=cuda_device))
+    decode_batched(blocks, [b[: f.size] for b, f in zip(bufs, blocks_flat)], tables,
+                   blocks_per_task=blocks_per_task)
+    torch.cuda.synchronize()
+    for i, (buf, flat) in enumerate(zip(bufs, blocks_flat)):
+        got = buf.cpu().numpy()
+        assert np.array_equal(got[: flat.size], flat), f"block {i}"
+        assert (got[flat.size:] == 0x3C).all(), f"block {i} wrote past its end"
+    return tables
+
+
+@pytest.mark.parametrize("blocks_per_task", [1, 3, 16, 100000])
+def test_batched_decode_of_mixed_blocks(blocks_per_task, cuda_device):
+    """Random blocks of every distribution kind and size (some only the
+    multi-symbol table can decode, some too small to batch) in one call."""
+    _say(f"batched mixed blocks_per_task={blocks_per_task}")
+    flats = [_random_block(s) for s in range(30, 42)]
+    flats.append(np.array([0x41, 0xC2], np.uint8))  # a two-element block
+    tables = _batched_case(flats, cuda_device, blocks_per_task)
+    assert {t.kind for t in tables} == {MULTI, DFA}
+
+
+def test_batched_decode_of_moe_experts(cuda_device):
+    """An MoE layer's attention block and 16 experts (the reference
+    compresses each expert as its own block) in one launch."""
+    from ecf8_amd import synth
+
+    _say("batched moe experts")
+    flats = [synth.flat_block(synth.synthetic_block(synth.QWEN3_MOE_ATTN, 0))[0]]
+    flats += [synth.flat_block(synth.synthetic_block(synth.QWEN3_MOE_EXPERT, 1 + e))[0]
+              for e in range(16)]
+    _batched_case([f.view(torch.uint8).numpy() for f in flats], cuda_device, 16)
