@@ -33,10 +33,14 @@ def compress_flat(flat_weights: torch.Tensor, bytes_per_thread: int = 8,
     split, count exponents in ascending order, length-limited codebook,
     LUTs, bitstream.  Returns the tensors plus ``entropy`` and ``table``."""
     exps, packed = get_exponents_and_other_4bits_fp8_e4m3(flat_weights)
-    vals, freqs = torch.unique(exps, return_counts=True)
-    p = freqs / freqs.sum()
+    # a 16-bin count is O(n); the reference's ascending-symbol counter order
+    # (scripts/compress.py:205, 213-215) is kept by listing present symbols
+    counts = torch.bincount(exps.reshape(-1), minlength=16)
+    present = counts > 0
+    freqs = counts[present]
+    p = freqs.double() / freqs.sum()
     entropy = float(-torch.sum(p * torch.log2(p)).item()) if freqs.numel() else 0.0
-    counter = {int(v): int(f) for v, f in zip(vals.tolist(), freqs.tolist())}
+    counter = {int(v): int(counts[v]) for v in torch.nonzero(present).reshape(-1).tolist()}
     codec, _, table = get_nbit_codec(counter, max_n_bits=16)
     luts = get_luts_from_huffman_table(table)
     encoded, gaps, op = encode_exponents_for_cuda(exps, codec, bytes_per_thread, threads_per_block)
