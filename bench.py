@@ -217,6 +217,77 @@ def _qwen3_moe_layer_workload(args, dev):
     return calls, verify, alg, n, config, None
 
 
+def e2e_generate(args):
+    """Qwen3-8B-shaped causal LM (36 layers, random init, FP8 linears with
+    128x128 block scales; embedding and lm_head bf16), batch 16, random
+    prompts of 128 tokens, greedy decoding of --new-tokens tokens: first
+    with the FP8 weights resident, then with every layer ECF8-compressed and
+    decoded by its forward-pre-hook before the layer's FP8 linears run.
+    Both runs use the same engine (eager prefill, one HIP graph replay per
+    decode step) and must produce identical tokens."""
+    import torch
+
+    from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model, timed_generate
+    from ecf8_amd.run import TensorManager
+
+    dev = torch.device("cuda", 0)
+    cfg = Qwen3Config()
+    B, T, new = args.batch, args.prompt_len, args.new_tokens
+    t0 = time.time()
+    model, drawn = random_model(cfg, dev, distinct_layers=args.distinct_layers, seed=args.seed)
+    print(f"[bench] model built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(args.seed + 7)
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=g)
+    results = {}
+    for mode in ("fp8", "ecf8"):
+        if mode == "ecf8":
+            t0 = time.time()
+            compress_layers(model, drawn)
+            torch.cuda.synchronize()
+            print(f"[bench] layers compressed in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+        TensorManager.clear_device()
+        torch.cuda.empty_cache()
+        runner = Qwen3Runner(model, B, T, T + new, dev)
+        runner.capture()
+        runner.generate(prompt, min(new, 8))  # warm-up
+        r = timed_generate(runner, prompt, new)
+        print(f"[bench] {mode}: {r['tokens_per_s']:.1f} tokens/s, latency {r['latency_s']:.3f}s, "
+              f"peak {r['peak_mib']:.0f} MiB", file=sys.stderr, flush=True)
+        r["weights_mib"] = sum(t.numel() * t.element_size() for t in
+                               list(model.parameters()) + list(model.buffers())) / 2**20
+        results[mode] = r
+        del runner
+    same = torch.equal(results["fp8"]["tokens"], results["ecf8"]["tokens"])
+    fp8, ecf8 = results["fp8"], results["ecf8"]
+    line = {
+        "metric": "e2e tokens/s, Qwen3-8B-shape bs16 (ECF8-compressed, per-layer decode before the FP8 GEMMs)",
+        "value": round(ecf8["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (random-init weights, random prompts)",
+        "config": {"workload": "qwen3-8b-generate", "layers": cfg.layers, "hidden": cfg.hidden,
+                   "intermediate": cfg.intermediate, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
+                   "vocab": cfg.vocab, "batch": B, "prompt_len": T, "new_tokens": new,
+                   "distinct_layer_weights": args.distinct_layers, "decoding": "greedy"},
+        "uncompressed_fp8": {"tokens_per_s": round(fp8["tokens_per_s"], 1),
+                             "latency_s": round(fp8["latency_s"], 4),
+                             "peak_mib": round(fp8["peak_mib"], 1),
+                             "weights_mib": round(fp8["weights_mib"], 1)},
+        "ecf8": {"tokens_per_s": round(ecf8["tokens_per_s"], 1),
+                 "latency_s": round(ecf8["latency_s"], 4),
+                 "peak_mib": round(ecf8["peak_mib"], 1),
+                 "weights_mib": round(ecf8["weights_mib"], 1)},
+        "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
+        "identical_tokens": same,
+    }
+    print(json.dumps(line), flush=True)
+    if not same:
+        sys.exit(1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,9 +296,15 @@ def main():
     ap.add_argument("--copies", type=int, default=4, help="rotated input/output sets")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer"),
+    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "qwen3-8b-generate"),
                     default="qwen3-8b-layer",
-                    help="qwen3-moe-layer: attention + 128 experts in one batched launch")
+                    help="qwen3-moe-layer: attention + 128 experts in one batched launch; "
+                         "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8")
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--prompt-len", type=int, default=128)
+    ap.add_argument("--new-tokens", type=int, default=1024)
+    ap.add_argument("--distinct-layers", type=int, default=2,
+                    help="generate: layers drawn independently (the rest copy them)")
     ap.add_argument("--mode", choices=("decode", "copy"), default="decode",
                     help="copy: time a plain 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -237,6 +314,8 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         return copy_calibration(args.steps, args.warmup)
+    if args.workload == "qwen3-8b-generate":
+        return e2e_generate(args)
 
     import torch
 

@@ -29,6 +29,7 @@ class ECF8Error(RuntimeError):
 
 _lib = None
 _vp, _i64, _i32, _u32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
+_f32 = ctypes.c_float
 
 _SIGNATURES = {
     "ecf8_version": ([], ctypes.c_char_p),
@@ -47,6 +48,16 @@ _SIGNATURES = {
         [_vp, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, ctypes.c_char_p, ctypes.c_size_t],
         _i32,
     ),
+    # include/ecf8_llm.h: the consumer kernels
+    "ecf8_fp8_linear": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp], _i32),
+    "ecf8_rmsnorm": ([_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp, _vp], _i32),
+    "ecf8_silu_mul_quant": ([_vp, _i64, _i64, _vp, _vp, _vp], _i32),
+    "ecf8_act_quant": ([_vp, _i64, _i64, _vp, _vp, _vp], _i32),
+    "ecf8_qk_norm_rope": ([_vp, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _vp,
+                           _vp, _vp, _vp], _i32),
+    "ecf8_attention_work_floats": ([_i64, _i32, _i64], _i64),
+    "ecf8_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _i64, _vp, _vp, _vp,
+                               _vp], _i32),
 }
 
 EXPORTED = tuple(_SIGNATURES)

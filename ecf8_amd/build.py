@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libecf8.so")
 SOURCES = [os.path.join(HERE, "csrc", f)
-           for f in ("ecf8_decode.hip", "ecf8_tables.cpp", "ecf8_host.cpp")]
+           for f in ("ecf8_decode.hip", "ecf8_llm.hip", "ecf8_tables.cpp", "ecf8_host.cpp")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -27,7 +27,7 @@ FLAGS = [
     "-shared",
     # the HIP runtime torch ships accepts code object v5
     "-mcode-object-version=5",
-    # never emit packed-FP32 VALU ops (none are needed by this integer code)
+    # never emit packed-FP32 VALU ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-I" + os.path.join(REPO, "include"),

@@ -1,0 +1,633 @@
+// Consumer side of the decode path on gfx950: the block-scaled FP8 linear
+// that reads the decoded e4m3fn weights, and the few fused kernels a
+// Qwen3-shaped decoder layer needs around it (activation quantization,
+// residual + RMSNorm, SiLU gating, per-head norm + rotary embedding + KV
+// cache write, split-sequence decode attention).
+//
+// Numerics follow the fine-grained FP8 scheme of the FP8 checkpoints the
+// reference runs (transformers' FP8Linear, used by dfloat/run/run.py's
+// DFloatModel for Qwen3-8B-FP8): weights e4m3fn with one fp32 scale per
+// 128x128 block, activations quantized on the fly to e4m3fn with one fp32
+// scale per row and 128-column group (scale = amax / 448), products
+// accumulated in fp32 per 128-column group and scaled by both scales.
+//
+// Every kernel is deterministic: reductions run in a fixed order, so a
+// model decoded from ECF8 and the same model kept in FP8 produce identical
+// logits.
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "ecf8.h"
+#include "ecf8_llm.h"
+
+namespace {
+
+constexpr int kGroup = 128;          // quantization group along K
+constexpr float kFp8Max = 448.f;     // largest finite e4m3fn value
+constexpr int kHeadDim = 128;
+constexpr int kAttnChunk = 256;      // positions per attention workgroup
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read once per launch)
+__device__ __forceinline__ uint4 load_stream16(const uint8_t *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float bf16_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// fp32 -> bf16, round to nearest even (the rounding torch uses)
+__device__ __forceinline__ uint32_t f32_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// fp32 -> e4m3fn, round to nearest even; |y| is clamped to 448 first, so
+// the result is always finite (callers pass values already scaled into
+// range).  Subnormals (|y| < 2^-6) have a step of 2^-9.
+__device__ __forceinline__ uint32_t f32_e4m3(float y) {
+  const uint32_t sign = (__float_as_uint(y) >> 24) & 0x80u;
+  const float a = fminf(fabsf(y), kFp8Max);
+  uint32_t code;
+  if (a < 0.015625f) {
+    code = (uint32_t)rintf(a * 512.f);  // 0..8; 8 is the smallest normal
+  } else {
+    const uint32_t b = __float_as_uint(a);
+    const uint32_t e = (b >> 23) - 120u;  // biased e4m3 exponent (bias 7)
+    const uint32_t m = b & 0x7fffffu;
+    uint32_t q = m >> 20;
+    const uint32_t rem = m & 0xfffffu;
+    q += (rem > 0x80000u) || (rem == 0x80000u && (q & 1u));
+    code = (e << 3) + q;  // a mantissa carry moves into the exponent
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return __shfl(v, 0);  // every lane takes lane 0's association order
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Quantize 16 consecutive values held by one thread; the 8 threads of a
+// 128-column group are 8 consecutive lanes.  Writes 16 e4m3fn bytes and,
+// from the group's first thread, the group scale.
+__device__ __forceinline__ void quant16(const float (&v)[16], uint8_t *q_out, float *s_out,
+                                        bool first_of_group) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  const float s = amax > 0.f ? amax / kFp8Max : 1.f;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    w[j] = f32_e4m3(v[4 * j] / s) | (f32_e4m3(v[4 * j + 1] / s) << 8) |
+           (f32_e4m3(v[4 * j + 2] / s) << 16) | (f32_e4m3(v[4 * j + 3] / s) << 24);
+  }
+  *reinterpret_cast<uint4 *>(q_out) = make_uint4(w[0], w[1], w[2], w[3]);
+  if (first_of_group) *s_out = s;
+}
+
+__device__ __forceinline__ void load16_bf16(const uint16_t *p, float (&v)[16]) {
+  const uint4 a = *reinterpret_cast<const uint4 *>(p);
+  const uint4 b = *reinterpret_cast<const uint4 *>(p + 8);
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[2 * i] = bf16_f32(w[i] & 0xffffu);
+    v[2 * i + 1] = bf16_f32(w[i] >> 16);
+  }
+}
+
+// ------------------------------------------------------------ FP8 linear
+
+struct LinearSegs {
+  const uint8_t *w[ECF8_LINEAR_MAX_SEGS];
+  const float *ws[ECF8_LINEAR_MAX_SEGS];
+  int n_end[ECF8_LINEAR_MAX_SEGS];  // cumulative output columns
+  int col[ECF8_LINEAR_MAX_SEGS];    // first output column of the segment
+  int count;
+};
+
+// out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * w[n,k]) * as[m,g] * ws[n/128, g]
+//
+// One workgroup = 8 waves = one 16-column tile (times MT 16-row tiles),
+// the K groups split round-robin over the waves and summed through LDS in
+// wave order.  A wave runs v_mfma_f32_16x16x32_fp8_fp8: lane l holds row
+// l%16 of both operands and bytes [16*(l/16), +16) and [64 + 16*(l/16), +16)
+// of each 128-byte group, i.e. each 16-byte load feeds two MFMAs.  The K
+// order inside a group is a permutation shared by both operands, so the
+// dot product is unchanged.
+template <int MT>
+__global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restrict__ aq,
+                                                         const float *__restrict__ as, int M, int K,
+                                                         LinearSegs segs, uint16_t *__restrict__ out,
+                                                         int ldo) {
+  __shared__ float red[8][MT * 4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kgroups = K / kGroup;
+
+  int n0 = blockIdx.x * 16;
+  const uint8_t *w = segs.w[0];
+  const float *ws = segs.ws[0];
+  int col = segs.col[0], seg_start = 0;
+#pragma unroll
+  for (int s = 1; s < ECF8_LINEAR_MAX_SEGS; ++s) {
+    if (s < segs.count && n0 >= segs.n_end[s - 1]) {
+      w = segs.w[s];
+      ws = segs.ws[s];
+      col = segs.col[s];
+      seg_start = segs.n_end[s - 1];
+    }
+  }
+  n0 -= seg_start;
+
+  const int r = lane & 15, g = lane >> 4;
+  const int m0 = blockIdx.y * 16 * MT;
+  const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+  const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
+
+  float acc[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[t][i] = 0.f;
+
+  constexpr int kUnroll = 4;
+  for (int kb = wave; kb < kgroups; kb += 8 * kUnroll) {
+    uint4 wv[kUnroll][2];
+    float wsv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int kg = kb + 8 * u;
+      if (kg < kgroups) {
+        wv[u][0] = load_stream16(wrow + kg * kGroup);
+        wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+        wsv[u] = wsrow[kg];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int kg = kb + 8 * u;
+      if (kg >= kgroups) break;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int m = m0 + t * 16 + r;
+        uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0;
+        if (m < M) {
+          const uint8_t *ap = aq + (size_t)m * K + kg * kGroup + 16 * g;
+          a0 = *reinterpret_cast<const uint4 *>(ap);
+          a1 = *reinterpret_cast<const uint4 *>(ap + 64);
+        }
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)a0.y << 32) | a0.x), (long)(((uint64_t)wv[u][0].y << 32) | wv[u][0].x), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)a0.w << 32) | a0.z), (long)(((uint64_t)wv[u][0].w << 32) | wv[u][0].z), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)a1.y << 32) | a1.x), (long)(((uint64_t)wv[u][1].y << 32) | wv[u][1].x), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)a1.w << 32) | a1.z), (long)(((uint64_t)wv[u][1].w << 32) | wv[u][1].z), d, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int mi = m0 + t * 16 + 4 * g + i;
+          const float sa = mi < M ? as[(size_t)mi * kgroups + kg] : 0.f;
+          acc[t][i] = fmaf(d[i], sa * wsv[u], acc[t][i]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][t * 4 + i][lane] = acc[t][i];
+  __syncthreads();
+  for (int v = threadIdx.x; v < MT * 4 * 64; v += 512) {
+    const int ti = v >> 6, l = v & 63;
+    float sum = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < 8; ++wv) sum += red[wv][ti][l];
+    const int m = m0 + (ti >> 2) * 16 + 4 * (l >> 4) + (ti & 3);
+    if (m < M) out[(size_t)m * ldo + col + n0 + (l & 15)] = (uint16_t)f32_bf16(sum);
+  }
+}
+
+// ------------------------------------------------- quantizing row kernels
+
+// residual += x (if x); y = residual * rsqrt(mean(residual^2) + eps) * w;
+// y -> e4m3fn + group scales, or -> bf16.  One 256-thread workgroup per
+// row of 4096 (16 values per thread).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict__ x,
+                                                      float *__restrict__ res,
+                                                      const uint16_t *__restrict__ w, float eps,
+                                                      int K, uint8_t *__restrict__ oq,
+                                                      float *__restrict__ os,
+                                                      uint16_t *__restrict__ ob) {
+  __shared__ float part[4];
+  const int m = blockIdx.x, t = threadIdx.x;
+  const size_t base = (size_t)m * K + 16 * t;
+  float v[16];
+  float4 *rp = reinterpret_cast<float4 *>(res + base);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float4 f = rp[j];
+    v[4 * j] = f.x;
+    v[4 * j + 1] = f.y;
+    v[4 * j + 2] = f.z;
+    v[4 * j + 3] = f.w;
+  }
+  if (x) {
+    float xv[16];
+    load16_bf16(x + base, xv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] += xv[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rp[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) part[t >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rs = rsqrtf(total / (float)K + eps);
+  float wv[16];
+  load16_bf16(w + 16 * t, wv);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = v[i] * rs * wv[i];
+  if (ob) {
+    uint32_t p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = f32_bf16(v[2 * i]) | (f32_bf16(v[2 * i + 1]) << 16);
+    uint4 *op = reinterpret_cast<uint4 *>(ob + base);
+    op[0] = make_uint4(p[0], p[1], p[2], p[3]);
+    op[1] = make_uint4(p[4], p[5], p[6], p[7]);
+  } else {
+    quant16(v, oq + base, os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
+  }
+}
+
+// h = silu(gate) * up over [M, 2I] (gate columns [0, I), up [I, 2I)),
+// quantized; grid (I / 4096, M).
+__global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t *__restrict__ gu, int I,
+                                                             uint8_t *__restrict__ oq,
+                                                             float *__restrict__ os) {
+  const int m = blockIdx.y, e = blockIdx.x * 4096 + 16 * threadIdx.x;
+  float g[16], u[16];
+  load16_bf16(gu + (size_t)m * 2 * I + e, g);
+  load16_bf16(gu + (size_t)m * 2 * I + I + e, u);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) g[i] = g[i] / (1.f + expf(-g[i])) * u[i];
+  quant16(g, oq + (size_t)m * I + e, os + (size_t)m * (I / kGroup) + (e >> 7),
+          (threadIdx.x & 7) == 0);
+}
+
+// plain bf16 -> e4m3fn per 1x128 group; grid (K / 4096, M)
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restrict__ x, int K,
+                                                        uint8_t *__restrict__ oq,
+                                                        float *__restrict__ os) {
+  const int m = blockIdx.y, e = blockIdx.x * 4096 + 16 * threadIdx.x;
+  float v[16];
+  load16_bf16(x + (size_t)m * K + e, v);
+  quant16(v, oq + (size_t)m * K + e, os + (size_t)m * (K / kGroup) + (e >> 7),
+          (threadIdx.x & 7) == 0);
+}
+
+// --------------------------------------------- per-head norm + rotary + KV
+
+// One wave per (token, head) of the fused qkv projection output
+// [B*T, (Hq + 2 Hkv) * 128]: q and k heads get RMSNorm over the head
+// (weights qn / kn) and the rotary embedding at position pos[0] + t
+// (rotate-half convention, cos/sin tables [Lmax, 64]); q goes to
+// q_out [B, Hq, T, 128], k and v to the caches [B, Hkv, Lmax, 128].
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const uint16_t *__restrict__ qkv, int T, int Hq, int Hkv, const uint16_t *__restrict__ qn,
+    const uint16_t *__restrict__ kn, float eps, const float *__restrict__ cosv,
+    const float *__restrict__ sinv, const int *__restrict__ pos, int Lmax,
+    uint16_t *__restrict__ q_out, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    int n_items) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= n_items) return;
+  const int H = Hq + 2 * Hkv;
+  const int tok = item / H, hh = item % H;
+  const int b = tok / T, t = tok % T;
+  const int p = pos[0] + t;
+  if (p < 0 || p >= Lmax) return;
+  const uint32_t x2 = *reinterpret_cast<const uint32_t *>(qkv + (size_t)tok * H * kHeadDim +
+                                                          hh * kHeadDim + 2 * lane);
+  uint32_t outw;
+  if (hh >= Hq + Hkv) {
+    outw = x2;
+  } else {
+    float x0 = bf16_f32(x2 & 0xffffu), x1 = bf16_f32(x2 >> 16);
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float rs = rsqrtf(ss / (float)kHeadDim + eps);
+    const uint16_t *nw = hh < Hq ? qn : kn;
+    const uint32_t w2 = *reinterpret_cast<const uint32_t *>(nw + 2 * lane);
+    x0 = x0 * rs * bf16_f32(w2 & 0xffffu);
+    x1 = x1 * rs * bf16_f32(w2 >> 16);
+    const float y0 = __shfl_xor(x0, 32), y1 = __shfl_xor(x1, 32);  // dims d +- 64
+    const int j = (2 * lane) & 63;
+    const float c0 = cosv[p * 64 + j], c1 = cosv[p * 64 + j + 1];
+    const float s0 = sinv[p * 64 + j], s1 = sinv[p * 64 + j + 1];
+    const float sg = lane < 32 ? -1.f : 1.f;
+    x0 = x0 * c0 + sg * y0 * s0;
+    x1 = x1 * c1 + sg * y1 * s1;
+    outw = f32_bf16(x0) | (f32_bf16(x1) << 16);
+  }
+  uint16_t *dst;
+  if (hh < Hq) {
+    dst = q_out + (((size_t)b * Hq + hh) * T + t) * kHeadDim;
+  } else if (hh < Hq + Hkv) {
+    dst = kc + (((size_t)b * Hkv + (hh - Hq)) * Lmax + p) * kHeadDim;
+  } else {
+    dst = vc + (((size_t)b * Hkv + (hh - Hq - Hkv)) * Lmax + p) * kHeadDim;
+  }
+  *reinterpret_cast<uint32_t *>(dst + 2 * lane) = outw;
+}
+
+// ------------------------------------------------------ decode attention
+
+// Split-sequence attention for one new token per sequence: workgroup
+// (b * Hkv + kh, split) handles positions [split*256, +256) of the L =
+// pos[0] + 1 cached ones for the G = Hq / Hkv query heads sharing kv head
+// kh.  Scores: one lane per position; softmax partials per head; PV: one
+// thread per (head, dim pair).  Partials go to work: m, l [B*Hq, S] and
+// acc [B*Hq, S, 128].
+template <int G>
+__global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restrict__ q,
+                                                         const uint16_t *__restrict__ kc,
+                                                         const uint16_t *__restrict__ vc,
+                                                         const int *__restrict__ pos, int Hkv,
+                                                         int Lmax, int S, float *__restrict__ wm,
+                                                         float *__restrict__ wl,
+                                                         float *__restrict__ wacc) {
+  __shared__ float qs[G][kHeadDim];
+  __shared__ float pw[G][kAttnChunk];
+  __shared__ float red[G][4];
+  const int bk = blockIdx.x, split = blockIdx.y;
+  const int b = bk / Hkv, kh = bk % Hkv;
+  const int Hq = Hkv * G;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int L = pos[0] + 1;
+  L = L < 1 ? 1 : (L > Lmax ? Lmax : L);
+  const int c0 = split * kAttnChunk;
+  const size_t head0 = (size_t)b * Hq + kh * G;
+  if (c0 >= L) {
+    if (t < G) {
+      wm[(head0 + t) * S + split] = -INFINITY;
+      wl[(head0 + t) * S + split] = 0.f;
+    }
+    return;
+  }
+  const int n = min(kAttnChunk, L - c0);
+  const float scale = rsqrtf((float)kHeadDim);
+  for (int i = t; i < G * kHeadDim; i += 256) {
+    qs[i / kHeadDim][i % kHeadDim] = bf16_f32(q[(head0 + i / kHeadDim) * kHeadDim + i % kHeadDim]) * scale;
+  }
+  __syncthreads();
+
+  const int j = 64 * wave + lane;  // position within the chunk
+  float s[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) s[h] = 0.f;
+  const bool valid = j < n;
+  if (valid) {
+    const uint4 *kr = reinterpret_cast<const uint4 *>(kc + (((size_t)b * Hkv + kh) * Lmax + c0 + j) * kHeadDim);
+#pragma unroll 4
+    for (int c = 0; c < kHeadDim / 8; ++c) {
+      const uint4 kv = kr[c];
+      const uint32_t wds[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float k0 = bf16_f32(wds[e] & 0xffffu), k1 = bf16_f32(wds[e] >> 16);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          s[h] = fmaf(qs[h][8 * c + 2 * e], k0, s[h]);
+          s[h] = fmaf(qs[h][8 * c + 2 * e + 1], k1, s[h]);
+        }
+      }
+    }
+  }
+  float mh[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float mw = wave_max(valid ? s[h] : -INFINITY);
+    if (lane == 0) red[h][wave] = mw;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) mh[h] = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float e = valid ? expf(s[h] - mh[h]) : 0.f;
+    pw[h][j] = e;
+    const float sw = wave_sum(e);
+    if (lane == 0) red[h][wave] = sw;
+  }
+  __syncthreads();
+  if (t < G) {
+    wm[(head0 + t) * S + split] = mh[t];
+    wl[(head0 + t) * S + split] = (red[t][0] + red[t][1]) + (red[t][2] + red[t][3]);
+  }
+  const uint16_t *vr = vc + (((size_t)b * Hkv + kh) * Lmax + c0) * kHeadDim + 2 * lane;
+  for (int h = wave; h < G; h += 4) {
+    float a0 = 0.f, a1 = 0.f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+      uint32_t vv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vv[u] = *reinterpret_cast<const uint32_t *>(vr + (size_t)(i + u) * kHeadDim);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float p = pw[h][i + u];
+        a0 = fmaf(p, bf16_f32(vv[u] & 0xffffu), a0);
+        a1 = fmaf(p, bf16_f32(vv[u] >> 16), a1);
+      }
+    }
+    for (; i < n; ++i) {
+      const uint32_t v2 = *reinterpret_cast<const uint32_t *>(vr + (size_t)i * kHeadDim);
+      const float p = pw[h][i];
+      a0 = fmaf(p, bf16_f32(v2 & 0xffffu), a0);
+      a1 = fmaf(p, bf16_f32(v2 >> 16), a1);
+    }
+    float *dst = wacc + ((head0 + h) * S + split) * kHeadDim + 2 * lane;
+    dst[0] = a0;
+    dst[1] = a1;
+  }
+}
+
+// Merge the splits of one (b, head) and quantize the head's 128 outputs
+// (one activation group of the o projection); optionally also write bf16.
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restrict__ wm,
+                                                          const float *__restrict__ wl,
+                                                          const float *__restrict__ wacc,
+                                                          const int *__restrict__ pos, int Lmax,
+                                                          int S, uint8_t *__restrict__ oq,
+                                                          float *__restrict__ os,
+                                                          uint16_t *__restrict__ ob) {
+  const int bh = blockIdx.x, lane = threadIdx.x;
+  int L = pos[0] + 1;
+  L = L < 1 ? 1 : (L > Lmax ? Lmax : L);
+  const int used = (L + kAttnChunk - 1) / kAttnChunk;
+  float mx = -INFINITY;
+  for (int s = 0; s < used; ++s) mx = fmaxf(mx, wm[(size_t)bh * S + s]);
+  float l = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int s = 0; s < used; ++s) {
+    const float f = expf(wm[(size_t)bh * S + s] - mx);
+    l = fmaf(f, wl[(size_t)bh * S + s], l);
+    const float *ap = wacc + ((size_t)bh * S + s) * kHeadDim + 2 * lane;
+    a0 = fmaf(f, ap[0], a0);
+    a1 = fmaf(f, ap[1], a1);
+  }
+  a0 /= l;
+  a1 /= l;
+  if (ob) reinterpret_cast<uint32_t *>(ob)[(size_t)bh * 64 + lane] = f32_bf16(a0) | (f32_bf16(a1) << 16);
+  float amax = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
+  const float sc = amax > 0.f ? amax / kFp8Max : 1.f;
+  const uint32_t q2 = f32_e4m3(a0 / sc) | (f32_e4m3(a1 / sc) << 8);
+  reinterpret_cast<uint16_t *>(oq)[(size_t)bh * 64 + lane] = (uint16_t)q2;
+  if (lane == 0) os[bh] = sc;
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+inline int launched() { return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP; }
+
+}  // namespace
+
+extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64_t K,
+                               const ecf8_linear_seg *segs, int n_segs, void *out, int64_t ldo,
+                               void *stream) {
+  if (!aq || !as || !segs || !out || M <= 0 || K <= 0 || n_segs < 1 ||
+      n_segs > ECF8_LINEAR_MAX_SEGS)
+    return ECF8_ERR_INVALID_ARG;
+  if (K % kGroup || M > (1 << 24) || K > (1 << 20)) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(aq, 16) || !aligned(out, 4) || !aligned(as, 4)) return ECF8_ERR_MISALIGNED;
+  LinearSegs s{};
+  int64_t n_total = 0;
+  for (int i = 0; i < n_segs; ++i) {
+    const ecf8_linear_seg &g = segs[i];
+    if (!g.weight || !g.weight_scale || g.n <= 0 || g.out_col < 0) return ECF8_ERR_INVALID_ARG;
+    if (g.n % kGroup) return ECF8_ERR_UNSUPPORTED;
+    if (!aligned(g.weight, 16) || !aligned(g.weight_scale, 4)) return ECF8_ERR_MISALIGNED;
+    if (g.out_col + g.n > ldo) return ECF8_ERR_CAPACITY;
+    n_total += g.n;
+    s.w[i] = static_cast<const uint8_t *>(g.weight);
+    s.ws[i] = g.weight_scale;
+    s.n_end[i] = (int)n_total;
+    s.col[i] = (int)g.out_col;
+  }
+  if (n_total > (1 << 24)) return ECF8_ERR_UNSUPPORTED;
+  s.count = n_segs;
+  const auto *a = static_cast<const uint8_t *>(aq);
+  auto *o = static_cast<uint16_t *>(out);
+  if (M <= 16) {
+    dim3 grid((unsigned)(n_total / 16), 1);
+    fp8_linear_kernel<1><<<grid, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o, (int)ldo);
+  } else {
+    dim3 grid((unsigned)(n_total / 16), (unsigned)((M + 63) / 64));
+    fp8_linear_kernel<4><<<grid, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o, (int)ldo);
+  }
+  return launched();
+}
+
+extern "C" int ecf8_rmsnorm(const void *x, float *residual, const void *weight, float eps, int64_t M,
+                            int64_t K, void *out_q, float *out_scale, void *out_bf16, void *stream) {
+  if (!residual || !weight || M <= 0 || (!out_bf16 && (!out_q || !out_scale)))
+    return ECF8_ERR_INVALID_ARG;
+  if (K != 4096) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(residual, 16) || (x && !aligned(x, 16)) || !aligned(weight, 16) ||
+      (out_q && !aligned(out_q, 16)) || (out_bf16 && !aligned(out_bf16, 16)))
+    return ECF8_ERR_MISALIGNED;
+  rmsnorm_kernel<<<(unsigned)M, 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(x), residual, static_cast<const uint16_t *>(weight), eps, (int)K,
+      static_cast<uint8_t *>(out_q), out_scale, static_cast<uint16_t *>(out_bf16));
+  return launched();
+}
+
+extern "C" int ecf8_silu_mul_quant(const void *gate_up, int64_t M, int64_t I, void *out_q,
+                                   float *out_scale, void *stream) {
+  if (!gate_up || !out_q || !out_scale || M <= 0 || I <= 0) return ECF8_ERR_INVALID_ARG;
+  if (I % 4096 || M > 65535) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(gate_up, 16) || !aligned(out_q, 16)) return ECF8_ERR_MISALIGNED;
+  silu_mul_quant_kernel<<<dim3((unsigned)(I / 4096), (unsigned)M), 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(gate_up), (int)I, static_cast<uint8_t *>(out_q), out_scale);
+  return launched();
+}
+
+extern "C" int ecf8_act_quant(const void *x, int64_t M, int64_t K, void *out_q, float *out_scale,
+                              void *stream) {
+  if (!x || !out_q || !out_scale || M <= 0 || K <= 0) return ECF8_ERR_INVALID_ARG;
+  if (K % 4096 || M > 65535) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(x, 16) || !aligned(out_q, 16)) return ECF8_ERR_MISALIGNED;
+  act_quant_kernel<<<dim3((unsigned)(K / 4096), (unsigned)M), 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(x), (int)K, static_cast<uint8_t *>(out_q), out_scale);
+  return launched();
+}
+
+extern "C" int ecf8_qk_norm_rope(const void *qkv, int64_t B, int64_t T, int Hq, int Hkv,
+                                 const void *q_norm, const void *k_norm, float eps, const float *cos_t,
+                                 const float *sin_t, const int *pos, int64_t Lmax, void *q_out,
+                                 void *k_cache, void *v_cache, void *stream) {
+  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q_out || !k_cache || !v_cache ||
+      B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || Lmax <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  const int64_t items = B * T * (Hq + 2 * Hkv);
+  if (items > (int64_t)1 << 30) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(qkv, 4) || !aligned(q_norm, 4) || !aligned(k_norm, 4) || !aligned(q_out, 4) ||
+      !aligned(k_cache, 4) || !aligned(v_cache, 4))
+    return ECF8_ERR_MISALIGNED;
+  qk_norm_rope_kernel<<<(unsigned)((items + 3) / 4), 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(qkv), (int)T, Hq, Hkv, static_cast<const uint16_t *>(q_norm),
+      static_cast<const uint16_t *>(k_norm), eps, cos_t, sin_t, pos, (int)Lmax,
+      static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_cache),
+      static_cast<uint16_t *>(v_cache), (int)items);
+  return launched();
+}
+
+extern "C" int64_t ecf8_attention_work_floats(int64_t B, int Hq, int64_t Lmax) {
+  if (B <= 0 || Hq <= 0 || Lmax <= 0) return -1;
+  const int64_t S = (Lmax + kAttnChunk - 1) / kAttnChunk;
+  return B * Hq * S * (kHeadDim + 2);
+}
+
+extern "C" int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cache,
+                                     const int *pos, int64_t B, int Hq, int Hkv, int64_t Lmax,
+                                     float *work, int64_t work_floats, void *out_q,
+                                     float *out_scale, void *out_bf16, void *stream) {
+  if (!q || !k_cache || !v_cache || !pos || !work || !out_q || !out_scale || B <= 0 || Hq <= 0 ||
+      Hkv <= 0 || Lmax <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (Hq != 4 * Hkv || B * Hkv > 65535 || Lmax > (1 << 24)) return ECF8_ERR_UNSUPPORTED;
+  const int64_t S = (Lmax + kAttnChunk - 1) / kAttnChunk;
+  if (work_floats < B * Hq * S * (kHeadDim + 2)) return ECF8_ERR_CAPACITY;
+  if (!aligned(q, 4) || !aligned(k_cache, 16) || !aligned(v_cache, 4) || !aligned(work, 8) ||
+      !aligned(out_q, 2) || (out_bf16 && !aligned(out_bf16, 4)))
+    return ECF8_ERR_MISALIGNED;
+  float *wm = work, *wl = work + B * Hq * S, *wacc = work + 2 * B * Hq * S;
+  attn_split_kernel<4><<<dim3((unsigned)(B * Hkv), (unsigned)S), 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k_cache),
+      static_cast<const uint16_t *>(v_cache), pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc);
+  attn_combine_kernel<<<(unsigned)(B * Hq), 64, 0, as_stream(stream)>>>(
+      wm, wl, wacc, pos, (int)Lmax, (int)S, static_cast<uint8_t *>(out_q), out_scale,
+      static_cast<uint16_t *>(out_bf16));
+  return launched();
+}

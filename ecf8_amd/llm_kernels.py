@@ -1,0 +1,197 @@
+"""Python wrappers of the consumer kernels (include/ecf8_llm.h): the
+block-scaled FP8 linear that reads decoded weights and the fused kernels of
+a Qwen3-shaped decoder layer.  Every call launches on torch's current stream
+of the tensors' device; shapes, dtypes and contiguity are checked here, the
+library checks sizes and alignment again and returns a status."""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import ECF8Error, check, lib
+
+GROUP = 128
+MAX_SEGS = 3
+
+
+class _Seg(ctypes.Structure):
+    _fields_ = [("weight", ctypes.c_void_p), ("weight_scale", ctypes.c_void_p),
+                ("n", ctypes.c_int64), ("out_col", ctypes.c_int64)]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, dtype, name: str, dev=None):
+    if not t.is_cuda:
+        raise ECF8Error(f"{name} must be a CUDA tensor")
+    if dev is not None and t.device != dev:
+        raise ECF8Error(f"{name} must be on {dev}")
+    if t.dtype != dtype:
+        raise ECF8Error(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ECF8Error(f"{name} must be contiguous")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _rows(M, K, *tensors):
+    """Every given tensor is 2-D [>= M, K]."""
+    for t in tensors:
+        if t is not None and (t.dim() != 2 or t.shape[1] != K or t.shape[0] < M):
+            raise ECF8Error(f"tensor {tuple(t.shape)} is not [>= {M}, {K}]")
+
+
+class LinearPlan:
+    """Precomputed argument block of one (possibly fused) FP8 linear: the
+    segment table is built once, so a call costs one ctypes launch."""
+
+    def __init__(self, weights, out: torch.Tensor):
+        """``weights``: list of (weight e4m3fn [n, K], weight_scale_inv f32
+        [n/128, K/128]); outputs are written side by side into ``out``
+        columns in that order."""
+        if not 1 <= len(weights) <= MAX_SEGS:
+            raise ECF8Error(f"1..{MAX_SEGS} weight segments per linear")
+        dev = out.device
+        _need(out, torch.bfloat16, "out", dev)
+        K = weights[0][0].shape[1]
+        segs = (_Seg * len(weights))()
+        col = 0
+        for i, (w, s) in enumerate(weights):
+            _need(w, torch.float8_e4m3fn, "weight", dev)
+            _need(s, torch.float32, "weight_scale_inv", dev)
+            n, k = w.shape
+            if k != K or n % GROUP or K % GROUP:
+                raise ECF8Error(f"weight {tuple(w.shape)} does not fit K={K} in 128-multiples")
+            if tuple(s.shape) != (n // GROUP, K // GROUP):
+                raise ECF8Error(f"weight_scale_inv {tuple(s.shape)} for weight {tuple(w.shape)}")
+            segs[i] = _Seg(w.data_ptr(), s.data_ptr(), n, col)
+            col += n
+        if out.shape[-1] < col:
+            raise ECF8Error(f"out has {out.shape[-1]} columns, {col} needed")
+        self.segs, self.count, self.K, self.N, self.out, self.ldo = segs, len(weights), K, col, out, out.shape[-1]
+        self._keep = [t for pair in weights for t in pair]
+
+    def __call__(self, aq: torch.Tensor, a_scale: torch.Tensor, M: int):
+        _need(aq, torch.float8_e4m3fn, "aq", self.out.device)
+        _need(a_scale, torch.float32, "a_scale", self.out.device)
+        if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < M
+                or tuple(a_scale.shape[1:]) != (self.K // GROUP,) or a_scale.shape[0] < M):
+            raise ECF8Error("activation shape does not match the linear")
+        if self.out.shape[0] < M:
+            raise ECF8Error("out has fewer rows than M")
+        check(lib().ecf8_fp8_linear(aq.data_ptr(), a_scale.data_ptr(), M, self.K, self.segs,
+                                    self.count, self.out.data_ptr(), self.ldo, _stream(aq)),
+              "ecf8_fp8_linear")
+        return self.out
+
+
+def fp8_linear(aq, a_scale, weights, out, M=None):
+    """One-shot form of LinearPlan: out[:, cols] = aq @ w.T per segment."""
+    return LinearPlan(weights, out)(aq, a_scale, aq.shape[0] if M is None else M)
+
+
+def rmsnorm(residual, weight, eps, M, x=None, out_q=None, out_scale=None, out_bf16=None):
+    """residual[:M] += x[:M] (if x); normalized rows -> fp8 + scales, or bf16."""
+    dev = residual.device
+    _need(residual, torch.float32, "residual", dev)
+    _need(weight, torch.bfloat16, "weight", dev)
+    K = residual.shape[-1]
+    if x is not None:
+        _need(x, torch.bfloat16, "x", dev)
+    if out_bf16 is not None:
+        _need(out_bf16, torch.bfloat16, "out_bf16", dev)
+    else:
+        _need(out_q, torch.float8_e4m3fn, "out_q", dev)
+        _need(out_scale, torch.float32, "out_scale", dev)
+    _rows(M, K, residual, x, out_q, out_bf16)
+    if weight.numel() != K or (out_scale is not None and out_scale.shape[-1] != K // GROUP):
+        raise ECF8Error("norm weight / scale shape does not match the rows")
+    check(lib().ecf8_rmsnorm(_ptr(x), residual.data_ptr(), weight.data_ptr(), float(eps), M, K,
+                             _ptr(out_q), _ptr(out_scale), _ptr(out_bf16), _stream(residual)),
+          "ecf8_rmsnorm")
+
+
+def silu_mul_quant(gate_up, M, out_q, out_scale):
+    dev = gate_up.device
+    _need(gate_up, torch.bfloat16, "gate_up", dev)
+    _need(out_q, torch.float8_e4m3fn, "out_q", dev)
+    _need(out_scale, torch.float32, "out_scale", dev)
+    inter = gate_up.shape[-1] // 2
+    _rows(M, 2 * inter, gate_up)
+    _rows(M, inter, out_q)
+    if out_scale.shape[-1] != inter // GROUP or out_scale.shape[0] < M:
+        raise ECF8Error("out_scale shape does not match")
+    check(lib().ecf8_silu_mul_quant(gate_up.data_ptr(), M, inter, out_q.data_ptr(),
+                                    out_scale.data_ptr(), _stream(gate_up)), "ecf8_silu_mul_quant")
+
+
+def act_quant(x, M, out_q, out_scale):
+    dev = x.device
+    _need(x, torch.bfloat16, "x", dev)
+    _need(out_q, torch.float8_e4m3fn, "out_q", dev)
+    _need(out_scale, torch.float32, "out_scale", dev)
+    _rows(M, x.shape[-1], x, out_q)
+    if out_scale.shape[-1] != x.shape[-1] // GROUP or out_scale.shape[0] < M:
+        raise ECF8Error("out_scale shape does not match")
+    check(lib().ecf8_act_quant(x.data_ptr(), M, x.shape[-1], out_q.data_ptr(), out_scale.data_ptr(),
+                               _stream(x)), "ecf8_act_quant")
+
+
+def qk_norm_rope(qkv, B, T, Hq, Hkv, q_norm, k_norm, eps, cos_t, sin_t, pos, q_out, k_cache,
+                 v_cache):
+    dev = qkv.device
+    for t, n in ((qkv, "qkv"), (q_norm, "q_norm"), (k_norm, "k_norm"), (q_out, "q_out"),
+                 (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _need(t, torch.bfloat16, n, dev)
+    _need(cos_t, torch.float32, "cos", dev)
+    _need(sin_t, torch.float32, "sin", dev)
+    _need(pos, torch.int32, "pos", dev)
+    Lmax = k_cache.shape[2]
+    if tuple(k_cache.shape) != (B, Hkv, Lmax, 128) or k_cache.shape != v_cache.shape:
+        raise ECF8Error("caches must be [B, Hkv, Lmax, 128]")
+    if q_out.numel() < B * Hq * T * 128 or qkv.numel() < B * T * (Hq + 2 * Hkv) * 128:
+        raise ECF8Error("q_out / qkv too small")
+    if cos_t.shape != (Lmax, 64) or sin_t.shape != (Lmax, 64):
+        raise ECF8Error("rotary tables must be [Lmax, 64]")
+    check(lib().ecf8_qk_norm_rope(qkv.data_ptr(), B, T, Hq, Hkv, q_norm.data_ptr(),
+                                  k_norm.data_ptr(), float(eps), cos_t.data_ptr(), sin_t.data_ptr(),
+                                  pos.data_ptr(), Lmax, q_out.data_ptr(), k_cache.data_ptr(),
+                                  v_cache.data_ptr(), _stream(qkv)), "ecf8_qk_norm_rope")
+
+
+def attention_work(B, Hq, Lmax, device) -> torch.Tensor:
+    n = lib().ecf8_attention_work_floats(B, Hq, Lmax)
+    if n < 0:
+        raise ECF8Error("bad attention work size")
+    return torch.empty(n, dtype=torch.float32, device=device)
+
+
+def decode_attention(q, k_cache, v_cache, pos, work, out_q, out_scale, Hq, out_bf16=None):
+    """q: the first B*Hq*128 elements of ``q`` are [B, Hq, 128]."""
+    dev = q.device
+    B, Hkv, Lmax, D = k_cache.shape
+    if q.numel() < B * Hq * 128:
+        raise ECF8Error("q too small")
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _need(t, torch.bfloat16, n, dev)
+    _need(pos, torch.int32, "pos", dev)
+    _need(work, torch.float32, "work", dev)
+    _need(out_q, torch.float8_e4m3fn, "out_q", dev)
+    _need(out_scale, torch.float32, "out_scale", dev)
+    if out_bf16 is not None:
+        _need(out_bf16, torch.bfloat16, "out_bf16", dev)
+    if D != 128 or v_cache.shape != k_cache.shape:
+        raise ECF8Error("caches must be [B, Hkv, Lmax, 128]")
+    if (out_q.numel() < B * Hq * 128 or out_scale.numel() < B * Hq
+            or (out_bf16 is not None and out_bf16.numel() < B * Hq * 128)):
+        raise ECF8Error("outputs too small")
+    check(lib().ecf8_decode_attention(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                      pos.data_ptr(), B, Hq, Hkv, Lmax, work.data_ptr(),
+                                      work.numel(), out_q.data_ptr(), out_scale.data_ptr(),
+                                      _ptr(out_bf16), _stream(q)), "ecf8_decode_attention")

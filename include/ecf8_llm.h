@@ -1,0 +1,108 @@
+/*
+ * ecf8_llm.h -- C ABI of the consumer kernels in libecf8.so: the
+ * block-scaled FP8 linear that reads decoded weights, and the fused
+ * kernels of a Qwen3-shaped decoder layer around it.
+ *
+ * None of these entry points replaces a reference interface one to one.
+ * The reference runs its decoded weights through transformers' FP8Linear
+ * (fine-grained FP8: weights e4m3fn with fp32 scales per 128x128 block,
+ * activations quantized per 1x128 group, transformers
+ * integrations/finegrained_fp8.py:182-350), inside the forward that
+ * dfloat/run/run.py:84-155 hooks.  These kernels are that consumer on
+ * gfx950, so a compressed model and its uncompressed FP8 original can be
+ * run and timed end to end by one engine.
+ *
+ * Conventions as in ecf8.h: device pointers, stream as void*, ECF8_*
+ * status, asynchronous, no allocation.  bf16 tensors are passed as void*
+ * (2-byte elements); fp8 tensors are e4m3fn bytes.  All deterministic.
+ */
+#ifndef ECF8_LLM_H
+#define ECF8_LLM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ECF8_LINEAR_MAX_SEGS 3
+
+/* One weight matrix of a (possibly fused) linear: weight e4m3fn [n, K]
+ * row-major (16-byte aligned), weight_scale fp32 [n/128, K/128]; its
+ * outputs go to columns [out_col, out_col + n) of the output. */
+typedef struct ecf8_linear_seg {
+  const void *weight;
+  const float *weight_scale;
+  int64_t n;
+  int64_t out_col;
+} ecf8_linear_seg;
+
+/*
+ * out[m, seg.out_col + j] (bf16, row stride ldo) =
+ *   sum_g (sum_{k in g} aq[m, k] * w[j, k]) * as[m, g] * ws[j/128, g]
+ * for each of n_segs (1..3) segments, e.g. q/k/v or gate/up in one launch.
+ * aq: e4m3fn [M, K] (16-byte aligned), as: fp32 [M, K/128].  K and every
+ * seg.n must be multiples of 128.
+ */
+int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64_t K,
+                    const ecf8_linear_seg *segs, int n_segs, void *out, int64_t ldo,
+                    void *stream);
+
+/*
+ * Residual add + RMSNorm over rows of K = 4096:
+ *   residual[m] += x[m]  (x bf16 [M, K], or NULL for no add; residual fp32)
+ *   y = residual[m] * rsqrt(mean(residual[m]^2) + eps) * weight  (bf16 weight)
+ * y goes to out_bf16 (bf16 [M, K]) when that is non-NULL, otherwise it is
+ * quantized to out_q (e4m3fn [M, K]) + out_scale (fp32 [M, K/128]).
+ */
+int ecf8_rmsnorm(const void *x, float *residual, const void *weight, float eps, int64_t M,
+                 int64_t K, void *out_q, float *out_scale, void *out_bf16, void *stream);
+
+/* h = silu(gate) * up for gate_up bf16 [M, 2I] (gate in columns [0, I)),
+ * quantized to out_q e4m3fn [M, I] + out_scale fp32 [M, I/128].
+ * I must be a multiple of 4096. */
+int ecf8_silu_mul_quant(const void *gate_up, int64_t M, int64_t I, void *out_q,
+                        float *out_scale, void *stream);
+
+/* bf16 [M, K] -> e4m3fn + fp32 scale per 1x128 group (scale = amax/448,
+ * 1 for an all-zero group; q = round_nearest_even(x / scale)).
+ * K must be a multiple of 4096. */
+int ecf8_act_quant(const void *x, int64_t M, int64_t K, void *out_q, float *out_scale,
+                   void *stream);
+
+/*
+ * For the fused projection output qkv bf16 [B*T, (Hq + 2*Hkv) * 128]
+ * (q heads, then k heads, then v heads), token t of sequence b at position
+ * p = pos[0] + t (pos: device int32):
+ *   q, k: RMSNorm over the head (bf16 weights q_norm / k_norm [128]), then
+ *         the rotary embedding, rotate-half form, cos_t/sin_t fp32 [Lmax, 64];
+ *   q -> q_out bf16 [B, Hq, T, 128];
+ *   k, v -> k_cache / v_cache bf16 [B, Hkv, Lmax, 128] at position p.
+ * Tokens whose p falls outside [0, Lmax) are skipped.
+ */
+int ecf8_qk_norm_rope(const void *qkv, int64_t B, int64_t T, int Hq, int Hkv, const void *q_norm,
+                      const void *k_norm, float eps, const float *cos_t, const float *sin_t,
+                      const int *pos, int64_t Lmax, void *q_out, void *k_cache, void *v_cache,
+                      void *stream);
+
+/* fp32 elements of the work buffer ecf8_decode_attention needs. */
+int64_t ecf8_attention_work_floats(int64_t B, int Hq, int64_t Lmax);
+
+/*
+ * Attention of one new token per sequence (q bf16 [B, Hq, 128], scaled by
+ * 1/sqrt(128)) over cached positions [0, pos[0]] (pos: device int32, the
+ * new token's position, already written to the caches), grouped-query with
+ * Hq = 4 * Hkv.  The result per (b, head) is quantized as one 128-group:
+ * out_q e4m3fn [B, Hq*128], out_scale fp32 [B, Hq]; out_bf16 (optional,
+ * bf16 [B, Hq*128]) receives the unquantized result.
+ */
+int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int *pos,
+                          int64_t B, int Hq, int Hkv, int64_t Lmax, float *work,
+                          int64_t work_floats, void *out_q, float *out_scale, void *out_bf16,
+                          void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ECF8_LLM_H */

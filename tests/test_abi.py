@@ -1,6 +1,6 @@
 """The C-ABI library loads, binds torch's HIP runtime, exports every function
-include/ecf8.h declares, and rejects bad arguments before touching the GPU.
-CPU only: no call here reaches a HIP API."""
+the headers under include/ declare, and rejects bad arguments before
+touching the GPU.  CPU only: no call here reaches a HIP API."""
 
 from __future__ import annotations
 
@@ -10,14 +10,17 @@ import re
 
 import pytest
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
-                      "ecf8.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+HEADER = os.path.join(INCLUDE, "ecf8.h")
 
 
 def _declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ecf8_[a-z_0-9]+)\s*\(", text)))
+    names = set()
+    for h in sorted(os.listdir(INCLUDE)):
+        if h.endswith(".h"):
+            text = re.sub(r"/\*.*?\*/", "", open(os.path.join(INCLUDE, h)).read(), flags=re.S)
+            names |= set(re.findall(r"\b(ecf8_[a-z_0-9]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_binding_table():
@@ -127,3 +130,35 @@ def test_block_descriptor_layout_matches_the_header():
     assert [BLOCK_DESC_DTYPE.fields[f][1] for f in fields] == [0, 8, 16, 24, 32, 40, 48, 56, 64,
                                                                72, 76]
     assert np.dtype("<i4").itemsize == 4
+
+
+def test_consumer_kernels_reject_before_launch():
+    """include/ecf8_llm.h entry points check arguments before any HIP call."""
+    import ctypes
+
+    from ecf8_amd._lib import lib
+    from ecf8_amd.llm_kernels import _Seg
+
+    L = lib()
+    fake = 1 << 20  # never dereferenced: every call below is rejected first
+    seg = (_Seg * 1)(_Seg(fake, fake, 128, 0))
+    assert L.ecf8_fp8_linear(None, fake, 16, 4096, seg, 1, fake, 128, None) == 1
+    assert L.ecf8_fp8_linear(fake, fake, 16, 4000, seg, 1, fake, 128, None) == 2   # K % 128
+    assert L.ecf8_fp8_linear(fake, fake, 16, 4096, seg, 4, fake, 128, None) == 1   # > 3 segments
+    assert L.ecf8_fp8_linear(fake + 1, fake, 16, 4096, seg, 1, fake, 128, None) == 3
+    assert L.ecf8_fp8_linear(fake, fake, 16, 4096, seg, 1, fake, 64, None) == 6    # ldo too small
+    bad_n = (_Seg * 1)(_Seg(fake, fake, 100, 0))
+    assert L.ecf8_fp8_linear(fake, fake, 16, 4096, bad_n, 1, fake, 128, None) == 2
+    assert L.ecf8_rmsnorm(None, None, fake, ctypes.c_float(1e-6), 4, 4096, fake, fake, None, None) == 1
+    assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 4096, None, fake, None, None) == 1
+    assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 2048, fake, fake, None, None) == 2
+    assert L.ecf8_silu_mul_quant(fake, 4, 1000, fake, fake, None) == 2
+    assert L.ecf8_act_quant(fake, 4, 4096, None, fake, None) == 1
+    assert L.ecf8_qk_norm_rope(fake, 1, 1, 32, 8, fake, fake, ctypes.c_float(1e-6), fake, fake,
+                               None, 64, fake, fake, fake, None) == 1
+    assert L.ecf8_attention_work_floats(2, 32, 300) == 2 * 32 * 2 * 130
+    assert L.ecf8_attention_work_floats(0, 32, 300) == -1
+    assert L.ecf8_decode_attention(fake, fake, fake, fake, 2, 32, 16, 300, fake, 10 ** 6, fake,
+                                   fake, None, None) == 2   # Hq != 4 Hkv
+    assert L.ecf8_decode_attention(fake, fake, fake, fake, 2, 32, 8, 300, fake, 10, fake, fake,
+                                   None, None) == 6         # work too small

@@ -1,0 +1,445 @@
+"""GPU numerics of the consumer kernels (include/ecf8_llm.h) against plain
+torch fp32/fp64 restatements of the same math, and the end-to-end Qwen3-shaped
+model: a model decoded from ECF8 produces exactly the tokens and logits of
+the same model kept in FP8 (same kernels, bit-exact weights), eager and
+graph-replayed, and its prefill logits match a torch fp32 forward of the
+same architecture.
+
+Tolerances (written per test): bf16 outputs 2^-7 relative; e4m3fn outputs
+are checked after dequantization against the unquantized reference with
+the format's half-ulp (2^-4 relative, plus the subnormal step) and a small
+allowance for the kernels' single-precision rsqrt/exp."""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _rand_fp8(shape, gen, dev):
+    """Finite random e4m3fn bytes (0x7F / 0xFF are NaN)."""
+    b = torch.randint(0, 256, shape, generator=gen, dtype=torch.int32).to(torch.uint8)
+    b[(b & 0x7F) == 0x7F] = 0x7E
+    return b.view(FP8).to(dev)
+
+
+def _ref_quant(x):
+    """The activation quantization the kernels implement, on the CPU:
+    scale = amax / 448 per 1x128 group (1 if all zero), q = RNE(x / scale)."""
+    x = x.float().cpu()
+    M, Kd = x.shape
+    g = x.view(M, Kd // 128, 128)
+    amax = g.abs().amax(-1)
+    s = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = (g / s[..., None]).to(FP8).view(M, Kd)
+    return q, s
+
+
+def _dequant(q, s):
+    M, Kd = q.shape
+    return (q.float().view(M, Kd // 128, 128) * s.float()[..., None]).view(M, Kd)
+
+
+def _assert_fp8_close(q, s, ref, rel=2 ** -4 + 2e-3):
+    """Dequantized e4m3fn vs the unquantized reference."""
+    got = _dequant(q.cpu(), s.cpu())
+    ref = ref.float().cpu()
+    M, Kd = ref.shape
+    step = (s.cpu().float()[..., None] * 2 ** -9).expand(M, Kd // 128, 128).reshape(M, Kd)
+    err = (got - ref).abs()
+    bound = rel * ref.abs() + step + 1e-6
+    assert bool((err <= bound).all()), f"max excess {(err - bound).max().item()}"
+
+
+# ------------------------------------------------------------ quantization
+
+
+def test_act_quant_matches_torch_cast(cuda_device):
+    from ecf8_amd.llm_kernels import act_quant
+
+    gen = torch.Generator().manual_seed(1)
+    M, Kd = 7, 8192
+    x = (torch.randn(M, Kd, generator=gen) * torch.logspace(-6, 3, Kd)[torch.randperm(Kd, generator=gen)])
+    x[2, 128:256] = 0.0   # an all-zero group gets scale 1
+    x[3, :5] = torch.tensor([448.0, -1e-8, 3e-3, 2 ** -10, -(2 ** -7)])
+    x = x.to(torch.bfloat16)
+    q = torch.empty(M, Kd, dtype=FP8, device=cuda_device)
+    s = torch.empty(M, Kd // 128, device=cuda_device)
+    act_quant(x.to(cuda_device), M, q, s)
+    qr, sr = _ref_quant(x)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+
+
+# ------------------------------------------------------------ FP8 linear
+
+
+def _linear_ref(aq, a_s, segs):
+    """fp64: sum_g (sum_{k in g} a*w) * a_s[m,g] * w_s[n/128,g], per segment."""
+    a = aq.cpu().double()
+    M, Kd = a.shape
+    outs = []
+    for w, ws in segs:
+        wd = w.cpu().double()
+        n = wd.shape[0]
+        part = torch.einsum("mgk,ngk->mng", a.view(M, Kd // 128, 128), wd.view(n, Kd // 128, 128))
+        scale = a_s.cpu().double()[:, None, :] * ws.cpu().double().repeat_interleave(128, 0)[None]
+        outs.append((part * scale).sum(-1))
+    return torch.cat(outs, dim=1)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 64, 130])
+def test_fp8_linear_matches_fp64(cuda_device, M):
+    from ecf8_amd.llm_kernels import LinearPlan
+
+    _say(f"[llm] fp8_linear M={M}")
+    gen = torch.Generator().manual_seed(M)
+    Kd = 1024
+    shapes = [256, 128, 384]
+    aq = _rand_fp8((M, Kd), gen, cuda_device)
+    a_s = (torch.rand(M, Kd // 128, generator=gen) * 1e-2 + 1e-4).to(cuda_device)
+    segs = []
+    for n in shapes:
+        w = _rand_fp8((n, Kd), gen, cuda_device)
+        ws = (torch.rand(n // 128, Kd // 128, generator=gen) * 1e-3 + 1e-5).to(cuda_device)
+        segs.append((w, ws))
+    ldo = sum(shapes) + 64
+    out = torch.full((M, ldo), 7.0, dtype=torch.bfloat16, device=cuda_device)
+    LinearPlan(segs, out)(aq, a_s, M)
+    ref = _linear_ref(aq, a_s, segs)
+    got = out[:, : sum(shapes)].double().cpu()
+    tol = 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()
+    assert bool(((got - ref).abs() <= tol).all())
+    assert bool((out[:, sum(shapes):].cpu() == 7.0).all())  # columns past the segments untouched
+
+
+def test_fp8_linear_is_deterministic(cuda_device):
+    from ecf8_amd.llm_kernels import LinearPlan
+
+    gen = torch.Generator().manual_seed(5)
+    aq = _rand_fp8((16, 4096), gen, cuda_device)
+    a_s = torch.rand(16, 32, generator=gen).to(cuda_device)
+    w = _rand_fp8((512, 4096), gen, cuda_device)
+    ws = torch.rand(4, 32, generator=gen).to(cuda_device)
+    out = torch.empty(16, 512, dtype=torch.bfloat16, device=cuda_device)
+    p = LinearPlan([(w, ws)], out)
+    first = p(aq, a_s, 16).clone()
+    for _ in range(3):
+        assert torch.equal(p(aq, a_s, 16), first)
+
+
+# ------------------------------------------------------------ row kernels
+
+
+def _rms_ref(r, x, w, eps):
+    r2 = r + x.float() if x is not None else r.clone()
+    y = r2 * torch.rsqrt(r2.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    return r2, y
+
+
+@pytest.mark.parametrize("with_x", [False, True])
+def test_rmsnorm_residual_and_outputs(cuda_device, with_x):
+    from ecf8_amd.llm_kernels import rmsnorm
+
+    gen = torch.Generator().manual_seed(3)
+    M, Kd = 9, 4096
+    r = torch.randn(M, Kd, generator=gen) * 3
+    x = (torch.randn(M, Kd, generator=gen)).to(torch.bfloat16) if with_x else None
+    w = (1 + 0.1 * torch.randn(Kd, generator=gen)).to(torch.bfloat16)
+    r_ref, y_ref = _rms_ref(r, x, w, 1e-6)
+    dev = cuda_device
+    # bf16 output
+    rd = r.to(dev)
+    ob = torch.empty(M, Kd, dtype=torch.bfloat16, device=dev)
+    rmsnorm(rd, w.to(dev), 1e-6, M, x=None if x is None else x.to(dev), out_bf16=ob)
+    assert torch.equal(rd.cpu(), r_ref)  # one IEEE add per element
+    assert torch.allclose(ob.float().cpu(), y_ref, rtol=2 ** -7, atol=1e-6)
+    # fp8 output
+    rd = r.to(dev)
+    q = torch.empty(M, Kd, dtype=FP8, device=dev)
+    s = torch.empty(M, Kd // 128, device=dev)
+    rmsnorm(rd, w.to(dev), 1e-6, M, x=None if x is None else x.to(dev), out_q=q, out_scale=s)
+    _assert_fp8_close(q, s, y_ref)
+
+
+def test_silu_mul_quant(cuda_device):
+    from ecf8_amd.llm_kernels import silu_mul_quant
+
+    gen = torch.Generator().manual_seed(4)
+    M, I = 6, 8192
+    gu = (torch.randn(M, 2 * I, generator=gen) * 4).to(torch.bfloat16)
+    g, u = gu.float()[:, :I], gu.float()[:, I:]
+    ref = g * torch.sigmoid(g) * u
+    q = torch.empty(M, I, dtype=FP8, device=cuda_device)
+    s = torch.empty(M, I // 128, device=cuda_device)
+    silu_mul_quant(gu.to(cuda_device), M, q, s)
+    _assert_fp8_close(q, s, ref)
+
+
+# ------------------------------------------------------ rotary + caches
+
+
+def _rope_tables(Lmax, theta=1e6):
+    inv = 1.0 / (theta ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    ang = torch.arange(Lmax, dtype=torch.float64)[:, None] * inv[None]
+    return torch.cos(ang).float(), torch.sin(ang).float()
+
+
+def _qk_ref(x, w, cos, sin, eps):
+    """HF Qwen3: RMSNorm over the head, then q*cos + rotate_half(q)*sin."""
+    y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    c = torch.cat([cos, cos], -1)
+    s_ = torch.cat([sin, sin], -1)
+    rot = torch.cat([-y[..., 64:], y[..., :64]], -1)
+    return y * c + rot * s_
+
+
+def test_qk_norm_rope_writes_q_and_caches(cuda_device):
+    from ecf8_amd.llm_kernels import qk_norm_rope
+
+    gen = torch.Generator().manual_seed(6)
+    B, T, Hq, Hkv, Lmax, pos0 = 3, 5, 8, 2, 32, 7
+    dev = cuda_device
+    qkv = torch.randn(B * T, (Hq + 2 * Hkv) * 128, generator=gen).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16)
+    cos, sin = _rope_tables(Lmax)
+    q_out = torch.zeros(B * Hq * T * 128, dtype=torch.bfloat16, device=dev)
+    kc = torch.full((B, Hkv, Lmax, 128), 3.0, dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, 3.0)
+    pos = torch.tensor([pos0], dtype=torch.int32, device=dev)
+    qk_norm_rope(qkv.to(dev), B, T, Hq, Hkv, qn.to(dev), kn.to(dev), 1e-6, cos.to(dev),
+                 sin.to(dev), pos, q_out, kc, vc)
+    x = qkv.float().view(B, T, Hq + 2 * Hkv, 128)
+    p = torch.arange(pos0, pos0 + T)
+    cq, sq = cos[p][None, :, None], sin[p][None, :, None]
+    q_ref = _qk_ref(x[:, :, :Hq], qn, cq, sq, 1e-6).permute(0, 2, 1, 3)
+    k_ref = _qk_ref(x[:, :, Hq:Hq + Hkv], kn, cq, sq, 1e-6).permute(0, 2, 1, 3)
+    v_ref = x[:, :, Hq + Hkv:].permute(0, 2, 1, 3)
+    tol = dict(rtol=2 ** -7, atol=2e-2)
+    assert torch.allclose(q_out.view(B, Hq, T, 128).float().cpu(), q_ref, **tol)
+    assert torch.allclose(kc[:, :, pos0:pos0 + T].float().cpu(), k_ref, **tol)
+    assert torch.equal(vc[:, :, pos0:pos0 + T].float().cpu(), v_ref)
+    outside = torch.ones(Lmax, dtype=torch.bool)
+    outside[pos0:pos0 + T] = False
+    assert bool((kc[:, :, outside].cpu() == 3.0).all()) and bool((vc[:, :, outside].cpu() == 3.0).all())
+
+
+# ------------------------------------------------------------ attention
+
+
+@pytest.mark.parametrize("pos0", [0, 255, 256, 517])
+def test_decode_attention_matches_fp32(cuda_device, pos0):
+    from ecf8_amd.llm_kernels import attention_work, decode_attention
+
+    _say(f"[llm] decode_attention pos={pos0}")
+    gen = torch.Generator().manual_seed(pos0)
+    B, Hkv, Hq, Lmax = 3, 2, 8, 600
+    dev = cuda_device
+    q = torch.randn(B, Hq, 128, generator=gen).to(torch.bfloat16)
+    kc = (torch.randn(B, Hkv, Lmax, 128, generator=gen) * 2).to(torch.bfloat16)
+    vc = torch.randn(B, Hkv, Lmax, 128, generator=gen).to(torch.bfloat16)
+    pos = torch.tensor([pos0], dtype=torch.int32, device=dev)
+    work = attention_work(B, Hq, Lmax, dev)
+    oq = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+    os_ = torch.empty(B, Hq, device=dev)
+    ob = torch.empty(B, Hq * 128, dtype=torch.bfloat16, device=dev)
+    decode_attention(q.to(dev), kc.to(dev), vc.to(dev), pos, work, oq, os_, Hq, out_bf16=ob)
+    L = pos0 + 1
+    k = kc[:, :, :L].float().repeat_interleave(Hq // Hkv, 1)
+    v = vc[:, :, :L].float().repeat_interleave(Hq // Hkv, 1)
+    sc = torch.matmul(q.float()[:, :, None], k.transpose(-1, -2).contiguous())[:, :, 0] / math.sqrt(128)
+    ref = torch.matmul(torch.softmax(sc, -1)[:, :, None], v)[:, :, 0].reshape(B, Hq * 128)
+    assert torch.allclose(ob.float().cpu(), ref, rtol=2 ** -7, atol=1e-4)
+    _assert_fp8_close(oq, os_, ref, rel=2 ** -4 + 5e-3)
+
+
+# ------------------------------------------------------------ end to end
+
+
+SMALL = dict(layers=2, intermediate=4096, vocab=1024)
+
+
+@pytest.fixture(scope="module")
+def small_models(cuda_device):
+    from ecf8_amd.llm import Qwen3Config, compress_layers, random_model
+
+    cfg = Qwen3Config(**SMALL)
+    plain, drawn = random_model(cfg, cuda_device, seed=1)
+    comp, _ = random_model(cfg, cuda_device, seed=1)
+    compress_layers(comp, drawn)
+    return cfg, plain, comp
+
+
+def _prompt(cfg, B, T):
+    g = torch.Generator().manual_seed(11)
+    return torch.randint(0, cfg.vocab, (B, T), generator=g)
+
+
+def test_compressed_model_matches_uncompressed_exactly(small_models, cuda_device):
+    from ecf8_amd.llm import Qwen3Runner
+    from ecf8_amd.run import TensorManager
+
+    cfg, plain, comp = small_models
+    B, T, new = 2, 16, 8
+    prompt = _prompt(cfg, B, T)
+    results = {}
+    for name, model in (("fp8", plain), ("ecf8", comp)):
+        for graph in (False, True):
+            _say(f"[llm] e2e {name} graph={graph}")
+            TensorManager.clear_device()
+            r = Qwen3Runner(model, B, T, T + new, cuda_device)
+            if graph:
+                r.capture()
+            toks = r.generate(prompt, new).cpu()
+            last = r.logits.float().cpu()
+            results[(name, graph)] = (toks, last)
+    base_t, base_l = results[("fp8", False)]
+    for key, (t, l) in results.items():
+        assert torch.equal(t, base_t), key
+        assert torch.equal(l, base_l), key
+    assert len(set(base_t.reshape(-1).tolist())) > 1
+
+
+def _torch_forward(model, prompt):
+    """fp32 torch forward of the prompt with the same quantization points
+    as the kernels (activations per 1x128 group before every linear)."""
+    cfg = model.config
+    B, T = prompt.shape
+    Hq, Hkv = cfg.heads, cfg.kv_heads
+    emb = model.model.embed_tokens.weight.float().cpu()
+    r = emb[prompt.reshape(-1)]
+
+    def lin(x, mod):
+        q, s = _ref_quant(x)
+        w = mod.weight.float().cpu()
+        ws = mod.weight_scale_inv.cpu().repeat_interleave(128, 0).repeat_interleave(128, 1)
+        return _dequant(q, s) @ (w * ws[: w.shape[0], : w.shape[1]]).t()
+
+    def norm(x, w):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.eps) * w.float().cpu()
+
+    cos, sin = _rope_tables(T, cfg.rope_theta)
+    for layer in model.model.layers:
+        a, m = layer.self_attn, layer.mlp
+        h = norm(r, layer.input_layernorm.weight)
+        q = lin(h, a.q_proj).to(torch.bfloat16).float().view(B, T, Hq, 128)
+        k = lin(h, a.k_proj).to(torch.bfloat16).float().view(B, T, Hkv, 128)
+        v = lin(h, a.v_proj).to(torch.bfloat16).float().view(B, T, Hkv, 128)
+        # q and k are stored as bf16 after the rotary embedding
+        q = _qk_ref(q, a.q_norm.weight.cpu(), cos[None, :, None], sin[None, :, None], cfg.eps)
+        k = _qk_ref(k, a.k_norm.weight.cpu(), cos[None, :, None], sin[None, :, None], cfg.eps)
+        q, k = q.to(torch.bfloat16).float(), k.to(torch.bfloat16).float()
+        q, k, v = (t.permute(0, 2, 1, 3) for t in (q, k, v))
+        k = k.repeat_interleave(Hq // Hkv, 1)
+        v = v.repeat_interleave(Hq // Hkv, 1)
+        s = torch.matmul(q, k.transpose(-1, -2).contiguous()) / math.sqrt(128)
+        s.masked_fill_(torch.ones(T, T, dtype=torch.bool).triu(1), float("-inf"))
+        o = torch.matmul(torch.softmax(s, -1), v).permute(0, 2, 1, 3).reshape(B * T, Hq * 128)
+        r = r + lin(o.to(torch.bfloat16).float(), a.o_proj).to(torch.bfloat16).float()
+        h = norm(r, layer.post_attention_layernorm.weight)
+        g = lin(h, m.gate_proj).to(torch.bfloat16).float()
+        u = lin(h, m.up_proj).to(torch.bfloat16).float()
+        r = r + lin(g * torch.sigmoid(g) * u, m.down_proj).to(torch.bfloat16).float()
+    h = norm(r, model.model.norm.weight).to(torch.bfloat16).float()
+    last = h.view(B, T, -1)[:, -1]
+    return last @ model.lm_head.weight.float().cpu().t()
+
+
+def _rel(a, b):
+    a, b = a.float().cpu().reshape(-1), b.float().cpu().reshape(-1)
+    return ((a - b).norm() / b.norm()).item()
+
+
+def _lin_deq(x_deq, mod):
+    w = mod.weight.float().cpu()
+    ws = mod.weight_scale_inv.cpu().repeat_interleave(128, 0).repeat_interleave(128, 1)
+    return x_deq @ (w * ws[: w.shape[0], : w.shape[1]]).t()
+
+
+def test_prefill_layer_stages_match_torch(small_models, cuda_device):
+    """One decoder layer of the prefill, stage by stage, each stage's torch
+    reference fed with the engine's own inputs to that stage: the wiring
+    (norm placement, q/k/v split, head layout, GQA mapping, residual flow,
+    gate/up order) is checked to bf16 rounding (relative L2 <= 1e-2; the
+    inputs' fp8 codes differ from the reference quantizer's in ~0.04 % of
+    elements, from single-precision rsqrt)."""
+    from ecf8_amd.llm import Qwen3Runner
+
+    cfg, plain, _ = small_models
+    B, T = 2, 16
+    M = B * T
+    prompt = _prompt(cfg, B, T)
+    r = Qwen3Runner(plain, B, T, T + 1, cuda_device)
+    layer = plain.model.layers[0]
+    a, m = layer.self_attn, layer.mlp
+    emb = torch.nn.functional.embedding(prompt.to(cuda_device).reshape(-1),
+                                        plain.model.embed_tokens.weight)
+    r.res[:M].copy_(emb)
+    r.pos.zero_()
+    res0 = r.res[:M].float().cpu().clone()
+    layer(r, 0, None, True)
+    torch.cuda.synchronize()
+
+    def norm(x, w):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.eps) * w.float().cpu()
+
+    def lin_q(x, mod):
+        q, s = _ref_quant(x)
+        return _lin_deq(_dequant(q, s), mod)
+
+    h = norm(res0, layer.input_layernorm.weight)
+    qkv_ref = torch.cat([lin_q(h, a.q_proj), lin_q(h, a.k_proj), lin_q(h, a.v_proj)], 1)
+    assert _rel(r.qkv[:M], qkv_ref) < 1e-2
+    x = r.qkv[:M].float().cpu().view(B, T, 48, 128)
+    cos, sin = _rope_tables(T, cfg.rope_theta)
+    cq, sq = cos[None, :, None], sin[None, :, None]
+    q_ref = _qk_ref(x[:, :, :32], a.q_norm.weight.cpu(), cq, sq, cfg.eps).permute(0, 2, 1, 3)
+    k_ref = _qk_ref(x[:, :, 32:40], a.k_norm.weight.cpu(), cq, sq, cfg.eps).permute(0, 2, 1, 3)
+    q = r.q[: B * 32 * T * 128].view(B, 32, T, 128)
+    assert _rel(q, q_ref) < 1e-2 and _rel(r.kc[0][:, :, :T], k_ref) < 1e-2
+    assert torch.equal(r.vc[0][:, :, :T].float().cpu(), x[:, :, 40:].permute(0, 2, 1, 3))
+    qf, kf = q.float().cpu(), r.kc[0][:, :, :T].float().cpu().repeat_interleave(4, 1)
+    vf = r.vc[0][:, :, :T].float().cpu().repeat_interleave(4, 1)
+    sc = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) / math.sqrt(128)
+    sc.masked_fill_(torch.ones(T, T, dtype=torch.bool).triu(1), float("-inf"))
+    o_ref = torch.matmul(torch.softmax(sc, -1), vf).permute(0, 2, 1, 3).reshape(M, 4096)
+    assert _rel(r.attn[:M], o_ref) < 1e-2
+    assert _rel(r.o[:M], lin_q(r.attn[:M].float().cpu(), a.o_proj)) < 1e-2
+    res1 = res0 + r.o[:M].float().cpu()
+    assert torch.equal(r.res[:M].cpu(), res1)
+    h2 = norm(res1, layer.post_attention_layernorm.weight)
+    gu_ref = torch.cat([lin_q(h2, m.gate_proj), lin_q(h2, m.up_proj)], 1)
+    assert _rel(r.gu[:M], gu_ref) < 1e-2
+    g, u = r.gu[:M].float().cpu()[:, :4096], r.gu[:M].float().cpu()[:, 4096:]
+    assert _rel(r.down[:M], lin_q(g * torch.sigmoid(g) * u, m.down_proj)) < 1e-2
+
+
+def test_prefill_logits_follow_a_torch_forward(small_models, cuda_device):
+    """Whole-model check of the prefill logits.  The random-init network
+    amplifies the rare fp8 code differences between the engine and the
+    reference quantizer layer after layer, so the bound is loose (cosine
+    > 0.99); the per-stage test above carries the tight checks."""
+    from ecf8_amd.llm import Qwen3Runner
+
+    cfg, plain, _ = small_models
+    B, T = 2, 16
+    prompt = _prompt(cfg, B, T)
+    r = Qwen3Runner(plain, B, T, T + 1, cuda_device)
+    got = r.prefill(prompt).float().cpu()
+    ref = _torch_forward(plain, prompt)
+    cos = torch.nn.functional.cosine_similarity(got.reshape(-1), ref.reshape(-1), dim=0).item()
+    _say(f"[llm] prefill logits cosine {cos:.6f}")
+    assert cos > 0.99, cos
