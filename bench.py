@@ -228,6 +228,7 @@ def e2e_generate(args):
     import torch
 
     from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model, timed_generate
+    from ecf8_amd.prefetch import LayerPrefetcher
     from ecf8_amd.run import TensorManager
 
     dev = torch.device("cuda", 0)
@@ -239,12 +240,15 @@ def e2e_generate(args):
     g = torch.Generator().manual_seed(args.seed + 7)
     prompt = torch.randint(0, cfg.vocab, (B, T), generator=g)
     results = {}
-    for mode in ("fp8", "ecf8"):
+    for mode in ("fp8", "ecf8", "ecf8_prefetch"):
         if mode == "ecf8":
             t0 = time.time()
             compress_layers(model, drawn)
             torch.cuda.synchronize()
             print(f"[bench] layers compressed in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+        if mode == "ecf8_prefetch":
+            LayerPrefetcher(model.model.layers, dev,
+                            workgroups_per_cu=args.prefetch_workgroups).install()
         TensorManager.clear_device()
         torch.cuda.empty_cache()
         runner = Qwen3Runner(model, B, T, T + new, dev)
@@ -257,8 +261,14 @@ def e2e_generate(args):
                                list(model.parameters()) + list(model.buffers())) / 2**20
         results[mode] = r
         del runner
-    same = torch.equal(results["fp8"]["tokens"], results["ecf8"]["tokens"])
-    fp8, ecf8 = results["fp8"], results["ecf8"]
+    same = all(torch.equal(results["fp8"]["tokens"], results[m]["tokens"])
+               for m in ("ecf8", "ecf8_prefetch"))
+    fp8, ecf8 = results["fp8"], results["ecf8_prefetch"]
+
+    def summary(r):
+        return {"tokens_per_s": round(r["tokens_per_s"], 1), "latency_s": round(r["latency_s"], 4),
+                "peak_mib": round(r["peak_mib"], 1), "weights_mib": round(r["weights_mib"], 1)}
+
     line = {
         "metric": "e2e tokens/s, Qwen3-8B-shape bs16 (ECF8-compressed, per-layer decode before the FP8 GEMMs)",
         "value": round(ecf8["tokens_per_s"], 1),
@@ -271,15 +281,11 @@ def e2e_generate(args):
         "config": {"workload": "qwen3-8b-generate", "layers": cfg.layers, "hidden": cfg.hidden,
                    "intermediate": cfg.intermediate, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
                    "vocab": cfg.vocab, "batch": B, "prompt_len": T, "new_tokens": new,
-                   "distinct_layer_weights": args.distinct_layers, "decoding": "greedy"},
-        "uncompressed_fp8": {"tokens_per_s": round(fp8["tokens_per_s"], 1),
-                             "latency_s": round(fp8["latency_s"], 4),
-                             "peak_mib": round(fp8["peak_mib"], 1),
-                             "weights_mib": round(fp8["weights_mib"], 1)},
-        "ecf8": {"tokens_per_s": round(ecf8["tokens_per_s"], 1),
-                 "latency_s": round(ecf8["latency_s"], 4),
-                 "peak_mib": round(ecf8["peak_mib"], 1),
-                 "weights_mib": round(ecf8["weights_mib"], 1)},
+                   "distinct_layer_weights": args.distinct_layers, "decoding": "greedy",
+                   "ecf8_decode": "next layer decoded on a side stream (double-buffered)"},
+        "uncompressed_fp8": summary(fp8),
+        "ecf8": summary(ecf8),
+        "ecf8_in_hook": summary(results["ecf8"]),
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,
     }
@@ -303,6 +309,8 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt-len", type=int, default=128)
     ap.add_argument("--new-tokens", type=int, default=1024)
+    ap.add_argument("--prefetch-workgroups", type=int, default=2,
+                    help="generate: resident side-stream decode workgroups per CU")
     ap.add_argument("--distinct-layers", type=int, default=2,
                     help="generate: layers drawn independently (the rest copy them)")
     ap.add_argument("--mode", choices=("decode", "copy"), default="decode",

@@ -306,6 +306,17 @@ def test_compressed_model_matches_uncompressed_exactly(small_models, cuda_device
             toks = r.generate(prompt, new).cpu()
             last = r.logits.float().cpu()
             results[(name, graph)] = (toks, last)
+    from ecf8_amd.prefetch import LayerPrefetcher
+
+    LayerPrefetcher(comp.model.layers, cuda_device).install()
+    for graph in (False, True):
+        _say(f"[llm] e2e ecf8 prefetch graph={graph}")
+        r = Qwen3Runner(comp, B, T, T + new, cuda_device)
+        if graph:
+            r.capture()
+        for rep in range(2):  # the second run starts from the state the first left
+            toks = r.generate(prompt, new).cpu()
+            results[("ecf8_prefetch", graph, rep)] = (toks, r.logits.float().cpu())
     base_t, base_l = results[("fp8", False)]
     for key, (t, l) in results.items():
         assert torch.equal(t, base_t), key
