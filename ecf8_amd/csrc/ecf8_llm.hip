@@ -226,6 +226,103 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
   }
 }
 
+// Small-M form (M <= 16, the decode step): one 16-row MFMA tile, WAVES
+// waves splitting K round-robin in batches of 4 groups.  Every load a batch
+// needs (weights from HBM, activations and both scales from L2) is issued
+// before its first MFMA, so a batch costs one memory round trip.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
+    const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, LinearSegs segs,
+    uint16_t *__restrict__ out, int ldo) {
+  __shared__ float red[WAVES][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kgroups = K / kGroup;
+
+  int n0 = blockIdx.x * 16;
+  const uint8_t *w = segs.w[0];
+  const float *ws = segs.ws[0];
+  int col = segs.col[0], seg_start = 0;
+#pragma unroll
+  for (int s = 1; s < ECF8_LINEAR_MAX_SEGS; ++s) {
+    if (s < segs.count && n0 >= segs.n_end[s - 1]) {
+      w = segs.w[s];
+      ws = segs.ws[s];
+      col = segs.col[s];
+      seg_start = segs.n_end[s - 1];
+    }
+  }
+  n0 -= seg_start;
+
+  const int r = lane & 15, g = lane >> 4;
+  const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+  const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
+  const bool row_ok = r < M;
+  const uint8_t *arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+  bool srow_ok[4];
+  const float *srow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    srow_ok[i] = 4 * g + i < M;
+    srow[i] = as + (size_t)(srow_ok[i] ? 4 * g + i : 0) * kgroups;
+  }
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  constexpr int kU = 4;
+  for (int kb = wave; kb < kgroups; kb += WAVES * kU) {
+    uint4 wv[kU][2], av[kU][2];
+    float wsv[kU], sav[kU][4];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kg = kb + WAVES * u;
+      if (kg < kgroups) {
+        wv[u][0] = load_stream16(wrow + kg * kGroup);
+        wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+        wsv[u] = wsrow[kg];
+        // rows past M read row 0 (always valid) and are zeroed after the load
+        av[u][0] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
+        av[u][1] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sav[u][i] = srow[i][kg];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kg = kb + WAVES * u;
+      if (kg >= kgroups) break;
+      if (!row_ok) av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sav[u][i] = srow_ok[i] ? sav[u][i] : 0.f;
+      v4f d = {0.f, 0.f, 0.f, 0.f};
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][0].y << 32) | av[u][0].x),
+          (long)(((uint64_t)wv[u][0].y << 32) | wv[u][0].x), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][0].w << 32) | av[u][0].z),
+          (long)(((uint64_t)wv[u][0].w << 32) | wv[u][0].z), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][1].y << 32) | av[u][1].x),
+          (long)(((uint64_t)wv[u][1].y << 32) | wv[u][1].x), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][1].w << 32) | av[u][1].z),
+          (long)(((uint64_t)wv[u][1].w << 32) | wv[u][1].z), d, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[u][i] * wsv[u], acc[i]);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int i = threadIdx.x >> 6, l = threadIdx.x & 63;
+    float sum = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < WAVES; ++wv) sum += red[wv][i][l];
+    const int m = 4 * (l >> 4) + i;
+    if (m < M) out[(size_t)m * ldo + col + n0 + (l & 15)] = (uint16_t)f32_bf16(sum);
+  }
+}
+
 // ------------------------------------------------- quantizing row kernels
 
 // residual += x (if x); y = residual * rsqrt(mean(residual^2) + eps) * w;
@@ -380,6 +477,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restr
                                                          float *__restrict__ wacc) {
   __shared__ float qs[G][kHeadDim];
   __shared__ float pw[G][kAttnChunk];
+  __shared__ float part[4 * G * kHeadDim];  // PV partials [wave][head][dim]
   __shared__ float red[G][4];
   const int bk = blockIdx.x, split = blockIdx.y;
   const int b = bk / Hkv, kh = bk % Hkv;
@@ -409,11 +507,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restr
   for (int h = 0; h < G; ++h) s[h] = 0.f;
   const bool valid = j < n;
   if (valid) {
+    // the whole 256-byte key row in flight at once
     const uint4 *kr = reinterpret_cast<const uint4 *>(kc + (((size_t)b * Hkv + kh) * Lmax + c0 + j) * kHeadDim);
-#pragma unroll 4
+    uint4 kv[kHeadDim / 8];
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 8; ++c) kv[c] = kr[c];
+#pragma unroll
     for (int c = 0; c < kHeadDim / 8; ++c) {
-      const uint4 kv = kr[c];
-      const uint32_t wds[4] = {kv.x, kv.y, kv.z, kv.w};
+      const uint32_t wds[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float k0 = bf16_f32(wds[e] & 0xffffu), k1 = bf16_f32(wds[e] >> 16);
@@ -447,30 +548,57 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restr
     wm[(head0 + t) * S + split] = mh[t];
     wl[(head0 + t) * S + split] = (red[t][0] + red[t][1]) + (red[t][2] + red[t][3]);
   }
-  const uint16_t *vr = vc + (((size_t)b * Hkv + kh) * Lmax + c0) * kHeadDim + 2 * lane;
-  for (int h = wave; h < G; h += 4) {
-    float a0 = 0.f, a1 = 0.f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-      uint32_t vv[8];
+  // PV: wave w takes positions [64w, 64w + 64) of the chunk, four rows per
+  // step (lane / 16), eight dims per lane (16-byte loads), all 16 row loads
+  // in flight; positions past n read row n - 1 with weight 0.
+  const int dg = lane & 15, rr = lane >> 4;
+  const uint16_t *vbase = vc + (((size_t)b * Hkv + kh) * Lmax + c0) * kHeadDim + 8 * dg;
+  uint4 vv[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) vv[u] = *reinterpret_cast<const uint32_t *>(vr + (size_t)(i + u) * kHeadDim);
+  for (int st = 0; st < 16; ++st) {
+    const int jj = min(64 * wave + 4 * st + rr, n - 1);
+    vv[st] = *reinterpret_cast<const uint4 *>(vbase + (size_t)jj * kHeadDim);
+  }
+  float acc[G][8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float p = pw[h][i + u];
-        a0 = fmaf(p, bf16_f32(vv[u] & 0xffffu), a0);
-        a1 = fmaf(p, bf16_f32(vv[u] >> 16), a1);
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+#pragma unroll
+  for (int st = 0; st < 16; ++st) {
+    const int jp = 64 * wave + 4 * st + rr;
+    const uint32_t wds[4] = {vv[st].x, vv[st].y, vv[st].z, vv[st].w};
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float p = pw[h][jp];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[h][2 * e] = fmaf(p, bf16_f32(wds[e] & 0xffffu), acc[h][2 * e]);
+        acc[h][2 * e + 1] = fmaf(p, bf16_f32(wds[e] >> 16), acc[h][2 * e + 1]);
       }
     }
-    for (; i < n; ++i) {
-      const uint32_t v2 = *reinterpret_cast<const uint32_t *>(vr + (size_t)i * kHeadDim);
-      const float p = pw[h][i];
-      a0 = fmaf(p, bf16_f32(v2 & 0xffffu), a0);
-      a1 = fmaf(p, bf16_f32(v2 >> 16), a1);
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[h][e];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[h][e] = v;
     }
-    float *dst = wacc + ((head0 + h) * S + split) * kHeadDim + 2 * lane;
-    dst[0] = a0;
-    dst[1] = a1;
+  if (rr == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[(wave * G + h) * kHeadDim + 8 * dg + e] = acc[h][e];
+  }
+  __syncthreads();
+  for (int v = t; v < G * kHeadDim; v += 256) {
+    const int h = v / kHeadDim, d = v % kHeadDim;
+    const float sum = (part[(0 * G + h) * kHeadDim + d] + part[(1 * G + h) * kHeadDim + d]) +
+                      (part[(2 * G + h) * kHeadDim + d] + part[(3 * G + h) * kHeadDim + d]);
+    wacc[((head0 + h) * S + split) * kHeadDim + d] = sum;
   }
 }
 
@@ -540,8 +668,13 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
   const auto *a = static_cast<const uint8_t *>(aq);
   auto *o = static_cast<uint16_t *>(out);
   if (M <= 16) {
-    dim3 grid((unsigned)(n_total / 16), 1);
-    fp8_linear_kernel<1><<<grid, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o, (int)ldo);
+    // long K: 16 waves, so each wave's share stays within two batches
+    if (K / kGroup >= 64)
+      fp8_linear16_kernel<16><<<(unsigned)(n_total / 16), 1024, 0, as_stream(stream)>>>(
+          a, as, (int)M, (int)K, s, o, (int)ldo);
+    else
+      fp8_linear16_kernel<8><<<(unsigned)(n_total / 16), 512, 0, as_stream(stream)>>>(
+          a, as, (int)M, (int)K, s, o, (int)ldo);
   } else {
     dim3 grid((unsigned)(n_total / 16), (unsigned)((M + 63) / 64));
     fp8_linear_kernel<4><<<grid, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o, (int)ldo);

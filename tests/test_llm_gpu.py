@@ -100,13 +100,15 @@ def _linear_ref(aq, a_s, segs):
     return torch.cat(outs, dim=1)
 
 
-@pytest.mark.parametrize("M", [1, 5, 16, 17, 64, 130])
-def test_fp8_linear_matches_fp64(cuda_device, M):
+@pytest.mark.parametrize("M,Kd", [(1, 1024), (5, 1024), (16, 1024), (16, 8192), (3, 12288),
+                                  (17, 1024), (64, 1024), (130, 1024)])
+def test_fp8_linear_matches_fp64(cuda_device, M, Kd):
+    """M <= 16 runs the one-tile kernel (8 waves, or 16 from K = 8192 on);
+    larger M the 64-row tile kernel."""
     from ecf8_amd.llm_kernels import LinearPlan
 
-    _say(f"[llm] fp8_linear M={M}")
-    gen = torch.Generator().manual_seed(M)
-    Kd = 1024
+    _say(f"[llm] fp8_linear M={M} K={Kd}")
+    gen = torch.Generator().manual_seed(M * 7 + Kd)
     shapes = [256, 128, 384]
     aq = _rand_fp8((M, Kd), gen, cuda_device)
     a_s = (torch.rand(M, Kd // 128, generator=gen) * 1e-2 + 1e-4).to(cuda_device)
