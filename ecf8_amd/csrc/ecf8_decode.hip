@@ -50,8 +50,13 @@ namespace {
 
 using namespace ecf8;
 
+// (a & m) | (b & ~m) as one v_bfi_b32.  Written out, the compiler expands
+// it to two ANDs and an OR when m is a constant (gfx9 VOP3 takes no literal
+// operand, so the mask comes from an SGPR).
 __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
-  return (a & m) | (b & ~m);
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
+  return r;
 }
 
 // 8 FP8 bytes from 8 exponent nibbles (E, element k in bits 4k..4k+3) and
@@ -458,14 +463,22 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s
     uint32_t pos4 = min(((uint32_t)br.lead << 2) + (uint32_t)excl4, (uint32_t)stage_dw << 5);
     auto put = [&](uint32_t syms, uint32_t n4) {
       const uint64_t v = (uint64_t)syms << (pos4 & 31u);
-      uint32_t *const q = stage + (pos4 >> 5);
+      uint32_t *const q = stage + __builtin_amdgcn_ubfe(pos4, 5, 27);
       atomicOr(q, (uint32_t)v);
       atomicOr(q + 1, (uint32_t)(v >> 32));
       pos4 += n4;
     };
     auto put2 = [&](uint32_t ea, uint32_t eb) {
-      const uint32_t na4 = ea & 0xFFu;
-      put(((eb >> 16) << na4) | (ea >> 16), na4 + (eb & 0xFFu));
+      // (eb.hi16 << count4(ea)) | ea.hi16 in two SDWA ops (count4 <= 16, so
+      // the whole dword is a valid shift amount)
+      uint32_t t, syms;
+      asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:WORD_1"
+          : "=v"(t) : "v"(ea), "v"(eb));
+      asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:WORD_1"
+          : "=v"(syms) : "v"(t), "v"(ea));
+      put(syms, (ea & 0xFFu) + (eb & 0xFFu));
     };
     if (!any_exact || !exact) {
       put2(e0, e1);
@@ -478,23 +491,23 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s
     }
     __syncthreads();
 
-    // the next block's chunk and positions, fetched a whole decode phase ago
-    g_cur = (uint32_t)fb_pf * kThreads + tid;
-    const uint3 nxt = chunk_bytes(nxt_raw, encoded, n_bytes, g_cur, !kChecked);
-    const uint32_t nxt_gap = gap_of(nxt_raw.gap_byte, g_cur);
-    const uint32_t nop_lo = __builtin_amdgcn_readlane(nopv, 0);
-    const uint32_t nop_hi = __builtin_amdgcn_readlane(nopv, 1);
-
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
     write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, s_edge, tid);
     // the next iteration writes the other staging buffer; its barrier after
     // the scan orders this sweep before any reuse of this one
     if (fb_next >= fb_end) break;
+    // The next block's chunk and positions, fetched a whole decode phase
+    // ago, are read only now, after this block's stores were issued: the
+    // memory counter also counts stores, and waiting for a load waits for
+    // every older store too.  Here the only older stores are the previous
+    // block's, issued an iteration ago; read before the stores above, the
+    // wait would have drained them mid-iteration.
+    g_cur = (uint32_t)fb_pf * kThreads + tid;
+    cur = chunk_bytes(nxt_raw, encoded, n_bytes, g_cur, !kChecked);
+    gap = gap_of(nxt_raw.gap_byte, g_cur);
+    op_lo = __builtin_amdgcn_readlane(nopv, 0);
+    op_hi = __builtin_amdgcn_readlane(nopv, 1);
     fb = fb_next;
-    cur = nxt;
-    gap = nxt_gap;
-    op_lo = nop_lo;
-    op_hi = nop_hi;
   }
   __syncthreads();
   flush_edges(s_edge, out, tid);
