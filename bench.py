@@ -294,6 +294,77 @@ def e2e_generate(args):
         sys.exit(1)
 
 
+def dit_generate(args):
+    """FLUX.1-dev-shaped DiT (19 double + 38 single blocks, hidden 3072),
+    one 1024x1024 image: 4096 latent tokens of 64 channels and 512 text
+    tokens of 4096, embedded guidance 3.5, --dit-steps Euler steps at batch
+    1; first with the FP8 weights resident, then with every block
+    ECF8-compressed and decoded by its forward-pre-hook.  Both runs must
+    produce identical latents."""
+    import torch
+
+    from ecf8_amd.dit import FluxConfig, compress_blocks, random_pipeline, timed_generate
+    from ecf8_amd.run import TensorManager
+
+    dev = torch.device("cuda", 0)
+    cfg = FluxConfig()
+    t0 = time.time()
+    pipe, drawn = random_pipeline(cfg, dev, distinct=args.distinct_layers, seed=args.seed)
+    print(f"[bench] DiT built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(args.seed + 11)
+    lat = torch.randn(1, 4096, cfg.in_channels, generator=g).to(torch.bfloat16).to(dev)
+    txt = torch.randn(1, 512, cfg.txt_dim, generator=g).to(torch.bfloat16).to(dev)
+    pooled = torch.randn(1, cfg.pooled_dim, generator=g).to(torch.bfloat16).to(dev)
+    results = {}
+    for mode in ("fp8", "ecf8"):
+        if mode == "ecf8":
+            t0 = time.time()
+            compress_blocks(pipe, drawn)
+            torch.cuda.synchronize()
+            print(f"[bench] blocks compressed in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+        TensorManager.clear_device()
+        torch.cuda.empty_cache()
+        timed_generate(pipe, lat, txt, pooled, 1, (64, 64))  # warm-up
+        r = timed_generate(pipe, lat, txt, pooled, args.dit_steps, (64, 64))
+        r["weights_mib"] = sum(t.numel() * t.element_size() for t in
+                               list(pipe.parameters()) + list(pipe.buffers())) / 2**20
+        print(f"[bench] {mode}: {r['seconds']:.3f} s/image, peak {r['peak_mib']:.0f} MiB",
+              file=sys.stderr, flush=True)
+        results[mode] = r
+    same = torch.equal(results["fp8"]["latents"].view(torch.int16),
+                       results["ecf8"]["latents"].view(torch.int16))
+    fp8, ecf8 = results["fp8"], results["ecf8"]
+
+    def summary(r):
+        return {"seconds_per_image": round(r["seconds"], 3), "peak_mib": round(r["peak_mib"], 1),
+                "weights_mib": round(r["weights_mib"], 1)}
+
+    line = {
+        "metric": "DiT s/image, FLUX.1-dev-shape 1024x1024 (ECF8-compressed blocks)",
+        "value": round(ecf8["seconds"], 3),
+        "unit": "s/image",
+        "n_gpus": 1,
+        "higher_is_better": False,
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random latents and text embeddings)",
+        "config": {"workload": "flux-dit-generate", "double_blocks": cfg.double,
+                   "single_blocks": cfg.single, "hidden": cfg.hidden, "heads": cfg.heads,
+                   "mlp": cfg.mlp, "image_tokens": 4096, "text_tokens": 512, "batch": 1,
+                   "steps": args.dit_steps, "guidance": 3.5,
+                   "distinct_block_weights": args.distinct_layers,
+                   "linears": "FP8 weights dequantized to bf16 per call + library bf16 GEMM",
+                   "attention": "fp32"},
+        "uncompressed_fp8": summary(fp8),
+        "ecf8": summary(ecf8),
+        "ratio_vs_uncompressed": round(fp8["seconds"] / ecf8["seconds"], 4),
+        "identical_latents": same,
+    }
+    print(json.dumps(line), flush=True)
+    if not same:
+        sys.exit(1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -302,10 +373,13 @@ def main():
     ap.add_argument("--copies", type=int, default=4, help="rotated input/output sets")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "qwen3-8b-generate"),
+    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "qwen3-8b-generate",
+                                           "flux-dit-generate"),
                     default="qwen3-8b-layer",
                     help="qwen3-moe-layer: attention + 128 experts in one batched launch; "
-                         "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8")
+                         "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8; "
+                         "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8")
+    ap.add_argument("--dit-steps", type=int, default=28)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt-len", type=int, default=128)
     ap.add_argument("--new-tokens", type=int, default=1024)
@@ -324,6 +398,8 @@ def main():
         return copy_calibration(args.steps, args.warmup)
     if args.workload == "qwen3-8b-generate":
         return e2e_generate(args)
+    if args.workload == "flux-dit-generate":
+        return dit_generate(args)
 
     import torch
 

@@ -55,6 +55,7 @@ _SIGNATURES = {
     "ecf8_act_quant": ([_vp, _i64, _i64, _vp, _vp, _vp], _i32),
     "ecf8_qk_norm_rope": ([_vp, _i64, _i64, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _i64, _vp,
                            _vp, _vp, _vp], _i32),
+    "ecf8_dequant_fp8_block": ([_vp, _vp, _i64, _i64, _vp, _vp], _i32),
     "ecf8_attention_work_floats": ([_i64, _i32, _i64], _i64),
     "ecf8_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _i64, _vp, _vp, _vp,
                                _vp], _i32),

@@ -635,6 +635,43 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
   if (lane == 0) os[bh] = sc;
 }
 
+// ---------------------------------------------------- FP8 block dequantize
+
+// e4m3fn byte -> fp32 (exact; 0x7F / 0xFF, the NaN codes, become NaN)
+__device__ __forceinline__ float e4m3_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
+  if (e == 0) return __uint_as_float(sign | __float_as_uint((float)m * 0.001953125f));  // m * 2^-9
+  if (e == 15 && m == 7) return __uint_as_float(sign | 0x7FC00000u);
+  return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// out[r, c] = bf16(w[r, c] * scale[r / 128, c / 128]); one thread per 16
+// consecutive bytes of a row (always inside one 128-column group).
+__global__ __launch_bounds__(256) void dequant_fp8_block_kernel(const uint8_t *__restrict__ w,
+                                                                const float *__restrict__ scale,
+                                                                int64_t n, int64_t k,
+                                                                uint16_t *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte unit
+  const int64_t units_per_row = k / 16;
+  if (i >= n * units_per_row) return;
+  const int64_t r = i / units_per_row, c = (i % units_per_row) * 16;
+  const float sc = scale[(r / kGroup) * (k / kGroup) + c / kGroup];
+  const uint4 b = *reinterpret_cast<const uint4 *>(w + r * k + c);
+  const uint32_t wd[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float v0 = e4m3_f32(wd[j] & 0xFFu) * sc, v1 = e4m3_f32((wd[j] >> 8) & 0xFFu) * sc;
+    const float v2 = e4m3_f32((wd[j] >> 16) & 0xFFu) * sc, v3 = e4m3_f32(wd[j] >> 24) * sc;
+    o[2 * j] = f32_bf16(v0) | (f32_bf16(v1) << 16);
+    o[2 * j + 1] = f32_bf16(v2) | (f32_bf16(v3) << 16);
+  }
+  uint4 *op = reinterpret_cast<uint4 *>(out + r * k + c);
+  op[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  op[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 inline int launched() { return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP; }
@@ -733,6 +770,18 @@ extern "C" int ecf8_qk_norm_rope(const void *qkv, int64_t B, int64_t T, int Hq, 
       static_cast<const uint16_t *>(k_norm), eps, cos_t, sin_t, pos, (int)Lmax,
       static_cast<uint16_t *>(q_out), static_cast<uint16_t *>(k_cache),
       static_cast<uint16_t *>(v_cache), (int)items);
+  return launched();
+}
+
+extern "C" int ecf8_dequant_fp8_block(const void *weight, const float *weight_scale, int64_t n,
+                                      int64_t k, void *out, void *stream) {
+  if (!weight || !weight_scale || !out || n <= 0 || k <= 0) return ECF8_ERR_INVALID_ARG;
+  if (n % kGroup || k % kGroup || n * k > ((int64_t)1 << 40)) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(weight, 16) || !aligned(out, 16) || !aligned(weight_scale, 4))
+    return ECF8_ERR_MISALIGNED;
+  const int64_t units = n * (k / 16);
+  dequant_fp8_block_kernel<<<(unsigned)((units + 255) / 256), 256, 0, as_stream(stream)>>>(
+      static_cast<const uint8_t *>(weight), weight_scale, n, k, static_cast<uint16_t *>(out));
   return launched();
 }
 

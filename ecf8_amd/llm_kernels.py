@@ -195,3 +195,21 @@ def decode_attention(q, k_cache, v_cache, pos, work, out_q, out_scale, Hq, out_b
                                       pos.data_ptr(), B, Hq, Hkv, Lmax, work.data_ptr(),
                                       work.numel(), out_q.data_ptr(), out_scale.data_ptr(),
                                       _ptr(out_bf16), _stream(q)), "ecf8_decode_attention")
+
+
+def dequant_fp8_block(weight, scale_inv, out=None):
+    """bf16 [n, k] = e4m3fn weight x its 128x128 block scales."""
+    dev = weight.device
+    _need(weight, torch.float8_e4m3fn, "weight", dev)
+    _need(scale_inv, torch.float32, "weight_scale_inv", dev)
+    n, k = weight.shape
+    if tuple(scale_inv.shape) != (n // GROUP, k // GROUP):
+        raise ECF8Error("weight_scale_inv shape does not match the weight")
+    if out is None:
+        out = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    _need(out, torch.bfloat16, "out", dev)
+    if out.numel() < n * k:
+        raise ECF8Error("out too small")
+    check(lib().ecf8_dequant_fp8_block(weight.data_ptr(), scale_inv.data_ptr(), n, k,
+                                       out.data_ptr(), _stream(weight)), "ecf8_dequant_fp8_block")
+    return out.view(-1)[: n * k].view(n, k)

@@ -85,6 +85,13 @@ int ecf8_qk_norm_rope(const void *qkv, int64_t B, int64_t T, int Hq, int Hkv, co
                       const int *pos, int64_t Lmax, void *q_out, void *k_cache, void *v_cache,
                       void *stream);
 
+/* out bf16 [n, k] = weight e4m3fn [n, k] x weight_scale fp32 [n/128, k/128]
+ * (per 128x128 block), rounded to nearest even: the weights of a linear
+ * whose activations are too many rows for the small-M kernel, handed to a
+ * library bf16 GEMM.  n and k multiples of 128. */
+int ecf8_dequant_fp8_block(const void *weight, const float *weight_scale, int64_t n, int64_t k,
+                           void *out, void *stream);
+
 /* fp32 elements of the work buffer ecf8_decode_attention needs. */
 int64_t ecf8_attention_work_floats(int64_t B, int Hq, int64_t Lmax);
 

@@ -44,3 +44,27 @@ def test_linear_shapes_follow_the_qwen3_8b_layer():
     from ecf8_amd.synth import QWEN3_8B_LAYER
 
     assert Qwen3Config().linear_shapes() == QWEN3_8B_LAYER
+
+
+def test_dit_blocks_compress_with_the_reference_patterns():
+    """FLUX-shaped DiT blocks are compressed per dfloat/const.py's
+    diffsynth-flux-fp8 patterns: 8 Linears per double block, 3 per single
+    block, and each stored block decodes (oracle) to its original weights."""
+    from ecf8_amd.dit import (DOUBLE_LINEARS, SINGLE_LINEARS, FluxConfig, compress_blocks,
+                              random_pipeline)
+
+    cfg = FluxConfig(hidden=256, heads=2, mlp=512, double=2, single=3, txt_dim=128,
+                     pooled_dim=128)
+    pipe, drawn = random_pipeline(cfg, "cpu", distinct=2, seed=5)
+    groups = ((pipe.dit.blocks, DOUBLE_LINEARS), (pipe.dit.single_blocks, SINGLE_LINEARS))
+    originals = [[{n: b.get_submodule(n).weight.detach().view(torch.uint8).clone() for n in names}
+                  for b in blocks] for blocks, names in groups]
+    compress_blocks(pipe, drawn)
+    for (blocks, names), orig in zip(groups, originals):
+        for blk, o in zip(blocks, orig):
+            assert len(blk._forward_pre_hooks) == 1
+            assert [type(m).__name__ for m in blk.weight_injection_modules] == ["_Lin"] * len(names)
+            flat = oc.decode(blk.luts.numpy(), blk.encoded.numpy(), blk.packed_other_4bits.numpy(),
+                             blk.output_positions.numpy(), blk.gaps.numpy())
+            for n, part in zip(names, np.split(flat, blk.split_positions)):
+                assert np.array_equal(part, o[n].numpy().reshape(-1)), n
