@@ -78,6 +78,37 @@ def cpu_baseline(block, n_elements, alg_bytes, repeats=3):
     }
 
 
+def cpu_encode(flat, sample: int = 1048576):
+    """CPU encode timings (the reference's CPU path is its encoder,
+    dfloat/utils.py:373-499): the product's C++ encoder (ecf8_encode_exponents,
+    one thread) over the whole layer, and the oracle's per-symbol Python
+    restatement of the reference loop over the first `sample` elements."""
+    import torch
+
+    from ecf8_amd.compress import compress_flat
+    from oracle import codec as oc
+
+    n = flat.numel()
+    t0 = time.perf_counter()
+    compress_flat(flat)  # split + counts + codebook + LUTs + C++ bitstream encoder
+    full = time.perf_counter() - t0
+    part = flat[:sample].view(torch.uint8).numpy()
+    t0 = time.perf_counter()
+    oc.compress_block(part)
+    py = time.perf_counter() - t0
+    return {
+        "product_cpp": {"value": round(n / full / 1e6, 2), "unit": "M elements/s",
+                        "cores": torch.get_num_threads(),
+                        "sample": f"whole layer ({n} elements): split and counts (torch, "
+                                  f"{torch.get_num_threads()} threads), codebook, LUTs, bitstream "
+                                  f"(C++ encoder, 1 thread), {full:.2f} s"},
+        "reference_loop_python": {"value": round(sample / py / 1e6, 4), "unit": "M elements/s",
+                                  "cores": 1, "kind": "port",
+                                  "sample": f"first {sample} elements, per-symbol Python "
+                                            f"restatement of dfloat/utils.py:373-499, {py:.2f} s"},
+    }
+
+
 def copy_calibration(steps, warmup):
     """A plain device-to-device copy of known size (1 GiB read + 1 GiB
     written per launch): the reference point for scaling the HBM counters
@@ -158,7 +189,7 @@ def _qwen3_layer_workload(args, dev):
         "bytes_per_thread": 8,
         "table_kind": "dfa" if sets[0]["table"].kind == 1 else "multi",
     }
-    return calls, verify, alg, n, config, (block, n)
+    return calls, verify, alg, n, config, (block, n, flat)
 
 
 def _qwen3_moe_layer_workload(args, dev):
@@ -456,9 +487,10 @@ def main():
     gbps = alg / (ms_per_step * 1e-3) / 1e9
     kernel_gbps = alg / (avg_launch_ms * 1e-3) / 1e9
 
-    cpu = None
+    cpu = enc = None
     if not args.no_cpu_baseline and cpu_case is not None:
         cpu = cpu_baseline(cpu_case[0], cpu_case[1], alg)
+        enc = cpu_encode(cpu_case[2])
     line = {
         "metric": "ECF8 decode GB/s + % HBM roofline; e2e tokens/s, Qwen3-8B-shape bs16",
         "value": round(gbps, 1),
@@ -482,6 +514,7 @@ def main():
             "traffic": _traffic_from_profile(pmc_profile),
         },
         "cpu_baseline": cpu,
+        "cpu_encode": enc,
         "wall_s_timed": round(wall, 4),
         "bit_exact": ok,
     }
