@@ -228,8 +228,50 @@ def _qwen3_moe_layer_workload(args, dev):
     hstream = torch.cuda.current_stream(dev).cuda_stream
     calls = [(L.ecf8_decode_batched, (p.descs.data_ptr(), p.count, p.n_tasks, p.blocks_per_task,
                                       p.cap, 512, hstream)) for p in plans]
+    routed = None
+    if args.routed_tokens:
+        # decode only the attention block and the experts a top-k router
+        # picks for `routed_tokens` tokens (uniform random routing, 8
+        # routings rotated), selected on the device
+        from ecf8_amd.decode import BatchSelect
+
+        rng = torch.Generator().manual_seed(args.seed + 3)
+        per_block = [algorithmic_bytes(f.numel(), c["encoded"].numel(), c["luts"].shape[0])[0]
+                     for f, c in zip(flats, comp)]
+        sels = [BatchSelect(p) for p in plans]
+        flag_sets, alg_sets, n_sel = [], [], []
+        for _ in range(8):
+            picked = torch.stack([torch.randperm(128, generator=rng)[: args.top_k]
+                                  for _ in range(args.routed_tokens)]).unique()
+            flags = torch.zeros(len(flats), dtype=torch.int32)
+            flags[0] = 1
+            flags[1 + picked] = 1
+            flag_sets.append(flags.to(dev))
+            alg_sets.append(sum(b for b, f in zip(per_block, flags.tolist()) if f))
+            n_sel.append(int(flags.sum()) - 1)
+        calls = []
+        for i in range(8):
+            sel = sels[i % len(sels)]
+            calls.append((lambda f, sel=sel: (sel(f), 0)[1], (flag_sets[i],)))
+        alg = sum(alg_sets) // len(alg_sets)
+        routed = {"tokens": args.routed_tokens, "top_k": args.top_k,
+                  "experts_decoded_mean": round(sum(n_sel) / len(n_sel), 1),
+                  "algorithmic_bytes_mean": alg}
 
     def verify():
+        if routed is not None:
+            # one routed call on sentinel-filled outputs: the selected blocks
+            # decode exactly, the others are untouched
+            for o in first_outs:
+                o.view(torch.uint8).fill_(0x3C)
+            sels[0](flag_sets[0])
+            torch.cuda.synchronize()
+            ok = True
+            for o, f, s_ in zip(first_outs, flats, flag_sets[0].tolist()):
+                got = o.view(torch.uint8)
+                ok &= (torch.equal(got.cpu(), f.view(torch.uint8)) if s_
+                       else bool((got == 0x3C).all()))
+            return ok
         return all(torch.equal(o.view(torch.uint8).cpu(), f.view(torch.uint8))
                    for o, f in zip(first_outs, flats))
 
@@ -245,6 +287,10 @@ def _qwen3_moe_layer_workload(args, dev):
         "threads_per_block": 512,
         "bytes_per_thread": 8,
     }
+    if routed is not None:
+        config["workload"] = "qwen3-moe-layer-routed-decode"
+        config["routed"] = routed
+        config["algorithmic_bytes"] = alg
     return calls, verify, alg, n, config, None
 
 
@@ -424,6 +470,10 @@ def main():
                          "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8; "
                          "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8")
     ap.add_argument("--dit-steps", type=int, default=28)
+    ap.add_argument("--routed-tokens", type=int, default=0,
+                    help="qwen3-moe-layer: decode only the experts a top-k router picks for "
+                         "this many tokens (device-side selection)")
+    ap.add_argument("--top-k", type=int, default=8)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt-len", type=int, default=128)
     ap.add_argument("--new-tokens", type=int, default=1024)
@@ -450,8 +500,8 @@ def main():
     dev = torch.device("cuda", 0)
     setup = _qwen3_layer_workload if args.workload == "qwen3-8b-layer" else _qwen3_moe_layer_workload
     calls, verify, alg, n, config, cpu_case = setup(args, dev)
-    pmc_profile = ("decode_qwen3_layer_pmc.md" if args.workload == "qwen3-8b-layer"
-                   else "decode_qwen3_moe_layer_pmc.md")
+    pmc_profile = {"qwen3-8b-layer-decode": "decode_qwen3_layer_pmc.md",
+                   "qwen3-moe-layer-decode": "decode_qwen3_moe_layer_pmc.md"}.get(config["workload"])
 
     def step(i):
         fn, cargs = calls[i % len(calls)]
@@ -511,7 +561,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": _traffic_from_profile(pmc_profile),
+            "traffic": _traffic_from_profile(pmc_profile) if pmc_profile else None,
         },
         "cpu_baseline": cpu,
         "cpu_encode": enc,

@@ -35,6 +35,7 @@ _SIGNATURES = {
     "ecf8_version": ([], ctypes.c_char_p),
     "ecf8_status_string": ([_i32], ctypes.c_char_p),
     "ecf8_decode_batched": ([_vp, _i32, _i32, _i32, _i64, _i32, _vp], _i32),
+    "ecf8_decode_batched_select": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ecf8_build_table_host": ([_vp, _i32, _i32, _vp, _vp], _i32),
     "ecf8_build_table": ([_vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "ecf8_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _i32, _i32,

@@ -89,14 +89,17 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
 // Sum of the totals of the waves before this one (s_wave_sum[w] = total of
 // wave w): lanes 0..kWaves-1 load one total each, a DPP prefix inside the
 // first row adds them up, and this wave's entry is read back.
+// Optionally also the total over all waves.
 template <int kWaves>
-__device__ __forceinline__ int waves_before(const int *s_wave_sum, int lane, int wave) {
+__device__ __forceinline__ int waves_before(const int *s_wave_sum, int lane, int wave,
+                                            int *total = nullptr) {
   const int own = lane < kWaves ? s_wave_sum[lane] : 0;
   int t = own;
   if (kWaves > 1) t += __builtin_amdgcn_update_dpp(0, t, 0x111, 0xF, 0xF, true);  // row_shr:1
   if (kWaves > 2) t += __builtin_amdgcn_update_dpp(0, t, 0x112, 0xF, 0xF, true);  // row_shr:2
   if (kWaves > 4) t += __builtin_amdgcn_update_dpp(0, t, 0x114, 0xF, 0xF, true);  // row_shr:4
   if (kWaves > 8) t += __builtin_amdgcn_update_dpp(0, t, 0x118, 0xF, 0xF, true);  // row_shr:8
+  if (total) *total = __builtin_amdgcn_readlane(t, kWaves - 1);
   return __builtin_amdgcn_readlane(t - own, __builtin_amdgcn_readfirstlane(wave));
 }
 
@@ -548,16 +551,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
 // tensor; desc[d].task_begin is the first task of tensor d.  Each workgroup
 // takes tasks blockIdx.x, + gridDim.x, ..., loading the task's table before
 // decoding it.
+//
+// dev_counts (optional): {count, n_tasks} read from device memory instead
+// of the arguments, as written by select_blocks_kernel.
 template <int kThreads>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_batched_kernel(
     const ecf8_block_desc *__restrict__ descs, int count, int n_tasks, int blocks_per_task,
-    int stage_cap) {
+    int stage_cap, const int *__restrict__ dev_counts) {
   constexpr int kWaves = kThreads / 64;
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ int s_wave_sum[kWaves];
   __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
 
+  if (dev_counts) {  // never above the launch's bounds
+    count = min(count, __builtin_amdgcn_readfirstlane(dev_counts[0]));
+    n_tasks = min(n_tasks, __builtin_amdgcn_readfirstlane(dev_counts[1]));
+  }
   const int tid = threadIdx.x;
   if (tid < kEdgeDwords) s_edge[tid] = 0u;
   constexpr uint32_t kBlockBytes = (uint32_t)kThreads * kChunkBytes;
@@ -590,6 +600,52 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
                       reinterpret_cast<const uint32_t *>(d.output_positions), d.gaps,
                       d.outputs, (uint32_t)d.n_elements};
     dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, fb0, tasks, n_fb);
+  }
+}
+
+// Compact the descriptors whose select flag is nonzero (e.g. the attention
+// block and the experts the router picked this step) into `out`, in order,
+// with task_begin recomputed for the compacted list, and write {count,
+// n_tasks} to `counts` for decode_dfa_batched_kernel.  One workgroup of
+// 1024 threads walks the descriptors in chunks of 1024.
+__global__ __launch_bounds__(1024) void select_blocks_kernel(
+    const ecf8_block_desc *__restrict__ in, int count, const int32_t *__restrict__ select,
+    int blocks_per_task, int64_t block_bytes, ecf8_block_desc *__restrict__ out,
+    int *__restrict__ counts) {
+  constexpr int kWaves = 16;
+  __shared__ int s_sel[kWaves], s_task[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int base_sel = 0, base_task = 0;
+  for (int c0 = 0; c0 < count; c0 += 1024) {
+    const int d = c0 + tid;
+    int sel = 0, tasks = 0;
+    if (d < count && select[d] != 0) {
+      const int64_t nb = in[d].n_bytes > 0 ? in[d].n_bytes : 0;
+      const int64_t n_fb = (nb + block_bytes - 1) / block_bytes;
+      sel = 1;
+      tasks = (int)((n_fb + blocks_per_task - 1) / blocks_per_task);
+    }
+    const int isel = wave_inclusive_scan(sel), itask = wave_inclusive_scan(tasks);
+    if (lane == 63) {
+      s_sel[wave] = isel;
+      s_task[wave] = itask;
+    }
+    __syncthreads();
+    int total_sel = 0, total_task = 0;
+    const int before_sel = waves_before<kWaves>(s_sel, lane, wave, &total_sel);
+    const int before_task = waves_before<kWaves>(s_task, lane, wave, &total_task);
+    if (sel) {
+      ecf8_block_desc e = in[d];
+      e.task_begin = base_task + before_task + itask - tasks;
+      out[base_sel + before_sel + isel - 1] = e;
+    }
+    base_sel += total_sel;
+    base_task += total_task;
+    __syncthreads();  // the totals are rewritten by the next chunk
+  }
+  if (tid == 0) {
+    counts[0] = base_sel;
+    counts[1] = base_task;
   }
 }
 
@@ -954,7 +1010,7 @@ int launch_decode(DecodeArgs a, int64_t max_block_elements, bool dfa, int tpb_sl
 
 template <int kThreads>
 int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int blocks_per_task,
-                       int cap, hipStream_t stream, int slot) {
+                       int cap, hipStream_t stream, int slot, const int *dev_counts = nullptr) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(cap) + kSpillDwords);
   const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
@@ -964,7 +1020,7 @@ int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int
                                  slot, n_tasks, &grid);
   if (rc != ECF8_OK) return rc;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, stream, descs, count,
-                     n_tasks, blocks_per_task, cap);
+                     n_tasks, blocks_per_task, cap, dev_counts);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
@@ -994,6 +1050,48 @@ extern "C" int ecf8_decode_batched(const ecf8_block_desc *descs, int count, int 
       return launch_dfa_batched<512>(descs, count, n_tasks, blocks_per_task, cap, s, 18);
     default:
       return launch_dfa_batched<1024>(descs, count, n_tasks, blocks_per_task, cap, s, 19);
+  }
+}
+
+extern "C" int ecf8_decode_batched_select(const ecf8_block_desc *descs, int count,
+                                          const int32_t *select, ecf8_block_desc *work_descs,
+                                          int32_t *work_counts, int blocks_per_task,
+                                          int64_t max_block_elements, int threads_per_block,
+                                          void *stream) {
+  if (count < 0 || blocks_per_task < 1) return ECF8_ERR_INVALID_ARG;
+  if (count == 0) return ECF8_OK;
+  if (!descs || !select || !work_descs || !work_counts) return ECF8_ERR_INVALID_ARG;
+  if (((uintptr_t)descs & 7) || ((uintptr_t)work_descs & 7) || ((uintptr_t)select & 3) ||
+      ((uintptr_t)work_counts & 3))
+    return ECF8_ERR_MISALIGNED;
+  if (threads_per_block != 128 && threads_per_block != 256 && threads_per_block != 512 &&
+      threads_per_block != 1024)
+    return ECF8_ERR_UNSUPPORTED;
+  const int64_t max_syms = (int64_t)threads_per_block * kChunkBits;
+  int cap = (max_block_elements <= 0 || max_block_elements > max_syms) ? (int)max_syms
+                                                                        : (int)max_block_elements;
+  if (cap < 16) cap = 16;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t block_bytes = (int64_t)threads_per_block * kChunkBytes;
+  hipLaunchKernelGGL(select_blocks_kernel, dim3(1), dim3(1024), 0, s, descs, count, select,
+                     blocks_per_task, block_bytes, work_descs, work_counts);
+  if (hipGetLastError() != hipSuccess) return ECF8_ERR_HIP;
+  // the task count is only known on the device: a full persistent grid,
+  // each workgroup stops at the selected task count
+  const int n_tasks_bound = INT32_MAX;
+  switch (threads_per_block) {
+    case 128:
+      return launch_dfa_batched<128>(work_descs, count, n_tasks_bound, blocks_per_task, cap, s, 16,
+                                     work_counts);
+    case 256:
+      return launch_dfa_batched<256>(work_descs, count, n_tasks_bound, blocks_per_task, cap, s, 17,
+                                     work_counts);
+    case 512:
+      return launch_dfa_batched<512>(work_descs, count, n_tasks_bound, blocks_per_task, cap, s, 18,
+                                     work_counts);
+    default:
+      return launch_dfa_batched<1024>(work_descs, count, n_tasks_bound, blocks_per_task, cap, s,
+                                      19, work_counts);
   }
 }
 

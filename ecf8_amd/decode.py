@@ -269,6 +269,39 @@ def decode_batched(plan, outs=None, tables=None, stream=None, **kwargs):
     return plan
 
 
+class BatchSelect:
+    """Decode a device-chosen subset of a BatchPlan's blocks per call
+    (ecf8_decode_batched_select): e.g. the attention block plus the experts
+    the router picked, from a flags tensor the model writes on the device.
+    Allocates its work descriptors once; a call reads nothing back to the
+    host, so it can be captured in a HIP graph and replayed with new flags.
+    Every block of the plan must be batchable (no ``singles``)."""
+
+    def __init__(self, plan: BatchPlan):
+        if plan.singles:
+            raise ECF8Error("selection needs every block in the batched launch "
+                            "(automaton tables, >= 16 elements)")
+        if not plan.count:
+            raise ECF8Error("empty plan")
+        self.plan = plan
+        dev = plan.descs.device
+        self.work = torch.empty_like(plan.descs)
+        self.counts = torch.zeros(2, dtype=torch.int32, device=dev)
+
+    def __call__(self, select: torch.Tensor, stream=None):
+        p = self.plan
+        dev = p.descs.device
+        if (not select.is_cuda or select.device != dev or select.dtype != torch.int32
+                or not select.is_contiguous() or select.numel() < p.count):
+            raise ECF8Error(f"select must be a contiguous int32 tensor of >= {p.count} flags on {dev}")
+        with torch.cuda.device(dev):
+            check(lib().ecf8_decode_batched_select(p.descs.data_ptr(), p.count, select.data_ptr(),
+                                                   self.work.data_ptr(), self.counts.data_ptr(),
+                                                   p.blocks_per_task, p.cap, p.threads_per_block,
+                                                   _stream_handle(dev, stream)),
+                  "ecf8_decode_batched_select")
+
+
 def _check_block(out, b, t, n, threads_per_block, bytes_per_thread, dev):
     for name in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps"):
         v = b[name]

@@ -162,3 +162,18 @@ def test_consumer_kernels_reject_before_launch():
                                    fake, None, None) == 2   # Hq != 4 Hkv
     assert L.ecf8_decode_attention(fake, fake, fake, fake, 2, 32, 8, 300, fake, 10, fake, fake,
                                    None, None) == 6         # work too small
+
+
+def test_batched_select_rejects_before_launch():
+    from ecf8_amd._lib import lib
+
+    L = lib()
+    fake = 1 << 20
+    f = L.ecf8_decode_batched_select
+    assert f(fake, -1, fake, fake, fake, 4, 0, 512, None) == 1
+    assert f(fake, 3, fake, fake, fake, 0, 0, 512, None) == 1       # blocks_per_task < 1
+    assert f(fake, 0, None, None, None, 4, 0, 512, None) == 0       # nothing to do
+    assert f(fake, 3, None, fake, fake, 4, 0, 512, None) == 1
+    assert f(fake + 4, 3, fake, fake, fake, 4, 0, 512, None) == 3  # descs misaligned
+    assert f(fake, 3, fake + 2, fake, fake, 4, 0, 512, None) == 3  # flags misaligned
+    assert f(fake, 3, fake, fake, fake, 4, 0, 300, None) == 2

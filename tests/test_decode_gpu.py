@@ -450,3 +450,83 @@ def test_batched_decode_of_moe_experts(cuda_device):
     flats += [synth.flat_block(synth.synthetic_block(synth.QWEN3_MOE_EXPERT, 1 + e))[0]
               for e in range(16)]
     _batched_case([f.view(torch.uint8).numpy() for f in flats], cuda_device, 16)
+
+
+def _select_case(cuda_device, n_experts=12, blocks_per_task=4):
+    """An attention block and n_experts small expert blocks (all automaton
+    tables), outputs filled with a sentinel."""
+    from ecf8_amd import synth
+    from ecf8_amd.decode import BatchSelect, build_table, prepare_batch
+
+    shapes = {"down_proj": (256, 384, 0.02), "gate_proj": (384, 256, 0.02),
+              "up_proj": (384, 256, 0.02)}
+    flats = [synth.flat_block(synth.synthetic_block(synth.QWEN3_MOE_ATTN, 0))[0]]
+    flats += [synth.flat_block(synth.synthetic_block(shapes, 10 + e))[0] for e in range(n_experts)]
+    flats = [f.view(torch.uint8).numpy() for f in flats]
+    blocks = [_dev_block(_compress(f), cuda_device) for f in flats]
+    tables = [build_table(b["luts"]) for b in blocks]
+    assert all(t.kind == DFA for t in tables)
+    bufs = [torch.full((f.size + 32,), 0x3C, dtype=torch.uint8, device=cuda_device) for f in flats]
+    plan = prepare_batch(blocks, [b[: f.size] for b, f in zip(bufs, flats)], tables,
+                         blocks_per_task=blocks_per_task)
+    return flats, bufs, BatchSelect(plan)
+
+
+def _check_selected(flats, bufs, flags):
+    for i, (buf, flat) in enumerate(zip(bufs, flats)):
+        got = buf.cpu().numpy()
+        if flags[i]:
+            assert np.array_equal(got[: flat.size], flat), f"selected block {i}"
+        else:
+            assert (got[: flat.size] == 0x3C).all(), f"unselected block {i} was written"
+        assert (got[flat.size:] == 0x3C).all(), f"block {i} wrote past its end"
+
+
+def test_batched_select_decodes_only_the_selected_blocks(cuda_device):
+    """ecf8_decode_batched_select: the attention block plus a random subset
+    of experts per call (flags on the device), several selections in a row,
+    none and all included."""
+    _say("batched select")
+    flats, bufs, sel = _select_case(cuda_device)
+    rng = np.random.default_rng(3)
+    cases = [np.ones(len(flats), np.int32), np.zeros(len(flats), np.int32)]
+    for _ in range(4):
+        f = (rng.random(len(flats)) < 0.5).astype(np.int32)
+        f[0] = 1
+        cases.append(f)
+    for flags in cases:
+        for b in bufs:
+            b.fill_(0x3C)
+        sel(torch.from_numpy(flags).to(cuda_device))
+        torch.cuda.synchronize()
+        _check_selected(flats, bufs, flags)
+        n_sel, n_tasks = sel.counts.cpu().tolist()
+        assert n_sel == int(flags.sum())
+
+
+def test_batched_select_replays_in_a_graph_with_new_flags(cuda_device):
+    """The select call captured once in a HIP graph decodes whatever the
+    flags tensor holds at each replay (eager work between replays)."""
+    _say("batched select graph")
+    flats, bufs, sel = _select_case(cuda_device, n_experts=8)
+    flags_dev = torch.zeros(len(flats), dtype=torch.int32, device=cuda_device)
+    s = torch.cuda.Stream(cuda_device)
+    s.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(s):
+        sel(flags_dev)  # warm-up (launch caches)
+    torch.cuda.current_stream(cuda_device).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sel(flags_dev)
+    rng = np.random.default_rng(5)
+    for _ in range(3):
+        f = (rng.random(len(flats)) < 0.5).astype(np.int32)
+        f[0] = 1
+        for b in bufs:
+            b.fill_(0x3C)
+        flags_dev.copy_(torch.from_numpy(f).to(cuda_device))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _check_selected(flats, bufs, f)
