@@ -323,6 +323,129 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
   }
 }
 
+// Persistent small-M form for K = 4096 (32 groups, 4 per wave): each
+// workgroup keeps its waves' activation groups and scales in registers and
+// walks the 16-column tiles blockIdx.x, + gridDim.x, ...; the next tile's
+// weights are loaded while the current tile's MFMAs run.  Used when there
+// are more tiles than resident workgroups (the gate/up projection).
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
+    const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, LinearSegs segs,
+    uint16_t *__restrict__ out, int ldo, int n_tiles) {
+  constexpr int K = 4096, kgroups = K / kGroup, kU = kgroups / WAVES;
+  __shared__ float red[WAVES][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const bool row_ok = r < M;
+
+  // this wave's groups: wave, wave + WAVES, ...
+  uint4 av[kU][2];
+  float sav[kU][4];
+  {
+    const uint8_t *arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kg = wave + WAVES * u;
+      av[u][0] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
+      av[u][1] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+      if (!row_ok) av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mi = 4 * g + i;
+        const float v = as[(size_t)(mi < M ? mi : 0) * kgroups + kg];
+        sav[u][i] = mi < M ? v : 0.f;
+      }
+    }
+  }
+
+  auto tile_base = [&](int tile, const uint8_t *&w, const float *&ws, int &col, int &n0) {
+    n0 = tile * 16;
+    w = segs.w[0];
+    ws = segs.ws[0];
+    col = segs.col[0];
+    int seg_start = 0;
+#pragma unroll
+    for (int s2 = 1; s2 < ECF8_LINEAR_MAX_SEGS; ++s2) {
+      if (s2 < segs.count && n0 >= segs.n_end[s2 - 1]) {
+        w = segs.w[s2];
+        ws = segs.ws[s2];
+        col = segs.col[s2];
+        seg_start = segs.n_end[s2 - 1];
+      }
+    }
+    n0 -= seg_start;
+  };
+  auto load_w = [&](int tile, uint4 (&wv)[kU][2], float (&wsv)[kU]) {
+    const uint8_t *w;
+    const float *ws;
+    int col, n0;
+    tile_base(tile, w, ws, col, n0);
+    const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+    const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kg = wave + WAVES * u;
+      wv[u][0] = load_stream16(wrow + kg * kGroup);
+      wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+      wsv[u] = wsrow[kg];
+    }
+  };
+
+  uint4 wcur[kU][2], wnxt[kU][2];
+  float scur[kU], snxt[kU];
+  int tile = blockIdx.x;
+  if (tile >= n_tiles) return;  // uniform
+  load_w(tile, wcur, scur);
+  for (;;) {
+    const int next = tile + (int)gridDim.x;
+    const bool more = next < n_tiles;  // uniform
+    if (more) load_w(next, wnxt, snxt);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      v4f d = {0.f, 0.f, 0.f, 0.f};
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][0].y << 32) | av[u][0].x),
+          (long)(((uint64_t)wcur[u][0].y << 32) | wcur[u][0].x), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][0].w << 32) | av[u][0].z),
+          (long)(((uint64_t)wcur[u][0].w << 32) | wcur[u][0].z), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][1].y << 32) | av[u][1].x),
+          (long)(((uint64_t)wcur[u][1].y << 32) | wcur[u][1].x), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av[u][1].w << 32) | av[u][1].z),
+          (long)(((uint64_t)wcur[u][1].w << 32) | wcur[u][1].z), d, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[u][i] * scur[u], acc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int i = threadIdx.x >> 6, l = threadIdx.x & 63;
+      float sum = 0.f;
+#pragma unroll
+      for (int wv2 = 0; wv2 < WAVES; ++wv2) sum += red[wv2][i][l];
+      const int m = 4 * (l >> 4) + i;
+      const uint8_t *w;
+      const float *ws;
+      int col, n0;
+      tile_base(tile, w, ws, col, n0);
+      if (m < M) out[(size_t)m * ldo + col + n0 + (l & 15)] = (uint16_t)f32_bf16(sum);
+    }
+    if (!more) break;
+    __syncthreads();  // red is rewritten by the next tile
+    tile = next;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      wcur[u][0] = wnxt[u][0];
+      wcur[u][1] = wnxt[u][1];
+      scur[u] = snxt[u];
+    }
+  }
+}
+
 // ------------------------------------------------- quantizing row kernels
 
 // residual += x (if x); y = residual * rsqrt(mean(residual^2) + eps) * w;
@@ -705,6 +828,16 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
   const auto *a = static_cast<const uint8_t *>(aq);
   auto *o = static_cast<uint16_t *>(out);
   if (M <= 16) {
+    const unsigned n_tiles = (unsigned)(n_total / 16);
+    int dev = 0, cus = 0;
+    // more tiles than two workgroups per CU at K = 4096: the persistent form
+    if (K == 4096 && hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n_tiles > 2u * (unsigned)cus) {
+      fp8_linear16p_kernel<16><<<(unsigned)cus, 1024, 0, as_stream(stream)>>>(
+          a, as, (int)M, s, o, (int)ldo, (int)n_tiles);
+      return launched();
+    }
     // long K: 16 waves, so each wave's share stays within two batches
     if (K / kGroup >= 64)
       fp8_linear16_kernel<16><<<(unsigned)(n_total / 16), 1024, 0, as_stream(stream)>>>(

@@ -127,6 +127,27 @@ def test_fp8_linear_matches_fp64(cuda_device, M, Kd):
     assert bool((out[:, sum(shapes):].cpu() == 7.0).all())  # columns past the segments untouched
 
 
+def test_fp8_linear_persistent_path_matches_fp64(cuda_device):
+    """More 16-column tiles than one workgroup per CU at K = 4096 (the
+    gate/up shape) takes the persistent kernel that keeps the activations
+    in registers and prefetches the next tile."""
+    from ecf8_amd.llm_kernels import LinearPlan
+
+    gen = torch.Generator().manual_seed(9)
+    M, Kd = 16, 4096
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    n = 16 * (cus + 40) // 128 * 128 + 128  # > cus tiles, a 128-multiple
+    aq = _rand_fp8((M, Kd), gen, cuda_device)
+    a_s = (torch.rand(M, Kd // 128, generator=gen) * 1e-2 + 1e-4).to(cuda_device)
+    w = _rand_fp8((n, Kd), gen, cuda_device)
+    ws = (torch.rand(n // 128, Kd // 128, generator=gen) * 1e-3 + 1e-5).to(cuda_device)
+    out = torch.empty(M, n, dtype=torch.bfloat16, device=cuda_device)
+    LinearPlan([(w, ws)], out)(aq, a_s, M)
+    ref = _linear_ref(aq, a_s, [(w, ws)])
+    got = out.double().cpu()
+    assert bool(((got - ref).abs() <= 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()).all())
+
+
 def test_fp8_linear_is_deterministic(cuda_device):
     from ecf8_amd.llm_kernels import LinearPlan
 
