@@ -107,6 +107,8 @@ def rmsnorm(residual, weight, eps, M, x=None, out_q=None, out_scale=None, out_bf
     if out_bf16 is not None:
         _need(out_bf16, torch.bfloat16, "out_bf16", dev)
     else:
+        if out_q is None or out_scale is None:
+            raise ECF8Error("rmsnorm needs out_bf16, or out_q and out_scale")
         _need(out_q, torch.float8_e4m3fn, "out_q", dev)
         _need(out_scale, torch.float32, "out_scale", dev)
     _rows(M, K, residual, x, out_q, out_bf16)
@@ -152,6 +154,8 @@ def qk_norm_rope(qkv, B, T, Hq, Hkv, q_norm, k_norm, eps, cos_t, sin_t, pos, q_o
     _need(cos_t, torch.float32, "cos", dev)
     _need(sin_t, torch.float32, "sin", dev)
     _need(pos, torch.int32, "pos", dev)
+    if pos.numel() < 1 or q_norm.numel() != 128 or k_norm.numel() != 128:
+        raise ECF8Error("pos must hold the position; q_norm / k_norm must be [128]")
     Lmax = k_cache.shape[2]
     if tuple(k_cache.shape) != (B, Hkv, Lmax, 128) or k_cache.shape != v_cache.shape:
         raise ECF8Error("caches must be [B, Hkv, Lmax, 128]")
@@ -181,6 +185,8 @@ def decode_attention(q, k_cache, v_cache, pos, work, out_q, out_scale, Hq, out_b
     for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _need(t, torch.bfloat16, n, dev)
     _need(pos, torch.int32, "pos", dev)
+    if pos.numel() < 1:
+        raise ECF8Error("pos must hold the position")
     _need(work, torch.float32, "work", dev)
     _need(out_q, torch.float8_e4m3fn, "out_q", dev)
     _need(out_scale, torch.float32, "out_scale", dev)

@@ -289,6 +289,36 @@ def test_decode_attention_matches_fp32(cuda_device, pos0):
     _assert_fp8_close(oq, os_, ref, rel=2 ** -4 + 5e-3)
 
 
+def test_wrappers_reject_bad_arguments_before_launch(cuda_device):
+    """Missing outputs, short norm weights and an empty position tensor are
+    refused on the host; nothing is launched."""
+    from ecf8_amd._lib import ECF8Error
+    from ecf8_amd.llm_kernels import attention_work, decode_attention, qk_norm_rope, rmsnorm
+
+    dev = cuda_device
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    res = torch.zeros(2, 4096, device=dev)
+    with pytest.raises(ECF8Error, match="out_bf16, or out_q"):
+        rmsnorm(res, torch.ones(4096, **bf), 1e-6, 2)
+    B, T, Hq, Hkv, Lmax = 1, 1, 8, 2, 16
+    qkv = torch.zeros(B * T, (Hq + 2 * Hkv) * 128, **bf)
+    cos = torch.ones(Lmax, 64, device=dev)
+    q_out = torch.zeros(B * Hq * T * 128, **bf)
+    kc = torch.zeros(B, Hkv, Lmax, 128, **bf)
+    vc = torch.zeros_like(kc)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    with pytest.raises(ECF8Error, match="q_norm"):
+        qk_norm_rope(qkv, B, T, Hq, Hkv, torch.ones(64, **bf), torch.ones(128, **bf), 1e-6, cos,
+                     cos, pos, q_out, kc, vc)
+    with pytest.raises(ECF8Error, match="pos"):
+        qk_norm_rope(qkv, B, T, Hq, Hkv, torch.ones(128, **bf), torch.ones(128, **bf), 1e-6, cos,
+                     cos, pos[:0], q_out, kc, vc)
+    work = attention_work(B, Hq, Lmax, dev)
+    oq = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+    with pytest.raises(ECF8Error, match="pos"):
+        decode_attention(q_out, kc, vc, pos[:0], work, oq, torch.empty(B, Hq, device=dev), Hq)
+
+
 # ------------------------------------------------------------ end to end
 
 
