@@ -449,15 +449,18 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
 // ------------------------------------------------- quantizing row kernels
 
 // residual += x (if x); y = residual * rsqrt(mean(residual^2) + eps) * w;
-// y -> e4m3fn + group scales, or -> bf16.  One 256-thread workgroup per
-// row of 4096 (16 values per thread).
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict__ x,
-                                                      float *__restrict__ res,
-                                                      const uint16_t *__restrict__ w, float eps,
-                                                      int K, uint8_t *__restrict__ oq,
-                                                      float *__restrict__ os,
-                                                      uint16_t *__restrict__ ob) {
-  __shared__ float part[4];
+// y -> e4m3fn + group scales, or -> bf16.  One workgroup per row of
+// K = 16 * kThreads (4096: 256 threads, 2048: 128), 16 values per thread.
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t *__restrict__ x,
+                                                           float *__restrict__ res,
+                                                           const uint16_t *__restrict__ w,
+                                                           float eps, int K,
+                                                           uint8_t *__restrict__ oq,
+                                                           float *__restrict__ os,
+                                                           uint16_t *__restrict__ ob) {
+  static_assert(kThreads == 128 || kThreads == 256, "rows of 2048 or 4096");
+  __shared__ float part[kThreads / 64];
   const int m = blockIdx.x, t = threadIdx.x;
   const size_t base = (size_t)m * K + 16 * t;
   float v[16];
@@ -484,7 +487,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
   ss = wave_sum(ss);
   if ((t & 63) == 0) part[t >> 6] = ss;
   __syncthreads();
-  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  float total;
+  if constexpr (kThreads == 256)
+    total = (part[0] + part[1]) + (part[2] + part[3]);
+  else
+    total = part[0] + part[1];
   const float rs = rsqrtf(total / (float)K + eps);
   float wv[16];
   load16_bf16(w + 16 * t, wv);
@@ -503,11 +510,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
 }
 
 // h = silu(gate) * up over [M, 2I] (gate columns [0, I), up [I, 2I)),
-// quantized; grid (I / 4096, M).
+// quantized; grid (ceil(I / 4096), M).  I is a multiple of 128, so the 8
+// threads of a group are all inside the row or all past it.
 __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t *__restrict__ gu, int I,
                                                              uint8_t *__restrict__ oq,
                                                              float *__restrict__ os) {
   const int m = blockIdx.y, e = blockIdx.x * 4096 + 16 * threadIdx.x;
+  if (e >= I) return;
   float g[16], u[16];
   load16_bf16(gu + (size_t)m * 2 * I + e, g);
   load16_bf16(gu + (size_t)m * 2 * I + I + e, u);
@@ -517,11 +526,13 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t *__r
           (threadIdx.x & 7) == 0);
 }
 
-// plain bf16 -> e4m3fn per 1x128 group; grid (K / 4096, M)
+// plain bf16 -> e4m3fn per 1x128 group; grid (ceil(K / 4096), M), K a
+// multiple of 128
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restrict__ x, int K,
                                                         uint8_t *__restrict__ oq,
                                                         float *__restrict__ os) {
   const int m = blockIdx.y, e = blockIdx.x * 4096 + 16 * threadIdx.x;
+  if (e >= K) return;
   float v[16];
   load16_bf16(x + (size_t)m * K + e, v);
   quant16(v, oq + (size_t)m * K + e, os + (size_t)m * (K / kGroup) + (e >> 7),
@@ -795,6 +806,303 @@ __global__ __launch_bounds__(256) void dequant_fp8_block_kernel(const uint8_t *_
   op[1] = make_uint4(o[4], o[5], o[6], o[7]);
 }
 
+// ------------------------------------------------------------ MoE routing
+
+// Router of one token per workgroup (256 threads = 4 waves): logit[e] =
+// x[m] . wr[e] over H (bf16 inputs, fp32 products accumulated per lane in
+// order, then summed across the wave in a fixed tree); softmax over the E
+// experts in fp32; the top_k largest probabilities (ties to the lower
+// expert index), renormalized to sum 1.  E <= 256, H a multiple of 512 and
+// at most 8192, top_k <= 16.
+__global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *__restrict__ x,
+                                                        const uint16_t *__restrict__ wr, int H,
+                                                        int E, int top_k,
+                                                        int *__restrict__ topk_idx,
+                                                        float *__restrict__ topk_w) {
+  constexpr int kMaxChunks = 16;  // H <= 16 * 512
+  __shared__ float logit[256];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int chunks = H / 512;
+  // lane l holds x[512 j + 8 l, +8) for every chunk j
+  float xv[kMaxChunks][8];
+#pragma unroll
+  for (int j = 0; j < kMaxChunks; ++j) {
+    if (j < chunks) {
+      float v[16];
+      const uint4 a = *reinterpret_cast<const uint4 *>(x + (size_t)m * H + 512 * j + 8 * lane);
+      const uint32_t wd[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_f32(wd[i] & 0xffffu);
+        v[2 * i + 1] = bf16_f32(wd[i] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[j][i] = v[i];
+    }
+  }
+  for (int e = wave; e < E; e += 4) {
+    const uint16_t *we = wr + (size_t)e * H + 8 * lane;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxChunks; ++j) {
+      if (j < chunks) {
+        const uint4 b = *reinterpret_cast<const uint4 *>(we + 512 * j);
+        const uint32_t wd[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = fmaf(xv[j][2 * i], bf16_f32(wd[i] & 0xffffu), acc);
+          acc = fmaf(xv[j][2 * i + 1], bf16_f32(wd[i] >> 16), acc);
+        }
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logit[e] = acc;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // lane l holds experts l, l + 64, l + 128, l + 192
+  float p[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = e < E ? logit[e] : -INFINITY;
+    mx = fmaxf(mx, p[i]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = e < E ? expf(p[i] - mx) : 0.f;
+    sum += p[i];
+  }
+  sum = wave_sum(sum);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = lane + 64 * i < E ? p[i] / sum : -1.f;  // -1: not a choice
+  float my_w = 0.f, sel_sum = 0.f;
+  int my_i = 0;
+  for (int k = 0; k < top_k; ++k) {
+    float bv = -2.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (p[i] > bv) {
+        bv = p[i];
+        bi = lane + 64 * i;
+      }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    // every lane now holds the same (bv, bi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i == bi) p[i] = -1.f;
+    sel_sum += bv;
+    if (lane == k) {
+      my_w = bv;
+      my_i = bi;
+    }
+  }
+  if (lane < top_k) {
+    topk_idx[(size_t)m * top_k + lane] = my_i;
+    topk_w[(size_t)m * top_k + lane] = my_w / sel_sum;
+  }
+}
+
+// Group the P = M * top_k (token, expert) pairs by expert (one workgroup,
+// P <= 256, E <= 256): pairs of expert e take sorted positions
+// [offsets[e], offsets[e + 1]) in token order; pair_tok / pair_w give each
+// sorted position's token and routing weight, pair_pos each pair's sorted
+// position; active[0, n_active) lists the experts with pairs in increasing
+// order; select[e] (optional) = 1 if expert e has pairs.  Expert ids
+// outside [0, E) are clamped into it.
+__global__ __launch_bounds__(256) void moe_group_kernel(
+    const int *__restrict__ topk_idx, const float *__restrict__ topk_w, int P, int top_k, int E,
+    int *__restrict__ offsets, int *__restrict__ active, int *__restrict__ n_active,
+    int *__restrict__ pair_tok, float *__restrict__ pair_w, int *__restrict__ pair_pos,
+    int *__restrict__ select) {
+  __shared__ int s_e[256];
+  __shared__ int s_cnt[256];
+  __shared__ int s_off[257];
+  const int t = threadIdx.x;
+  int e = -1;
+  if (t < P) e = min(max(topk_idx[t], 0), E - 1);
+  s_e[t] = e;
+  __syncthreads();
+  if (t < E) {
+    int c = 0;
+    for (int q = 0; q < P; ++q) c += s_e[q] == t;
+    s_cnt[t] = c;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int off = 0, na = 0;
+    for (int i = 0; i < E; ++i) {
+      s_off[i] = off;
+      off += s_cnt[i];
+      if (s_cnt[i]) active[na++] = i;
+    }
+    s_off[E] = off;
+    *n_active = na;
+  }
+  __syncthreads();
+  for (int i = t; i <= E; i += 256) offsets[i] = s_off[i];
+  if (select && t < E) select[t] = s_cnt[t] > 0 ? 1 : 0;
+  if (t < P) {
+    int rank = 0;
+    for (int q = 0; q < t; ++q) rank += s_e[q] == e;
+    const int q = s_off[e] + rank;
+    pair_tok[q] = t / top_k;
+    pair_w[q] = topk_w[t];
+    pair_pos[t] = q;
+  }
+}
+
+// Grouped small-M FP8 linear over the active experts: workgroup (tile,
+// slot) computes output columns [16 tile, +16) of expert e = active[slot]
+// for its rows [offsets[e], offsets[e + 1]) in chunks of 16:
+//   out[q, col] = sum_g (sum_{k in g} aq[row(q), k] * w_e[n, k]) * as[row(q), g] * ws_e[n/128, g]
+// with row(q) = row_of[q] (a gather, e.g. the token of a sorted pair) or q.
+// Segment s of an expert (e.g. gate, up) owns output columns
+// [s * seg_n, +seg_n).  Slots past n_active exit at once, so the grid can
+// be sized for every expert and captured in a graph.
+struct MoeLinear {
+  const uint8_t *aq;
+  const float *as;
+  const int *row_of;
+  const int *offsets;
+  const int *active;
+  const int *n_active;
+  const uint64_t *w;   // [E * n_segs] weight addresses
+  const uint64_t *ws;  // [E * n_segs] scale addresses
+  uint16_t *out;
+  int n_segs, seg_n, K, ldo;
+};
+
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
+  __shared__ float red[WAVES][4][64];
+  const int slot = blockIdx.y;
+  if (slot >= a.n_active[0]) return;  // uniform
+  const int e = a.active[slot];
+  const int r0 = a.offsets[e], rows = a.offsets[e + 1] - r0;
+  const int seg = (int)(blockIdx.x * 16) / a.seg_n;
+  const int n0 = (int)(blockIdx.x * 16) - seg * a.seg_n;
+  const uint8_t *w = reinterpret_cast<const uint8_t *>(a.w[(size_t)e * a.n_segs + seg]);
+  const float *ws = reinterpret_cast<const float *>(a.ws[(size_t)e * a.n_segs + seg]);
+  const int col = seg * a.seg_n;
+  const int K = a.K, kgroups = K / kGroup;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+  const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
+
+  for (int rc = 0; rc < rows; rc += 16) {
+    const int mrows = min(16, rows - rc);
+    const bool row_ok = r < mrows;
+    const int q = r0 + rc + (row_ok ? r : 0);
+    const uint8_t *arow = a.aq + (size_t)(a.row_of ? a.row_of[q] : q) * K + 16 * g;
+    bool srow_ok[4];
+    const float *srow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      srow_ok[i] = 4 * g + i < mrows;
+      const int qi = r0 + rc + (srow_ok[i] ? 4 * g + i : 0);
+      srow[i] = a.as + (size_t)(a.row_of ? a.row_of[qi] : qi) * kgroups;
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    constexpr int kU = 4;
+    for (int kb = wave; kb < kgroups; kb += WAVES * kU) {
+      uint4 wv[kU][2], av[kU][2];
+      float wsv[kU], sav[kU][4];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int kg = kb + WAVES * u;
+        if (kg < kgroups) {
+          wv[u][0] = load_stream16(wrow + kg * kGroup);
+          wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+          wsv[u] = wsrow[kg];
+          av[u][0] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
+          av[u][1] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sav[u][i] = srow[i][kg];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int kg = kb + WAVES * u;
+        if (kg >= kgroups) break;
+        if (!row_ok) av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sav[u][i] = srow_ok[i] ? sav[u][i] : 0.f;
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av[u][0].y << 32) | av[u][0].x),
+            (long)(((uint64_t)wv[u][0].y << 32) | wv[u][0].x), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av[u][0].w << 32) | av[u][0].z),
+            (long)(((uint64_t)wv[u][0].w << 32) | wv[u][0].z), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av[u][1].y << 32) | av[u][1].x),
+            (long)(((uint64_t)wv[u][1].y << 32) | wv[u][1].x), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av[u][1].w << 32) | av[u][1].z),
+            (long)(((uint64_t)wv[u][1].w << 32) | wv[u][1].z), d, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[u][i] * wsv[u], acc[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int i = threadIdx.x >> 6, l = threadIdx.x & 63;
+      float sum = 0.f;
+#pragma unroll
+      for (int wv2 = 0; wv2 < WAVES; ++wv2) sum += red[wv2][i][l];
+      const int m = 4 * (l >> 4) + i;
+      if (m < mrows)
+        a.out[(size_t)(r0 + rc + m) * a.ldo + col + n0 + (l & 15)] = (uint16_t)f32_bf16(sum);
+    }
+    __syncthreads();  // red is rewritten by the next chunk
+  }
+}
+
+// y[m, :] = sum_k pair_w[q] * down[q, :] over q = pair_pos[m * top_k + k],
+// k = 0 .. top_k - 1 in order, accumulated in fp32; bf16 out [M, H].  One
+// workgroup per token, 8 columns per thread.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ down,
+                                                          int ldd, const int *__restrict__ pair_pos,
+                                                          const float *__restrict__ pair_w,
+                                                          int top_k, int H,
+                                                          uint16_t *__restrict__ out) {
+  const int m = blockIdx.x;
+  for (int c = 8 * threadIdx.x; c < H; c += 8 * 256) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < top_k; ++k) {
+      const int q = pair_pos[(size_t)m * top_k + k];
+      const float wq = pair_w[q];
+      const uint4 v = *reinterpret_cast<const uint4 *>(down + (size_t)q * ldd + c);
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = fmaf(wq, bf16_f32(wd[i] & 0xffffu), acc[2 * i]);
+        acc[2 * i + 1] = fmaf(wq, bf16_f32(wd[i] >> 16), acc[2 * i + 1]);
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f32_bf16(acc[2 * i]) | (f32_bf16(acc[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4 *>(out + (size_t)m * H + c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 inline int launched() { return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP; }
@@ -856,22 +1164,30 @@ extern "C" int ecf8_rmsnorm(const void *x, float *residual, const void *weight, 
                             int64_t K, void *out_q, float *out_scale, void *out_bf16, void *stream) {
   if (!residual || !weight || M <= 0 || (!out_bf16 && (!out_q || !out_scale)))
     return ECF8_ERR_INVALID_ARG;
-  if (K != 4096) return ECF8_ERR_UNSUPPORTED;
+  if ((K != 4096 && K != 2048) || M > 0x7fffffff) return ECF8_ERR_UNSUPPORTED;
   if (!aligned(residual, 16) || (x && !aligned(x, 16)) || !aligned(weight, 16) ||
       (out_q && !aligned(out_q, 16)) || (out_bf16 && !aligned(out_bf16, 16)))
     return ECF8_ERR_MISALIGNED;
-  rmsnorm_kernel<<<(unsigned)M, 256, 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(x), residual, static_cast<const uint16_t *>(weight), eps, (int)K,
-      static_cast<uint8_t *>(out_q), out_scale, static_cast<uint16_t *>(out_bf16));
+  const auto *xp = static_cast<const uint16_t *>(x);
+  const auto *wp = static_cast<const uint16_t *>(weight);
+  auto *qp = static_cast<uint8_t *>(out_q);
+  auto *bp = static_cast<uint16_t *>(out_bf16);
+  if (K == 4096)
+    rmsnorm_kernel<256><<<(unsigned)M, 256, 0, as_stream(stream)>>>(xp, residual, wp, eps, (int)K,
+                                                                    qp, out_scale, bp);
+  else
+    rmsnorm_kernel<128><<<(unsigned)M, 128, 0, as_stream(stream)>>>(xp, residual, wp, eps, (int)K,
+                                                                    qp, out_scale, bp);
   return launched();
 }
 
 extern "C" int ecf8_silu_mul_quant(const void *gate_up, int64_t M, int64_t I, void *out_q,
                                    float *out_scale, void *stream) {
   if (!gate_up || !out_q || !out_scale || M <= 0 || I <= 0) return ECF8_ERR_INVALID_ARG;
-  if (I % 4096 || M > 65535) return ECF8_ERR_UNSUPPORTED;
+  if (I % kGroup || I > (1 << 24) || M > 65535) return ECF8_ERR_UNSUPPORTED;
   if (!aligned(gate_up, 16) || !aligned(out_q, 16)) return ECF8_ERR_MISALIGNED;
-  silu_mul_quant_kernel<<<dim3((unsigned)(I / 4096), (unsigned)M), 256, 0, as_stream(stream)>>>(
+  silu_mul_quant_kernel<<<dim3((unsigned)((I + 4095) / 4096), (unsigned)M), 256, 0,
+                          as_stream(stream)>>>(
       static_cast<const uint16_t *>(gate_up), (int)I, static_cast<uint8_t *>(out_q), out_scale);
   return launched();
 }
@@ -879,9 +1195,10 @@ extern "C" int ecf8_silu_mul_quant(const void *gate_up, int64_t M, int64_t I, vo
 extern "C" int ecf8_act_quant(const void *x, int64_t M, int64_t K, void *out_q, float *out_scale,
                               void *stream) {
   if (!x || !out_q || !out_scale || M <= 0 || K <= 0) return ECF8_ERR_INVALID_ARG;
-  if (K % 4096 || M > 65535) return ECF8_ERR_UNSUPPORTED;
+  if (K % kGroup || K > (1 << 24) || M > 65535) return ECF8_ERR_UNSUPPORTED;
   if (!aligned(x, 16) || !aligned(out_q, 16)) return ECF8_ERR_MISALIGNED;
-  act_quant_kernel<<<dim3((unsigned)(K / 4096), (unsigned)M), 256, 0, as_stream(stream)>>>(
+  act_quant_kernel<<<dim3((unsigned)((K + 4095) / 4096), (unsigned)M), 256, 0,
+                     as_stream(stream)>>>(
       static_cast<const uint16_t *>(x), (int)K, static_cast<uint8_t *>(out_q), out_scale);
   return launched();
 }
@@ -931,18 +1248,93 @@ extern "C" int ecf8_decode_attention(const void *q, const void *k_cache, const v
   if (!q || !k_cache || !v_cache || !pos || !work || !out_q || !out_scale || B <= 0 || Hq <= 0 ||
       Hkv <= 0 || Lmax <= 0)
     return ECF8_ERR_INVALID_ARG;
-  if (Hq != 4 * Hkv || B * Hkv > 65535 || Lmax > (1 << 24)) return ECF8_ERR_UNSUPPORTED;
+  if ((Hq != 4 * Hkv && Hq != 8 * Hkv) || B * Hkv > 65535 || Lmax > (1 << 24))
+    return ECF8_ERR_UNSUPPORTED;
   const int64_t S = (Lmax + kAttnChunk - 1) / kAttnChunk;
   if (work_floats < B * Hq * S * (kHeadDim + 2)) return ECF8_ERR_CAPACITY;
   if (!aligned(q, 4) || !aligned(k_cache, 16) || !aligned(v_cache, 4) || !aligned(work, 8) ||
       !aligned(out_q, 2) || (out_bf16 && !aligned(out_bf16, 4)))
     return ECF8_ERR_MISALIGNED;
   float *wm = work, *wl = work + B * Hq * S, *wacc = work + 2 * B * Hq * S;
-  attn_split_kernel<4><<<dim3((unsigned)(B * Hkv), (unsigned)S), 256, 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k_cache),
-      static_cast<const uint16_t *>(v_cache), pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc);
+  const dim3 grid((unsigned)(B * Hkv), (unsigned)S);
+  const auto *qp = static_cast<const uint16_t *>(q);
+  const auto *kp = static_cast<const uint16_t *>(k_cache);
+  const auto *vp = static_cast<const uint16_t *>(v_cache);
+  if (Hq == 4 * Hkv)
+    attn_split_kernel<4><<<grid, 256, 0, as_stream(stream)>>>(qp, kp, vp, pos, Hkv, (int)Lmax,
+                                                              (int)S, wm, wl, wacc);
+  else
+    attn_split_kernel<8><<<grid, 256, 0, as_stream(stream)>>>(qp, kp, vp, pos, Hkv, (int)Lmax,
+                                                              (int)S, wm, wl, wacc);
   attn_combine_kernel<<<(unsigned)(B * Hq), 64, 0, as_stream(stream)>>>(
       wm, wl, wacc, pos, (int)Lmax, (int)S, static_cast<uint8_t *>(out_q), out_scale,
       static_cast<uint16_t *>(out_bf16));
+  return launched();
+}
+
+extern "C" int ecf8_moe_route(const void *x, const void *router_w, int64_t M, int64_t H, int E,
+                              int top_k, int *topk_idx, float *topk_w, void *stream) {
+  if (!x || !router_w || !topk_idx || !topk_w || M <= 0 || H <= 0 || E <= 0 || top_k <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (H % 512 || H > 8192 || E > 256 || top_k > 16 || top_k > E || M > 0x7fffffff)
+    return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(x, 16) || !aligned(router_w, 16) || !aligned(topk_idx, 4) || !aligned(topk_w, 4))
+    return ECF8_ERR_MISALIGNED;
+  moe_route_kernel<<<(unsigned)M, 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(router_w), (int)H, E, top_k,
+      topk_idx, topk_w);
+  return launched();
+}
+
+extern "C" int ecf8_moe_group(const int *topk_idx, const float *topk_w, int64_t M, int top_k, int E,
+                              int *offsets, int *active, int *n_active, int *pair_tok,
+                              float *pair_w, int *pair_pos, int *select, void *stream) {
+  if (!topk_idx || !topk_w || !offsets || !active || !n_active || !pair_tok || !pair_w ||
+      !pair_pos || M <= 0 || top_k <= 0 || E <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (M * top_k > 256 || E > 256) return ECF8_ERR_UNSUPPORTED;
+  moe_group_kernel<<<1, 256, 0, as_stream(stream)>>>(topk_idx, topk_w, (int)(M * top_k), top_k, E,
+                                                     offsets, active, n_active, pair_tok, pair_w,
+                                                     pair_pos, select);
+  return launched();
+}
+
+extern "C" int ecf8_moe_linear(const void *aq, const float *as, const int *row_of,
+                               const int *offsets, const int *active, const int *n_active,
+                               int n_experts, const void *const *weights,
+                               const float *const *weight_scales, int n_segs, int64_t seg_n,
+                               int64_t K, void *out, int64_t ldo, void *stream) {
+  if (!aq || !as || !offsets || !active || !n_active || !weights || !weight_scales || !out ||
+      n_experts <= 0 || n_segs < 1 || n_segs > ECF8_LINEAR_MAX_SEGS || seg_n <= 0 || K <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (seg_n % kGroup || K % kGroup || K > (1 << 20) || n_segs * seg_n > (1 << 20) ||
+      n_experts > 65535)
+    return ECF8_ERR_UNSUPPORTED;
+  if (ldo < n_segs * seg_n) return ECF8_ERR_CAPACITY;
+  if (!aligned(aq, 16) || !aligned(as, 4) || !aligned(out, 4) || !aligned(weights, 8) ||
+      !aligned(weight_scales, 8))
+    return ECF8_ERR_MISALIGNED;
+  MoeLinear a{static_cast<const uint8_t *>(aq), as, row_of, offsets, active, n_active,
+              reinterpret_cast<const uint64_t *>(weights),
+              reinterpret_cast<const uint64_t *>(weight_scales), static_cast<uint16_t *>(out),
+              n_segs, (int)seg_n, (int)K, (int)ldo};
+  const dim3 grid((unsigned)(n_segs * seg_n / 16), (unsigned)n_experts);
+  if (K / kGroup >= 16)
+    moe_linear16_kernel<8><<<grid, 512, 0, as_stream(stream)>>>(a);
+  else
+    moe_linear16_kernel<4><<<grid, 256, 0, as_stream(stream)>>>(a);
+  return launched();
+}
+
+extern "C" int ecf8_moe_combine(const void *down, int64_t ldd, const int *pair_pos,
+                                const float *pair_w, int64_t M, int top_k, int64_t H, void *out,
+                                void *stream) {
+  if (!down || !pair_pos || !pair_w || !out || M <= 0 || top_k <= 0 || H <= 0 || ldd < H)
+    return ECF8_ERR_INVALID_ARG;
+  if (H % 8 || ldd % 8 || M > 0x7fffffff) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(down, 16) || !aligned(out, 16)) return ECF8_ERR_MISALIGNED;
+  moe_combine_kernel<<<(unsigned)M, 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t *>(down), (int)ldd, pair_pos, pair_w, top_k, (int)H,
+      static_cast<uint16_t *>(out));
   return launched();
 }

@@ -219,3 +219,117 @@ def dequant_fp8_block(weight, scale_inv, out=None):
     check(lib().ecf8_dequant_fp8_block(weight.data_ptr(), scale_inv.data_ptr(), n, k,
                                        out.data_ptr(), _stream(weight)), "ecf8_dequant_fp8_block")
     return out.view(-1)[: n * k].view(n, k)
+
+
+# ------------------------------------------------------------------ MoE
+
+
+class MoeRouting:
+    """Device buffers of one routing step for up to ``M`` tokens
+    (``M * top_k <= 256``): the router's choices, the pairs grouped by
+    expert, and the per-expert flags the routed decode takes."""
+
+    def __init__(self, M: int, top_k: int, n_experts: int, device):
+        if M * top_k > 256 or n_experts > 256:
+            raise ECF8Error("routing holds at most 256 (token, expert) pairs and 256 experts")
+        P = M * top_k
+        i32 = dict(dtype=torch.int32, device=device)
+        self.M, self.top_k, self.E = M, top_k, n_experts
+        self.topk_idx = torch.zeros(M, top_k, **i32)
+        self.topk_w = torch.zeros(M, top_k, dtype=torch.float32, device=device)
+        self.offsets = torch.zeros(n_experts + 1, **i32)
+        self.active = torch.zeros(n_experts, **i32)
+        self.n_active = torch.zeros(1, **i32)
+        self.pair_tok = torch.zeros(P, **i32)
+        self.pair_w = torch.zeros(P, dtype=torch.float32, device=device)
+        self.pair_pos = torch.zeros(P, **i32)
+        self.select = torch.zeros(n_experts, **i32)
+
+
+def moe_route(x, router_w, M: int, r: MoeRouting):
+    """Router of M tokens: x bf16 [>= M, H], router_w bf16 [E, H]."""
+    dev = x.device
+    _need(x, torch.bfloat16, "x", dev)
+    _need(router_w, torch.bfloat16, "router_w", dev)
+    H = x.shape[-1]
+    _rows(M, H, x)
+    if tuple(router_w.shape) != (r.E, H) or not 1 <= M <= r.M:
+        raise ECF8Error(f"router_w must be [{r.E}, {H}] and 1 <= M <= {r.M}")
+    check(lib().ecf8_moe_route(x.data_ptr(), router_w.data_ptr(), M, H, r.E, r.top_k,
+                               r.topk_idx.data_ptr(), r.topk_w.data_ptr(), _stream(x)),
+          "ecf8_moe_route")
+
+
+def moe_group(r: MoeRouting, M: int):
+    """Group the routed pairs of the first M tokens by expert."""
+    if not 1 <= M <= r.M:
+        raise ECF8Error(f"1 <= M <= {r.M}")
+    check(lib().ecf8_moe_group(r.topk_idx.data_ptr(), r.topk_w.data_ptr(), M, r.top_k, r.E,
+                               r.offsets.data_ptr(), r.active.data_ptr(), r.n_active.data_ptr(),
+                               r.pair_tok.data_ptr(), r.pair_w.data_ptr(), r.pair_pos.data_ptr(),
+                               r.select.data_ptr(), _stream(r.topk_idx)), "ecf8_moe_group")
+
+
+class MoeLinearPlan:
+    """Device address tables of one grouped expert linear: ``experts`` is a
+    list (one per expert) of 1..3 segments (weight e4m3fn [seg_n, K],
+    weight_scale_inv f32 [seg_n/128, K/128]), e.g. (gate, up) or (down,).
+    Segment s of every expert writes output columns [s*seg_n, +seg_n)."""
+
+    def __init__(self, experts, out: torch.Tensor):
+        dev = out.device
+        _need(out, torch.bfloat16, "out", dev)
+        n_segs = len(experts[0])
+        if not 1 <= n_segs <= MAX_SEGS or any(len(e) != n_segs for e in experts):
+            raise ECF8Error(f"every expert needs the same 1..{MAX_SEGS} segments")
+        seg_n, K = experts[0][0][0].shape
+        ws, ss = [], []
+        for segs in experts:
+            for w, s in segs:
+                _need(w, torch.float8_e4m3fn, "weight", dev)
+                _need(s, torch.float32, "weight_scale_inv", dev)
+                if tuple(w.shape) != (seg_n, K) or tuple(s.shape) != (seg_n // GROUP, K // GROUP):
+                    raise ECF8Error(f"expert weight {tuple(w.shape)} / scale {tuple(s.shape)} "
+                                    f"do not match [{seg_n}, {K}]")
+                ws.append(w.data_ptr())
+                ss.append(s.data_ptr())
+        if seg_n % GROUP or K % GROUP or out.shape[-1] < n_segs * seg_n:
+            raise ECF8Error("seg_n and K must be multiples of 128 and fit out")
+        self.w_table = torch.tensor(ws, dtype=torch.int64).to(dev)
+        self.s_table = torch.tensor(ss, dtype=torch.int64).to(dev)
+        self.E, self.n_segs, self.seg_n, self.K, self.out = len(experts), n_segs, seg_n, K, out
+        self._keep = [t for segs in experts for pair in segs for t in pair]
+
+    def __call__(self, aq, a_scale, r: MoeRouting, gather: bool):
+        """``gather``: activation rows are tokens (aq [>= M, K], row of a
+        sorted pair = its token); otherwise aq has one row per sorted pair."""
+        dev = self.out.device
+        _need(aq, torch.float8_e4m3fn, "aq", dev)
+        _need(a_scale, torch.float32, "a_scale", dev)
+        P = r.M * r.top_k
+        rows = r.M if gather else P
+        if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < rows
+                or tuple(a_scale.shape[1:]) != (self.K // GROUP,) or a_scale.shape[0] < rows
+                or self.out.shape[0] < P or r.E != self.E):
+            raise ECF8Error("activation / output shape does not match the grouped linear")
+        check(lib().ecf8_moe_linear(aq.data_ptr(), a_scale.data_ptr(),
+                                    r.pair_tok.data_ptr() if gather else None,
+                                    r.offsets.data_ptr(), r.active.data_ptr(), r.n_active.data_ptr(),
+                                    self.E, self.w_table.data_ptr(), self.s_table.data_ptr(),
+                                    self.n_segs, self.seg_n, self.K, self.out.data_ptr(),
+                                    self.out.shape[-1], _stream(aq)), "ecf8_moe_linear")
+        return self.out
+
+
+def moe_combine(down, r: MoeRouting, M: int, out):
+    """out[m] = sum_k w * down[pair of (m, k)] (bf16 [>= M, H])."""
+    dev = down.device
+    _need(down, torch.bfloat16, "down", dev)
+    _need(out, torch.bfloat16, "out", dev)
+    H = out.shape[-1]
+    if (down.dim() != 2 or down.shape[0] < M * r.top_k or down.shape[1] < H or out.shape[0] < M
+            or not 1 <= M <= r.M):
+        raise ECF8Error("down / out shape does not match the routing")
+    check(lib().ecf8_moe_combine(down.data_ptr(), down.shape[1], r.pair_pos.data_ptr(),
+                                 r.pair_w.data_ptr(), M, r.top_k, H, out.data_ptr(), _stream(down)),
+          "ecf8_moe_combine")

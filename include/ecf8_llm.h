@@ -49,7 +49,7 @@ int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64_t K,
                     void *stream);
 
 /*
- * Residual add + RMSNorm over rows of K = 4096:
+ * Residual add + RMSNorm over rows of K = 4096 or 2048:
  *   residual[m] += x[m]  (x bf16 [M, K], or NULL for no add; residual fp32)
  *   y = residual[m] * rsqrt(mean(residual[m]^2) + eps) * weight  (bf16 weight)
  * y goes to out_bf16 (bf16 [M, K]) when that is non-NULL, otherwise it is
@@ -60,13 +60,13 @@ int ecf8_rmsnorm(const void *x, float *residual, const void *weight, float eps, 
 
 /* h = silu(gate) * up for gate_up bf16 [M, 2I] (gate in columns [0, I)),
  * quantized to out_q e4m3fn [M, I] + out_scale fp32 [M, I/128].
- * I must be a multiple of 4096. */
+ * I must be a multiple of 128. */
 int ecf8_silu_mul_quant(const void *gate_up, int64_t M, int64_t I, void *out_q,
                         float *out_scale, void *stream);
 
 /* bf16 [M, K] -> e4m3fn + fp32 scale per 1x128 group (scale = amax/448,
  * 1 for an all-zero group; q = round_nearest_even(x / scale)).
- * K must be a multiple of 4096. */
+ * K must be a multiple of 128. */
 int ecf8_act_quant(const void *x, int64_t M, int64_t K, void *out_q, float *out_scale,
                    void *stream);
 
@@ -99,7 +99,7 @@ int64_t ecf8_attention_work_floats(int64_t B, int Hq, int64_t Lmax);
  * Attention of one new token per sequence (q bf16 [B, Hq, 128], scaled by
  * 1/sqrt(128)) over cached positions [0, pos[0]] (pos: device int32, the
  * new token's position, already written to the caches), grouped-query with
- * Hq = 4 * Hkv.  The result per (b, head) is quantized as one 128-group:
+ * Hq = 4 * Hkv or 8 * Hkv.  The result per (b, head) is quantized as one 128-group:
  * out_q e4m3fn [B, Hq*128], out_scale fp32 [B, Hq]; out_bf16 (optional,
  * bf16 [B, Hq*128]) receives the unquantized result.
  */
@@ -107,6 +107,55 @@ int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cach
                           int64_t B, int Hq, int Hkv, int64_t Lmax, float *work,
                           int64_t work_floats, void *out_q, float *out_scale, void *out_bf16,
                           void *stream);
+
+/* ---------------------------------------------------------------- MoE
+ * The routed-expert MLP of a Qwen3-MoE-shaped layer
+ * (transformers' Qwen3MoeSparseMoeBlock: softmax router, top-k experts,
+ * weights renormalized to sum 1), whose experts are the compressed blocks
+ * model.layers.N.mlp.experts.E of the reference's qwen3moe patterns
+ * (dfloat/const.py:15-21).  No entry point replaces a reference interface:
+ * the reference runs transformers' own MoE forward over hooked experts.
+ */
+
+/* Router: logits = x [M, H] (bf16) . router_w [E, H]^T (bf16) in fp32,
+ * softmax over E, the top_k largest probabilities (ties to the lower
+ * expert), renormalized to sum 1: topk_idx int32 [M, top_k] (descending
+ * probability), topk_w fp32 [M, top_k].  H a multiple of 512, <= 8192;
+ * E <= 256; top_k <= 16. */
+int ecf8_moe_route(const void *x, const void *router_w, int64_t M, int64_t H, int E, int top_k,
+                   int *topk_idx, float *topk_w, void *stream);
+
+/* Group the P = M * top_k (token, expert) pairs by expert (P <= 256,
+ * E <= 256): expert e's pairs take sorted positions [offsets[e],
+ * offsets[e + 1]) in token order (offsets int32 [E + 1]); pair_tok int32
+ * [P] / pair_w fp32 [P]: token and weight of each sorted position;
+ * pair_pos int32 [P]: sorted position of pair (m, k) at m * top_k + k;
+ * active int32 [E]: the experts with pairs, increasing, n_active int32 [1]
+ * of them; select (optional) int32 [E]: 1 where an expert has pairs, the
+ * flags ecf8_decode_batched_select takes. */
+int ecf8_moe_group(const int *topk_idx, const float *topk_w, int64_t M, int top_k, int E,
+                   int *offsets, int *active, int *n_active, int *pair_tok, float *pair_w,
+                   int *pair_pos, int *select, void *stream);
+
+/* Grouped FP8 linear over the active experts (offsets / active / n_active
+ * from ecf8_moe_group, all device memory):
+ *   out[q, s * seg_n + j] = linear(aq[row(q)], weights[e * n_segs + s])[j]
+ * for every sorted position q of expert e, with the block-scaled math of
+ * ecf8_fp8_linear; row(q) = row_of[q] (e.g. pair_tok: gather the token's
+ * activation row) or q when row_of is NULL.  weights / weight_scales are
+ * device arrays of n_experts * n_segs addresses (e4m3fn [seg_n, K] and
+ * fp32 [seg_n/128, K/128]); active entries must be < n_experts.  The grid
+ * covers every expert and idle slots exit, so the launch can be captured
+ * in a graph. */
+int ecf8_moe_linear(const void *aq, const float *as, const int *row_of, const int *offsets,
+                    const int *active, const int *n_active, int n_experts,
+                    const void *const *weights, const float *const *weight_scales, int n_segs,
+                    int64_t seg_n, int64_t K, void *out, int64_t ldo, void *stream);
+
+/* out bf16 [M, H] = sum_k pair_w[q] * down[q, :] (down bf16, row stride
+ * ldd) over q = pair_pos[m * top_k + k], k in order, accumulated in fp32. */
+int ecf8_moe_combine(const void *down, int64_t ldd, const int *pair_pos, const float *pair_w,
+                     int64_t M, int top_k, int64_t H, void *out, void *stream);
 
 #ifdef __cplusplus
 }

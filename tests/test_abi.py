@@ -151,7 +151,7 @@ def test_consumer_kernels_reject_before_launch():
     assert L.ecf8_fp8_linear(fake, fake, 16, 4096, bad_n, 1, fake, 128, None) == 2
     assert L.ecf8_rmsnorm(None, None, fake, ctypes.c_float(1e-6), 4, 4096, fake, fake, None, None) == 1
     assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 4096, None, fake, None, None) == 1
-    assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 2048, fake, fake, None, None) == 2
+    assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 3072, fake, fake, None, None) == 2
     assert L.ecf8_silu_mul_quant(fake, 4, 1000, fake, fake, None) == 2
     assert L.ecf8_act_quant(fake, 4, 4096, None, fake, None) == 1
     assert L.ecf8_qk_norm_rope(fake, 1, 1, 32, 8, fake, fake, ctypes.c_float(1e-6), fake, fake,
@@ -177,3 +177,31 @@ def test_batched_select_rejects_before_launch():
     assert f(fake + 4, 3, fake, fake, fake, 4, 0, 512, None) == 3  # descs misaligned
     assert f(fake, 3, fake + 2, fake, fake, 4, 0, 512, None) == 3  # flags misaligned
     assert f(fake, 3, fake, fake, fake, 4, 0, 300, None) == 2
+
+
+def test_moe_kernels_reject_before_launch():
+    from ecf8_amd._lib import lib
+
+    L = lib()
+    fake = 1 << 20
+    assert L.ecf8_moe_route(None, fake, 16, 2048, 128, 8, fake, fake, None) == 1
+    assert L.ecf8_moe_route(fake, fake, 16, 1000, 128, 8, fake, fake, None) == 2   # H % 512
+    assert L.ecf8_moe_route(fake, fake, 16, 2048, 300, 8, fake, fake, None) == 2   # E > 256
+    assert L.ecf8_moe_route(fake, fake, 16, 2048, 128, 20, fake, fake, None) == 2  # top_k > 16
+    assert L.ecf8_moe_route(fake + 2, fake, 16, 2048, 128, 8, fake, fake, None) == 3
+    g = L.ecf8_moe_group
+    assert g(None, fake, 16, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 1
+    assert g(fake, fake, 40, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 2  # P > 256
+    lin = L.ecf8_moe_linear
+    assert lin(None, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1536,
+               None) == 1
+    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 700, 2048, fake, 1536,
+               None) == 2   # seg_n % 128
+    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1000,
+               None) == 6   # ldo < n_segs * seg_n
+    assert lin(fake + 4, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1536,
+               None) == 3
+    c = L.ecf8_moe_combine
+    assert c(fake, 1024, fake, fake, 16, 8, 2048, fake, None) == 1   # ldd < H
+    assert c(fake, 2052, fake, fake, 16, 8, 2052, fake, None) == 2   # H % 8
+    assert c(fake + 2, 2048, fake, fake, 16, 8, 2048, fake, None) == 3

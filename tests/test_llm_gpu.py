@@ -83,6 +83,25 @@ def test_act_quant_matches_torch_cast(cuda_device):
     assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
 
 
+@pytest.mark.parametrize("Kd", [768, 2048, 4096 + 640])
+def test_act_quant_rows_of_any_group_multiple(cuda_device, Kd):
+    """Rows that are not a multiple of 4096 (the MoE shapes): the workgroup
+    covering a row's tail writes nothing past the row."""
+    from ecf8_amd.llm_kernels import act_quant
+
+    gen = torch.Generator().manual_seed(Kd)
+    M = 5
+    x = (torch.randn(M, Kd, generator=gen) * 3).to(torch.bfloat16)
+    flat = torch.full((M * Kd + 4096,), 0x11, dtype=torch.uint8, device=cuda_device)
+    q = flat[: M * Kd].view(FP8).view(M, Kd)
+    s = torch.empty(M, Kd // 128, device=cuda_device)
+    act_quant(x.to(cuda_device), M, q, s)
+    qr, sr = _ref_quant(x)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+    assert bool((flat[M * Kd:].cpu() == 0x11).all())
+
+
 # ------------------------------------------------------------ FP8 linear
 
 
@@ -172,12 +191,13 @@ def _rms_ref(r, x, w, eps):
     return r2, y
 
 
+@pytest.mark.parametrize("Kd", [4096, 2048])
 @pytest.mark.parametrize("with_x", [False, True])
-def test_rmsnorm_residual_and_outputs(cuda_device, with_x):
+def test_rmsnorm_residual_and_outputs(cuda_device, with_x, Kd):
     from ecf8_amd.llm_kernels import rmsnorm
 
     gen = torch.Generator().manual_seed(3)
-    M, Kd = 9, 4096
+    M = 9
     r = torch.randn(M, Kd, generator=gen) * 3
     x = (torch.randn(M, Kd, generator=gen)).to(torch.bfloat16) if with_x else None
     w = (1 + 0.1 * torch.randn(Kd, generator=gen)).to(torch.bfloat16)
@@ -197,11 +217,12 @@ def test_rmsnorm_residual_and_outputs(cuda_device, with_x):
     _assert_fp8_close(q, s, y_ref)
 
 
-def test_silu_mul_quant(cuda_device):
+@pytest.mark.parametrize("I", [8192, 768])
+def test_silu_mul_quant(cuda_device, I):
     from ecf8_amd.llm_kernels import silu_mul_quant
 
     gen = torch.Generator().manual_seed(4)
-    M, I = 6, 8192
+    M = 6
     gu = (torch.randn(M, 2 * I, generator=gen) * 4).to(torch.bfloat16)
     g, u = gu.float()[:, :I], gu.float()[:, I:]
     ref = g * torch.sigmoid(g) * u
@@ -263,13 +284,15 @@ def test_qk_norm_rope_writes_q_and_caches(cuda_device):
 # ------------------------------------------------------------ attention
 
 
-@pytest.mark.parametrize("pos0", [0, 255, 256, 517])
-def test_decode_attention_matches_fp32(cuda_device, pos0):
+@pytest.mark.parametrize("pos0,G", [(0, 4), (255, 4), (256, 4), (517, 4), (0, 8), (517, 8)])
+def test_decode_attention_matches_fp32(cuda_device, pos0, G):
+    """G query heads per KV head: 4 (Qwen3-8B) or 8 (Qwen3-30B-A3B)."""
     from ecf8_amd.llm_kernels import attention_work, decode_attention
 
-    _say(f"[llm] decode_attention pos={pos0}")
+    _say(f"[llm] decode_attention pos={pos0} G={G}")
     gen = torch.Generator().manual_seed(pos0)
-    B, Hkv, Hq, Lmax = 3, 2, 8, 600
+    B, Hkv, Lmax = 3, 2, 600
+    Hq = G * Hkv
     dev = cuda_device
     q = torch.randn(B, Hq, 128, generator=gen).to(torch.bfloat16)
     kc = (torch.randn(B, Hkv, Lmax, 128, generator=gen) * 2).to(torch.bfloat16)

@@ -1,0 +1,164 @@
+"""GPU numerics of the routed-expert kernels (include/ecf8_llm.h, MoE part)
+against plain torch / numpy restatements: the router's top-k choice and
+weights, the grouping of (token, expert) pairs, the grouped FP8 expert
+linear (fp64 per-pair reference), and the weighted combine.
+
+Tolerances: router probabilities 1e-5 absolute (fp32 dot products summed
+in a different order than torch's); linear outputs 2^-7 relative plus
+1e-4 of the largest magnitude (bf16 output rounding); combine 2^-7
+relative (bf16)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+
+
+def _rand_fp8(shape, gen, dev):
+    b = torch.randint(0, 256, shape, generator=gen, dtype=torch.int32).to(torch.uint8)
+    b[(b & 0x7F) == 0x7F] = 0x7E
+    return b.view(FP8).to(dev)
+
+
+def _groups_ref(idx, E):
+    """Counting sort of the pairs (m, k) by expert, token order inside an
+    expert: offsets, the active experts, and each pair's sorted position."""
+    flat = idx.reshape(-1).tolist()
+    counts = np.bincount(flat, minlength=E)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    pos, seen = [], np.zeros(E, np.int64)
+    for e in flat:
+        pos.append(offsets[e] + seen[e])
+        seen[e] += 1
+    return offsets, np.nonzero(counts)[0], np.array(pos)
+
+
+@pytest.mark.parametrize("M,E,top_k,H", [(16, 128, 8, 2048), (3, 64, 4, 512), (1, 128, 8, 2048)])
+def test_router_picks_the_top_k_and_renormalizes(cuda_device, M, E, top_k, H):
+    from ecf8_amd.llm_kernels import MoeRouting, moe_route
+
+    gen = torch.Generator().manual_seed(M * 100 + E)
+    x = torch.randn(M, H, generator=gen).to(torch.bfloat16)
+    wr = (torch.randn(E, H, generator=gen) * 0.05).to(torch.bfloat16)
+    r = MoeRouting(M, top_k, E, cuda_device)
+    moe_route(x.to(cuda_device), wr.to(cuda_device), M, r)
+    probs = torch.softmax(x.double() @ wr.double().T, dim=-1)
+    ref_p, _ = torch.topk(probs, top_k, dim=-1)
+    idx = r.topk_idx.cpu().long()
+    got_p = probs.gather(1, idx)
+    # the chosen experts carry the top-k probabilities, in descending order
+    assert torch.allclose(got_p, ref_p, atol=1e-5, rtol=0)
+    assert bool((got_p[:, :-1] >= got_p[:, 1:] - 1e-6).all())
+    assert all(len(set(row)) == top_k for row in idx.tolist())
+    w = r.topk_w.cpu().double()
+    assert torch.allclose(w, ref_p / ref_p.sum(-1, keepdim=True), atol=1e-5, rtol=0)
+    assert torch.allclose(w.sum(-1), torch.ones(M, dtype=torch.float64), atol=1e-6)
+
+
+@pytest.mark.parametrize("M,top_k,E", [(16, 8, 128), (5, 3, 16), (32, 8, 256)])
+def test_group_sorts_pairs_by_expert(cuda_device, M, top_k, E):
+    from ecf8_amd.llm_kernels import MoeRouting, moe_group
+
+    rng = np.random.default_rng(M + E)
+    idx = np.stack([rng.choice(E, top_k, replace=False) for _ in range(M)]).astype(np.int32)
+    w = rng.random((M, top_k)).astype(np.float32)
+    r = MoeRouting(M, top_k, E, cuda_device)
+    r.topk_idx.copy_(torch.from_numpy(idx))
+    r.topk_w.copy_(torch.from_numpy(w))
+    moe_group(r, M)
+    offsets, active, pos = _groups_ref(idx, E)
+    n_act = int(r.n_active.item())
+    assert n_act == len(active)
+    assert np.array_equal(r.offsets.cpu().numpy(), offsets)
+    assert np.array_equal(r.active.cpu().numpy()[:n_act], active)
+    assert np.array_equal(r.pair_pos.cpu().numpy(), pos)
+    tok = np.repeat(np.arange(M), top_k)
+    got_tok = r.pair_tok.cpu().numpy()
+    got_w = r.pair_w.cpu().numpy()
+    assert np.array_equal(got_tok[pos], tok)
+    assert np.array_equal(got_w[pos], w.reshape(-1))
+    sel = np.zeros(E, np.int32)
+    sel[active] = 1
+    assert np.array_equal(r.select.cpu().numpy(), sel)
+
+
+def _pair_linear_ref(a_rows, a_s_rows, w, ws):
+    """fp64 block-scaled product of the given activation rows with one
+    expert's weight (the math of the dense FP8 linear)."""
+    a = a_rows.cpu().double()
+    M, K = a.shape
+    wd = w.cpu().double()
+    n = wd.shape[0]
+    part = torch.einsum("mgk,ngk->mng", a.view(M, K // 128, 128), wd.view(n, K // 128, 128))
+    scale = a_s_rows.cpu().double()[:, None, :] * ws.cpu().double().repeat_interleave(128, 0)[None]
+    return (part * scale).sum(-1)
+
+
+@pytest.mark.parametrize("gather", [True, False])
+def test_grouped_expert_linear_matches_fp64(cuda_device, gather):
+    """gate/up form (gather the token rows, two segments) and down form (one
+    row per sorted pair, one segment, K below 16 groups)."""
+    from ecf8_amd.llm_kernels import MoeLinearPlan, MoeRouting, moe_group
+
+    dev = cuda_device
+    gen = torch.Generator().manual_seed(11 if gather else 12)
+    rng = np.random.default_rng(3)
+    M, top_k, E = 16, 4, 12
+    K, seg_n, n_segs = (1024, 256, 2) if gather else (768, 384, 1)
+    idx = np.stack([rng.choice(E, top_k, replace=False) for _ in range(M)]).astype(np.int32)
+    idx[:, 0] = 5  # one expert with all 16 tokens
+    r = MoeRouting(M, top_k, E, dev)
+    r.topk_idx.copy_(torch.from_numpy(idx))
+    r.topk_w.fill_(0.25)
+    moe_group(r, M)
+    P = M * top_k
+    rows = M if gather else P
+    aq = _rand_fp8((rows, K), gen, dev)
+    a_s = (torch.rand(rows, K // 128, generator=gen) * 1e-2 + 1e-4).to(dev)
+    experts = []
+    for _ in range(E):
+        segs = []
+        for _ in range(n_segs):
+            w = _rand_fp8((seg_n, K), gen, dev)
+            ws = (torch.rand(seg_n // 128, K // 128, generator=gen) * 1e-3 + 1e-5).to(dev)
+            segs.append((w, ws))
+        experts.append(segs)
+    ldo = n_segs * seg_n + 32
+    out = torch.full((P, ldo), 7.0, dtype=torch.bfloat16, device=dev)
+    MoeLinearPlan(experts, out)(aq, a_s, r, gather=gather)
+    offsets, active, _ = _groups_ref(idx, E)
+    tok = r.pair_tok.cpu().long()
+    got = out.double().cpu()
+    for e in active:
+        q = torch.arange(int(offsets[e]), int(offsets[e + 1]))
+        src = tok[q] if gather else q
+        ref = torch.cat([_pair_linear_ref(aq.cpu()[src], a_s.cpu()[src], w, ws)
+                         for w, ws in experts[e]], dim=1)
+        g = got[q, : n_segs * seg_n]
+        assert bool(((g - ref).abs() <= 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()).all()), e
+    assert bool((out[:, n_segs * seg_n:].cpu() == 7.0).all())
+
+
+def test_combine_weights_the_pairs_in_order(cuda_device):
+    from ecf8_amd.llm_kernels import MoeRouting, moe_combine, moe_group
+
+    dev = cuda_device
+    rng = np.random.default_rng(8)
+    M, top_k, E, H = 16, 8, 128, 2048
+    idx = np.stack([rng.choice(E, top_k, replace=False) for _ in range(M)]).astype(np.int32)
+    w = rng.random((M, top_k)).astype(np.float32)
+    r = MoeRouting(M, top_k, E, dev)
+    r.topk_idx.copy_(torch.from_numpy(idx))
+    r.topk_w.copy_(torch.from_numpy(w))
+    moe_group(r, M)
+    down = torch.randn(M * top_k, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    moe_combine(down.to(dev), r, M, out)
+    pos = torch.from_numpy(_groups_ref(idx, E)[2]).view(M, top_k)
+    ref = (torch.from_numpy(w).double()[..., None] * down.double()[pos]).sum(1)
+    assert torch.allclose(out.double().cpu(), ref, rtol=2 ** -7, atol=1e-3)
