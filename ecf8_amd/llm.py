@@ -131,47 +131,12 @@ def _rotary_tables(cfg: Qwen3Config, max_len: int, device):
             torch.sin(ang).float().to(device).contiguous())
 
 
-class Qwen3Runner:
-    """Prefill + greedy decode of a fixed batch on one device."""
-
-    def __init__(self, model: Qwen3ForCausalLM, batch: int, prompt_len: int, max_len: int,
-                 device=None):
-        cfg = model.config
-        if cfg.hidden != 4096 or cfg.head_dim != 128 or cfg.heads != 4 * cfg.kv_heads:
-            raise ECF8Error("the fused kernels need hidden 4096, head_dim 128, heads = 4 kv heads")
-        if cfg.intermediate % 4096:
-            raise ECF8Error("intermediate size must be a multiple of 4096")
-        self.model, self.cfg = model, cfg
-        self.dev = torch.device(device) if device is not None else model.lm_head.weight.device
-        self.B, self.T, self.Lmax = batch, prompt_len, max_len
-        dev, B = self.dev, batch
-        M = B * prompt_len
-        Hq, Hkv, D = cfg.heads, cfg.kv_heads, cfg.head_dim
-        bf = dict(dtype=torch.bfloat16, device=dev)
-        self.kc = [torch.empty(B, Hkv, max_len, D, **bf) for _ in range(cfg.layers)]
-        self.vc = [torch.empty(B, Hkv, max_len, D, **bf) for _ in range(cfg.layers)]
-        self.cos, self.sin = _rotary_tables(cfg, max_len, dev)
-        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.step = torch.zeros(1, dtype=torch.int64, device=dev)
-        self.res = torch.empty(M, cfg.hidden, dtype=torch.float32, device=dev)
-        self.aq = {k: torch.empty(M, k, dtype=torch.float8_e4m3fn, device=dev)
-                   for k in sorted({cfg.hidden, cfg.intermediate, Hq * D})}
-        self.as_ = {k: torch.empty(M, k // 128, dtype=torch.float32, device=dev) for k in self.aq}
-        self.qkv = torch.empty(M, (Hq + 2 * Hkv) * D, **bf)
-        self.q = torch.empty(B * Hq * prompt_len * D, **bf)
-        self.attn = torch.empty(M, Hq * D, **bf)
-        self.o = torch.empty(M, cfg.hidden, **bf)
-        self.gu = torch.empty(M, 2 * cfg.intermediate, **bf)
-        self.down = torch.empty(M, cfg.hidden, **bf)
-        self.h = torch.empty(M, cfg.hidden, **bf)
-        self.work = K.attention_work(B, Hq, max_len, dev)
-        self.next_tok = torch.zeros(B, dtype=torch.int64, device=dev)
-        self.tokens = torch.zeros(B, max_len, dtype=torch.int64, device=dev)
-        self.graph = None
-        self.logits = None  # logits of the last decode step
-        self._plans = {}
-
-    # ------------------------------------------------------------ layer
+class _GreedyRunner:
+    """Generation mechanics shared by the dense and the MoE runners: a
+    subclass provides ``layer()`` and the buffers named here (``res``, ``h``,
+    ``q``, ``kc``/``vc``, ``attn``, ``pos``, ``step``, ``tokens``,
+    ``next_tok``); prefill runs eagerly, a decode step can be captured as one
+    HIP graph."""
 
     def _plan(self, layer, index, which, weights, out):
         """Linear argument blocks are cached per (layer, which, weight
@@ -183,41 +148,6 @@ class Qwen3Runner:
             p = K.LinearPlan(weights, out)
             self._plans[key] = p
         return p
-
-    def layer(self, layer: DecoderLayer, index: int, x_prev, prefill: bool):
-        cfg = self.cfg
-        B, T = self.B, (self.T if prefill else 1)
-        M = B * T
-        H, I, Hq, Hkv = cfg.hidden, cfg.intermediate, cfg.heads, cfg.kv_heads
-        a, m = layer.self_attn, layer.mlp
-        aqH, asH = self.aq[H], self.as_[H]
-        K.rmsnorm(self.res, layer.input_layernorm.weight, cfg.eps, M, x=x_prev, out_q=aqH,
-                  out_scale=asH)
-        self._plan(layer, index, "qkv", [(a.q_proj.weight, a.q_proj.weight_scale_inv),
-                                         (a.k_proj.weight, a.k_proj.weight_scale_inv),
-                                         (a.v_proj.weight, a.v_proj.weight_scale_inv)],
-                   self.qkv)(aqH, asH, M)
-        K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
-                       self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
-        aqA, asA = self.aq[Hq * 128], self.as_[Hq * 128]
-        if prefill:
-            self._prefill_attention(index, T)
-            K.act_quant(self.attn, M, aqA, asA)
-        else:
-            K.decode_attention(self.q, self.kc[index], self.vc[index], self.pos, self.work, aqA,
-                               asA, Hq)
-        self._plan(layer, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
-                   self.o)(aqA, asA, M)
-        K.rmsnorm(self.res, layer.post_attention_layernorm.weight, cfg.eps, M, x=self.o,
-                  out_q=aqH, out_scale=asH)
-        self._plan(layer, index, "gu", [(m.gate_proj.weight, m.gate_proj.weight_scale_inv),
-                                        (m.up_proj.weight, m.up_proj.weight_scale_inv)],
-                   self.gu)(aqH, asH, M)
-        aqI, asI = self.aq[I], self.as_[I]
-        K.silu_mul_quant(self.gu, M, aqI, asI)
-        self._plan(layer, index, "down", [(m.down_proj.weight, m.down_proj.weight_scale_inv)],
-                   self.down)(aqI, asI, M)
-        return self.down
 
     def _prefill_attention(self, index: int, T: int):
         """Causal attention of the prompt in fp32 (torch), positions 0..T-1."""
@@ -232,8 +162,6 @@ class Qwen3Runner:
         s.masked_fill_(mask, float("-inf"))
         o = torch.matmul(torch.softmax(s, dim=-1), v)
         self.attn[: B * T].copy_(o.permute(0, 2, 1, 3).reshape(B * T, Hq * 128))
-
-    # ------------------------------------------------------------ model
 
     def _forward(self, prefill: bool):
         """All layers + final norm + lm_head; returns bf16 logits [B, vocab]
@@ -312,6 +240,84 @@ class Qwen3Runner:
             else:
                 self.logits = self._decode_body()
         return self.tokens[:, :new_tokens]
+
+
+class Qwen3Runner(_GreedyRunner):
+    """Prefill + greedy decode of a fixed batch on one device."""
+
+    def __init__(self, model: Qwen3ForCausalLM, batch: int, prompt_len: int, max_len: int,
+                 device=None):
+        cfg = model.config
+        if cfg.hidden != 4096 or cfg.head_dim != 128 or cfg.heads != 4 * cfg.kv_heads:
+            raise ECF8Error("the fused kernels need hidden 4096, head_dim 128, heads = 4 kv heads")
+        if cfg.intermediate % 4096:
+            raise ECF8Error("intermediate size must be a multiple of 4096")
+        self.model, self.cfg = model, cfg
+        self.dev = torch.device(device) if device is not None else model.lm_head.weight.device
+        self.B, self.T, self.Lmax = batch, prompt_len, max_len
+        dev, B = self.dev, batch
+        M = B * prompt_len
+        Hq, Hkv, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.kc = [torch.empty(B, Hkv, max_len, D, **bf) for _ in range(cfg.layers)]
+        self.vc = [torch.empty(B, Hkv, max_len, D, **bf) for _ in range(cfg.layers)]
+        self.cos, self.sin = _rotary_tables(cfg, max_len, dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.step = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.res = torch.empty(M, cfg.hidden, dtype=torch.float32, device=dev)
+        self.aq = {k: torch.empty(M, k, dtype=torch.float8_e4m3fn, device=dev)
+                   for k in sorted({cfg.hidden, cfg.intermediate, Hq * D})}
+        self.as_ = {k: torch.empty(M, k // 128, dtype=torch.float32, device=dev) for k in self.aq}
+        self.qkv = torch.empty(M, (Hq + 2 * Hkv) * D, **bf)
+        self.q = torch.empty(B * Hq * prompt_len * D, **bf)
+        self.attn = torch.empty(M, Hq * D, **bf)
+        self.o = torch.empty(M, cfg.hidden, **bf)
+        self.gu = torch.empty(M, 2 * cfg.intermediate, **bf)
+        self.down = torch.empty(M, cfg.hidden, **bf)
+        self.h = torch.empty(M, cfg.hidden, **bf)
+        self.work = K.attention_work(B, Hq, max_len, dev)
+        self.next_tok = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.tokens = torch.zeros(B, max_len, dtype=torch.int64, device=dev)
+        self.graph = None
+        self.logits = None  # logits of the last decode step
+        self._plans = {}
+
+    # ------------------------------------------------------------ layer
+
+    def layer(self, layer: DecoderLayer, index: int, x_prev, prefill: bool):
+        cfg = self.cfg
+        B, T = self.B, (self.T if prefill else 1)
+        M = B * T
+        H, I, Hq, Hkv = cfg.hidden, cfg.intermediate, cfg.heads, cfg.kv_heads
+        a, m = layer.self_attn, layer.mlp
+        aqH, asH = self.aq[H], self.as_[H]
+        K.rmsnorm(self.res, layer.input_layernorm.weight, cfg.eps, M, x=x_prev, out_q=aqH,
+                  out_scale=asH)
+        self._plan(layer, index, "qkv", [(a.q_proj.weight, a.q_proj.weight_scale_inv),
+                                         (a.k_proj.weight, a.k_proj.weight_scale_inv),
+                                         (a.v_proj.weight, a.v_proj.weight_scale_inv)],
+                   self.qkv)(aqH, asH, M)
+        K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
+                       self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
+        aqA, asA = self.aq[Hq * 128], self.as_[Hq * 128]
+        if prefill:
+            self._prefill_attention(index, T)
+            K.act_quant(self.attn, M, aqA, asA)
+        else:
+            K.decode_attention(self.q, self.kc[index], self.vc[index], self.pos, self.work, aqA,
+                               asA, Hq)
+        self._plan(layer, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
+                   self.o)(aqA, asA, M)
+        K.rmsnorm(self.res, layer.post_attention_layernorm.weight, cfg.eps, M, x=self.o,
+                  out_q=aqH, out_scale=asH)
+        self._plan(layer, index, "gu", [(m.gate_proj.weight, m.gate_proj.weight_scale_inv),
+                                        (m.up_proj.weight, m.up_proj.weight_scale_inv)],
+                   self.gu)(aqH, asH, M)
+        aqI, asI = self.aq[I], self.as_[I]
+        K.silu_mul_quant(self.gu, M, aqI, asI)
+        self._plan(layer, index, "down", [(m.down_proj.weight, m.down_proj.weight_scale_inv)],
+                   self.down)(aqI, asI, M)
+        return self.down
 
 
 # ------------------------------------------------------------ construction

@@ -300,14 +300,19 @@ class MoeLinearPlan:
         self.E, self.n_segs, self.seg_n, self.K, self.out = len(experts), n_segs, seg_n, K, out
         self._keep = [t for segs in experts for pair in segs for t in pair]
 
-    def __call__(self, aq, a_scale, r: MoeRouting, gather: bool):
+    def __call__(self, aq, a_scale, r: MoeRouting, gather: bool, M: int | None = None):
         """``gather``: activation rows are tokens (aq [>= M, K], row of a
-        sorted pair = its token); otherwise aq has one row per sorted pair."""
+        sorted pair = its token); otherwise aq has one row per sorted pair
+        ([>= M * top_k, K]).  M: the tokens routed into ``r`` (default: its
+        capacity)."""
         dev = self.out.device
         _need(aq, torch.float8_e4m3fn, "aq", dev)
         _need(a_scale, torch.float32, "a_scale", dev)
+        M = r.M if M is None else M
+        if not 1 <= M <= r.M:
+            raise ECF8Error(f"1 <= M <= {r.M}")
         P = r.M * r.top_k
-        rows = r.M if gather else P
+        rows = M if gather else M * r.top_k
         if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < rows
                 or tuple(a_scale.shape[1:]) != (self.K // GROUP,) or a_scale.shape[0] < rows
                 or self.out.shape[0] < P or r.E != self.E):

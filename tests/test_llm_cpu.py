@@ -68,3 +68,37 @@ def test_dit_blocks_compress_with_the_reference_patterns():
                              blk.output_positions.numpy(), blk.gaps.numpy())
             for n, part in zip(names, np.split(flat, blk.split_positions)):
                 assert np.array_equal(part, o[n].numpy().reshape(-1)), n
+
+
+def test_moe_blocks_compress_with_the_reference_patterns():
+    """A Qwen3-MoE-shaped model is cut as dfloat/const.py's qwen3moe
+    patterns cut it: each layer's self_attn (k, o, q, v) and each expert
+    (down, gate, up) is one block, and every stored block decodes (oracle)
+    to its original weights in name-sorted order."""
+    from ecf8_amd.moe import (ATTN_LINEARS, EXPERT_LINEARS, Qwen3MoeConfig, compress_moe_layers,
+                              random_moe_model)
+
+    cfg = Qwen3MoeConfig(hidden=512, layers=3, heads=8, kv_heads=1, experts=4, top_k=2,
+                         moe_intermediate=256, vocab=128)
+    model, drawn = random_moe_model(cfg, "cpu", distinct_layers=2, seed=4)
+    blocks = []
+    for layer in model.model.layers:
+        blocks.append((layer.self_attn, ATTN_LINEARS))
+        blocks += [(ex, EXPERT_LINEARS) for ex in layer.mlp.experts]
+    originals = [{n: m.get_submodule(n).weight.detach().view(torch.uint8).clone() for n in names}
+                 for m, names in blocks]
+    compress_moe_layers(model, drawn)
+    for (m, names), orig in zip(blocks, originals):
+        assert len(m._forward_pre_hooks) == 1
+        assert [type(x).__name__ for x in m.weight_injection_modules] == ["FP8Linear"] * len(names)
+        flat = oc.decode(m.luts.numpy(), m.encoded.numpy(), m.packed_other_4bits.numpy(),
+                         m.output_positions.numpy(), m.gaps.numpy())
+        for n, part in zip(names, np.split(flat, m.split_positions)):
+            assert np.array_equal(part, orig[n].numpy().reshape(-1)), n
+    # the router stays a dense bf16 Linear, outside every pattern
+    assert model.model.layers[0].mlp.gate.weight.dtype == torch.bfloat16
+    # layer 2 reuses layer 0's draw, in its own memory
+    assert torch.equal(model.model.layers[2].mlp.experts[1].encoded,
+                       model.model.layers[0].mlp.experts[1].encoded)
+    assert (model.model.layers[2].mlp.experts[1].encoded.data_ptr()
+            != model.model.layers[0].mlp.experts[1].encoded.data_ptr())
