@@ -915,30 +915,37 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *__restri
   }
 }
 
-// Group the P = M * top_k (token, expert) pairs by expert (one workgroup,
-// P <= 256, E <= 256): pairs of expert e take sorted positions
-// [offsets[e], offsets[e + 1]) in token order; pair_tok / pair_w give each
-// sorted position's token and routing weight, pair_pos each pair's sorted
-// position; active[0, n_active) lists the experts with pairs in increasing
-// order; select[e] (optional) = 1 if expert e has pairs.  Expert ids
-// outside [0, E) are clamped into it.
-__global__ __launch_bounds__(256) void moe_group_kernel(
+// Group the P = M * top_k (token, expert) pairs by expert (one workgroup
+// of 1024 threads, P <= 8192, E <= 256): pairs of expert e take sorted
+// positions [offsets[e], offsets[e + 1]) in token order; pair_tok / pair_w
+// give each sorted position's token and routing weight, pair_pos each
+// pair's sorted position; active[0, n_active) lists the experts with pairs
+// in increasing order; select[e] (optional) = 1 if expert e has pairs.
+// Expert ids outside [0, E) are clamped into it.  Two passes over chunks of
+// 1024 pairs: integer counts per expert, then each pair's rank = pairs of
+// its expert in earlier chunks + earlier pairs of its chunk.
+__global__ __launch_bounds__(1024) void moe_group_kernel(
     const int *__restrict__ topk_idx, const float *__restrict__ topk_w, int P, int top_k, int E,
     int *__restrict__ offsets, int *__restrict__ active, int *__restrict__ n_active,
     int *__restrict__ pair_tok, float *__restrict__ pair_w, int *__restrict__ pair_pos,
     int *__restrict__ select) {
-  __shared__ int s_e[256];
+  constexpr int kChunk = 1024;
+  __shared__ int s_e[kChunk];
   __shared__ int s_cnt[256];
   __shared__ int s_off[257];
   const int t = threadIdx.x;
-  int e = -1;
-  if (t < P) e = min(max(topk_idx[t], 0), E - 1);
-  s_e[t] = e;
-  __syncthreads();
-  if (t < E) {
-    int c = 0;
-    for (int q = 0; q < P; ++q) c += s_e[q] == t;
-    s_cnt[t] = c;
+  auto expert_of = [&](int p) { return p < P ? min(max(topk_idx[p], 0), E - 1) : -1; };
+  if (t < 256) s_cnt[t] = 0;
+  for (int c0 = 0; c0 < P; c0 += kChunk) {
+    const int n = min(kChunk, P - c0);
+    __syncthreads();  // s_e of the previous chunk is no longer read
+    s_e[t] = expert_of(c0 + t);
+    __syncthreads();
+    if (t < E) {
+      int c = 0;
+      for (int q = 0; q < n; ++q) c += s_e[q] == t;
+      s_cnt[t] += c;
+    }
   }
   __syncthreads();
   if (t == 0) {
@@ -952,15 +959,30 @@ __global__ __launch_bounds__(256) void moe_group_kernel(
     *n_active = na;
   }
   __syncthreads();
-  for (int i = t; i <= E; i += 256) offsets[i] = s_off[i];
+  for (int i = t; i <= E; i += kChunk) offsets[i] = s_off[i];
   if (select && t < E) select[t] = s_cnt[t] > 0 ? 1 : 0;
-  if (t < P) {
-    int rank = 0;
-    for (int q = 0; q < t; ++q) rank += s_e[q] == e;
-    const int q = s_off[e] + rank;
-    pair_tok[q] = t / top_k;
-    pair_w[q] = topk_w[t];
-    pair_pos[t] = q;
+  __syncthreads();
+  if (t < 256) s_cnt[t] = 0;  // now: pairs of each expert in earlier chunks
+  for (int c0 = 0; c0 < P; c0 += kChunk) {
+    const int n = min(kChunk, P - c0);
+    __syncthreads();
+    const int e = expert_of(c0 + t);
+    s_e[t] = e;
+    __syncthreads();
+    if (t < n) {
+      int rank = s_cnt[e];
+      for (int q = 0; q < t; ++q) rank += s_e[q] == e;
+      const int q = s_off[e] + rank;
+      pair_tok[q] = (c0 + t) / top_k;
+      pair_w[q] = topk_w[c0 + t];
+      pair_pos[c0 + t] = q;
+    }
+    __syncthreads();  // every rank read s_cnt before it grows
+    if (t < E) {
+      int c = 0;
+      for (int q = 0; q < n; ++q) c += s_e[q] == t;
+      s_cnt[t] += c;
+    }
   }
 }
 
@@ -1292,8 +1314,8 @@ extern "C" int ecf8_moe_group(const int *topk_idx, const float *topk_w, int64_t 
   if (!topk_idx || !topk_w || !offsets || !active || !n_active || !pair_tok || !pair_w ||
       !pair_pos || M <= 0 || top_k <= 0 || E <= 0)
     return ECF8_ERR_INVALID_ARG;
-  if (M * top_k > 256 || E > 256) return ECF8_ERR_UNSUPPORTED;
-  moe_group_kernel<<<1, 256, 0, as_stream(stream)>>>(topk_idx, topk_w, (int)(M * top_k), top_k, E,
+  if (M * top_k > 8192 || E > 256) return ECF8_ERR_UNSUPPORTED;
+  moe_group_kernel<<<1, 1024, 0, as_stream(stream)>>>(topk_idx, topk_w, (int)(M * top_k), top_k, E,
                                                      offsets, active, n_active, pair_tok, pair_w,
                                                      pair_pos, select);
   return launched();

@@ -226,12 +226,12 @@ def dequant_fp8_block(weight, scale_inv, out=None):
 
 class MoeRouting:
     """Device buffers of one routing step for up to ``M`` tokens
-    (``M * top_k <= 256``): the router's choices, the pairs grouped by
+    (``M * top_k <= 8192``): the router's choices, the pairs grouped by
     expert, and the per-expert flags the routed decode takes."""
 
     def __init__(self, M: int, top_k: int, n_experts: int, device):
-        if M * top_k > 256 or n_experts > 256:
-            raise ECF8Error("routing holds at most 256 (token, expert) pairs and 256 experts")
+        if M * top_k > 8192 or n_experts > 256:
+            raise ECF8Error("routing holds at most 8192 (token, expert) pairs and 256 experts")
         P = M * top_k
         i32 = dict(dtype=torch.int32, device=device)
         self.M, self.top_k, self.E = M, top_k, n_experts

@@ -177,11 +177,11 @@ class _LayerExperts:
 
 class Qwen3MoeRunner(_GreedyRunner):
     """Prefill + greedy decode of a fixed batch on one device.  The prompt's
-    MoE runs in chunks of ``prefill_chunk`` tokens (at most 256 (token,
+    MoE runs in chunks of ``prefill_chunk`` tokens (at most 8192 (token,
     expert) pairs per routing step)."""
 
     def __init__(self, model: Qwen3MoeForCausalLM, batch: int, prompt_len: int, max_len: int,
-                 device=None, prefill_chunk: int = 32):
+                 device=None, prefill_chunk: int = 512):
         cfg = model.config
         if cfg.hidden not in (2048, 4096) or cfg.head_dim != 128:
             raise ECF8Error("the fused kernels need hidden 2048 or 4096 and head_dim 128")
@@ -189,9 +189,9 @@ class Qwen3MoeRunner(_GreedyRunner):
             raise ECF8Error("query heads must be 4 or 8 per KV head")
         if cfg.moe_intermediate % 128 or cfg.experts > 256:
             raise ECF8Error("expert intermediate must be a multiple of 128; at most 256 experts")
-        chunk = min(prefill_chunk, 256 // cfg.top_k)
-        if batch * cfg.top_k > 256 or chunk < 1:
-            raise ECF8Error("a decode step routes at most 256 (token, expert) pairs")
+        chunk = min(prefill_chunk, 8192 // cfg.top_k)
+        if batch * cfg.top_k > 8192 or chunk < 1:
+            raise ECF8Error("a decode step routes at most 8192 (token, expert) pairs")
         self.model, self.cfg = model, cfg
         self.dev = torch.device(device) if device is not None else model.lm_head.weight.device
         self.B, self.T, self.Lmax, self.chunk = batch, prompt_len, max_len, chunk

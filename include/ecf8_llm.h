@@ -125,7 +125,7 @@ int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cach
 int ecf8_moe_route(const void *x, const void *router_w, int64_t M, int64_t H, int E, int top_k,
                    int *topk_idx, float *topk_w, void *stream);
 
-/* Group the P = M * top_k (token, expert) pairs by expert (P <= 256,
+/* Group the P = M * top_k (token, expert) pairs by expert (P <= 8192,
  * E <= 256): expert e's pairs take sorted positions [offsets[e],
  * offsets[e + 1]) in token order (offsets int32 [E + 1]); pair_tok int32
  * [P] / pair_w fp32 [P]: token and weight of each sorted position;

@@ -191,7 +191,7 @@ def test_moe_kernels_reject_before_launch():
     assert L.ecf8_moe_route(fake + 2, fake, 16, 2048, 128, 8, fake, fake, None) == 3
     g = L.ecf8_moe_group
     assert g(None, fake, 16, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 1
-    assert g(fake, fake, 40, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 2  # P > 256
+    assert g(fake, fake, 1100, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 2  # P > 8192
     lin = L.ecf8_moe_linear
     assert lin(None, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1536,
                None) == 1
