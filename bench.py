@@ -371,6 +371,93 @@ def e2e_generate(args):
         sys.exit(1)
 
 
+def moe_generate(args):
+    """Qwen3-30B-A3B-shaped MoE causal LM (48 layers, hidden 2048, 32 query /
+    4 KV heads, 128 experts of intermediate 768, top-8 routing; random init,
+    FP8 attention and expert linears with 128x128 block scales, bf16 router,
+    embedding and lm_head), batch 16, random prompts of 128 tokens, greedy
+    decoding of --new-tokens (default 512) tokens: first with the FP8
+    weights resident, then with every attention block and expert
+    ECF8-compressed.  The attention block is decoded by its forward-pre-hook.
+    Per decode step, only the experts the router picked are decoded, in one
+    batched launch per layer, selected on the device.  Both runs use the same
+    engine (eager prefill, one HIP graph replay per decode step) and must
+    produce identical tokens."""
+    import torch
+
+    from ecf8_amd.llm import timed_generate
+    from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, random_moe_model
+    from ecf8_amd.run import TensorManager
+
+    dev = torch.device("cuda", 0)
+    cfg = Qwen3MoeConfig()
+    B, T = args.batch, args.prompt_len
+    new = args.new_tokens if args.new_tokens is not None else 512
+    t0 = time.time()
+    model, drawn = random_moe_model(cfg, dev, distinct_layers=args.distinct_layers, seed=args.seed)
+    print(f"[bench] model built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(args.seed + 7)
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=g)
+    results = {}
+    for mode in ("fp8", "ecf8"):
+        if mode == "ecf8":
+            t0 = time.time()
+            compress_moe_layers(model, drawn)
+            torch.cuda.synchronize()
+            print(f"[bench] blocks compressed in {time.time() - t0:.1f}s", file=sys.stderr,
+                  flush=True)
+        TensorManager.clear_device()
+        torch.cuda.empty_cache()
+        t0 = time.time()
+        runner = Qwen3MoeRunner(model, B, T, T + new, dev)
+        runner.capture()
+        print(f"[bench] {mode}: runner ready in {time.time() - t0:.1f}s", file=sys.stderr,
+              flush=True)
+        runner.generate(prompt, min(new, 8))  # warm-up
+        r = timed_generate(runner, prompt, new)
+        # experts the last step's router picked, in the last layer
+        r["experts_routed_last_step"] = int(runner.route.n_active.item())
+        print(f"[bench] {mode}: {r['tokens_per_s']:.1f} tokens/s, latency {r['latency_s']:.3f}s, "
+              f"peak {r['peak_mib']:.0f} MiB", file=sys.stderr, flush=True)
+        r["weights_mib"] = sum(t.numel() * t.element_size() for t in
+                               list(model.parameters()) + list(model.buffers())) / 2**20
+        results[mode] = r
+        del runner
+    same = torch.equal(results["fp8"]["tokens"], results["ecf8"]["tokens"])
+    fp8, ecf8 = results["fp8"], results["ecf8"]
+
+    def summary(r):
+        return {"tokens_per_s": round(r["tokens_per_s"], 1), "latency_s": round(r["latency_s"], 4),
+                "peak_mib": round(r["peak_mib"], 1), "weights_mib": round(r["weights_mib"], 1)}
+
+    line = {
+        "metric": "e2e tokens/s, Qwen3-30B-A3B-shape MoE bs16 (ECF8 attention blocks and "
+                  "experts; routed experts decoded in one batched launch per layer)",
+        "value": round(ecf8["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (random-init weights, random prompts)",
+        "config": {"workload": "qwen3-moe-generate", "layers": cfg.layers, "hidden": cfg.hidden,
+                   "heads": cfg.heads, "kv_heads": cfg.kv_heads, "experts": cfg.experts,
+                   "top_k": cfg.top_k, "moe_intermediate": cfg.moe_intermediate,
+                   "vocab": cfg.vocab, "batch": B, "prompt_len": T, "new_tokens": new,
+                   "distinct_layer_weights": args.distinct_layers, "decoding": "greedy",
+                   "ecf8_decode": "attention block in its hook; routed experts per step "
+                                  "(device-side selection, one batched launch per layer)"},
+        "uncompressed_fp8": summary(fp8),
+        "ecf8": summary(ecf8),
+        "experts_routed_last_step": ecf8["experts_routed_last_step"],
+        "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
+        "identical_tokens": same,
+    }
+    print(json.dumps(line), flush=True)
+    if not same:
+        sys.exit(1)
+
+
 def dit_generate(args):
     """FLUX.1-dev-shaped DiT (19 double + 38 single blocks, hidden 3072),
     one 1024x1024 image: 4096 latent tokens of 64 channels and 512 text
@@ -464,10 +551,11 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "qwen3-8b-generate",
-                                           "flux-dit-generate"),
+                                           "qwen3-moe-generate", "flux-dit-generate"),
                     default="qwen3-8b-layer",
                     help="qwen3-moe-layer: attention + 128 experts in one batched launch; "
                          "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8; "
+                         "qwen3-moe-generate: the same for the 30B-A3B-shaped MoE; "
                          "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8")
     ap.add_argument("--dit-steps", type=int, default=28)
     ap.add_argument("--routed-tokens", type=int, default=0,
@@ -476,7 +564,8 @@ def main():
     ap.add_argument("--top-k", type=int, default=8)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt-len", type=int, default=128)
-    ap.add_argument("--new-tokens", type=int, default=1024)
+    ap.add_argument("--new-tokens", type=int, default=None,
+                    help="generate: new tokens per sequence (1024 dense, 512 MoE)")
     ap.add_argument("--prefetch-workgroups", type=int, default=2,
                     help="generate: resident side-stream decode workgroups per CU")
     ap.add_argument("--distinct-layers", type=int, default=2,
@@ -491,7 +580,11 @@ def main():
     if args.mode == "copy":
         return copy_calibration(args.steps, args.warmup)
     if args.workload == "qwen3-8b-generate":
+        if args.new_tokens is None:
+            args.new_tokens = 1024
         return e2e_generate(args)
+    if args.workload == "qwen3-moe-generate":
+        return moe_generate(args)
     if args.workload == "flux-dit-generate":
         return dit_generate(args)
 

@@ -808,73 +808,79 @@ __global__ __launch_bounds__(256) void dequant_fp8_block_kernel(const uint8_t *_
 
 // ------------------------------------------------------------ MoE routing
 
-// Router of one token per workgroup (256 threads = 4 waves): logit[e] =
-// x[m] . wr[e] over H (bf16 inputs, fp32 products accumulated per lane in
-// order, then summed across the wave in a fixed tree); softmax over the E
-// experts in fp32; the top_k largest probabilities (ties to the lower
-// expert index), renormalized to sum 1.  E <= 256, H a multiple of 512 and
-// at most 8192, top_k <= 16.
-__global__ __launch_bounds__(256) void moe_route_kernel(const uint16_t *__restrict__ x,
-                                                        const uint16_t *__restrict__ wr, int H,
-                                                        int E, int top_k,
-                                                        int *__restrict__ topk_idx,
-                                                        float *__restrict__ topk_w) {
-  constexpr int kMaxChunks = 16;  // H <= 16 * 512
-  __shared__ float logit[256];
-  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int chunks = H / 512;
-  // lane l holds x[512 j + 8 l, +8) for every chunk j
-  float xv[kMaxChunks][8];
+// Router logits: logits[m, e] = x[m] . wr[e] over H (bf16 inputs, fp32
+// products accumulated per lane in order, then summed across the wave in a
+// fixed tree).  Workgroup (ex, tb): wave w takes expert 4 ex + w and tokens
+// [4 tb, +4); every load of a 2048-column slice is issued before its FMAs.
+// H a multiple of 512.
+__global__ __launch_bounds__(256) void moe_logits_kernel(const uint16_t *__restrict__ x,
+                                                         const uint16_t *__restrict__ wr, int M,
+                                                         int H, int E,
+                                                         float *__restrict__ logits) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * 4 + wave;
+  const int m0 = blockIdx.y * 4;
+  if (e >= E) return;  // uniform per wave; no barrier below
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int h0 = 0; h0 < H; h0 += 2048) {
+    uint4 wv[4], xv[4][4];
 #pragma unroll
-  for (int j = 0; j < kMaxChunks; ++j) {
-    if (j < chunks) {
-      float v[16];
-      const uint4 a = *reinterpret_cast<const uint4 *>(x + (size_t)m * H + 512 * j + 8 * lane);
-      const uint32_t wd[4] = {a.x, a.y, a.z, a.w};
+    for (int j = 0; j < 4; ++j) {
+      const int c = h0 + 512 * j + 8 * lane;
+      const bool in = h0 + 512 * j < H;
+      wv[j] = in ? *reinterpret_cast<const uint4 *>(wr + (size_t)e * H + c) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf16_f32(wd[i] & 0xffffu);
-        v[2 * i + 1] = bf16_f32(wd[i] >> 16);
+      for (int t = 0; t < 4; ++t) {
+        const int m = min(m0 + t, M - 1);  // rows past M re-read row M - 1, unused
+        xv[t][j] = in ? *reinterpret_cast<const uint4 *>(x + (size_t)m * H + c)
+                      : make_uint4(0, 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xv[j][i] = v[i];
     }
-  }
-  for (int e = wave; e < E; e += 4) {
-    const uint16_t *we = wr + (size_t)e * H + 8 * lane;
-    float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxChunks; ++j) {
-      if (j < chunks) {
-        const uint4 b = *reinterpret_cast<const uint4 *>(we + 512 * j);
-        const uint32_t wd[4] = {b.x, b.y, b.z, b.w};
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t xw[4] = {xv[t][j].x, xv[t][j].y, xv[t][j].z, xv[t][j].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          acc = fmaf(xv[j][2 * i], bf16_f32(wd[i] & 0xffffu), acc);
-          acc = fmaf(xv[j][2 * i + 1], bf16_f32(wd[i] >> 16), acc);
+          acc[t] = fmaf(bf16_f32(xw[i] & 0xffffu), bf16_f32(ww[i] & 0xffffu), acc[t]);
+          acc[t] = fmaf(bf16_f32(xw[i] >> 16), bf16_f32(ww[i] >> 16), acc[t]);
         }
       }
     }
-    acc = wave_sum(acc);
-    if (lane == 0) logit[e] = acc;
   }
-  __syncthreads();
-  if (wave != 0) return;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float v = wave_sum(acc[t]);
+    if (lane == 0 && m0 + t < M) logits[(size_t)(m0 + t) * E + e] = v;
+  }
+}
+
+// Top-k of one token per wave (4 tokens per 256-thread workgroup): softmax
+// over the E <= 256 logits in fp32, the top_k largest probabilities (ties
+// to the lower expert index), renormalized to sum 1.
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__ logits, int M,
+                                                       int E, int top_k,
+                                                       int *__restrict__ topk_idx,
+                                                       float *__restrict__ topk_w) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;  // uniform per wave; no barrier below
   // lane l holds experts l, l + 64, l + 128, l + 192
   float p[4];
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    p[i] = e < E ? logit[e] : -INFINITY;
+    p[i] = e < E ? logits[(size_t)m * E + e] : -INFINITY;
     mx = fmaxf(mx, p[i]);
   }
   mx = wave_max(mx);
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int e = lane + 64 * i;
-    p[i] = e < E ? expf(p[i] - mx) : 0.f;
+    p[i] = lane + 64 * i < E ? expf(p[i] - mx) : 0.f;
     sum += p[i];
   }
   sum = wave_sum(sum);
@@ -948,15 +954,41 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
     }
   }
   __syncthreads();
-  if (t == 0) {
-    int off = 0, na = 0;
-    for (int i = 0; i < E; ++i) {
-      s_off[i] = off;
-      off += s_cnt[i];
-      if (s_cnt[i]) active[na++] = i;
+  if (t < 64) {
+    // wave 0: exclusive prefix of the counts and of the active flags over
+    // E <= 256 experts, 4 consecutive experts per lane
+    int c[4], f[4], sc = 0, sf = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * t + i;
+      c[i] = e < E ? s_cnt[e] : 0;
+      f[i] = c[i] > 0;
+      sc += c[i];
+      sf += f[i];
     }
-    s_off[E] = off;
-    *n_active = na;
+    int ic = sc, jf = sf;  // inclusive scans across lanes
+    for (int o = 1; o < 64; o <<= 1) {
+      const int uc = __shfl_up(ic, o), uf = __shfl_up(jf, o);
+      if (t >= o) {
+        ic += uc;
+        jf += uf;
+      }
+    }
+    int off = ic - sc, na = jf - sf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * t + i;
+      if (e < E) {
+        s_off[e] = off;
+        if (f[i]) active[na] = e;
+      }
+      off += c[i];
+      na += f[i];
+    }
+    if (t == 63) {
+      s_off[E] = ic;
+      *n_active = jf;
+    }
   }
   __syncthreads();
   for (int i = t; i <= E; i += kChunk) offsets[i] = s_off[i];
@@ -1007,7 +1039,7 @@ struct MoeLinear {
   int n_segs, seg_n, K, ldo;
 };
 
-template <int WAVES>
+template <int WAVES, int kU>
 __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
   __shared__ float red[WAVES][4][64];
   const int slot = blockIdx.y;
@@ -1039,7 +1071,6 @@ __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
       srow[i] = a.as + (size_t)(a.row_of ? a.row_of[qi] : qi) * kgroups;
     }
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    constexpr int kU = 4;
     for (int kb = wave; kb < kgroups; kb += WAVES * kU) {
       uint4 wv[kU][2], av[kU][2];
       float wsv[kU], sav[kU][4];
@@ -1295,16 +1326,22 @@ extern "C" int ecf8_decode_attention(const void *q, const void *k_cache, const v
 }
 
 extern "C" int ecf8_moe_route(const void *x, const void *router_w, int64_t M, int64_t H, int E,
-                              int top_k, int *topk_idx, float *topk_w, void *stream) {
-  if (!x || !router_w || !topk_idx || !topk_w || M <= 0 || H <= 0 || E <= 0 || top_k <= 0)
+                              int top_k, float *logits, int *topk_idx, float *topk_w,
+                              void *stream) {
+  if (!x || !router_w || !logits || !topk_idx || !topk_w || M <= 0 || H <= 0 || E <= 0 ||
+      top_k <= 0)
     return ECF8_ERR_INVALID_ARG;
-  if (H % 512 || H > 8192 || E > 256 || top_k > 16 || top_k > E || M > 0x7fffffff)
+  if (H % 512 || H > (1 << 20) || E > 256 || top_k > 16 || top_k > E || M > (1 << 16))
     return ECF8_ERR_UNSUPPORTED;
-  if (!aligned(x, 16) || !aligned(router_w, 16) || !aligned(topk_idx, 4) || !aligned(topk_w, 4))
+  if (!aligned(x, 16) || !aligned(router_w, 16) || !aligned(logits, 4) || !aligned(topk_idx, 4) ||
+      !aligned(topk_w, 4))
     return ECF8_ERR_MISALIGNED;
-  moe_route_kernel<<<(unsigned)M, 256, 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(router_w), (int)H, E, top_k,
-      topk_idx, topk_w);
+  moe_logits_kernel<<<dim3((unsigned)((E + 3) / 4), (unsigned)((M + 3) / 4)), 256, 0,
+                      as_stream(stream)>>>(static_cast<const uint16_t *>(x),
+                                           static_cast<const uint16_t *>(router_w), (int)M,
+                                           (int)H, E, logits);
+  moe_topk_kernel<<<(unsigned)((M + 3) / 4), 256, 0, as_stream(stream)>>>(logits, (int)M, E,
+                                                                          top_k, topk_idx, topk_w);
   return launched();
 }
 
@@ -1341,10 +1378,14 @@ extern "C" int ecf8_moe_linear(const void *aq, const float *as, const int *row_o
               reinterpret_cast<const uint64_t *>(weight_scales), static_cast<uint16_t *>(out),
               n_segs, (int)seg_n, (int)K, (int)ldo};
   const dim3 grid((unsigned)(n_segs * seg_n / 16), (unsigned)n_experts);
-  if (K / kGroup >= 16)
-    moe_linear16_kernel<8><<<grid, 512, 0, as_stream(stream)>>>(a);
+  // each wave's share of the K groups in one batch of loads where it fits
+  const int64_t kg = K / kGroup;
+  if (kg <= 8)
+    moe_linear16_kernel<4, 2><<<grid, 256, 0, as_stream(stream)>>>(a);
+  else if (kg <= 16)
+    moe_linear16_kernel<8, 2><<<grid, 512, 0, as_stream(stream)>>>(a);
   else
-    moe_linear16_kernel<4><<<grid, 256, 0, as_stream(stream)>>>(a);
+    moe_linear16_kernel<8, 4><<<grid, 512, 0, as_stream(stream)>>>(a);
   return launched();
 }
 

@@ -235,6 +235,7 @@ class MoeRouting:
         P = M * top_k
         i32 = dict(dtype=torch.int32, device=device)
         self.M, self.top_k, self.E = M, top_k, n_experts
+        self.logits = torch.zeros(M, n_experts, dtype=torch.float32, device=device)
         self.topk_idx = torch.zeros(M, top_k, **i32)
         self.topk_w = torch.zeros(M, top_k, dtype=torch.float32, device=device)
         self.offsets = torch.zeros(n_experts + 1, **i32)
@@ -256,8 +257,8 @@ def moe_route(x, router_w, M: int, r: MoeRouting):
     if tuple(router_w.shape) != (r.E, H) or not 1 <= M <= r.M:
         raise ECF8Error(f"router_w must be [{r.E}, {H}] and 1 <= M <= {r.M}")
     check(lib().ecf8_moe_route(x.data_ptr(), router_w.data_ptr(), M, H, r.E, r.top_k,
-                               r.topk_idx.data_ptr(), r.topk_w.data_ptr(), _stream(x)),
-          "ecf8_moe_route")
+                               r.logits.data_ptr(), r.topk_idx.data_ptr(), r.topk_w.data_ptr(),
+                               _stream(x)), "ecf8_moe_route")
 
 
 def moe_group(r: MoeRouting, M: int):

@@ -117,13 +117,14 @@ int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cach
  * the reference runs transformers' own MoE forward over hooked experts.
  */
 
-/* Router: logits = x [M, H] (bf16) . router_w [E, H]^T (bf16) in fp32,
- * softmax over E, the top_k largest probabilities (ties to the lower
- * expert), renormalized to sum 1: topk_idx int32 [M, top_k] (descending
- * probability), topk_w fp32 [M, top_k].  H a multiple of 512, <= 8192;
- * E <= 256; top_k <= 16. */
+/* Router: logits fp32 [M, E] (a work buffer the caller owns) = x [M, H]
+ * (bf16) . router_w [E, H]^T (bf16) with fp32 products, softmax over E,
+ * the top_k largest probabilities (ties to the lower expert), renormalized
+ * to sum 1: topk_idx int32 [M, top_k] (descending probability), topk_w
+ * fp32 [M, top_k].  Two launches.  H a multiple of 512; E <= 256;
+ * top_k <= 16; M <= 65536. */
 int ecf8_moe_route(const void *x, const void *router_w, int64_t M, int64_t H, int E, int top_k,
-                   int *topk_idx, float *topk_w, void *stream);
+                   float *logits, int *topk_idx, float *topk_w, void *stream);
 
 /* Group the P = M * top_k (token, expert) pairs by expert (P <= 8192,
  * E <= 256): expert e's pairs take sorted positions [offsets[e],

@@ -184,11 +184,14 @@ def test_moe_kernels_reject_before_launch():
 
     L = lib()
     fake = 1 << 20
-    assert L.ecf8_moe_route(None, fake, 16, 2048, 128, 8, fake, fake, None) == 1
-    assert L.ecf8_moe_route(fake, fake, 16, 1000, 128, 8, fake, fake, None) == 2   # H % 512
-    assert L.ecf8_moe_route(fake, fake, 16, 2048, 300, 8, fake, fake, None) == 2   # E > 256
-    assert L.ecf8_moe_route(fake, fake, 16, 2048, 128, 20, fake, fake, None) == 2  # top_k > 16
-    assert L.ecf8_moe_route(fake + 2, fake, 16, 2048, 128, 8, fake, fake, None) == 3
+    rt = L.ecf8_moe_route
+    assert rt(None, fake, 16, 2048, 128, 8, fake, fake, fake, None) == 1
+    assert rt(fake, fake, 16, 2048, 128, 8, None, fake, fake, None) == 1     # no logits buffer
+    assert rt(fake, fake, 16, 1000, 128, 8, fake, fake, fake, None) == 2     # H % 512
+    assert rt(fake, fake, 16, 2048, 300, 8, fake, fake, fake, None) == 2     # E > 256
+    assert rt(fake, fake, 16, 2048, 128, 20, fake, fake, fake, None) == 2    # top_k > 16
+    assert rt(fake, fake, 1 << 17, 2048, 128, 8, fake, fake, fake, None) == 2
+    assert rt(fake + 2, fake, 16, 2048, 128, 8, fake, fake, fake, None) == 3
     g = L.ecf8_moe_group
     assert g(None, fake, 16, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 1
     assert g(fake, fake, 1100, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 2  # P > 8192
