@@ -78,6 +78,8 @@ def _decode_call(**kw):
     (dict(out=0x6001), 3),      # 16-byte output alignment
     (dict(encoded=0x2008), 3),  # 16-byte bitstream alignment
     (dict(n_bytes=2**31), 2),   # positions are 32-bit, as in the reference
+    (dict(n=2**31), 2),
+    (dict(n=2**31 - 64), 2),    # the last 64 below 2^31 are kept clear of the clamped loads
     (dict(packed=0x3002), 3),
     (dict(gaps=0), 1),
     (dict(kind=2), 1),          # unknown table kind

@@ -146,13 +146,21 @@ def test_config1_4096x4096_bit_exact(kind, cuda_device, oracle_native):
     assert np.array_equal(want, got)
 
 
-def test_config2_qwen3_layer_bit_exact(cuda_device):
-    from ecf8_amd.decode import build_table
+@pytest.fixture(scope="module")
+def qwen3_layer_flat():
+    """One Qwen3-8B-shaped layer's weights, flattened in the reference's
+    order (uint8 view)."""
     from ecf8_amd.synth import flat_block, qwen3_8b_layer
 
-    _say("config2 qwen3-8b layer")
     flat, _ = flat_block(qwen3_8b_layer(seed=0))
-    flat_u8 = flat.view(torch.uint8).numpy()
+    return flat.view(torch.uint8)
+
+
+def test_config2_qwen3_layer_bit_exact(cuda_device, qwen3_layer_flat):
+    from ecf8_amd.decode import build_table
+
+    _say("config2 qwen3-8b layer")
+    flat_u8 = qwen3_layer_flat.numpy()
     block = _compress(flat_u8)
     d = _dev_block(block, cuda_device)
     assert build_table(d["luts"]).kind == DFA  # the automaton runs this workload
@@ -161,6 +169,35 @@ def test_config2_qwen3_layer_bit_exact(cuda_device):
         got = _gpu_decode(block, cuda_device, kind=kind)
         assert got.size == 192_937_984
         assert np.array_equal(got, flat_u8)
+
+
+def test_largest_block_the_format_allows(cuda_device, qwen3_layer_flat):
+    """One block of 2^31 - 2^17 elements, near the format's limit (32-bit
+    element and byte counts, dfloat/run/decode.cu:23-25; the host refuses
+    more than 2^31 - 65): the Qwen3 layer tiled 12 times, compressed as one
+    block, decoded bit-exact by the automaton kernel.  Positions past 2^30
+    exercise the kernel's 32-bit position arithmetic."""
+    from ecf8_amd.compress import compress_flat
+    from ecf8_amd.decode import build_table, decode_into, largest_block, min_code_bits
+
+    n = 2 ** 31 - 2 ** 17
+    reps = -(-n // qwen3_layer_flat.numel())
+    big = qwen3_layer_flat.repeat(reps)[:n]
+    _say(f"largest block: compressing {n} elements")
+    res = compress_flat(big.view(torch.float8_e4m3fn))
+    d = {k: res[k].contiguous().to(cuda_device) for k in KEYS}
+    table = build_table(d["luts"])
+    assert table.kind == DFA
+    out = torch.empty(n + 4096, dtype=torch.uint8, device=cuda_device)
+    out[n:] = 0x5A
+    _say("largest block: decoding")
+    decode_into(out, d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
+                d["gaps"], table=table, n_elements=n,
+                max_block_elements=largest_block(d["output_positions"]),
+                min_code_bits=min_code_bits(d["luts"]))
+    torch.cuda.synchronize()
+    assert torch.equal(out[:n], big.to(cuda_device))
+    assert bool((out[n:] == 0x5A).all())
 
 
 @pytest.mark.parametrize("kind", [MULTI, DFA])
