@@ -387,6 +387,7 @@ def moe_generate(args):
 
     from ecf8_amd.llm import timed_generate
     from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, random_moe_model
+    from ecf8_amd.prefetch import LayerPrefetcher
     from ecf8_amd.run import TensorManager
 
     dev = torch.device("cuda", 0)
@@ -399,13 +400,17 @@ def moe_generate(args):
     g = torch.Generator().manual_seed(args.seed + 7)
     prompt = torch.randint(0, cfg.vocab, (B, T), generator=g)
     results = {}
-    for mode in ("fp8", "ecf8"):
+    for mode in ("fp8", "ecf8", "ecf8_prefetch"):
         if mode == "ecf8":
             t0 = time.time()
             compress_moe_layers(model, drawn)
             torch.cuda.synchronize()
             print(f"[bench] blocks compressed in {time.time() - t0:.1f}s", file=sys.stderr,
                   flush=True)
+        if mode == "ecf8_prefetch":
+            # the next layer's attention block decoded on a side stream
+            LayerPrefetcher([layer.self_attn for layer in model.model.layers], dev,
+                            workgroups_per_cu=args.prefetch_workgroups).install()
         TensorManager.clear_device()
         torch.cuda.empty_cache()
         t0 = time.time()
@@ -423,8 +428,11 @@ def moe_generate(args):
                                list(model.parameters()) + list(model.buffers())) / 2**20
         results[mode] = r
         del runner
-    same = torch.equal(results["fp8"]["tokens"], results["ecf8"]["tokens"])
-    fp8, ecf8 = results["fp8"], results["ecf8"]
+    same = all(torch.equal(results["fp8"]["tokens"], results[m]["tokens"])
+               for m in ("ecf8", "ecf8_prefetch"))
+    fp8 = results["fp8"]
+    best = max(("ecf8", "ecf8_prefetch"), key=lambda m: results[m]["tokens_per_s"])
+    ecf8 = results[best]
 
     def summary(r):
         return {"tokens_per_s": round(r["tokens_per_s"], 1), "latency_s": round(r["latency_s"], 4),
@@ -449,6 +457,9 @@ def moe_generate(args):
                                   "(device-side selection, one batched launch per layer)"},
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
+        "ecf8_mode": best,
+        "ecf8_attention_in_hook": summary(results["ecf8"]),
+        "ecf8_attention_prefetched": summary(results["ecf8_prefetch"]),
         "experts_routed_last_step": ecf8["experts_routed_last_step"],
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,

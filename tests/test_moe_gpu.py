@@ -207,6 +207,18 @@ def test_compressed_moe_matches_uncompressed_exactly(small_moe_models, cuda_devi
             for rep in range(2):
                 toks = r.generate(prompt, new).cpu()
                 results[(name, graph, rep)] = (toks, r.logits.float().cpu())
+    from ecf8_amd.prefetch import LayerPrefetcher
+
+    # the next layer's attention block decoded on a side stream
+    LayerPrefetcher([layer.self_attn for layer in comp.model.layers], cuda_device).install()
+    for graph in (False, True):
+        print(f"[moe] e2e ecf8 prefetch graph={graph}", flush=True)
+        r = Qwen3MoeRunner(comp, B, T, T + new, cuda_device)
+        if graph:
+            r.capture()
+        for rep in range(2):
+            toks = r.generate(prompt, new).cpu()
+            results[("ecf8_prefetch", graph, rep)] = (toks, r.logits.float().cpu())
     base_t, base_l = results[("fp8", False, 0)]
     for key, (t, l) in results.items():
         assert torch.equal(t, base_t), key
