@@ -60,6 +60,8 @@ _SIGNATURES = {
     "ecf8_attention_work_floats": ([_i64, _i32, _i64], _i64),
     "ecf8_decode_attention": ([_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _i64, _vp, _vp, _vp,
                                _vp], _i32),
+    "ecf8_decode_attention_fused": ([_vp, _i64, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _i64,
+                                     _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
     "ecf8_moe_route": ([_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "ecf8_moe_group": ([_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "ecf8_moe_linear": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _i64,

@@ -541,6 +541,30 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restri
 
 // --------------------------------------------- per-head norm + rotary + KV
 
+// One wave, one head row of 128 bf16 values (lane l holds dims 2l, 2l+1):
+// RMSNorm over the head (bf16 weights nw), then the rotary embedding at
+// position p (rotate-half convention, cos/sin tables [Lmax, 64]); returns
+// the lane's two results as packed bf16.
+__device__ __forceinline__ uint32_t norm_rope_pair(uint32_t x2, const uint16_t *__restrict__ nw,
+                                                   float eps, const float *__restrict__ cosv,
+                                                   const float *__restrict__ sinv, int p,
+                                                   int lane) {
+  float x0 = bf16_f32(x2 & 0xffffu), x1 = bf16_f32(x2 >> 16);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float rs = rsqrtf(ss / (float)kHeadDim + eps);
+  const uint32_t w2 = *reinterpret_cast<const uint32_t *>(nw + 2 * lane);
+  x0 = x0 * rs * bf16_f32(w2 & 0xffffu);
+  x1 = x1 * rs * bf16_f32(w2 >> 16);
+  const float y0 = __shfl_xor(x0, 32), y1 = __shfl_xor(x1, 32);  // dims d +- 64
+  const int j = (2 * lane) & 63;
+  const float c0 = cosv[p * 64 + j], c1 = cosv[p * 64 + j + 1];
+  const float s0 = sinv[p * 64 + j], s1 = sinv[p * 64 + j + 1];
+  const float sg = lane < 32 ? -1.f : 1.f;
+  x0 = x0 * c0 + sg * y0 * s0;
+  x1 = x1 * c1 + sg * y1 * s1;
+  return f32_bf16(x0) | (f32_bf16(x1) << 16);
+}
+
 // One wave per (token, head) of the fused qkv projection output
 // [B*T, (Hq + 2 Hkv) * 128]: q and k heads get RMSNorm over the head
 // (weights qn / kn) and the rotary embedding at position pos[0] + t
@@ -562,26 +586,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   if (p < 0 || p >= Lmax) return;
   const uint32_t x2 = *reinterpret_cast<const uint32_t *>(qkv + (size_t)tok * H * kHeadDim +
                                                           hh * kHeadDim + 2 * lane);
-  uint32_t outw;
-  if (hh >= Hq + Hkv) {
-    outw = x2;
-  } else {
-    float x0 = bf16_f32(x2 & 0xffffu), x1 = bf16_f32(x2 >> 16);
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
-    const float rs = rsqrtf(ss / (float)kHeadDim + eps);
-    const uint16_t *nw = hh < Hq ? qn : kn;
-    const uint32_t w2 = *reinterpret_cast<const uint32_t *>(nw + 2 * lane);
-    x0 = x0 * rs * bf16_f32(w2 & 0xffffu);
-    x1 = x1 * rs * bf16_f32(w2 >> 16);
-    const float y0 = __shfl_xor(x0, 32), y1 = __shfl_xor(x1, 32);  // dims d +- 64
-    const int j = (2 * lane) & 63;
-    const float c0 = cosv[p * 64 + j], c1 = cosv[p * 64 + j + 1];
-    const float s0 = sinv[p * 64 + j], s1 = sinv[p * 64 + j + 1];
-    const float sg = lane < 32 ? -1.f : 1.f;
-    x0 = x0 * c0 + sg * y0 * s0;
-    x1 = x1 * c1 + sg * y1 * s1;
-    outw = f32_bf16(x0) | (f32_bf16(x1) << 16);
-  }
+  const uint32_t outw =
+      hh >= Hq + Hkv ? x2 : norm_rope_pair(x2, hh < Hq ? qn : kn, eps, cosv, sinv, p, lane);
   uint16_t *dst;
   if (hh < Hq) {
     dst = q_out + (((size_t)b * Hq + hh) * T + t) * kHeadDim;
@@ -595,20 +601,64 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 
 // ------------------------------------------------------ decode attention
 
+// Merge the splits [0, used) of one (b, head) (partials m, l [B*Hq, S] and
+// acc [B*Hq, S, 128]) and write the head's 128 outputs: quantized as one
+// o-projection group, and optionally as bf16.  One wave, two dims per lane.
+__device__ __forceinline__ void combine_head(const float *__restrict__ wm,
+                                             const float *__restrict__ wl,
+                                             const float *__restrict__ wacc, size_t bh, int S,
+                                             int used, int lane, uint8_t *__restrict__ oq,
+                                             float *__restrict__ os, uint16_t *__restrict__ ob) {
+  float mx = -INFINITY;
+  for (int s = 0; s < used; ++s) mx = fmaxf(mx, wm[bh * S + s]);
+  float l = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int s = 0; s < used; ++s) {
+    const float f = expf(wm[bh * S + s] - mx);
+    l = fmaf(f, wl[bh * S + s], l);
+    const float *ap = wacc + (bh * S + s) * kHeadDim + 2 * lane;
+    a0 = fmaf(f, ap[0], a0);
+    a1 = fmaf(f, ap[1], a1);
+  }
+  a0 /= l;
+  a1 /= l;
+  if (ob) reinterpret_cast<uint32_t *>(ob)[bh * 64 + lane] = f32_bf16(a0) | (f32_bf16(a1) << 16);
+  float amax = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
+  const float sc = amax > 0.f ? amax / kFp8Max : 1.f;
+  const uint32_t q2 = f32_e4m3(a0 / sc) | (f32_e4m3(a1 / sc) << 8);
+  reinterpret_cast<uint16_t *>(oq)[bh * 64 + lane] = (uint16_t)q2;
+  if (lane == 0) os[bh] = sc;
+}
+
+// What the fused form of the split kernel needs besides the caches.
+struct AttnFused {
+  const uint16_t *qkv;  // [B, (Hq + 2 Hkv) * 128], one new token per sequence
+  const uint16_t *qn, *kn;
+  float eps;
+  const float *cosv, *sinv;
+};
+
 // Split-sequence attention for one new token per sequence: workgroup
 // (b * Hkv + kh, split) handles positions [split*256, +256) of the L =
 // pos[0] + 1 cached ones for the G = Hq / Hkv query heads sharing kv head
 // kh.  Scores: one lane per position; softmax partials per head; PV: one
 // thread per (head, dim pair).  Partials go to work: m, l [B*Hq, S] and
 // acc [B*Hq, S, 128].
-template <int G>
+//
+// kFused: q comes from the projection output through the per-head norm and
+// rotary embedding (norm_rope_pair), and the split holding position pos[0]
+// first writes the new token's k and v to the caches -- the work of
+// qk_norm_rope_kernel, in the same arithmetic.  (Merging the splits in the
+// last workgroup to finish would need device-scope fences, which on this
+// multi-XCD part write back and invalidate the whole L2: the merge stays a
+// kernel of its own.)
+template <int G, bool kFused>
 __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restrict__ q,
-                                                         const uint16_t *__restrict__ kc,
-                                                         const uint16_t *__restrict__ vc,
+                                                         uint16_t *__restrict__ kc,
+                                                         uint16_t *__restrict__ vc,
                                                          const int *__restrict__ pos, int Hkv,
                                                          int Lmax, int S, float *__restrict__ wm,
                                                          float *__restrict__ wl,
-                                                         float *__restrict__ wacc) {
+                                                         float *__restrict__ wacc, AttnFused fu) {
   __shared__ float qs[G][kHeadDim];
   __shared__ float pw[G][kAttnChunk];
   __shared__ float part[4 * G * kHeadDim];  // PV partials [wave][head][dim]
@@ -617,7 +667,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restr
   const int b = bk / Hkv, kh = bk % Hkv;
   const int Hq = Hkv * G;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  int L = pos[0] + 1;
+  const int p = pos[0];
+  int L = p + 1;
   L = L < 1 ? 1 : (L > Lmax ? Lmax : L);
   const int c0 = split * kAttnChunk;
   const size_t head0 = (size_t)b * Hq + kh * G;
@@ -630,8 +681,32 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const uint16_t *__restr
   }
   const int n = min(kAttnChunk, L - c0);
   const float scale = rsqrtf((float)kHeadDim);
-  for (int i = t; i < G * kHeadDim; i += 256) {
-    qs[i / kHeadDim][i % kHeadDim] = bf16_f32(q[(head0 + i / kHeadDim) * kHeadDim + i % kHeadDim]) * scale;
+  if constexpr (kFused) {
+    const uint16_t *row = fu.qkv + (size_t)b * (Hq + 2 * Hkv) * kHeadDim;
+    const int pc = min(max(p, 0), Lmax - 1);  // rotary row (p is in range for a valid call)
+    for (int h = wave; h < G; h += 4) {
+      const uint32_t x2 =
+          *reinterpret_cast<const uint32_t *>(row + (kh * G + h) * kHeadDim + 2 * lane);
+      const uint32_t y2 = norm_rope_pair(x2, fu.qn, fu.eps, fu.cosv, fu.sinv, pc, lane);
+      qs[h][2 * lane] = bf16_f32(y2 & 0xffffu) * scale;
+      qs[h][2 * lane + 1] = bf16_f32(y2 >> 16) * scale;
+    }
+    if (p >= c0 && p < c0 + kAttnChunk && p < Lmax && wave < 2) {
+      // the new token's k (wave 0) and v (wave 1) go to the caches first
+      const int hh = Hq + wave * Hkv + kh;
+      const uint32_t x2 = *reinterpret_cast<const uint32_t *>(row + hh * kHeadDim + 2 * lane);
+      const uint32_t y2 = wave == 0 ? norm_rope_pair(x2, fu.kn, fu.eps, fu.cosv, fu.sinv, p, lane)
+                                    : x2;
+      uint16_t *cache = wave == 0 ? kc : vc;
+      *reinterpret_cast<uint32_t *>(cache + (((size_t)b * Hkv + kh) * Lmax + p) * kHeadDim +
+                                    2 * lane) = y2;
+    }
+    __threadfence_block();  // the row is read back below by other waves
+  } else {
+    for (int i = t; i < G * kHeadDim; i += 256) {
+      qs[i / kHeadDim][i % kHeadDim] =
+          bf16_f32(q[(head0 + i / kHeadDim) * kHeadDim + i % kHeadDim]) * scale;
+    }
   }
   __syncthreads();
 
@@ -745,28 +820,10 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
                                                           int S, uint8_t *__restrict__ oq,
                                                           float *__restrict__ os,
                                                           uint16_t *__restrict__ ob) {
-  const int bh = blockIdx.x, lane = threadIdx.x;
   int L = pos[0] + 1;
   L = L < 1 ? 1 : (L > Lmax ? Lmax : L);
   const int used = (L + kAttnChunk - 1) / kAttnChunk;
-  float mx = -INFINITY;
-  for (int s = 0; s < used; ++s) mx = fmaxf(mx, wm[(size_t)bh * S + s]);
-  float l = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int s = 0; s < used; ++s) {
-    const float f = expf(wm[(size_t)bh * S + s] - mx);
-    l = fmaf(f, wl[(size_t)bh * S + s], l);
-    const float *ap = wacc + ((size_t)bh * S + s) * kHeadDim + 2 * lane;
-    a0 = fmaf(f, ap[0], a0);
-    a1 = fmaf(f, ap[1], a1);
-  }
-  a0 /= l;
-  a1 /= l;
-  if (ob) reinterpret_cast<uint32_t *>(ob)[(size_t)bh * 64 + lane] = f32_bf16(a0) | (f32_bf16(a1) << 16);
-  float amax = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
-  const float sc = amax > 0.f ? amax / kFp8Max : 1.f;
-  const uint32_t q2 = f32_e4m3(a0 / sc) | (f32_e4m3(a1 / sc) << 8);
-  reinterpret_cast<uint16_t *>(oq)[(size_t)bh * 64 + lane] = (uint16_t)q2;
-  if (lane == 0) os[bh] = sc;
+  combine_head(wm, wl, wacc, blockIdx.x, S, used, threadIdx.x, oq, os, ob);
 }
 
 // ---------------------------------------------------- FP8 block dequantize
@@ -1311,14 +1368,50 @@ extern "C" int ecf8_decode_attention(const void *q, const void *k_cache, const v
   float *wm = work, *wl = work + B * Hq * S, *wacc = work + 2 * B * Hq * S;
   const dim3 grid((unsigned)(B * Hkv), (unsigned)S);
   const auto *qp = static_cast<const uint16_t *>(q);
-  const auto *kp = static_cast<const uint16_t *>(k_cache);
-  const auto *vp = static_cast<const uint16_t *>(v_cache);
+  auto *kp = static_cast<uint16_t *>(const_cast<void *>(k_cache));
+  auto *vp = static_cast<uint16_t *>(const_cast<void *>(v_cache));
+  const AttnFused none{};
   if (Hq == 4 * Hkv)
-    attn_split_kernel<4><<<grid, 256, 0, as_stream(stream)>>>(qp, kp, vp, pos, Hkv, (int)Lmax,
-                                                              (int)S, wm, wl, wacc);
+    attn_split_kernel<4, false><<<grid, 256, 0, as_stream(stream)>>>(
+        qp, kp, vp, pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc, none);
   else
-    attn_split_kernel<8><<<grid, 256, 0, as_stream(stream)>>>(qp, kp, vp, pos, Hkv, (int)Lmax,
-                                                              (int)S, wm, wl, wacc);
+    attn_split_kernel<8, false><<<grid, 256, 0, as_stream(stream)>>>(
+        qp, kp, vp, pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc, none);
+  attn_combine_kernel<<<(unsigned)(B * Hq), 64, 0, as_stream(stream)>>>(
+      wm, wl, wacc, pos, (int)Lmax, (int)S, static_cast<uint8_t *>(out_q), out_scale,
+      static_cast<uint16_t *>(out_bf16));
+  return launched();
+}
+
+extern "C" int ecf8_decode_attention_fused(const void *qkv, int64_t B, int Hq, int Hkv,
+                                           const void *q_norm, const void *k_norm, float eps,
+                                           const float *cos_t, const float *sin_t, const int *pos,
+                                           int64_t Lmax, void *k_cache, void *v_cache,
+                                           float *work, int64_t work_floats, void *out_q,
+                                           float *out_scale, void *out_bf16, void *stream) {
+  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !work ||
+      !out_q || !out_scale || B <= 0 || Hq <= 0 || Hkv <= 0 || Lmax <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if ((Hq != 4 * Hkv && Hq != 8 * Hkv) || B * Hkv > 65535 || Lmax > (1 << 24))
+    return ECF8_ERR_UNSUPPORTED;
+  const int64_t S = (Lmax + kAttnChunk - 1) / kAttnChunk;
+  if (work_floats < B * Hq * S * (kHeadDim + 2)) return ECF8_ERR_CAPACITY;
+  if (!aligned(qkv, 4) || !aligned(q_norm, 4) || !aligned(k_norm, 4) || !aligned(k_cache, 16) ||
+      !aligned(v_cache, 4) || !aligned(work, 8) || !aligned(out_q, 2) ||
+      (out_bf16 && !aligned(out_bf16, 4)))
+    return ECF8_ERR_MISALIGNED;
+  float *wm = work, *wl = work + B * Hq * S, *wacc = work + 2 * B * Hq * S;
+  const AttnFused fu{static_cast<const uint16_t *>(qkv), static_cast<const uint16_t *>(q_norm),
+                     static_cast<const uint16_t *>(k_norm), eps, cos_t, sin_t};
+  const dim3 grid((unsigned)(B * Hkv), (unsigned)S);
+  auto *kp = static_cast<uint16_t *>(k_cache);
+  auto *vp = static_cast<uint16_t *>(v_cache);
+  if (Hq == 4 * Hkv)
+    attn_split_kernel<4, true><<<grid, 256, 0, as_stream(stream)>>>(
+        nullptr, kp, vp, pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc, fu);
+  else
+    attn_split_kernel<8, true><<<grid, 256, 0, as_stream(stream)>>>(
+        nullptr, kp, vp, pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc, fu);
   attn_combine_kernel<<<(unsigned)(B * Hq), 64, 0, as_stream(stream)>>>(
       wm, wl, wacc, pos, (int)Lmax, (int)S, static_cast<uint8_t *>(out_q), out_scale,
       static_cast<uint16_t *>(out_bf16));

@@ -297,15 +297,16 @@ class Qwen3Runner(_GreedyRunner):
                                          (a.k_proj.weight, a.k_proj.weight_scale_inv),
                                          (a.v_proj.weight, a.v_proj.weight_scale_inv)],
                    self.qkv)(aqH, asH, M)
-        K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
-                       self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
         aqA, asA = self.aq[Hq * 128], self.as_[Hq * 128]
         if prefill:
+            K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
+                           self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
             self._prefill_attention(index, T)
             K.act_quant(self.attn, M, aqA, asA)
         else:
-            K.decode_attention(self.q, self.kc[index], self.vc[index], self.pos, self.work, aqA,
-                               asA, Hq)
+            K.decode_attention_fused(self.qkv, B, Hq, Hkv, a.q_norm.weight, a.k_norm.weight,
+                                     cfg.eps, self.cos, self.sin, self.pos, self.kc[index],
+                                     self.vc[index], self.work, aqA, asA)
         self._plan(layer, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
                    self.o)(aqA, asA, M)
         K.rmsnorm(self.res, layer.post_attention_layernorm.weight, cfg.eps, M, x=self.o,

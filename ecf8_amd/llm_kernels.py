@@ -170,10 +170,11 @@ def qk_norm_rope(qkv, B, T, Hq, Hkv, q_norm, k_norm, eps, cos_t, sin_t, pos, q_o
 
 
 def attention_work(B, Hq, Lmax, device) -> torch.Tensor:
+    """Work buffer of both attention forms (split partials)."""
     n = lib().ecf8_attention_work_floats(B, Hq, Lmax)
     if n < 0:
         raise ECF8Error("bad attention work size")
-    return torch.empty(n, dtype=torch.float32, device=device)
+    return torch.zeros(n, dtype=torch.float32, device=device)
 
 
 def decode_attention(q, k_cache, v_cache, pos, work, out_q, out_scale, Hq, out_bf16=None):
@@ -201,6 +202,41 @@ def decode_attention(q, k_cache, v_cache, pos, work, out_q, out_scale, Hq, out_b
                                       pos.data_ptr(), B, Hq, Hkv, Lmax, work.data_ptr(),
                                       work.numel(), out_q.data_ptr(), out_scale.data_ptr(),
                                       _ptr(out_bf16), _stream(q)), "ecf8_decode_attention")
+
+
+def decode_attention_fused(qkv, B, Hq, Hkv, q_norm, k_norm, eps, cos_t, sin_t, pos, k_cache,
+                           v_cache, work, out_q, out_scale, out_bf16=None):
+    """qk_norm_rope (one new token per sequence) folded into
+    decode_attention, same results: q/k/v from the projection output qkv
+    [>= B, (Hq + 2*Hkv) * 128], the new token's k/v written to the caches
+    at pos[0]."""
+    dev = qkv.device
+    for t, n in ((qkv, "qkv"), (q_norm, "q_norm"), (k_norm, "k_norm"), (k_cache, "k_cache"),
+                 (v_cache, "v_cache")):
+        _need(t, torch.bfloat16, n, dev)
+    _need(cos_t, torch.float32, "cos", dev)
+    _need(sin_t, torch.float32, "sin", dev)
+    _need(pos, torch.int32, "pos", dev)
+    _need(work, torch.float32, "work", dev)
+    _need(out_q, torch.float8_e4m3fn, "out_q", dev)
+    _need(out_scale, torch.float32, "out_scale", dev)
+    if out_bf16 is not None:
+        _need(out_bf16, torch.bfloat16, "out_bf16", dev)
+    Lmax = k_cache.shape[2]
+    if (tuple(k_cache.shape) != (B, Hkv, Lmax, 128) or v_cache.shape != k_cache.shape
+            or cos_t.shape != (Lmax, 64) or sin_t.shape != (Lmax, 64)):
+        raise ECF8Error("caches must be [B, Hkv, Lmax, 128], rotary tables [Lmax, 64]")
+    if (pos.numel() < 1 or q_norm.numel() != 128 or k_norm.numel() != 128
+            or qkv.numel() < B * (Hq + 2 * Hkv) * 128):
+        raise ECF8Error("pos, q_norm / k_norm [128] or qkv does not fit")
+    if (out_q.numel() < B * Hq * 128 or out_scale.numel() < B * Hq
+            or (out_bf16 is not None and out_bf16.numel() < B * Hq * 128)):
+        raise ECF8Error("outputs too small")
+    check(lib().ecf8_decode_attention_fused(
+        qkv.data_ptr(), B, Hq, Hkv, q_norm.data_ptr(), k_norm.data_ptr(), float(eps),
+        cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), Lmax, k_cache.data_ptr(),
+        v_cache.data_ptr(), work.data_ptr(), work.numel(), out_q.data_ptr(), out_scale.data_ptr(),
+        _ptr(out_bf16), _stream(qkv)), "ecf8_decode_attention_fused")
 
 
 def dequant_fp8_block(weight, scale_inv, out=None):

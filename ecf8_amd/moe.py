@@ -248,14 +248,15 @@ class Qwen3MoeRunner(_GreedyRunner):
                                      (a.k_proj.weight, a.k_proj.weight_scale_inv),
                                      (a.v_proj.weight, a.v_proj.weight_scale_inv)],
                    self.qkv)(self.aqH, self.asH, M)
-        K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
-                       self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
         if prefill:
+            K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
+                           self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
             self._prefill_attention(index, T)
             K.act_quant(self.attn, M, self.aqA, self.asA)
         else:
-            K.decode_attention(self.q, self.kc[index], self.vc[index], self.pos, self.work,
-                               self.aqA, self.asA, Hq)
+            K.decode_attention_fused(self.qkv, B, Hq, Hkv, a.q_norm.weight, a.k_norm.weight,
+                                     cfg.eps, self.cos, self.sin, self.pos, self.kc[index],
+                                     self.vc[index], self.work, self.aqA, self.asA)
         self._plan(a, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
                    self.o)(self.aqA, self.asA, M)
 

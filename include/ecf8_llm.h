@@ -92,7 +92,8 @@ int ecf8_qk_norm_rope(const void *qkv, int64_t B, int64_t T, int Hq, int Hkv, co
 int ecf8_dequant_fp8_block(const void *weight, const float *weight_scale, int64_t n, int64_t k,
                            void *out, void *stream);
 
-/* fp32 elements of the work buffer ecf8_decode_attention needs. */
+/* fp32 elements of the work buffer ecf8_decode_attention and
+ * ecf8_decode_attention_fused need. */
 int64_t ecf8_attention_work_floats(int64_t B, int Hq, int64_t Lmax);
 
 /*
@@ -107,6 +108,20 @@ int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cach
                           int64_t B, int Hq, int Hkv, int64_t Lmax, float *work,
                           int64_t work_floats, void *out_q, float *out_scale, void *out_bf16,
                           void *stream);
+
+/*
+ * ecf8_qk_norm_rope (T = 1) folded into ecf8_decode_attention, with the
+ * same arithmetic and results: q comes from the projection output qkv
+ * bf16 [B, (Hq + 2*Hkv) * 128] through the per-head norm and rotary
+ * embedding at position pos[0], and the workgroup whose split holds pos[0]
+ * writes the new token's k and v to the caches before reading them.  Two
+ * launches (the split kernel and the merge) instead of three.
+ */
+int ecf8_decode_attention_fused(const void *qkv, int64_t B, int Hq, int Hkv, const void *q_norm,
+                                const void *k_norm, float eps, const float *cos_t,
+                                const float *sin_t, const int *pos, int64_t Lmax, void *k_cache,
+                                void *v_cache, float *work, int64_t work_floats, void *out_q,
+                                float *out_scale, void *out_bf16, void *stream);
 
 /* ---------------------------------------------------------------- MoE
  * The routed-expert MLP of a Qwen3-MoE-shaped layer

@@ -164,6 +164,16 @@ def test_consumer_kernels_reject_before_launch():
                                    fake, None, None) == 2   # Hq != 4 Hkv
     assert L.ecf8_decode_attention(fake, fake, fake, fake, 2, 32, 8, 300, fake, 10, fake, fake,
                                    None, None) == 6         # work too small
+    fa = L.ecf8_decode_attention_fused
+    eps = ctypes.c_float(1e-6)
+    assert fa(None, 2, 32, 8, fake, fake, eps, fake, fake, fake, 300, fake, fake, fake, 10 ** 6,
+              fake, fake, None, None) == 1
+    assert fa(fake, 2, 32, 16, fake, fake, eps, fake, fake, fake, 300, fake, fake, fake, 10 ** 6,
+              fake, fake, None, None) == 2          # Hq / Hkv = 2
+    assert fa(fake, 2, 32, 8, fake, fake, eps, fake, fake, fake, 300, fake, fake, fake,
+              2 * 32 * 2 * 130 - 1, fake, fake, None, None) == 6   # work too small
+    assert fa(fake, 2, 32, 8, fake, fake, eps, fake, fake, fake, 300, fake, fake, fake + 4,
+              10 ** 6, fake, fake, None, None) == 3                # work 8-byte aligned
 
 
 def test_batched_select_rejects_before_launch():

@@ -530,3 +530,78 @@ def test_prefill_logits_follow_a_torch_forward(small_models, cuda_device):
     cos = torch.nn.functional.cosine_similarity(got.reshape(-1), ref.reshape(-1), dim=0).item()
     _say(f"[llm] prefill logits cosine {cos:.6f}")
     assert cos > 0.99, cos
+
+
+@pytest.mark.parametrize("G", [4, 8])
+def test_fused_attention_equals_the_unfused_pair(cuda_device, G):
+    """decode_attention_fused = qk_norm_rope (T = 1) + decode_attention, bit
+    for bit: outputs and the new token's cache rows, at positions inside,
+    at the start and at the end of a 256-position split; repeated calls
+    and graph replays with a moving position."""
+    from ecf8_amd.llm_kernels import (attention_work, decode_attention, decode_attention_fused,
+                                      qk_norm_rope)
+
+    dev = cuda_device
+    gen = torch.Generator().manual_seed(40 + G)
+    B, Hkv, Lmax = 3, 2, 600
+    Hq = G * Hkv
+    qkv = torch.randn(B, (Hq + 2 * Hkv) * 128, generator=gen).to(torch.bfloat16).to(dev)
+    qn = (1 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16).to(dev)
+    kn = (1 + 0.1 * torch.randn(128, generator=gen)).to(torch.bfloat16).to(dev)
+    cos, sin = (t.to(dev) for t in _rope_tables(Lmax))
+    kc0 = (torch.randn(B, Hkv, Lmax, 128, generator=gen) * 2).to(torch.bfloat16).to(dev)
+    vc0 = torch.randn(B, Hkv, Lmax, 128, generator=gen).to(torch.bfloat16).to(dev)
+    for p0 in (0, 255, 256, 517, Lmax - 1):
+        _say(f"[llm] fused attention G={G} pos={p0}")
+        pos = torch.tensor([p0], dtype=torch.int32, device=dev)
+        # unfused
+        kc, vc = kc0.clone(), vc0.clone()
+        q = torch.empty(B * Hq * 128, dtype=torch.bfloat16, device=dev)
+        qk_norm_rope(qkv, B, 1, Hq, Hkv, qn, kn, 1e-6, cos, sin, pos, q, kc, vc)
+        work = attention_work(B, Hq, Lmax, dev)
+        oq = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+        os_ = torch.empty(B, Hq, device=dev)
+        ob = torch.empty(B, Hq * 128, dtype=torch.bfloat16, device=dev)
+        decode_attention(q, kc, vc, pos, work, oq, os_, Hq, out_bf16=ob)
+        # fused, three calls in a row on one work buffer
+        kf, vf = kc0.clone(), vc0.clone()
+        workf = attention_work(B, Hq, Lmax, dev)
+        for _ in range(3):
+            oqf = torch.empty_like(oq)
+            osf = torch.empty_like(os_)
+            obf = torch.empty_like(ob)
+            decode_attention_fused(qkv, B, Hq, Hkv, qn, kn, 1e-6, cos, sin, pos, kf, vf, workf,
+                                   oqf, osf, out_bf16=obf)
+            torch.cuda.synchronize()
+            assert torch.equal(kf, kc) and torch.equal(vf, vc)
+            assert torch.equal(obf, ob)
+            assert torch.equal(osf, os_)
+            assert torch.equal(oqf.view(torch.uint8), oq.view(torch.uint8))
+    # graph replays with a moving position
+    pos = torch.tensor([300], dtype=torch.int32, device=dev)
+    kf, vf = kc0.clone(), vc0.clone()
+    workf = attention_work(B, Hq, Lmax, dev)
+    oqf = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+    osf = torch.empty(B, Hq, device=dev)
+    obf = torch.empty(B, Hq * 128, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        decode_attention_fused(qkv, B, Hq, Hkv, qn, kn, 1e-6, cos, sin, pos, kf, vf, workf, oqf,
+                               osf, out_bf16=obf)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        decode_attention_fused(qkv, B, Hq, Hkv, qn, kn, 1e-6, cos, sin, pos, kf, vf, workf, oqf,
+                               osf, out_bf16=obf)
+    for p0 in (301, 302, 511, 512):
+        pos.fill_(p0)
+        g.replay()
+        torch.cuda.synchronize()
+        kc, vc = kf.clone(), vf.clone()  # rows below p0 as the replays left them
+        q = torch.empty(B * Hq * 128, dtype=torch.bfloat16, device=dev)
+        qk_norm_rope(qkv, B, 1, Hq, Hkv, qn, kn, 1e-6, cos, sin, pos, q, kc, vc)
+        ob = torch.empty_like(obf)
+        decode_attention(q, kc, vc, pos, attention_work(B, Hq, Lmax, dev), torch.empty_like(oqf),
+                         torch.empty_like(osf), Hq, out_bf16=ob)
+        assert torch.equal(obf, ob), p0
