@@ -449,7 +449,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
 // ------------------------------------------------- quantizing row kernels
 
 // residual += x (if x); y = residual * rsqrt(mean(residual^2) + eps) * w;
-// y -> e4m3fn + group scales, or -> bf16.  One workgroup per row of
+// y -> bf16 (ob), and/or -> e4m3fn + group scales (oq, os; from the
+// bf16-rounded y when both are written).  One workgroup per row of
 // K = 16 * kThreads (4096: 256 threads, 2048: 128), 16 values per thread.
 template <int kThreads>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t *__restrict__ x,
@@ -504,6 +505,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t *__res
     uint4 *op = reinterpret_cast<uint4 *>(ob + base);
     op[0] = make_uint4(p[0], p[1], p[2], p[3]);
     op[1] = make_uint4(p[4], p[5], p[6], p[7]);
+    if (oq) {  // both outputs: quantize the bf16-rounded values
+      float r[16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        r[2 * i] = bf16_f32(p[i] & 0xffffu);
+        r[2 * i + 1] = bf16_f32(p[i] >> 16);
+      }
+      quant16(r, oq + base, os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
+    }
   } else {
     quant16(v, oq + base, os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
   }
@@ -1272,7 +1282,7 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
 
 extern "C" int ecf8_rmsnorm(const void *x, float *residual, const void *weight, float eps, int64_t M,
                             int64_t K, void *out_q, float *out_scale, void *out_bf16, void *stream) {
-  if (!residual || !weight || M <= 0 || (!out_bf16 && (!out_q || !out_scale)))
+  if (!residual || !weight || M <= 0 || (!out_bf16 && !out_q) || (!out_q != !out_scale))
     return ECF8_ERR_INVALID_ARG;
   if ((K != 4096 && K != 2048) || M > 0x7fffffff) return ECF8_ERR_UNSUPPORTED;
   if (!aligned(residual, 16) || (x && !aligned(x, 16)) || !aligned(weight, 16) ||

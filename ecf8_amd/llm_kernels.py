@@ -97,18 +97,19 @@ def fp8_linear(aq, a_scale, weights, out, M=None):
 
 
 def rmsnorm(residual, weight, eps, M, x=None, out_q=None, out_scale=None, out_bf16=None):
-    """residual[:M] += x[:M] (if x); normalized rows -> fp8 + scales, or bf16."""
+    """residual[:M] += x[:M] (if x); normalized rows -> bf16 and/or fp8 +
+    scales (with both, the fp8 form quantizes the bf16-rounded rows)."""
     dev = residual.device
     _need(residual, torch.float32, "residual", dev)
     _need(weight, torch.bfloat16, "weight", dev)
     K = residual.shape[-1]
     if x is not None:
         _need(x, torch.bfloat16, "x", dev)
+    if (out_q is None) != (out_scale is None) or (out_bf16 is None and out_q is None):
+        raise ECF8Error("rmsnorm needs out_bf16, or out_q and out_scale, or all three")
     if out_bf16 is not None:
         _need(out_bf16, torch.bfloat16, "out_bf16", dev)
-    else:
-        if out_q is None or out_scale is None:
-            raise ECF8Error("rmsnorm needs out_bf16, or out_q and out_scale")
+    if out_q is not None:
         _need(out_q, torch.float8_e4m3fn, "out_q", dev)
         _need(out_scale, torch.float32, "out_scale", dev)
     _rows(M, K, residual, x, out_q, out_bf16)

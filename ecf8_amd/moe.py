@@ -260,9 +260,13 @@ class Qwen3MoeRunner(_GreedyRunner):
         self._plan(a, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
                    self.o)(self.aqA, self.asA, M)
 
-    def _moe(self, mlp: SparseMoeBlock, index: int, M: int, prefill: bool):
+    def _moe(self, mlp: SparseMoeBlock, index: int, M: int, prefill: bool,
+             quantized: bool = False):
+        """Routed MLP of the normalized rows hb[:M]; ``quantized``: aqH /
+        asH already hold their fp8 form (the norm wrote both)."""
         cfg, r, ex = self.cfg, self.route, self.experts[index]
-        K.act_quant(self.hb, M, self.aqH, self.asH)  # the experts' input
+        if not quantized:
+            K.act_quant(self.hb, M, self.aqH, self.asH)  # the experts' input
         if prefill and ex.compressed:
             ex.decode_all()
         step = self.chunk if prefill else M
@@ -283,9 +287,10 @@ class Qwen3MoeRunner(_GreedyRunner):
         K.rmsnorm(self.res, layer.input_layernorm.weight, cfg.eps, M, x=x_prev, out_q=self.aqH,
                   out_scale=self.asH)
         layer.self_attn(self, index, prefill)
+        # bf16 rows for the router, fp8 rows for the experts, in one pass
         K.rmsnorm(self.res, layer.post_attention_layernorm.weight, cfg.eps, M, x=self.o,
-                  out_bf16=self.hb)
-        self._moe(layer.mlp, index, M, prefill)
+                  out_q=self.aqH, out_scale=self.asH, out_bf16=self.hb)
+        self._moe(layer.mlp, index, M, prefill, quantized=True)
         return self.y
 
 

@@ -52,8 +52,9 @@ int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64_t K,
  * Residual add + RMSNorm over rows of K = 4096 or 2048:
  *   residual[m] += x[m]  (x bf16 [M, K], or NULL for no add; residual fp32)
  *   y = residual[m] * rsqrt(mean(residual[m]^2) + eps) * weight  (bf16 weight)
- * y goes to out_bf16 (bf16 [M, K]) when that is non-NULL, otherwise it is
- * quantized to out_q (e4m3fn [M, K]) + out_scale (fp32 [M, K/128]).
+ * y goes to out_bf16 (bf16 [M, K]) and/or, quantized, to out_q (e4m3fn
+ * [M, K]) + out_scale (fp32 [M, K/128]); with both, the quantized form is
+ * that of the bf16-rounded y (what ecf8_act_quant of out_bf16 gives).
  */
 int ecf8_rmsnorm(const void *x, float *residual, const void *weight, float eps, int64_t M,
                  int64_t K, void *out_q, float *out_scale, void *out_bf16, void *stream);

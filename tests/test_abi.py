@@ -153,6 +153,7 @@ def test_consumer_kernels_reject_before_launch():
     assert L.ecf8_fp8_linear(fake, fake, 16, 4096, bad_n, 1, fake, 128, None) == 2
     assert L.ecf8_rmsnorm(None, None, fake, ctypes.c_float(1e-6), 4, 4096, fake, fake, None, None) == 1
     assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 4096, None, fake, None, None) == 1
+    assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 4096, fake, None, fake, None) == 1
     assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 3072, fake, fake, None, None) == 2
     assert L.ecf8_silu_mul_quant(fake, 4, 1000, fake, fake, None) == 2
     assert L.ecf8_act_quant(fake, 4, 4096, None, fake, None) == 1

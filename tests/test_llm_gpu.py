@@ -215,6 +215,17 @@ def test_rmsnorm_residual_and_outputs(cuda_device, with_x, Kd):
     s = torch.empty(M, Kd // 128, device=dev)
     rmsnorm(rd, w.to(dev), 1e-6, M, x=None if x is None else x.to(dev), out_q=q, out_scale=s)
     _assert_fp8_close(q, s, y_ref)
+    # both outputs: the fp8 form is act_quant of the bf16 form, bit for bit
+    rd = r.to(dev)
+    ob2 = torch.empty(M, Kd, dtype=torch.bfloat16, device=dev)
+    q2 = torch.empty(M, Kd, dtype=FP8, device=dev)
+    s2 = torch.empty(M, Kd // 128, device=dev)
+    rmsnorm(rd, w.to(dev), 1e-6, M, x=None if x is None else x.to(dev), out_q=q2, out_scale=s2,
+            out_bf16=ob2)
+    assert torch.equal(ob2, ob)
+    qr, sr = _ref_quant(ob2)
+    assert torch.equal(s2.cpu(), sr)
+    assert torch.equal(q2.cpu().view(torch.uint8), qr.view(torch.uint8))
 
 
 @pytest.mark.parametrize("I", [8192, 768])
