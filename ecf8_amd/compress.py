@@ -151,15 +151,20 @@ def fp8_layers_by_block(model, fp8_regex) -> dict:
 
 
 def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 512,
-                   bytes_per_thread: int = 8, bf16_regex=(), validate_device=None) -> dict:
+                   bytes_per_thread: int = 8, bf16_regex=(), validate_device=None,
+                   n_workers: int = 1) -> dict:
     """Compress every FP8 block of a local model and save it the way
     scripts/compress.py:490-680 does for a model without a hub config: each
     block's layers are removed and its compressed tensors registered as
     buffers on the block module (:583-612); the state dict goes to
     ``model.safetensors`` and the regexes to ``pattern_dict.json``
     ({"fp8": {regex: layer names}, "bf16": {...}}, :634-680); the format
-    parameters to ``dfloat_config.json``.  Blocks are compressed one after
-    another (the reference's --sequential path).  Returns the pattern dict."""
+    parameters to ``dfloat_config.json``.  ``n_workers`` > 1 compresses the
+    blocks in a thread pool, as the reference's pool does
+    (scripts/compress.py:320-361; the encoder and the tensor work release the
+    interpreter lock); 1 is the reference's --sequential path.  Registration,
+    validation and saving follow in block order either way.  Returns the
+    pattern dict."""
     import operator
 
     from safetensors.torch import load_file, save_file
@@ -169,8 +174,15 @@ def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 51
     regex_dict = {r: None for r in regexes}
     info = {"save_path": save_path, "model_fp8_regex": regexes,
             "bytes_per_thread": bytes_per_thread, "threads_per_block": threads_per_block}
-    for block_name, layers in fp8_layers_by_block(model, fp8_regex).items():
-        result = process_fp8_block((block_name, layers), info)
+    items = list(fp8_layers_by_block(model, fp8_regex).items())
+    if n_workers > 1 and len(items) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=min(n_workers, len(items))) as ex:
+            results = list(ex.map(lambda item: process_fp8_block(item, info), items))
+    else:
+        results = [process_fp8_block(item, info) for item in items]
+    for (block_name, _layers), result in zip(items, results):
         tensors = load_file(result["block_save_path"])
         if validate_device is not None:
             validate_cuda_decoding_fp8(result, tensors, validate_device)

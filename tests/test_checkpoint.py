@@ -79,6 +79,37 @@ def saved(tmp_path_factory):
     return d, pattern, originals
 
 
+def test_parallel_compression_writes_the_same_checkpoint(saved, tmp_path):
+    """Blocks compressed in a thread pool (the reference's parallel path)
+    give byte-identical block files and the same pattern dict."""
+    from safetensors.torch import load_file
+
+    from ecf8_amd.compress import compress_model
+
+    d0, pattern0, _ = saved
+    m, _ = _fp8_model()
+    d1 = str(tmp_path)
+    pattern1 = compress_model(m, [r"model\.layers\.\d+"], d1, bf16_regex=[r"lm_head"],
+                              n_workers=3)
+    assert pattern1 == pattern0
+    names = sorted(f for f in os.listdir(os.path.join(d0, "cache")) if f.endswith(".safetensors"))
+    assert names == sorted(f for f in os.listdir(os.path.join(d1, "cache"))
+                           if f.endswith(".safetensors"))
+    for f in names:
+        a, b = load_file(os.path.join(d0, "cache", f)), load_file(os.path.join(d1, "cache", f))
+        assert sorted(a) == sorted(b)
+        for k in a:
+            assert torch.equal(a[k], b[k]), (f, k)
+    s0, s1 = (load_file(os.path.join(d, "model.safetensors")) for d in (d0, d1))
+    assert sorted(s0) == sorted(s1)
+    compressed = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
+                  "split_positions")
+    keys = [k for k in s0 if k.rsplit(".", 1)[-1] in compressed]  # the rest is random init
+    assert len(keys) == 3 * len(compressed)
+    for k in keys:
+        assert torch.equal(s0[k], s1[k]), k
+
+
 def test_checkpoint_files_follow_the_reference_layout(saved):
     from safetensors.torch import load_file
 
