@@ -540,7 +540,7 @@ def dit_generate(args):
                    "steps": args.dit_steps, "guidance": 3.5,
                    "distinct_block_weights": args.distinct_layers,
                    "linears": "FP8 weights dequantized to bf16 per call + library bf16 GEMM",
-                   "attention": "fp32"},
+                   "attention": "bf16 operands, fp32 accumulation"},
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
         "ratio_vs_uncompressed": round(fp8["seconds"] / ecf8["seconds"], 4),

@@ -19,8 +19,9 @@ conditioning.  Random init.
 Compute: the FP8 Linears run at thousands of rows, where the work is
 matrix-bound, so each one dequantizes its e4m3fn weight with its 128x128
 block scales to bf16 (ecf8_dequant_fp8_block) and calls the library bf16
-GEMM; attention runs in fp32 (chunked over queries).  The same consumer
-runs for the compressed and the uncompressed model.
+GEMM; attention runs on bf16 operands with fp32 accumulation (chunked over
+queries), the precision of the reference's bf16 pipeline.  The same
+consumer runs for the compressed and the uncompressed model.
 """
 
 from __future__ import annotations
@@ -113,14 +114,20 @@ def _rope(x, cos, sin):
 
 
 def _attention(q, k, v, chunk: int = 1152):
-    """Softmax attention in fp32 (q, k, v fp32 [B, H, T, D]), chunked over
-    queries; every operand of a batched product is contiguous."""
+    """Softmax attention of q, k, v [B, H, T, D] (fp32 in, fp32 out), chunked
+    over queries, in the precision the reference's bf16 pipeline attends
+    in: bf16 operands for both products and for the softmax, every
+    reduction accumulated in fp32.  Every operand of a batched product is a
+    contiguous bf16 tensor."""
     scale = 1.0 / math.sqrt(q.shape[-1])
-    kt = k.transpose(-1, -2).contiguous()
-    out = torch.empty_like(q)
+    qb = (q * scale).to(torch.bfloat16).contiguous()
+    kt = k.to(torch.bfloat16).transpose(-1, -2).contiguous()
+    vb = v.to(torch.bfloat16).contiguous()
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     for i in range(0, q.shape[2], chunk):
-        s = torch.matmul(q[:, :, i:i + chunk].contiguous(), kt) * scale
-        out[:, :, i:i + chunk] = torch.matmul(torch.softmax(s, dim=-1), v)
+        s = torch.matmul(qb[:, :, i:i + chunk].contiguous(), kt)
+        p = torch.softmax(s, dim=-1).contiguous()  # fp32 accumulation, bf16 out
+        out[:, :, i:i + chunk] = torch.matmul(p, vb).float()
     return out
 
 
