@@ -577,8 +577,9 @@ def main():
     ap.add_argument("--prompt-len", type=int, default=128)
     ap.add_argument("--new-tokens", type=int, default=None,
                     help="generate: new tokens per sequence (1024 dense, 512 MoE)")
-    ap.add_argument("--prefetch-workgroups", type=int, default=2,
-                    help="generate: resident side-stream decode workgroups per CU")
+    ap.add_argument("--prefetch-workgroups", type=float, default=2,
+                    help="generate: side-stream decode workgroups per CU (fractions leave "
+                         "CUs free)")
     ap.add_argument("--distinct-layers", type=int, default=2,
                     help="generate: layers drawn independently (the rest copy them)")
     ap.add_argument("--mode", choices=("decode", "copy"), default="decode",

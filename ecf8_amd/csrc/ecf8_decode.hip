@@ -242,17 +242,23 @@ __device__ __forceinline__ void write_block(const uint32_t *stage, const BlockRa
 }
 
 // Store the in-range bytes of the edge segments parked by the last
-// write_block (lanes 0..31 of the workgroup, one byte each), then mark the
-// slots empty.  Called between a barrier that follows that write_block and
-// the barrier before the next one.
+// write_block (lanes first..first+31 of the workgroup, one byte each), then
+// mark the slots empty.  Called between a barrier that follows that
+// write_block and the barrier before the next one.  The callers pass the
+// last wave, which has the fewest segments to write, so the extra LDS round
+// trip lands on the wave with the most slack before the next barrier.
 __device__ __forceinline__ void flush_edges(uint32_t *s_edge, uint8_t *__restrict__ out,
-                                            int tid) {
-  if (tid < 32) {
-    uint32_t *const e = s_edge + (tid >> 4) * kEdgeSlotDwords;
-    const uint32_t i = (uint32_t)tid & 15u;
-    const uint32_t q = e[4] + i;
-    const uint32_t b = (e[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-    const bool in_range = q >= e[5] && q < e[6];
+                                            int tid, int first) {
+  const int t = tid - first;
+  if ((unsigned)t < 32u) {
+    uint32_t *const e = s_edge + (t >> 4) * kEdgeSlotDwords;
+    const uint32_t i = (uint32_t)t & 15u;
+    const uint4 meta = *reinterpret_cast<const uint4 *>(e + 4);  // gpos, start, end
+    uint32_t w = e[i >> 2];
+    asm volatile("" : "+v"(w));  // both reads before the range test: one LDS round trip
+    const uint32_t q = meta.x + i;
+    const uint32_t b = (w >> (8 * (i & 3))) & 0xFFu;
+    const bool in_range = q >= meta.y && q < meta.z;
     if (in_range) out[q] = (uint8_t)b;
     if (i == 0) {
       e[5] = 0u;
@@ -281,8 +287,12 @@ __device__ __forceinline__ void exact_walk(const uint3 &d, uint32_t gap,
   // a chunk of codes >= 2 bits owns at most 32; the cap bounds what a
   // corrupt table's exact row could make the staging ORs reach
   int left = kMaxLaneSyms;
-  const uint64_t hi = __builtin_bswap64(((uint64_t)d.y << 32) | d.x);
-  const uint32_t la = ((d.z & 0xFFu) << 8) | ((d.z >> 8) & 0xFFu);
+  // opaque copies: keeps the byte swaps inside the caller's (rare) branch
+  // instead of hoisted into the common path
+  uint32_t dx = d.x, dy = d.y, dz = d.z;
+  asm volatile("" : "+v"(dx), "+v"(dy), "+v"(dz));
+  const uint64_t hi = __builtin_bswap64(((uint64_t)dy << 32) | dx);
+  const uint32_t la = ((dz & 0xFFu) << 8) | ((dz >> 8) & 0xFFu);
   const uint32_t len_row = (uint32_t)(n_luts - 1) * 256;
   const uint32_t max_row = (uint32_t)(n_luts - 2);
   for (int q = (int)gap; q < kChunkBits;) {
@@ -453,7 +463,7 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s
     __syncthreads();
     const int excl4 = incl - cnt4 + waves_before<kWaves>(s_wave_sum, lane, wave);
     // the previous block's edge segments (parked before the barrier above)
-    flush_edges(s_edge, out, tid);
+    flush_edges(s_edge, out, tid, kThreads - 64);
 
     // ---- 3. OR the exponents into the staging buffer at their positions,
     // two automaton entries (at most 8 symbols, 32 bits) per 64-bit OR.
@@ -513,7 +523,7 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s
     fb = fb_next;
   }
   __syncthreads();
-  flush_edges(s_edge, out, tid);
+  flush_edges(s_edge, out, tid, kThreads - 64);
 }
 
 // One tensor: the persistent grid strides over its format-blocks.
@@ -853,7 +863,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     if (lane == 63) s_wave_sum[wave] = incl;
     __syncthreads();
     const int excl = incl - cnt + waves_before<kWaves>(s_wave_sum, lane, wave);
-    flush_edges(s_edge, out, tid);
+    flush_edges(s_edge, out, tid, kThreads - 64);
 
     // ---- 3. OR this lane's nibble run into the staging buffer
     int c = cnt;
@@ -890,7 +900,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
     op_hi = nop_hi;
   }
   __syncthreads();
-  flush_edges(s_edge, out, tid);
+  flush_edges(s_edge, out, tid, kThreads - 64);
 }
 
 // ===========================================================================

@@ -34,7 +34,7 @@ _KEYS = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
 
 
 class LayerPrefetcher:
-    def __init__(self, layers, device=None, workgroups_per_cu: int = 2,
+    def __init__(self, layers, device=None, workgroups_per_cu: float = 2,
                  threads_per_block: int = 512):
         layers = list(layers)
         if len(layers) < 2 or len(layers) % 2:
@@ -46,7 +46,8 @@ class LayerPrefetcher:
                      for _ in range(2)]
         self.side = torch.cuda.Stream(self.dev)
         cus = torch.cuda.get_device_properties(self.dev).multi_processor_count
-        slots = max(1, cus * workgroups_per_cu)
+        # fractions below 1 leave some CUs without a decode workgroup
+        slots = max(1, int(round(cus * workgroups_per_cu)))
         self.plans, self.views = [], []
         for i, (m, n) in enumerate(zip(layers, sizes)):
             m.__dict__["_ecf8_tpb"] = threads_per_block
