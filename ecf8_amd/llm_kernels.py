@@ -113,8 +113,9 @@ def rmsnorm(residual, weight, eps, M, x=None, out_q=None, out_scale=None, out_bf
         _need(out_q, torch.float8_e4m3fn, "out_q", dev)
         _need(out_scale, torch.float32, "out_scale", dev)
     _rows(M, K, residual, x, out_q, out_bf16)
-    if weight.numel() != K or (out_scale is not None and out_scale.shape[-1] != K // GROUP):
-        raise ECF8Error("norm weight / scale shape does not match the rows")
+    _rows(M, K // GROUP, out_scale)
+    if weight.numel() != K:
+        raise ECF8Error("norm weight shape does not match the rows")
     check(lib().ecf8_rmsnorm(_ptr(x), residual.data_ptr(), weight.data_ptr(), float(eps), M, K,
                              _ptr(out_q), _ptr(out_scale), _ptr(out_bf16), _stream(residual)),
           "ecf8_rmsnorm")
@@ -128,8 +129,7 @@ def silu_mul_quant(gate_up, M, out_q, out_scale):
     inter = gate_up.shape[-1] // 2
     _rows(M, 2 * inter, gate_up)
     _rows(M, inter, out_q)
-    if out_scale.shape[-1] != inter // GROUP or out_scale.shape[0] < M:
-        raise ECF8Error("out_scale shape does not match")
+    _rows(M, inter // GROUP, out_scale)
     check(lib().ecf8_silu_mul_quant(gate_up.data_ptr(), M, inter, out_q.data_ptr(),
                                     out_scale.data_ptr(), _stream(gate_up)), "ecf8_silu_mul_quant")
 
@@ -140,8 +140,7 @@ def act_quant(x, M, out_q, out_scale):
     _need(out_q, torch.float8_e4m3fn, "out_q", dev)
     _need(out_scale, torch.float32, "out_scale", dev)
     _rows(M, x.shape[-1], x, out_q)
-    if out_scale.shape[-1] != x.shape[-1] // GROUP or out_scale.shape[0] < M:
-        raise ECF8Error("out_scale shape does not match")
+    _rows(M, x.shape[-1] // GROUP, out_scale)
     check(lib().ecf8_act_quant(x.data_ptr(), M, x.shape[-1], out_q.data_ptr(), out_scale.data_ptr(),
                                _stream(x)), "ecf8_act_quant")
 

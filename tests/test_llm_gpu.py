@@ -324,16 +324,26 @@ def test_decode_attention_matches_fp32(cuda_device, pos0, G):
 
 
 def test_wrappers_reject_bad_arguments_before_launch(cuda_device):
-    """Missing outputs, short norm weights and an empty position tensor are
-    refused on the host; nothing is launched."""
+    """Missing outputs, short norm weights, scale buffers with too few rows
+    and an empty position tensor are refused on the host; nothing is
+    launched."""
     from ecf8_amd._lib import ECF8Error
-    from ecf8_amd.llm_kernels import attention_work, decode_attention, qk_norm_rope, rmsnorm
+    from ecf8_amd.llm_kernels import (act_quant, attention_work, decode_attention, qk_norm_rope,
+                                      rmsnorm, silu_mul_quant)
 
     dev = cuda_device
     bf = dict(dtype=torch.bfloat16, device=dev)
     res = torch.zeros(2, 4096, device=dev)
     with pytest.raises(ECF8Error, match="out_bf16, or out_q"):
         rmsnorm(res, torch.ones(4096, **bf), 1e-6, 2)
+    q8 = torch.empty(2, 4096, dtype=FP8, device=dev)
+    for short in (torch.empty(1, 32, device=dev), torch.empty(32, device=dev)):
+        with pytest.raises(ECF8Error, match="is not"):
+            rmsnorm(res, torch.ones(4096, **bf), 1e-6, 2, out_q=q8, out_scale=short)
+        with pytest.raises(ECF8Error, match="is not"):
+            act_quant(torch.zeros(2, 4096, **bf), 2, q8, short)
+        with pytest.raises(ECF8Error, match="is not"):
+            silu_mul_quant(torch.zeros(2, 8192, **bf), 2, q8, short)
     B, T, Hq, Hkv, Lmax = 1, 1, 8, 2, 16
     qkv = torch.zeros(B * T, (Hq + 2 * Hkv) * 128, **bf)
     cos = torch.ones(Lmax, 64, device=dev)
