@@ -40,16 +40,21 @@ ANY, MULTI, DFA = -1, 0, 1
 
 
 def _table_for(d, kind):
-    """Device table of the requested kind; None when the automaton cannot
-    represent these LUTs (then only the multi-symbol kernel applies)."""
-    from ecf8_amd.decode import ECF8Error, build_table
+    """Device table of the requested kind.  The automaton holds at most 4
+    symbols per input byte, so LUTs with a 1-bit code refuse it: then the
+    refusal is checked and the automatic choice (the multi-symbol table) is
+    returned instead."""
+    from ecf8_amd.decode import ECF8Error, build_table, min_code_bits
 
     try:
         return build_table(d["luts"], kind=kind)
     except ECF8Error:
-        if kind == DFA:
-            return None
-        raise
+        if kind != DFA:
+            raise
+    assert min_code_bits(d["luts"]) == 1, "automaton refused LUTs without a 1-bit code"
+    table = build_table(d["luts"], kind=ANY)
+    assert table.kind == MULTI
+    return table
 
 
 def _gpu_decode(block, dev, tpb=512, n_elements=None, out=None, kind=ANY):
@@ -57,8 +62,6 @@ def _gpu_decode(block, dev, tpb=512, n_elements=None, out=None, kind=ANY):
 
     d = _dev_block(block, dev)
     table = _table_for(d, kind)
-    if table is None:
-        pytest.skip("LUTs with a 1-bit code: no automaton table")
     if out is None and n_elements is None:
         r = decode(d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
                    d["gaps"], table=table, threads_per_block=tpb)
