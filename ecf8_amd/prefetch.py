@@ -115,3 +115,11 @@ class LayerPrefetcher:
             self._handles.append(m.register_forward_hook(self._post(i)))
         self.prime()
         return self
+
+    def uninstall(self):
+        """Remove the prefetching hooks (the layers are left without a
+        decode hook; install another prefetcher or the loader's hooks)."""
+        torch.cuda.current_stream(self.dev).wait_stream(self.side)
+        for h in self._handles:
+            h.remove()
+        self._handles = []

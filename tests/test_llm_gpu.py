@@ -405,15 +405,20 @@ def test_compressed_model_matches_uncompressed_exactly(small_models, cuda_device
             results[(name, graph)] = (toks, last)
     from ecf8_amd.prefetch import LayerPrefetcher
 
-    LayerPrefetcher(comp.model.layers, cuda_device).install()
-    for graph in (False, True):
-        _say(f"[llm] e2e ecf8 prefetch graph={graph}")
-        r = Qwen3Runner(comp, B, T, T + new, cuda_device)
-        if graph:
-            r.capture()
-        for rep in range(2):  # the second run starts from the state the first left
-            toks = r.generate(prompt, new).cpu()
-            results[("ecf8_prefetch", graph, rep)] = (toks, r.logits.float().cpu())
+    # the default grid (2 workgroups per CU), then a quarter of a workgroup
+    # per CU: most CUs without a decode workgroup, several tasks each
+    for wpc in (2, 0.25):
+        pf = LayerPrefetcher(comp.model.layers, cuda_device, workgroups_per_cu=wpc).install()
+        for graph in (False, True):
+            _say(f"[llm] e2e ecf8 prefetch wpc={wpc} graph={graph}")
+            r = Qwen3Runner(comp, B, T, T + new, cuda_device)
+            if graph:
+                r.capture()
+            for rep in range(2):  # the second run starts from the state the first left
+                toks = r.generate(prompt, new).cpu()
+                results[("ecf8_prefetch", wpc, graph, rep)] = (toks, r.logits.float().cpu())
+            del r
+        pf.uninstall()
     base_t, base_l = results[("fp8", False)]
     for key, (t, l) in results.items():
         assert torch.equal(t, base_t), key
