@@ -199,8 +199,16 @@ __device__ __forceinline__ void prefetch_nibbles(const BlockRange &br, const uin
   const int last_seg = br.nseg > 0 ? br.nseg - 1 : 0;
   const uint32_t q0 = (br.base >> 1) + 8u * (uint32_t)min(tid, last_seg);
   const uint32_t q1 = (br.base >> 1) + 8u * (uint32_t)min(tid + threads, last_seg);
-  pre0 = *reinterpret_cast<const uint2 *>(packed + (q0 < last8 ? q0 : last8));
-  pre1 = *reinterpret_cast<const uint2 *>(packed + (q1 < last8 ? q1 : last8));
+  // non-temporal: each nibble byte is read exactly once (measured on
+  // MI355X: 74.0 -> 72.1 us per Qwen3-8B layer).  The chunk loads stay
+  // ordinary: neighbouring lanes' 12-byte windows share cache lines.
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 a0 = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x2 *>(packed + (q0 < last8 ? q0 : last8)));
+  const u32x2 a1 = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x2 *>(packed + (q1 < last8 ? q1 : last8)));
+  pre0 = make_uint2(a0.x, a0.y);
+  pre1 = make_uint2(a1.x, a1.y);
 }
 
 // LDS slots for the two edge segments of a block (first and last, which it
