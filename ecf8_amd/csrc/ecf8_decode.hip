@@ -648,18 +648,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
       continue;
     const uint32_t n_bytes = (uint32_t)d.n_bytes;
     const int n_fb = (int)((n_bytes + kBlockBytes - 1) / kBlockBytes);
-    // the block's n_tasks tasks interleave its format-blocks (task r takes
-    // r, r + n_tasks, ...), so the workgroups running them at the same time
-    // sweep the block's bytes in order, as the one-block kernel does
+    // One tensor: its tasks interleave the format-blocks (task r takes r,
+    // r + tasks, ...), so the workgroups running at the same time sweep the
+    // bytes in order, as the one-tensor kernel does.  Several tensors (an
+    // MoE layer): task r takes a contiguous run of blocks instead.
+    // Measured on MI355X: a whole MoE layer 263 -> 253 us contiguous, while
+    // one Qwen3-8B layer on the side stream loses 3 % contiguous.
     const int tasks = (n_fb + blocks_per_task - 1) / blocks_per_task;
-    const int fb0 = task - d.task_begin;
-    if (fb0 >= tasks) continue;
+    const int r = task - d.task_begin;
+    if (r >= tasks) continue;
+    const bool contiguous = count > 1;  // uniform
+    const int fb_first = contiguous ? r * blocks_per_task : r;
+    const int fb_step = contiguous ? 1 : tasks;
+    const int fb_last = contiguous ? min(n_fb, (r + 1) * blocks_per_task) : n_fb;
     // the previous task ended with a barrier: no wave still reads s_dfa
     load_dfa<kThreads>(s_dfa, d.table, tid);
     const BlockArgs a{d.luts, d.n_luts, d.encoded, n_bytes, d.packed_other_4bits,
                       reinterpret_cast<const uint32_t *>(d.output_positions), d.gaps,
                       d.outputs, (uint32_t)d.n_elements};
-    dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, fb0, tasks, n_fb);
+    dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, fb_first,
+                                fb_step, fb_last);
   }
 }
 
