@@ -85,7 +85,7 @@ def cpu_encode(flat, sample: int = 1048576):
     restatement of the reference loop over the first `sample` elements."""
     import torch
 
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
     from oracle import codec as oc
 
     n = flat.numel()
@@ -138,7 +138,7 @@ def _qwen3_layer_workload(args, dev):
     import torch
 
     from ecf8_amd._lib import lib
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
     from ecf8_amd.decode import build_table, decode_into, largest_block, min_code_bits
     from ecf8_amd.synth import flat_block, qwen3_8b_layer
 
@@ -199,7 +199,7 @@ def _qwen3_moe_layer_workload(args, dev):
     import torch
 
     from ecf8_amd._lib import lib
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
     from ecf8_amd.decode import build_table, prepare_batch
     from ecf8_amd.synth import QWEN3_MOE_ATTN, QWEN3_MOE_EXPERT, flat_block, synthetic_block
 
@@ -306,7 +306,7 @@ def e2e_generate(args):
 
     from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model, timed_generate
     from ecf8_amd.prefetch import LayerPrefetcher
-    from ecf8_amd.run import TensorManager
+    from dfloat.run.run import TensorManager
 
     dev = torch.device("cuda", 0)
     cfg = Qwen3Config()
@@ -388,7 +388,7 @@ def moe_generate(args):
     from ecf8_amd.llm import timed_generate
     from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, random_moe_model
     from ecf8_amd.prefetch import LayerPrefetcher
-    from ecf8_amd.run import TensorManager
+    from dfloat.run.run import TensorManager
 
     dev = torch.device("cuda", 0)
     cfg = Qwen3MoeConfig()
@@ -479,7 +479,7 @@ def dit_generate(args):
     import torch
 
     from ecf8_amd.dit import FluxConfig, compress_blocks, random_pipeline, timed_generate
-    from ecf8_amd.run import TensorManager
+    from dfloat.run.run import TensorManager
 
     dev = torch.device("cuda", 0)
     cfg = FluxConfig()

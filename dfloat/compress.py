@@ -115,7 +115,7 @@ def validate_cuda_decoding_fp8(result, tensors, device) -> None:
     """GPU round trip of one cached block against its original FP8 bytes,
     the reference's check (scripts/compress.py:70-126), through the HIP
     decoder.  Raises AssertionError on any differing byte."""
-    from .decode import decode
+    from ecf8_amd.decode import decode
 
     dev = torch.device(device)
     moved = {k: tensors[k].to(dev) for k in ("luts", "encoded", "packed_other_4bits",
@@ -150,25 +150,53 @@ def fp8_layers_by_block(model, fp8_regex) -> dict:
     return {k: v for k, v in out.items() if v}
 
 
+def _layout(model, fp8_regex, layout: str) -> str:
+    if layout != "auto":
+        if layout not in ("hf", "diffsynth", "full"):
+            raise ValueError(f"unknown checkpoint layout {layout!r}")
+        return layout
+    if hasattr(model, "save_pretrained") and hasattr(model, "config"):
+        return "hf"
+    return "diffsynth" if isinstance(fp8_regex, dict) else "full"
+
+
 def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 512,
                    bytes_per_thread: int = 8, bf16_regex=(), validate_device=None,
-                   n_workers: int = 1) -> dict:
-    """Compress every FP8 block of a local model and save it the way
-    scripts/compress.py:490-680 does for a model without a hub config: each
-    block's layers are removed and its compressed tensors registered as
-    buffers on the block module (:583-612); the state dict goes to
-    ``model.safetensors`` and the regexes to ``pattern_dict.json``
-    ({"fp8": {regex: layer names}, "bf16": {...}}, :634-680); the format
-    parameters to ``dfloat_config.json``.  ``n_workers`` > 1 compresses the
-    blocks in a thread pool, as the reference's pool does
-    (scripts/compress.py:320-361; the encoder and the tensor work release the
-    interpreter lock); 1 is the reference's --sequential path.  Registration,
-    validation and saving follow in block order either way.  Returns the
-    pattern dict."""
+                   n_workers: int = 1, layout: str = "auto", tokenizer=None) -> dict:
+    """Compress every FP8 block of a local model and save the checkpoint the
+    way scripts/compress.py:490-680 does.
+
+    Each block's layers are removed and its compressed tensors registered as
+    buffers on the block module (:583-612); ``validate_device`` runs the
+    GPU round trip of every block first (:571-585); the block regexes and
+    their Linear names go to ``pattern_dict.json`` ({"fp8": {regex: layer
+    names}, "bf16": {regex: []}}, :634-680) and each block's entropy to
+    ``entropy.csv``.  The checkpoint itself, by ``layout``:
+
+    * ``"hf"`` (default for a transformers model): ``model.config`` gets
+      ``dfloat_config`` = {version, threads_per_block, bytes_per_thread} and
+      the model is written by ``save_pretrained``; ``tokenizer``, if given,
+      is saved beside it (:668-677).  ``DFloatModel.from_pretrained`` reads
+      this directory;
+    * ``"diffsynth"`` (default for a {regex: layer paths} pattern, the
+      DiffSynth pipelines): one ``<block>.safetensors`` per block with the
+      block module's state dict under its full names (:614-624), plus
+      ``dfloat_config.json``; the pipeline's other weights stay with the
+      original model.  ``DFloatDiffSynthModelFP8.from_pretrained`` reads it;
+    * ``"full"`` (default for any other module): the whole state dict in
+      ``model.safetensors`` plus ``dfloat_config.json``, for modules that
+      have neither a Hugging Face config nor a pipeline of their own.
+
+    ``n_workers`` > 1 compresses the blocks in a thread pool, as the
+    reference's pool does (scripts/compress.py:320-361; the encoder and the
+    tensor work release the interpreter lock); 1 is the reference's
+    --sequential path.  Registration, validation and saving follow in block
+    order either way.  Returns the pattern dict."""
     import operator
 
     from safetensors.torch import load_file, save_file
 
+    layout = _layout(model, fp8_regex, layout)
     os.makedirs(save_path, exist_ok=True)
     regexes = list(fp8_regex.keys()) if isinstance(fp8_regex, dict) else list(fp8_regex)
     regex_dict = {r: None for r in regexes}
@@ -182,10 +210,12 @@ def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 51
             results = list(ex.map(lambda item: process_fp8_block(item, info), items))
     else:
         results = [process_fp8_block(item, info) for item in items]
+    entropies = {}
     for (block_name, _layers), result in zip(items, results):
         tensors = load_file(result["block_save_path"])
         if validate_device is not None:
             validate_cuda_decoding_fp8(result, tensors, validate_device)
+        entropies[block_name] = result["entropy"]
         block = operator.attrgetter(block_name)(model)
         for layer_name in result["layers_to_delete"]:
             if layer_name == block_name:
@@ -196,6 +226,9 @@ def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 51
         for key in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
                     "split_positions"):
             block.register_buffer(key, tensors[key])
+        if layout == "diffsynth":
+            state = {f"{block_name}.{k}": v.contiguous() for k, v in block.state_dict().items()}
+            save_file(state, os.path.join(save_path, block_name + ".safetensors"))
         matched = result["matched_regex"]
         if matched:
             if regex_dict[matched] is None:
@@ -203,12 +236,24 @@ def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 51
             elif regex_dict[matched] != result["layer_names"]:
                 raise ValueError(f"{block_name}: layers {result['layer_names']} differ from "
                                  f"{regex_dict[matched]} of the other blocks of {matched}")
-    state = {k: v.contiguous() for k, v in model.state_dict().items()}
-    save_file(state, os.path.join(save_path, "model.safetensors"))
+    with open(os.path.join(save_path, "entropy.csv"), "w") as f:
+        f.write("block_name,entropy\n")
+        for name in sorted(entropies):
+            f.write(f"{name},{entropies[name]}\n")
+    dfloat_config = {"version": PACKAGE_FORMAT_VERSION, "threads_per_block": threads_per_block,
+                     "bytes_per_thread": bytes_per_thread}
+    if layout == "hf":
+        model.config.dfloat_config = dfloat_config
+        model.save_pretrained(save_path)
+        if tokenizer is not None:
+            tokenizer.save_pretrained(save_path)
+    else:
+        if layout == "full":
+            state = {k: v.contiguous() for k, v in model.state_dict().items()}
+            save_file(state, os.path.join(save_path, "model.safetensors"))
+        with open(os.path.join(save_path, "dfloat_config.json"), "w") as f:
+            json.dump(dfloat_config, f, indent=4)
     pattern_dict = {"fp8": regex_dict, "bf16": {r: [] for r in bf16_regex}}
     with open(os.path.join(save_path, "pattern_dict.json"), "w") as f:
         json.dump(pattern_dict, f, indent=4)
-    with open(os.path.join(save_path, "dfloat_config.json"), "w") as f:
-        json.dump({"version": PACKAGE_FORMAT_VERSION, "threads_per_block": threads_per_block,
-                   "bytes_per_thread": bytes_per_thread}, f, indent=4)
     return pattern_dict

@@ -1,4 +1,4 @@
-"""Drop-in runtime layer with the reference's names (dfloat/run/run.py).
+"""Runtime of the reference's ``dfloat.run`` (dfloat/run/run.py).
 
 * ``_decode``          callable with the cp.RawKernel call form the reference
                        uses (grid=, block=, shared_mem=, args=[...]);
@@ -7,10 +7,13 @@
                        into the buffer and inject ``.weight`` views;
 * ``load_and_replace_tensors[_parallel]`` / ``_process_compressed_tensor``
                        register compressed buffers + hooks from safetensors;
-* ``DFloatModel``      local-checkpoint loader (no hub download).
+* ``DFloatModel``, ``DFloatDiffSynthModelFP8``
+                       loaders of compressed checkpoints from local
+                       directories (no hub download).
 
-Launches go on torch's current stream of the module's device, so decode and
-the consuming GEMM are ordered without any cross-runtime synchronisation.
+Decode launches go on torch's current stream of the module's device through
+the C ABI of libecf8 (``ecf8_amd.decode``), so decode and the consuming GEMM
+are ordered without any cross-runtime synchronisation.
 """
 
 from __future__ import annotations
@@ -26,8 +29,8 @@ from typing import Dict, Optional, Union
 import torch
 import torch.nn as nn
 
-from . import decode as _dev
-from ._lib import ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8Error, check, lib
+from ecf8_amd import decode as _dev
+from ecf8_amd._lib import ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8Error, check, lib
 
 __all__ = [
     "DFloatModel",
@@ -36,8 +39,10 @@ __all__ = [
     "load_and_replace_tensors",
     "load_and_replace_tensors_parallel",
     "load_compressed_model",
+    "DFloatDiffSynthModelFP8",
     "TensorManager",
     "get_hook",
+    "get_no_split_classes",
 ]
 
 
@@ -342,13 +347,46 @@ def get_dfloat_model_name_or_path(repo_id: str, dfloat_dir: str = "../dfloat-mod
     return dfloat_repo_id, dfloat_model_id
 
 
+def get_no_split_classes(model, patterns) -> list:
+    """Class names of the modules whose full name matches one of ``patterns``,
+    in first-seen order (dfloat/run/run.py:461-470): the classes a device
+    placement must keep on one device."""
+    names = []
+    for full_name, module in model.named_modules():
+        if any(re.fullmatch(p, full_name) for p in patterns):
+            cls_name = type(module).__name__
+            if cls_name not in names:
+                names.append(cls_name)
+    return names
+
+
+def _write_model_size(dfloat_repo_id: str, rows) -> None:
+    """model_size.csv as the reference's loaders write it
+    (dfloat/run/run.py:522-535): the FP8 blocks' size before and after."""
+    with open(os.path.join(dfloat_repo_id, "model_size.csv"), "w") as f:
+        f.write("fp8_blocks,rest,total\n")
+        for inc, exc, tot in rows:
+            f.write(f"{inc},{exc},{tot}\n")
+
+
+def _warn_if_on_cpu(model) -> None:
+    if any(p.device.type == "cpu" for p in model.parameters()):
+        print("Warning: Some model layers are on CPU. For inference, ensure the model is fully "
+              "loaded onto CUDA-compatible GPUs.", file=stderr)
+
+
 class DFloatModel:
     """Compressed causal LM from local directories (dfloat/run/run.py:483-566).
 
-    ``dfloat_repo_id`` must be a local directory holding config.json with a
-    ``dfloat_config`` entry, pattern_dict.json and the compressed
-    safetensors; ``model_name_or_path`` a local directory of the original FP8
-    model.  Nothing is downloaded.
+    ``dfloat_repo_id``: a local directory holding the compressor's output for
+    a Hugging Face model (config.json with a ``dfloat_config`` entry,
+    pattern_dict.json and the safetensors with the compressed buffers).
+    ``model_name_or_path``: the original FP8 model, as a local directory.
+    Nothing is downloaded: a missing ``dfloat_repo_id`` raises
+    FileNotFoundError where the reference would call snapshot_download.
+    Placement: ``device`` moves the whole model; otherwise ``device_map``
+    "auto" spreads it over the visible GPUs with accelerate, keeping every
+    compressed block on one device (get_no_split_classes).
     """
 
     @classmethod
@@ -357,6 +395,8 @@ class DFloatModel:
                         max_memory: Optional[Dict[Union[int, str], Union[int, str]]] = None,
                         trust_remote_code: bool = True, **kwargs):
         from transformers import AutoConfig, AutoModelForCausalLM
+
+        from dfloat.utils import report_model_size
 
         if not os.path.isdir(dfloat_repo_id):
             raise FileNotFoundError(f"{dfloat_repo_id} is not a local directory "
@@ -367,12 +407,92 @@ class DFloatModel:
             attn_implementation=kwargs.get("attn_implementation"), low_cpu_mem_usage=True)
         model.eval()
         config = AutoConfig.from_pretrained(dfloat_repo_id)
-        dfloat_config = dict(getattr(config, "dfloat_config"))
+        if not hasattr(config, "dfloat_config"):
+            raise ValueError(f"{dfloat_repo_id}/config.json has no dfloat_config entry")
+        dfloat_config = dict(config.dfloat_config)
         with open(os.path.join(dfloat_repo_id, "pattern_dict.json")) as f:
             dfloat_config["pattern_dict"] = json.load(f)
+        before = report_model_size(model, include_pattern=dfloat_config["pattern_dict"]["fp8"])
         load_and_replace_tensors_parallel(model, dfloat_repo_id, dfloat_config)
+        total = report_model_size(model, include_pattern=None)[2]
+        _write_model_size(dfloat_repo_id, [before, (total - before[1], before[1], total)])
         if device:
             model = model.to(device)
-        elif device_map == "auto":
-            model = model.to("cuda")
+        else:
+            if device_map != "auto":
+                raise ValueError('device_map should be "auto" if no specific device is provided.')
+            model = _dispatch_auto(model, max_memory)
+        _warn_if_on_cpu(model)
         return model
+
+
+def _dispatch_auto(model, max_memory):
+    """Spread ``model`` over the visible GPUs with accelerate, keeping each
+    compressed block whole (dfloat/run/run.py:547-557)."""
+    from accelerate import dispatch_model, infer_auto_device_map
+    from accelerate.utils import get_balanced_memory
+
+    from dfloat.const import get_default_no_split_pattern
+
+    no_split = get_no_split_classes(model, get_default_no_split_pattern(type(model).__name__))
+    max_memory = get_balanced_memory(model, max_memory=max_memory,
+                                     no_split_module_classes=no_split)
+    device_map = infer_auto_device_map(model, max_memory=max_memory,
+                                       no_split_module_classes=no_split)
+    return dispatch_model(model, device_map)
+
+
+class DFloatDiffSynthModelFP8:
+    """Compressed DiffSynth pipeline from a local directory
+    (dfloat/run/run.py:569-729).
+
+    The reference builds the pipeline itself from a hub name through
+    DiffSynth (FLUX.1-dev, Wan2.1/2.2, Qwen-Image), which needs the network
+    and the DiffSynth package.  Here ``model_name_or_path`` may instead be an
+    already built pipeline (any ``nn.Module`` whose module names follow the
+    pipeline's, e.g. ``ecf8_amd.dit.FluxPipeline``); a hub name is built
+    through DiffSynth only if that package is importable.  Then, as the
+    reference does: VRAM management is enabled when the pipeline offers it,
+    dfloat_config.json and pattern_dict.json are read from
+    ``dfloat_repo_id``, the per-block safetensors registered with their
+    decode hooks, and the pipeline moved to ``device``.
+    """
+
+    @classmethod
+    def from_pretrained(cls, dfloat_repo_id: str, dfloat_model_id: str, model_name_or_path,
+                        device: Optional[str] = "cuda"):
+        from dfloat.utils import report_model_size
+
+        if not os.path.isdir(dfloat_repo_id):
+            raise FileNotFoundError(f"{dfloat_repo_id} is not a local directory "
+                                    f"(hub download of {dfloat_model_id} is not supported)")
+        if isinstance(model_name_or_path, str):
+            pipe = _diffsynth_pipeline(model_name_or_path)
+        else:
+            pipe = model_name_or_path
+        if hasattr(pipe, "enable_vram_management"):
+            pipe.device = device
+            pipe.enable_vram_management(num_persistent_param_in_dit=0)
+        with open(os.path.join(dfloat_repo_id, "dfloat_config.json")) as f:
+            dfloat_config = json.load(f)
+        with open(os.path.join(dfloat_repo_id, "pattern_dict.json")) as f:
+            dfloat_config["pattern_dict"] = json.load(f)
+        before = report_model_size(pipe, include_pattern=dfloat_config["pattern_dict"]["fp8"])
+        load_and_replace_tensors_parallel(pipe, dfloat_repo_id, dfloat_config)
+        total = report_model_size(pipe, include_pattern=None)[2]
+        _write_model_size(dfloat_repo_id, [before, (total - before[1], before[1], total)])
+        pipe.to(device)
+        pipe.eval()
+        _warn_if_on_cpu(pipe)
+        return pipe
+
+
+def _diffsynth_pipeline(model_name: str):
+    try:
+        import diffsynth  # noqa: F401
+    except ImportError:
+        raise ImportError(
+            f"building the {model_name} pipeline needs the DiffSynth package, which is not "
+            "installed; pass an already built pipeline as model_name_or_path") from None
+    raise ValueError(f"{model_name}: pass the built DiffSynth pipeline as model_name_or_path "
+                     "(pipelines are not downloaded)")

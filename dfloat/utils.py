@@ -2,13 +2,15 @@
 
 Offline, CPU-side producers of the decoder's input: FP8 split, block
 flattening, codebook, decode LUTs and the bitstream encoder (the latter in
-C++ inside libecf8, replacing the reference's per-symbol Python loop).
+C++ inside libecf8, replacing the reference's per-symbol Python loop), plus
+the module lookups and size report the compressor and loaders use.
 """
 
 from __future__ import annotations
 
 import ctypes
 import re
+from sys import stderr
 
 import numpy as np
 import torch
@@ -25,6 +27,11 @@ __all__ = [
     "locate_block_by_regex",
     "find_layers_by_data_type_and_layer_type",
     "find_layers_by_selection",
+    "find_layers_by_layer_type",
+    "find_layers_by_data_type",
+    "param_to_bytes",
+    "report_model_size",
+    "repo_id_to_model_id",
 ]
 
 
@@ -146,7 +153,7 @@ def encode_exponents_for_cuda(exponents_4bits, codec, bytes_per_thread: int = 8,
     """Encode 4-bit exponents into (encoded u8, gaps u8, output_positions u64)
     torch tensors; same outputs as dfloat/utils.py:502-530, computed by the
     C++ encoder in libecf8 (ecf8_encode_exponents)."""
-    from ._lib import check, lib
+    from ecf8_amd._lib import check, lib
 
     if isinstance(exponents_4bits, torch.Tensor):
         exps = exponents_4bits.detach().to("cpu", torch.uint8).contiguous().numpy()
@@ -211,3 +218,84 @@ def find_layers_by_selection(module, select, name=""):
         full = f"{name}.{child_name}" if name else child_name
         res.update(find_layers_by_selection(child, select, full))
     return dict(sorted(res.items()))
+
+
+def find_layers_by_layer_type(module, layers=(torch.nn.Linear,), name=""):
+    """Name-sorted {name: module} of the outermost modules whose type is one
+    of ``layers`` (dfloat/utils.py:120-132)."""
+    if type(module) in tuple(layers):
+        return {name: module}
+    res = {}
+    for child_name, child in module.named_children():
+        full = f"{name}.{child_name}" if name else child_name
+        res.update(find_layers_by_layer_type(child, layers, full))
+    return dict(sorted(res.items()))
+
+
+def find_layers_by_data_type(module, target_dtype=torch.bfloat16, name=""):
+    """Name-sorted {name: module} of the outermost modules whose ``weight``
+    has ``target_dtype`` (dfloat/utils.py:135-155)."""
+    if getattr(getattr(module, "weight", None), "dtype", None) == target_dtype:
+        return {name: module}
+    res = {}
+    for child_name, child in module.named_children():
+        full = f"{name}.{child_name}" if name else child_name
+        res.update(find_layers_by_data_type(child, target_dtype, full))
+    return dict(sorted(res.items()))
+
+
+# ------------------------------------------------------------- size report
+
+_ELEMENT_BYTES = {
+    1: (torch.uint8, torch.int8, torch.float8_e4m3fn),
+    2: (torch.float16, torch.bfloat16, torch.int16, torch.uint16),
+    4: (torch.float32, torch.int32, torch.uint32),
+    8: (torch.float64, torch.int64, torch.uint64),
+}
+
+
+def param_to_bytes(param) -> int:
+    """Storage bytes of a tensor for the dtypes a checkpoint holds
+    (dfloat/utils.py:11-21); ValueError for any other dtype."""
+    for size, dtypes in _ELEMENT_BYTES.items():
+        if param.dtype in dtypes:
+            return param.numel() * size
+    raise ValueError(f"Unrecognized parameter data type {param.dtype}.")
+
+
+def _included(name: str, include_pattern) -> bool:
+    if isinstance(include_pattern, list):
+        return any(re.search(p, name) for p in include_pattern)
+    for pattern, attrs in include_pattern.items():
+        if re.search(pattern, name) and any(a in name for a in (attrs or ())):
+            return True
+    return False
+
+
+def report_model_size(model, include_pattern):
+    """(included GiB, excluded GiB, total GiB) of ``model.state_dict()``
+    (dfloat/utils.py:24-67).  ``include_pattern``: a list of regexes searched
+    in each state-dict name; a dict {regex: attribute names}, where a name
+    counts when it matches the regex and contains one of the attributes; or
+    None (everything included).  The three figures go to stderr."""
+    if include_pattern is not None and not isinstance(include_pattern, (list, dict)):
+        raise ValueError("`include_pattern` must be either a list of strings or a dictionary, "
+                         "or None")
+    inc = exc = 0
+    for name, tensor in model.state_dict().items():
+        if include_pattern is None or _included(name, include_pattern):
+            inc += param_to_bytes(tensor)
+        else:
+            exc += param_to_bytes(tensor)
+    gib = 1024 ** 3
+    inc_gb, exc_gb, tot_gb = inc / gib, exc / gib, (inc + exc) / gib
+    print(f"Included model size: {inc_gb:0.4f} GB", file=stderr)
+    print(f"Excluded model size: {exc_gb:0.4f} GB", file=stderr)
+    print(f"Total model size: {tot_gb:0.4f} GB", file=stderr)
+    return inc_gb, exc_gb, tot_gb
+
+
+def repo_id_to_model_id(repo_id: str) -> str:
+    """Hub cache directory name of a repo id: "org/name" -> "models--org--name"
+    (dfloat/utils.py:70-72)."""
+    return "models--" + "--".join(repo_id.split("/"))

@@ -344,8 +344,8 @@ def compress_blocks(pipe: FluxPipeline, drawn=None, threads_per_block: int = 512
     """Compress every double and single block as the reference does
     (one block per ``dit.blocks.N`` / ``dit.single_blocks.N`` match) and
     install the decode hooks through the loader's registration."""
-    from .compress import compress_flat
-    from .run import _process_compressed_tensor
+    from dfloat.compress import compress_flat
+    from dfloat.run.run import _process_compressed_tensor
     from .synth import flat_block
 
     groups = ((pipe.dit.blocks, "dit.blocks", DOUBLE_REGEX, DOUBLE_LINEARS,

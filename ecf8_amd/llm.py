@@ -361,8 +361,8 @@ def compress_layers(model: Qwen3ForCausalLM, drawn=None, threads_per_block: int 
     (dfloat/run/run.py:406-458).  ``drawn`` (from random_model) lets layers
     that share weights share one compression; each layer still gets its own
     device copy of the compressed tensors."""
-    from .compress import compress_flat
-    from .run import _process_compressed_tensor
+    from dfloat.compress import compress_flat
+    from dfloat.run.run import _process_compressed_tensor
     from .synth import flat_block
 
     pattern = {LAYER_REGEX: list(LINEAR_NAMES)}

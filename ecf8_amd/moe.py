@@ -142,7 +142,7 @@ class _LayerExperts:
             if expert_buf is None or expert_buf.numel() < n_e * len(experts):
                 raise ECF8Error("expert buffer too small for the layer's experts")
             blocks, outs, tables, largest = [], [], [], 0
-            from .run import _module_state
+            from dfloat.run.run import _module_state
 
             for e, ex in enumerate(experts):
                 if ex.packed_other_4bits.numel() * 2 != n_e:
@@ -343,8 +343,8 @@ def compress_moe_layers(model: Qwen3MoeForCausalLM, drawn=None, threads_per_bloc
     (the reference's qwen3moe patterns) and register them through the
     loader's path.  ``drawn`` (from random_moe_model) lets layers that share
     weights share one compression; every layer gets its own device copy."""
-    from .compress import compress_flat
-    from .run import _process_compressed_tensor
+    from dfloat.compress import compress_flat
+    from dfloat.run.run import _process_compressed_tensor
     from .synth import flat_block
 
     cache = {}

@@ -28,7 +28,7 @@ from __future__ import annotations
 import torch
 
 from . import decode as _dev
-from .run import _inject, _module_state
+from dfloat.run.run import _inject, _module_state
 
 _KEYS = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
 

@@ -71,7 +71,7 @@ def _fp8_model(seed=0):
 
 @pytest.fixture(scope="module")
 def saved(tmp_path_factory):
-    from ecf8_amd.compress import compress_model
+    from dfloat.compress import compress_model
 
     d = str(tmp_path_factory.mktemp("ckpt"))
     m, originals = _fp8_model()
@@ -84,7 +84,7 @@ def test_parallel_compression_writes_the_same_checkpoint(saved, tmp_path):
     give byte-identical block files and the same pattern dict."""
     from safetensors.torch import load_file
 
-    from ecf8_amd.compress import compress_model
+    from dfloat.compress import compress_model
 
     d0, pattern0, _ = saved
     m, _ = _fp8_model()
@@ -114,8 +114,15 @@ def test_checkpoint_files_follow_the_reference_layout(saved):
     from safetensors.torch import load_file
 
     d, pattern, _ = saved
+    # a module with neither a Hugging Face config nor a pipeline pattern gets
+    # the whole state dict in one file
     assert sorted(f for f in os.listdir(d) if not os.path.isdir(os.path.join(d, f))) == [
-        "dfloat_config.json", "model.safetensors", "pattern_dict.json"]
+        "dfloat_config.json", "entropy.csv", "model.safetensors", "pattern_dict.json"]
+    with open(os.path.join(d, "entropy.csv")) as f:
+        rows = f.read().split()
+    assert rows[0] == "block_name,entropy"
+    assert [r.split(",")[0] for r in rows[1:]] == [f"model.layers.{i}" for i in range(3)]
+    assert all(1.0 < float(r.split(",")[1]) < 4.0 for r in rows[1:])
     assert json.load(open(os.path.join(d, "pattern_dict.json"))) == {
         "fp8": {r"model\.layers\.\d+": sorted(LINEARS)}, "bf16": {"lm_head": []}}
     cfg = json.load(open(os.path.join(d, "dfloat_config.json")))
@@ -146,7 +153,7 @@ def test_stored_blocks_decode_to_the_original_weights_on_cpu(saved):
 
 
 def test_load_registers_buffers_hooks_and_removes_weights(saved):
-    from ecf8_amd.run import load_compressed_model
+    from dfloat.run.run import load_compressed_model
 
     d, _, _ = saved
     fresh = _Model()
@@ -162,7 +169,7 @@ def test_load_registers_buffers_hooks_and_removes_weights(saved):
 
 @pytest.mark.gpu
 def test_loaded_checkpoint_injects_bit_exact_weights(saved, cuda_device):
-    from ecf8_amd.run import TensorManager, load_compressed_model
+    from dfloat.run.run import TensorManager, load_compressed_model
 
     d, _, originals = saved
     fresh = load_compressed_model(_Model(), d, parallel=True).to(cuda_device)

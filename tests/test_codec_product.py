@@ -31,7 +31,7 @@ def _random_counter(rng):
 
 @pytest.mark.parametrize("seed", range(200))
 def test_huffman_table_equals_restated_dahuffman(seed):
-    from ecf8_amd.huffman import HuffmanCodec
+    from dfloat.huffman import HuffmanCodec
 
     counter = _random_counter(np.random.default_rng(seed))
     ours = HuffmanCodec.from_frequencies(counter).get_code_table()
@@ -42,7 +42,7 @@ def test_huffman_table_equals_restated_dahuffman(seed):
 
 @pytest.mark.parametrize("seed", range(100))
 def test_luts_equal_oracle(seed):
-    from ecf8_amd.utils import get_luts_from_huffman_table, get_nbit_codec
+    from dfloat.utils import get_luts_from_huffman_table, get_nbit_codec
 
     counter = _random_counter(np.random.default_rng(1000 + seed))
     table = get_nbit_codec(counter, 16)[2]
@@ -53,7 +53,7 @@ def test_luts_equal_oracle(seed):
 
 @pytest.mark.parametrize("name", CASES)
 def test_product_compressor_reproduces_golden(name):
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
 
     g = _golden(name)
     tpb = int(g["threads_per_block"])
@@ -77,9 +77,9 @@ def test_oracle_reproduces_golden(name):
 
 @pytest.mark.parametrize("shape", [(4096, 4096), (1000, 2)])
 def test_product_encoder_equals_c_oracle_at_size(shape, oracle_native):
-    from ecf8_amd.huffman import HuffmanCodec
+    from dfloat.huffman import HuffmanCodec
     from ecf8_amd.synth import synthetic_fp8
-    from ecf8_amd.utils import encode_exponents_for_cuda, get_exponents_and_other_4bits_fp8_e4m3
+    from dfloat.utils import encode_exponents_for_cuda, get_exponents_and_other_4bits_fp8_e4m3
 
     if shape == (1000, 2):
         w = torch.from_numpy(np.random.default_rng(0).integers(0, 256, 2000, dtype=np.uint8))
@@ -162,8 +162,8 @@ def test_validator_rejects_fault(fault):
 
 def test_encoder_rejects_symbol_without_code():
     from ecf8_amd._lib import ECF8Error
-    from ecf8_amd.huffman import HuffmanCodec
-    from ecf8_amd.utils import encode_exponents_for_cuda
+    from dfloat.huffman import HuffmanCodec
+    from dfloat.utils import encode_exponents_for_cuda
 
     codec = HuffmanCodec.from_frequencies({3: 10, 4: 5})
     with pytest.raises(ECF8Error):

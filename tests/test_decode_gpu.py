@@ -74,7 +74,7 @@ def _gpu_decode(block, dev, tpb=512, n_elements=None, out=None, kind=ANY):
 
 
 def _compress(flat_u8: np.ndarray, tpb=512):
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
 
     flat = torch.from_numpy(np.ascontiguousarray(flat_u8)).view(torch.float8_e4m3fn)
     res = compress_flat(flat, 8, tpb)
@@ -180,7 +180,7 @@ def test_largest_block_the_format_allows(cuda_device, qwen3_layer_flat):
     more than 2^31 - 65): the Qwen3 layer tiled 12 times, compressed as one
     block, decoded bit-exact by the automaton kernel.  Positions past 2^30
     exercise the kernel's 32-bit position arithmetic."""
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
     from ecf8_amd.decode import build_table, decode_into, largest_block, min_code_bits
 
     n = 2 ** 31 - 2 ** 17
@@ -331,7 +331,7 @@ def test_min_code_bits_unknown_equals_derived(seed, cuda_device):
     from ecf8_amd.decode import decode, min_code_bits
 
     _say(f"min_code_bits seed {seed}")
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
 
     flat = _random_block(seed)
     res = compress_flat(torch.from_numpy(flat).view(torch.float8_e4m3fn))
@@ -373,7 +373,7 @@ def test_min_code_bits_above_the_truth_stays_in_bounds(cuda_device):
 def test_reference_call_form_of_decode(cuda_device):
     """_decode(grid=, block=, shared_mem=, args=[...]) exactly as
     scripts/compress.py:109-124 calls the CUDA kernel."""
-    from ecf8_amd.run import _decode
+    from dfloat.run.run import _decode
 
     flat = _random_block(20)
     d = _dev_block(_compress(flat), cuda_device)
@@ -390,7 +390,7 @@ def test_reference_call_form_of_decode(cuda_device):
 
 
 def test_validate_cuda_decoding_fp8_api(cuda_device):
-    from ecf8_amd.compress import compress_flat, validate_cuda_decoding_fp8
+    from dfloat.compress import compress_flat, validate_cuda_decoding_fp8
 
     flat = torch.from_numpy(_random_block(4)).view(torch.float8_e4m3fn)
     res = compress_flat(flat)
@@ -414,10 +414,10 @@ def test_forward_pre_hook_injects_bit_exact_weights(cuda_device):
     """Block-level hook flow: flatten name-sorted linears, compress, register
     buffers + hook the way the loader does (run.py:406-458), forward, and
     compare every injected .weight with the original FP8 tensor."""
-    from ecf8_amd.compress import compress_flat
-    from ecf8_amd.run import TensorManager, _process_compressed_tensor
+    from dfloat.compress import compress_flat
+    from dfloat.run.run import TensorManager, _process_compressed_tensor
     from ecf8_amd.synth import synthetic_fp8
-    from ecf8_amd.utils import flatten_block_of_weights
+    from dfloat.utils import flatten_block_of_weights
 
     shapes = {"attn.q": (256, 128), "attn.k": (128, 128), "mlp.up": (384, 128)}
     blk = _Block(shapes)

@@ -1,8 +1,9 @@
 """DFloatModel.from_pretrained (dfloat/run/run.py:483-566) over a real
 transformers model, on the CPU: a tiny random Qwen3ForCausalLM is saved
 locally, its decoder layers' Linears are given FP8 weights and compressed
-in the reference's layout (config.json carrying ``dfloat_config``,
-pattern_dict.json, the compressed safetensors), and the loader registers
+by ``compress_model``, which writes the reference's layout through
+``save_pretrained`` (config.json carrying ``dfloat_config``,
+pattern_dict.json, the compressed safetensors); the loader registers
 every layer's compressed block on a fresh instance of the original model.
 Each registered block decodes (oracle) to the FP8 weights that were
 compressed, and the dense weights it replaces are gone."""
@@ -34,7 +35,7 @@ def _tiny_config():
 def _checkpoint(tmp_path):
     """(original model dir, compressed dir, the original model, its FP8
     weights by Linear path)."""
-    from ecf8_amd.compress import compress_model
+    from dfloat.compress import compress_model
     from ecf8_amd.synth import synthetic_fp8
 
     torch.manual_seed(0)
@@ -51,21 +52,25 @@ def _checkpoint(tmp_path):
             w, _ = synthetic_fp8(lin.out_features, lin.in_features, 0.02, seed=li * 10 + k)
             lin.weight = torch.nn.Parameter(w, requires_grad=False)
             fp8[f"model.layers.{li}.{path}"] = w.view(torch.uint8).clone()
-    pattern = compress_model(model, [r"model\.layers\.\d+"], comp_dir, n_workers=2)
+    pattern = compress_model(model, [r"model\.layers\.\d+"], comp_dir, n_workers=2,
+                             bf16_regex=[r"model\.embed_tokens", r"lm_head"])
     assert pattern["fp8"][r"model\.layers\.\d+"] == list(LINEARS)
-    # the compressed model's config.json carries dfloat_config
-    # (scripts/compress.py:648-680)
-    with open(os.path.join(orig_dir, "config.json")) as f:
+    # the compressor writes the reference's layout for a transformers model
+    # (scripts/compress.py:668-677): config.json carries dfloat_config, and
+    # no separate dfloat_config.json is written
+    with open(os.path.join(comp_dir, "config.json")) as f:
         cfg = json.load(f)
-    with open(os.path.join(comp_dir, "dfloat_config.json")) as f:
-        cfg["dfloat_config"] = json.load(f)
-    with open(os.path.join(comp_dir, "config.json"), "w") as f:
-        json.dump(cfg, f)
+    assert cfg["dfloat_config"] == {"version": "0.2.0", "threads_per_block": 512,
+                                    "bytes_per_thread": 8}
+    assert not os.path.exists(os.path.join(comp_dir, "dfloat_config.json"))
+    with open(os.path.join(comp_dir, "pattern_dict.json")) as f:
+        assert json.load(f) == {"fp8": {r"model\.layers\.\d+": list(LINEARS)},
+                                "bf16": {r"model\.embed_tokens": [], r"lm_head": []}}
     return orig_dir, comp_dir, model, fp8
 
 
 def test_dfloat_model_loads_a_compressed_transformers_checkpoint(tmp_path):
-    from ecf8_amd.run import DFloatModel
+    from dfloat.run.run import DFloatModel
 
     orig_dir, comp_dir, model, fp8 = _checkpoint(tmp_path)
     loaded = DFloatModel.from_pretrained(comp_dir, "local/tiny-DF6.5", orig_dir, device="cpu")
@@ -89,7 +94,7 @@ def test_dfloat_model_hooks_inject_bit_exact_weights(tmp_path, cuda_device):
     """The same checkpoint loaded onto the GPU: each decoder layer's
     forward-pre-hook decodes its block with the HIP kernel and injects
     views equal to the FP8 weights that were compressed."""
-    from ecf8_amd.run import DFloatModel, TensorManager
+    from dfloat.run.run import DFloatModel, TensorManager
 
     orig_dir, comp_dir, _model, fp8 = _checkpoint(tmp_path)
     TensorManager.clear_device()

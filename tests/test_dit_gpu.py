@@ -30,7 +30,7 @@ SMALL = dict(hidden=256, heads=2, mlp=512, double=2, single=2, txt_dim=128, pool
 
 def test_compressed_dit_samples_exactly_like_fp8(cuda_device):
     from ecf8_amd.dit import FluxConfig, compress_blocks, generate, random_pipeline
-    from ecf8_amd.run import TensorManager
+    from dfloat.run.run import TensorManager
 
     cfg = FluxConfig(**SMALL)
     plain, drawn = random_pipeline(cfg, cuda_device, seed=3)

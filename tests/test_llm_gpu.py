@@ -387,7 +387,7 @@ def _prompt(cfg, B, T):
 
 def test_compressed_model_matches_uncompressed_exactly(small_models, cuda_device):
     from ecf8_amd.llm import Qwen3Runner
-    from ecf8_amd.run import TensorManager
+    from dfloat.run.run import TensorManager
 
     cfg, plain, comp = small_models
     B, T, new = 2, 16, 8

@@ -188,7 +188,7 @@ def test_compressed_moe_matches_uncompressed_exactly(small_moe_models, cuda_devi
     the router picks them (prompt: every expert), eager and graph-replayed:
     the same tokens and logits as the model kept in FP8."""
     from ecf8_amd.moe import Qwen3MoeRunner
-    from ecf8_amd.run import TensorManager
+    from dfloat.run.run import TensorManager
 
     cfg, plain, comp = small_moe_models
     B, T, new = 4, 40, 6

@@ -143,7 +143,7 @@ def test_dfa_walk_equals_oracle_on_random_codes(seed):
 
 
 def test_dfa_is_chosen_for_the_synthetic_weight_histogram():
-    from ecf8_amd.compress import compress_flat
+    from dfloat.compress import compress_flat
     from ecf8_amd.decode import ECF8_TABLE_ANY, ECF8_TABLE_DFA
     from ecf8_amd.synth import synthetic_fp8
 
