@@ -18,9 +18,7 @@ are ordered without any cross-runtime synchronisation.
 
 from __future__ import annotations
 
-import ctypes
 import json
-import math
 import os
 import re
 from sys import stderr
@@ -51,21 +49,14 @@ class _DecodeLauncher:
     "decode")`` (dfloat/run/run.py:24-33).  ``args`` are the reference
     kernel's: luts, encoded, packed_other_4bits, output_positions, gaps,
     outputs (device addresses), n_luts, n_bytes, n_elements
-    (decode.cu:16-26).  The derived table for the given LUTs is rebuilt into
-    a per-device scratch table on every call (the LUTs are read back to the
-    host, which synchronizes the stream); the hook path caches it per module
-    instead."""
-
-    def __init__(self):
-        self._tables = {}
-
-    def _table(self, device_index: int) -> torch.Tensor:
-        t = self._tables.get(device_index)
-        if t is None:
-            t = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32,
-                            device=torch.device("cuda", device_index))
-            self._tables[device_index] = t
-        return t
+    (decode.cu:16-26).  Like the reference's launch it is asynchronous on the
+    current stream: each call builds the derived table for the given LUTs on
+    the device (one workgroup, into a table buffer from torch's allocator on
+    that stream), then launches the decode, which reads the table's kind on
+    the device.  Nothing returns to the host, so the call can be captured in
+    a HIP graph, and a LUT buffer whose contents change between calls is
+    always decoded with its current contents.  The hook path builds each
+    module's table once instead."""
 
     def __call__(self, grid, block, args, shared_mem: int = 0, stream=None):
         luts, encoded, packed, op, gaps, outputs, n_luts, n_bytes, n_elements = args
@@ -77,15 +68,19 @@ class _DecodeLauncher:
         if nblk != _dev.n_format_blocks(n_bytes, tpb, bpt):
             raise ECF8Error(f"grid {nblk} does not cover {n_bytes} bytes with {tpb} threads")
         dev = torch.cuda.current_device()
-        table = self._table(dev)
-        s = (torch.cuda.current_stream(dev) if stream is None else stream).cuda_stream
+        st = torch.cuda.current_stream(dev) if stream is None else stream
+        with torch.cuda.stream(st):
+            table = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32,
+                                device=torch.device("cuda", dev))
+        s = st.cuda_stream
         L = lib()
-        kind = ctypes.c_int(-1)
-        check(L.ecf8_build_table(int(luts), int(n_luts), ECF8_TABLE_ANY, table.data_ptr(),
-                                 ctypes.byref(kind), s), "ecf8_build_table")
+        check(L.ecf8_build_table(int(luts), int(n_luts), ECF8_TABLE_ANY, table.data_ptr(), None, s),
+              "ecf8_build_table")
         check(L.ecf8_decode(int(luts), int(encoded), int(packed), int(op), int(gaps), int(outputs),
                             int(n_luts), int(n_bytes), int(n_elements), max_block, 0,
-                            table.data_ptr(), kind.value, tpb, bpt, s), "ecf8_decode")
+                            table.data_ptr(), ECF8_TABLE_ANY, tpb, bpt, s), "ecf8_decode")
+        # the table is freed back to torch's allocator on this stream: a later
+        # allocation on the stream runs after this decode
 
 
 _decode = _DecodeLauncher()

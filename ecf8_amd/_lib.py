@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must be loaded before libecf8.so)
 from .build import LIB_PATH
 
 ECF8_OK = 0
-ECF8_TABLE_BYTES = 24608
+ECF8_TABLE_BYTES = 24624
 ECF8_MAX_LUTS = 18
 ECF8_TABLE_ANY = -1
 ECF8_TABLE_MULTI = 0

@@ -581,7 +581,9 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s
 // SGPRs are capped at 80: measured on MI355X, above that fewer than 8 waves
 // per SIMD fit (3 workgroups of 512 per CU instead of 4); the few spills
 // the cap causes go to VGPR lanes.
-template <int kThreads, bool kChecked>
+// kKindCheck: the table's kind is only known on the device (built there by
+// ecf8_build_table); the grid exits unless the table is an automaton.
+template <int kThreads, bool kChecked, bool kKindCheck>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
     const uint8_t *__restrict__ encoded, uint32_t n_bytes,
@@ -596,6 +598,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   // dwords that take the ORs of positions past the buffer
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
 
+  if (kKindCheck && table[kDfaEntries] != (uint32_t)ECF8_TABLE_DFA) return;  // uniform
   const int tid = threadIdx.x;
   load_dfa_batched<kThreads>(s_dfa, table, tid);
   if (tid < kEdgeDwords) s_edge[tid] = 0u;
@@ -752,7 +755,9 @@ __host__ __device__ constexpr int run_slots_for(int min_bits) {
 }
 constexpr int kZeroEntry = kMultiEntries;  // all-zero table entry: a lookup that does nothing
 
-template <int kThreads, bool kChecked>
+// kKindCheck: as for decode_dfa_kernel, the grid exits unless the table is
+// a multi-symbol table.
+template <int kThreads, bool kChecked, bool kKindCheck>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void decode_multi_kernel(
     const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
     const uint8_t *__restrict__ encoded, uint32_t n_bytes, const uint8_t *__restrict__ packed,
@@ -765,6 +770,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
   __shared__ int s_wave_sum[kWaves];
   __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
 
+  if (kKindCheck && table[kDfaEntries] != (uint32_t)ECF8_TABLE_MULTI) return;  // uniform
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -983,8 +989,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
 
 // Per device: CU count, and per kernel variant the occupancy at the last
 // dynamic LDS size it was launched with.
-// {DFA, MULTI} x 4 block sizes x {unchecked, checked}, then batched DFA x 4
-constexpr int kVariants = 20;
+// {DFA, MULTI} x 4 block sizes x {unchecked, checked} (slots 0-15), batched
+// DFA x 4 (16-19), then the device-kind variants of DFA and MULTI (20-35)
+constexpr int kVariants = 36;
 struct LaunchCache {
   int device = -1;
   int cus = 0;
@@ -1041,12 +1048,12 @@ struct DecodeArgs {
   hipStream_t stream;
 };
 
-template <int kThreads, bool kChecked>
+template <int kThreads, bool kChecked, bool kKindCheck>
 int launch_dfa(const DecodeArgs &a, int slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(a.cap) + kSpillDwords);
   const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
-  auto kernel = decode_dfa_kernel<kThreads, kChecked>;
+  auto kernel = decode_dfa_kernel<kThreads, kChecked, kKindCheck>;
   int grid = 0;
   const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
                                  slot, a.n_fb, &grid);
@@ -1057,7 +1064,7 @@ int launch_dfa(const DecodeArgs &a, int slot) {
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
-template <int kThreads, bool kChecked>
+template <int kThreads, bool kChecked, bool kKindCheck>
 int launch_multi(const DecodeArgs &a, int slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   const int mb = a.min_code_bits >= 1 && a.min_code_bits <= 16 ? a.min_code_bits : 1;
@@ -1066,7 +1073,7 @@ int launch_multi(const DecodeArgs &a, int slot) {
       sizeof(uint32_t) * ((size_t)run_slots * kThreads + 2 * (size_t)stage_dwords(a.cap));
   const size_t max_dyn = sizeof(uint32_t) * ((size_t)run_slots_for(1) * kThreads +
                                              2 * (size_t)stage_dwords(kMaxSyms));
-  auto kernel = decode_multi_kernel<kThreads, kChecked>;
+  auto kernel = decode_multi_kernel<kThreads, kChecked, kKindCheck>;
   int grid = 0;
   const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
                                  slot, a.n_fb, &grid);
@@ -1077,8 +1084,11 @@ int launch_multi(const DecodeArgs &a, int slot) {
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
+// kind: ECF8_TABLE_DFA, ECF8_TABLE_MULTI, or ECF8_TABLE_ANY (read on the
+// device: both kernels are launched, and the one the table is not for exits
+// at once).
 template <int kThreads>
-int launch_decode(DecodeArgs a, int64_t max_block_elements, bool dfa, int tpb_slot) {
+int launch_decode(DecodeArgs a, int64_t max_block_elements, int kind, int tpb_slot) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   const int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms)
                       ? kMaxSyms
@@ -1086,10 +1096,22 @@ int launch_decode(DecodeArgs a, int64_t max_block_elements, bool dfa, int tpb_sl
   a.cap = cap < 16 ? 16 : cap;
   // the clamped vector loads need 12 bitstream bytes and 8 nibble bytes
   const bool checked = a.n_bytes < 12 || a.n_elements < 16;
-  const int slot = (dfa ? 0 : 8) + 2 * tpb_slot + (checked ? 1 : 0);
-  if (dfa)
-    return checked ? launch_dfa<kThreads, true>(a, slot) : launch_dfa<kThreads, false>(a, slot);
-  return checked ? launch_multi<kThreads, true>(a, slot) : launch_multi<kThreads, false>(a, slot);
+  const int c = checked ? 1 : 0;
+  if (kind == ECF8_TABLE_DFA) {
+    const int slot = 2 * tpb_slot + c;
+    return checked ? launch_dfa<kThreads, true, false>(a, slot)
+                   : launch_dfa<kThreads, false, false>(a, slot);
+  }
+  if (kind == ECF8_TABLE_MULTI) {
+    const int slot = 8 + 2 * tpb_slot + c;
+    return checked ? launch_multi<kThreads, true, false>(a, slot)
+                   : launch_multi<kThreads, false, false>(a, slot);
+  }
+  const int rc = checked ? launch_dfa<kThreads, true, true>(a, 20 + 2 * tpb_slot + c)
+                         : launch_dfa<kThreads, false, true>(a, 20 + 2 * tpb_slot + c);
+  if (rc != ECF8_OK) return rc;
+  return checked ? launch_multi<kThreads, true, true>(a, 28 + 2 * tpb_slot + c)
+                 : launch_multi<kThreads, false, true>(a, 28 + 2 * tpb_slot + c);
 }
 
 template <int kThreads>
@@ -1179,28 +1201,6 @@ extern "C" int ecf8_decode_batched_select(const ecf8_block_desc *descs, int coun
   }
 }
 
-extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, uint32_t *table,
-                                int *table_kind, void *stream) {
-  if (!luts || !table) return ECF8_ERR_INVALID_ARG;
-  if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
-  if (((uintptr_t)luts & 3) || ((uintptr_t)table & 3)) return ECF8_ERR_MISALIGNED;
-  hipStream_t s = (hipStream_t)stream;
-  std::vector<uint8_t> h_luts((size_t)n_luts * 256);
-  std::vector<uint32_t> h_table(ECF8_TABLE_BYTES / 4);
-  if (hipMemcpyAsync(h_luts.data(), luts, h_luts.size(), hipMemcpyDeviceToHost, s) != hipSuccess ||
-      hipStreamSynchronize(s) != hipSuccess)
-    return ECF8_ERR_HIP;
-  int kind = 0;
-  const int rc = ecf8_build_table_host(h_luts.data(), n_luts, want_kind, h_table.data(), &kind);
-  if (rc != ECF8_OK) return rc;
-  if (hipMemcpyAsync(table, h_table.data(), ECF8_TABLE_BYTES, hipMemcpyHostToDevice, s) !=
-          hipSuccess ||
-      hipStreamSynchronize(s) != hipSuccess)
-    return ECF8_ERR_HIP;
-  if (table_kind) *table_kind = kind;
-  return ECF8_OK;
-}
-
 extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
                            const uint8_t *packed_other_4bits, const uint64_t *output_positions,
                            const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
@@ -1213,7 +1213,9 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   if (n_bytes > INT32_MAX - 64 || n_elements > INT32_MAX - 64) return ECF8_ERR_UNSUPPORTED;
   if (bytes_per_thread != kChunkBytes) return ECF8_ERR_UNSUPPORTED;
   if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
-  if (table_kind != ECF8_TABLE_MULTI && table_kind != ECF8_TABLE_DFA) return ECF8_ERR_INVALID_ARG;
+  if (table_kind != ECF8_TABLE_MULTI && table_kind != ECF8_TABLE_DFA &&
+      table_kind != ECF8_TABLE_ANY)
+    return ECF8_ERR_INVALID_ARG;
   const int64_t fb_bytes = (int64_t)threads_per_block * bytes_per_thread;
   if (threads_per_block != 128 && threads_per_block != 256 && threads_per_block != 512 &&
       threads_per_block != 1024)
@@ -1229,15 +1231,14 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   DecodeArgs a{luts,      n_luts, table,      encoded, n_bytes, packed_other_4bits,
                output_positions, gaps, outputs, n_elements, n_fb, 0,
                min_code_bits, (hipStream_t)stream};
-  const bool dfa = table_kind == ECF8_TABLE_DFA;
   switch (threads_per_block) {
     case 128:
-      return launch_decode<128>(a, max_block_elements, dfa, 0);
+      return launch_decode<128>(a, max_block_elements, table_kind, 0);
     case 256:
-      return launch_decode<256>(a, max_block_elements, dfa, 1);
+      return launch_decode<256>(a, max_block_elements, table_kind, 1);
     case 512:
-      return launch_decode<512>(a, max_block_elements, dfa, 2);
+      return launch_decode<512>(a, max_block_elements, table_kind, 2);
     default:
-      return launch_decode<1024>(a, max_block_elements, dfa, 3);
+      return launch_decode<1024>(a, max_block_elements, table_kind, 3);
   }
 }

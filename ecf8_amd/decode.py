@@ -24,7 +24,8 @@ __all__ = ["DecodeTable", "build_table", "build_table_host", "decode_into", "dec
 
 class DecodeTable(NamedTuple):
     """A derived decode table on the device and its kind (ECF8_TABLE_DFA or
-    ECF8_TABLE_MULTI); the kind selects the decode kernel."""
+    ECF8_TABLE_MULTI, which selects the decode kernel, or ECF8_TABLE_ANY when
+    the kind is only known on the device)."""
 
     data: torch.Tensor
     kind: int
@@ -97,24 +98,33 @@ def build_table_host(luts, kind: int = ECF8_TABLE_ANY):
 
 
 def build_table(luts: torch.Tensor, out: torch.Tensor | None = None, stream=None,
-                kind: int = ECF8_TABLE_ANY) -> DecodeTable:
-    """Derived decode table for ``luts`` (a CUDA tensor), built on the host
-    and copied to ``luts``' device (into ``out`` if given).  Synchronizes:
-    call once per compressed block, at load time."""
+                kind: int = ECF8_TABLE_ANY, sync: bool = True) -> DecodeTable:
+    """Derived decode table for ``luts`` (a CUDA tensor), built on its
+    device by the table kernel (into ``out`` if given) on ``stream``.
+
+    ``sync=True`` reads the kind back (one stream synchronization: call once
+    per compressed block, at load time) so that decodes launch only the
+    kernel for that kind.  ``sync=False`` stays asynchronous -- nothing
+    returns to the host, so the call can be graph-captured -- and the
+    table's kind is ECF8_TABLE_ANY: decodes then read it on the device."""
     if not luts.is_cuda or luts.dtype != torch.uint8 or not luts.is_contiguous():
         raise ECF8Error("luts must be a contiguous uint8 CUDA tensor")
     n_luts = _n_luts(luts)
     if not 2 <= n_luts <= ECF8_MAX_LUTS:
         raise ECF8Error(f"n_luts={n_luts} outside [2, {ECF8_MAX_LUTS}]")
-    table, got = build_table_host(luts, kind)
-    host = torch.from_numpy(table.view(np.int32))
+    if not sync and kind == ECF8_TABLE_DFA:
+        raise ECF8Error("an automaton-only table needs sync=True to report a refusal")
     if out is None:
-        out = host.to(luts.device)
-    else:
-        if out.numel() * out.element_size() < ECF8_TABLE_BYTES or out.device != luts.device:
-            raise ECF8Error("table buffer too small or on another device")
-        out.view(torch.int32)[: host.numel()].copy_(host)
-    return DecodeTable(out, got)
+        out = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32, device=luts.device)
+    elif (out.numel() * out.element_size() < ECF8_TABLE_BYTES or out.device != luts.device
+          or not out.is_contiguous() or out.data_ptr() % 4):
+        raise ECF8Error("table buffer too small, misaligned or on another device")
+    got = ctypes.c_int(-1)
+    with torch.cuda.device(luts.device):
+        check(lib().ecf8_build_table(luts.data_ptr(), n_luts, int(kind), out.data_ptr(),
+                                     ctypes.byref(got) if sync else None,
+                                     _stream_handle(luts.device, stream)), "ecf8_build_table")
+    return DecodeTable(out, got.value if sync else ECF8_TABLE_ANY)
 
 
 def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,

@@ -27,8 +27,10 @@ extern "C" {
 #define ECF8_ERR_HIP 5               /* HIP runtime error (launch, device)     */
 #define ECF8_ERR_CAPACITY 6          /* caller buffer too small                */
 
-/* Bytes of a derived decode table buffer (either kind). */
-#define ECF8_TABLE_BYTES 24608
+/* Bytes of a derived decode table buffer (either kind): the table's entries,
+ * then at u32 index 6152 the kind it holds (ECF8_TABLE_DFA or
+ * ECF8_TABLE_MULTI), then zero padding. */
+#define ECF8_TABLE_BYTES 24624
 /* Kinds of derived decode table. */
 #define ECF8_TABLE_ANY (-1)   /* builder's choice: DFA when the LUTs allow it */
 #define ECF8_TABLE_MULTI 0    /* 12-bit multi-symbol table; any LUT stack      */
@@ -57,13 +59,19 @@ const char *ecf8_status_string(int status);
  *   ECF8_TABLE_MULTI  12-bit windows, up to 4 symbols per lookup; any LUTs
  * want_kind ECF8_TABLE_ANY picks DFA when possible; asking for DFA when it
  * is not possible returns ECF8_ERR_FORMAT.  *table_kind receives the kind
- * built; pass it to ecf8_decode.
+ * built; pass it to ecf8_decode.  The automaton's pending rows are numbered
+ * in a canonical order (prefix length, then bits), so both builders write
+ * the same bytes for the same LUTs.
  *
  * ecf8_build_table_host: luts and table in host memory
  *   (table: ECF8_TABLE_BYTES).
  * ecf8_build_table: luts (4-byte aligned) and table (ECF8_TABLE_BYTES,
- *   4-byte aligned) in device memory; copies the LUTs to the host and the
- *   table back on `stream`, and synchronizes `stream`.
+ *   4-byte aligned) in device memory, built by one workgroup on `stream`.
+ *   table_kind NULL: fully asynchronous (no host round trip, capturable in
+ *   a HIP graph); the kind is then only known on the device, so pass
+ *   ECF8_TABLE_ANY to ecf8_decode.  want_kind ECF8_TABLE_DFA requires a
+ *   non-NULL table_kind.  table_kind non-NULL: the kind word is copied back
+ *   and `stream` synchronized.
  */
 int ecf8_build_table_host(const uint8_t *luts, int n_luts, int want_kind, uint32_t *table,
                           int *table_kind);
@@ -82,7 +90,10 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, uint32_t *t
  *   gaps               device u8[n_fb*threads_per_block/2] (run.py:113)
  *   outputs            device u8[n_elements]   (run.py:114), 16-byte aligned
  *   table, table_kind  the derived table ecf8_build_table built for these
- *                      luts, and its kind
+ *                      luts, and its kind; ECF8_TABLE_ANY reads the kind
+ *                      from the table on the device (both decode kernels
+ *                      are launched and the one the table is not for exits
+ *                      at once), so no host round trip is needed
  *   max_block_elements largest output_positions[b+1] - output_positions[b]
  *                      (the reference derives shared_mem_size from it,
  *                      dfloat/run/run.py:453-458); sizes the kernel's LDS

@@ -83,7 +83,7 @@ def _decode_call(**kw):
     (dict(packed=0x3002), 3),
     (dict(gaps=0), 1),
     (dict(kind=2), 1),          # unknown table kind
-    (dict(kind=-1), 1),
+    (dict(kind=-2), 1),
 ])
 def test_decode_rejects_before_launch(kw, status):
     assert _decode_call(**kw) == status
@@ -103,6 +103,11 @@ def test_build_table_rejects_bad_lut_count():
                                   None) == 1
     assert lib().ecf8_build_table(ctypes.c_void_p(0x1001), 3, -1, ctypes.c_void_p(0x2000),
                                   ctypes.byref(kind), None) == 3
+    assert lib().ecf8_build_table(ctypes.c_void_p(0x1000), 3, 7, ctypes.c_void_p(0x2000),
+                                  ctypes.byref(kind), None) == 1
+    # an automaton-only table must be able to report a refusal to the host
+    assert lib().ecf8_build_table(ctypes.c_void_p(0x1000), 3, 1, ctypes.c_void_p(0x2000),
+                                  None, None) == 1
 
 
 @pytest.mark.parametrize("args,status", [

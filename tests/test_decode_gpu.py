@@ -370,12 +370,14 @@ def test_min_code_bits_above_the_truth_stays_in_bounds(cuda_device):
 # ------------------------------------------------------- drop-in call forms
 
 
-def test_reference_call_form_of_decode(cuda_device):
+@pytest.mark.parametrize("seed", [20, 21])
+def test_reference_call_form_of_decode(seed, cuda_device):
     """_decode(grid=, block=, shared_mem=, args=[...]) exactly as
-    scripts/compress.py:109-124 calls the CUDA kernel."""
+    scripts/compress.py:109-124 calls the CUDA kernel; seed 21 draws a
+    geometric histogram with a 1-bit code (the multi-symbol kernel)."""
     from dfloat.run.run import _decode
 
-    flat = _random_block(20)
+    flat = _random_block(seed)
     d = _dev_block(_compress(flat), cuda_device)
     n_bytes = d["encoded"].numel()
     op = d["output_positions"].view(torch.uint64).cpu().numpy().astype(np.int64)
@@ -387,6 +389,133 @@ def test_reference_call_form_of_decode(cuda_device):
                   d["luts"].shape[0], n_bytes, flat.size])
     torch.cuda.synchronize()
     assert np.array_equal(out.view(torch.uint8).cpu().numpy(), flat)
+
+
+def _lut_stacks():
+    """LUT stacks of every kind: the golden fixtures, random codes (with and
+    without 1-bit codes, long codes), and random bytes (malformed stacks)."""
+    stacks = [np.load(os.path.join(GOLDEN, f"{c}.npz"))["luts"] for c in CASES]
+    for seed in range(60):
+        flat = _random_block(1000 + seed)
+        stacks.append(oc.compress_block(flat, 8, 512)["luts"])
+    rng = np.random.default_rng(5)
+    for _ in range(40):
+        stacks.append(rng.integers(0, 256, (int(rng.integers(2, 19)), 256), dtype=np.uint8))
+    return stacks
+
+
+def test_device_table_builder_writes_the_host_builders_bytes(cuda_device):
+    """ecf8_build_table (one workgroup on the device) and
+    ecf8_build_table_host run the same steps: for every LUT stack and every
+    requested kind they write the same ECF8_TABLE_BYTES, kind word included,
+    and refuse the automaton for the same stacks."""
+    from ecf8_amd.decode import ECF8Error, build_table, build_table_host
+
+    stacks = _lut_stacks()
+    _say(f"device table builder: {len(stacks)} LUT stacks")
+    n_dfa = 0
+    for i, luts in enumerate(stacks):
+        d = torch.from_numpy(np.ascontiguousarray(luts)).to(cuda_device)
+        for kind in (ANY, MULTI, DFA):
+            try:
+                want, want_kind = build_table_host(luts, kind)
+            except ECF8Error:
+                assert kind == DFA
+                with pytest.raises(ECF8Error):
+                    build_table(d, kind=DFA)
+                continue
+            got = build_table(d, kind=kind)
+            assert got.kind == want_kind, (i, kind)
+            assert np.array_equal(got.data.cpu().numpy().view(np.uint32), want), (i, kind)
+            if kind == ANY:
+                n_dfa += want_kind == DFA
+                # asynchronous build: same bytes, kind known on the device only
+                lazy = build_table(d, kind=ANY, sync=False)
+                assert lazy.kind == ANY
+                torch.cuda.synchronize()
+                assert np.array_equal(lazy.data.cpu().numpy().view(np.uint32), want), i
+    assert n_dfa >= 20  # both kinds are exercised
+
+
+@pytest.mark.parametrize("seed", [0, 1, 4, 6])
+def test_decode_with_the_kind_read_on_the_device(seed, cuda_device):
+    """A table built asynchronously (kind ECF8_TABLE_ANY): the decode
+    launches both kernels and the one the table is not for exits; the output
+    is bit-exact for automaton and multi-symbol blocks alike."""
+    from ecf8_amd.decode import build_table, decode_into
+
+    flat = _random_block(seed)
+    d = _dev_block(_compress(flat), cuda_device)
+    table = build_table(d["luts"], sync=False)
+    out = torch.full((flat.size + 64,), 0x5A, dtype=torch.uint8, device=cuda_device)
+    decode_into(out, d["luts"], d["encoded"], d["packed_other_4bits"], d["output_positions"],
+                d["gaps"], table=table, n_elements=flat.size)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got[: flat.size], flat)
+    assert (got[flat.size:] == 0x5A).all()
+
+
+def _relabel(flat, perm):
+    """The same block with exponent e replaced by perm[e]: the same count
+    multiset, so the same bitstream size, under a different code table."""
+    e = (flat >> 3) & 0xF
+    return ((flat & 0x87) | (perm[e].astype(np.uint8) << 3)).astype(np.uint8)
+
+
+def test_reference_call_form_is_graph_capturable(cuda_device):
+    """_decode in the reference's call form is asynchronous: captured once
+    in a HIP graph, then replayed with new contents in the same buffers --
+    the same LUTs with a shuffled block, and other LUTs (exponents
+    relabelled) -- each replay bit-exact.  A 1-bit code (multi-symbol
+    kernel) is among the relabellings."""
+    from dfloat.run.run import _decode
+
+    rng = np.random.default_rng(11)
+    n = 200_000
+    syms = np.array([9, 10, 11, 12, 13, 14, 15, 8, 7, 6, 5, 0])
+    p = np.array([0.03, 0.06, 0.11, 0.21, 0.31, 0.23, 0.025, 0.01, 0.004, 0.001, 5e-4, 5e-5])
+    exps = rng.choice(syms, n, p=p / p.sum()).astype(np.uint8)
+    other = rng.integers(0, 16, n, dtype=np.uint8)
+    base = (((other & 8) << 4) | (exps << 3) | (other & 7)).astype(np.uint8)
+    variants = [base, rng.permutation(base)]
+    for s in range(40):  # relabellings whose LUT stack has the same number of rows
+        perm = np.random.default_rng(100 + s).permutation(16)
+        v = _relabel(base, perm)
+        if _compress(v)["luts"].shape == _compress(base)["luts"].shape:
+            variants.append(v)
+        if len(variants) == 5:
+            break
+    blocks = [_compress(v) for v in variants]
+    n_bytes = blocks[0]["encoded"].numel()
+    assert all(b["encoded"].numel() == n_bytes for b in blocks)
+    assert any(not torch.equal(b["luts"], blocks[0]["luts"]) for b in blocks)
+    d = _dev_block(blocks[0], cuda_device)
+    largest = max(int(np.diff(b["output_positions"].numpy().view(np.uint64).astype(np.int64)).max())
+                  for b in blocks)
+    out = torch.empty(n, dtype=torch.float8_e4m3fn, device=cuda_device)
+    call = dict(grid=(-(-n_bytes // 4096),), block=(512,), shared_mem=512 * 4 + 4 + largest,
+                args=[d["luts"].data_ptr(), d["encoded"].data_ptr(),
+                      d["packed_other_4bits"].data_ptr(), d["output_positions"].data_ptr(),
+                      d["gaps"].data_ptr(), out.data_ptr(), d["luts"].shape[0], n_bytes, n])
+    side = torch.cuda.Stream(cuda_device)
+    side.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(side):
+        _decode(**call)  # warm-up outside the capture
+    torch.cuda.current_stream(cuda_device).wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _decode(**call)
+    _say(f"graph-captured _decode: {len(blocks)} variants")
+    for rep in range(2):
+        for i, (flat, b) in enumerate(zip(variants, blocks)):
+            for k in KEYS:
+                d[k].copy_(b[k].contiguous().view(torch.uint8))
+            out.view(torch.uint8).fill_(0)
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(out.view(torch.uint8).cpu().numpy(), flat), (rep, i)
 
 
 def test_validate_cuda_decoding_fp8_api(cuda_device):

@@ -53,7 +53,7 @@ def _find(meta, *parts):
 
 
 def test_one_tensor_kernel_fits_eight_waves_per_simd(kernel_meta):
-    m = _find(kernel_meta, "decode_dfa_kernelILi512ELb0E")
+    m = _find(kernel_meta, "decode_dfa_kernelILi512ELb0ELb0E")
     assert m["vgpr_count"] <= 64, m
     assert m["sgpr_count"] <= 80, m
     assert m["vgpr_spill_count"] == 0 and m["sgpr_spill_count"] == 0, m
