@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <vector>
 
 #include "ecf8.h"
@@ -1201,12 +1202,15 @@ extern "C" int ecf8_decode_batched_select(const ecf8_block_desc *descs, int coun
   }
 }
 
-extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
-                           const uint8_t *packed_other_4bits, const uint64_t *output_positions,
-                           const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
-                           int64_t n_elements, int64_t max_block_elements, int min_code_bits,
-                           const uint32_t *table, int table_kind, int threads_per_block,
-                           int bytes_per_thread, void *stream) {
+namespace {
+
+// ecf8_decode's checks, then (launch) its kernels.  Every argument error is
+// returned before anything is launched.
+int decode_checked(const uint8_t *luts, const uint8_t *encoded, const uint8_t *packed_other_4bits,
+                   const uint64_t *output_positions, const uint8_t *gaps, uint8_t *outputs,
+                   int n_luts, int64_t n_bytes, int64_t n_elements, int64_t max_block_elements,
+                   int min_code_bits, const uint32_t *table, int table_kind,
+                   int threads_per_block, int bytes_per_thread, void *stream, bool launch) {
   if (n_bytes < 0 || n_elements < 0 || (n_elements & 1)) return ECF8_ERR_INVALID_ARG;
   // the reference's positions are 32-bit (decode.cu:23-25, 151); so is this
   // kernel's index arithmetic
@@ -1222,12 +1226,13 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
     return ECF8_ERR_UNSUPPORTED;
   const int64_t n_fb = (n_bytes + fb_bytes - 1) / fb_bytes;
   if (n_fb == 0) return ECF8_OK;
-  if (!luts || !encoded || !output_positions || !gaps || !table ||
+  if (!luts || !encoded || !output_positions || !gaps || (launch && !table) ||
       (n_elements > 0 && (!packed_other_4bits || !outputs)))
     return ECF8_ERR_INVALID_ARG;
   if (((uintptr_t)encoded & 15) || ((uintptr_t)packed_other_4bits & 7) ||
       ((uintptr_t)outputs & 15) || ((uintptr_t)table & 3) || ((uintptr_t)output_positions & 7))
     return ECF8_ERR_MISALIGNED;
+  if (!launch) return ECF8_OK;
   DecodeArgs a{luts,      n_luts, table,      encoded, n_bytes, packed_other_4bits,
                output_positions, gaps, outputs, n_elements, n_fb, 0,
                min_code_bits, (hipStream_t)stream};
@@ -1241,4 +1246,75 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
     default:
       return launch_decode<1024>(a, max_block_elements, table_kind, 3);
   }
+}
+
+}  // namespace
+
+extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
+                           const uint8_t *packed_other_4bits, const uint64_t *output_positions,
+                           const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
+                           int64_t n_elements, int64_t max_block_elements, int min_code_bits,
+                           const uint32_t *table, int table_kind, int threads_per_block,
+                           int bytes_per_thread, void *stream) {
+  return decode_checked(luts, encoded, packed_other_4bits, output_positions, gaps, outputs,
+                        n_luts, n_bytes, n_elements, max_block_elements, min_code_bits, table,
+                        table_kind, threads_per_block, bytes_per_thread, stream, true);
+}
+
+// ===========================================================================
+// Allocation-free decode
+// ===========================================================================
+//
+// The derived table of ecf8_decode_noalloc lives in `scratch`, one table per
+// device, held until the process ends.  Host code never passes the array's
+// name to a kernel: it is a host-side stand-in.  Its device address is taken
+// once per device with hipGetSymbolAddress and kept in g_scratch.
+
+static __device__ __align__(256) uint32_t scratch[ECF8_TABLE_BYTES / 4];
+
+namespace {
+
+uint32_t *g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The calling thread's current device's address of `scratch` (nullptr on a
+// HIP error), looked up on the first call on that device.
+uint32_t *scratch_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch[dev] = static_cast<uint32_t *>(ptr);
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" int ecf8_decode_noalloc(const uint8_t *luts, const uint8_t *encoded,
+                                   const uint8_t *packed_other_4bits,
+                                   const uint64_t *output_positions, const uint8_t *gaps,
+                                   uint8_t *outputs, int n_luts, int64_t n_bytes,
+                                   int64_t n_elements, int64_t max_block_elements,
+                                   int threads_per_block, int bytes_per_thread, void *stream) {
+  // Every argument error is returned before any HIP call.  One table of
+  // fixed size serves every input: no size can exceed `scratch` (the LUT
+  // stack is bounded by ECF8_MAX_LUTS, checked here too).
+  int rc = decode_checked(luts, encoded, packed_other_4bits, output_positions, gaps, outputs,
+                          n_luts, n_bytes, n_elements, max_block_elements, 0, nullptr,
+                          ECF8_TABLE_ANY, threads_per_block, bytes_per_thread, stream, false);
+  if (rc != ECF8_OK) return rc;
+  if (n_bytes == 0) return ECF8_OK;
+  if ((uintptr_t)luts & 3) return ECF8_ERR_MISALIGNED;
+  uint32_t *table = scratch_on_current_device();
+  if (!table) return ECF8_ERR_HIP;
+  // the table builder writes every word of the table, so the previous
+  // call's contents need no clearing
+  rc = ecf8_build_table(luts, n_luts, ECF8_TABLE_ANY, table, nullptr, stream);
+  if (rc != ECF8_OK) return rc;
+  return decode_checked(luts, encoded, packed_other_4bits, output_positions, gaps, outputs,
+                        n_luts, n_bytes, n_elements, max_block_elements, 0, table,
+                        ECF8_TABLE_ANY, threads_per_block, bytes_per_thread, stream, true);
 }

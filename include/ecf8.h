@@ -120,6 +120,25 @@ int ecf8_decode(const uint8_t *luts, const uint8_t *encoded, const uint8_t *pack
                 int threads_per_block, int bytes_per_thread, void *stream);
 
 /*
+ * ecf8_decode with the reference kernel's arguments only, allocating
+ * nothing and taking no workspace.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * derived table is built on `stream` into the library's static device
+ * array (ECF8_TABLE_BYTES per GPU, held until the process ends), and the
+ * decode reads its kind there.  Arguments, alignment and errors are those of
+ * ecf8_decode (min_code_bits is taken as unknown); every argument error is
+ * returned before any HIP call.  No input size can exceed the array: it
+ * always holds one table.  Calls that overlap on one GPU (several streams
+ * or host threads) race on that table; serialize them.
+ */
+int ecf8_decode_noalloc(const uint8_t *luts, const uint8_t *encoded,
+                        const uint8_t *packed_other_4bits, const uint64_t *output_positions,
+                        const uint8_t *gaps, uint8_t *outputs, int n_luts, int64_t n_bytes,
+                        int64_t n_elements, int64_t max_block_elements, int threads_per_block,
+                        int bytes_per_thread, void *stream);
+
+/*
  * One compressed block of a batched decode.  The array of descriptors lives
  * in device memory; every field keeps its ecf8_decode meaning and
  * requirements (bytes_per_thread 8; `table` must be an ECF8_TABLE_DFA table
