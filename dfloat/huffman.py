@@ -103,7 +103,9 @@ def get_nbit_codec(counter: dict, max_n_bits: int = 16):
     """Length-limited codebook (dfloat/utils.py:239-267): while the longest
     code exceeds ``max_n_bits`` the ``k`` rarest symbols (numpy argpartition
     over the counts, k = 2, 3, ...) are given count 1 and the table rebuilt.
-    Returns (codec, counter used, code table)."""
+    For 4-bit exponents the loop never runs: 16 symbols plus EOF are 17
+    leaves, whose deepest possible code is 16 bits.  Returns (codec, counter
+    used, code table)."""
     codec = HuffmanCodec.from_frequencies(counter)
     table = codec.get_code_table()
     longest = max(bits for bits, _ in table.values())

@@ -195,7 +195,7 @@ class BatchPlan:
     they point to must stay alive and in place while the plan is used."""
 
     def __init__(self, descs, count, n_tasks, blocks_per_task, cap, threads_per_block,
-                 singles, keep):
+                 singles, keep, desc_blocks=()):
         self.descs = descs            # u8 device tensor of ecf8_block_desc
         self.count = count
         self.n_tasks = n_tasks
@@ -203,6 +203,8 @@ class BatchPlan:
         self.cap = cap
         self.threads_per_block = threads_per_block
         self.singles = singles        # decode_into argument tuples of unbatched blocks
+        self.desc_blocks = list(desc_blocks)  # index (in the blocks given) of each descriptor
+        self.n_blocks = count + len(singles)
         self._keep = keep             # the referenced tensors
 
 
@@ -222,8 +224,8 @@ def prepare_batch(blocks, outs, tables, threads_per_block: int = 512, bytes_per_
     if not (len(blocks) == len(outs) == len(tables)):
         raise ECF8Error("blocks, outs and tables differ in length")
     keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
-    dev, rows, singles, largest = None, [], [], 0
-    for b, out, t in zip(blocks, outs, tables):
+    dev, rows, singles, largest, desc_blocks = None, [], [], 0, []
+    for i, (b, out, t) in enumerate(zip(blocks, outs, tables)):
         enc = b["encoded"]
         n = b["packed_other_4bits"].numel() * 2
         dev = enc.device if dev is None else dev
@@ -233,6 +235,7 @@ def prepare_batch(blocks, outs, tables, threads_per_block: int = 512, bytes_per_
             singles.append(((out, *(b[k] for k in keys)), t))
             continue
         _check_block(out, b, t, n, threads_per_block, bytes_per_thread, dev)
+        desc_blocks.append(i)
         rows.append((b["luts"].data_ptr(), enc.data_ptr(), b["packed_other_4bits"].data_ptr(),
                      b["output_positions"].data_ptr(), b["gaps"].data_ptr(), out.data_ptr(),
                      t.data.data_ptr(), enc.numel(), n, _n_luts(b["luts"]), 0))
@@ -253,7 +256,8 @@ def prepare_batch(blocks, outs, tables, threads_per_block: int = 512, bytes_per_
     d_descs = torch.from_numpy(descs.view(np.uint8).copy()).to(dev) if rows else None
     cap = int(max_block_elements) if max_block_elements is not None else largest
     return BatchPlan(d_descs, len(rows), int(n_task.sum()), blocks_per_task, cap,
-                     threads_per_block, singles, (list(blocks), list(outs), list(tables)))
+                     threads_per_block, singles, (list(blocks), list(outs), list(tables)),
+                     desc_blocks)
 
 
 def _resident_workgroups(dev) -> int:
@@ -281,31 +285,47 @@ def decode_batched(plan, outs=None, tables=None, stream=None, **kwargs):
 
 class BatchSelect:
     """Decode a device-chosen subset of a BatchPlan's blocks per call
-    (ecf8_decode_batched_select): e.g. the attention block plus the experts
-    the router picked, from a flags tensor the model writes on the device.
-    Allocates its work descriptors once; a call reads nothing back to the
-    host, so it can be captured in a HIP graph and replayed with new flags.
-    Every block of the plan must be batchable (no ``singles``)."""
+    (ecf8_decode_batched_select): e.g. the experts the router picked, from a
+    flags tensor (int32, one per block in the order given to prepare_batch)
+    that the model writes on the device.  Allocates its work descriptors
+    once; a call reads nothing back to the host, so it can be captured in a
+    HIP graph and replayed with new flags.
+
+    Blocks outside the batched kernel (a multi-symbol table, or under 16
+    elements) cannot be chosen on the device without a host read: they are
+    decoded on every call, selected or not, so a selected one is always
+    current (an unselected one's output is rewritten with the same bytes)."""
 
     def __init__(self, plan: BatchPlan):
-        if plan.singles:
-            raise ECF8Error("selection needs every block in the batched launch "
-                            "(automaton tables, >= 16 elements)")
-        if not plan.count:
+        if not plan.n_blocks:
             raise ECF8Error("empty plan")
         self.plan = plan
-        dev = plan.descs.device
-        self.work = torch.empty_like(plan.descs)
+        dev = (plan.descs.device if plan.count else plan.singles[0][0][1].device)
+        self.work = torch.empty_like(plan.descs) if plan.count else None
         self.counts = torch.zeros(2, dtype=torch.int32, device=dev)
+        # flags per block -> flags per descriptor, when some blocks are not in
+        # the batched launch
+        self.index = (torch.tensor(plan.desc_blocks, dtype=torch.int64, device=dev)
+                      if plan.singles and plan.count else None)
 
     def __call__(self, select: torch.Tensor, stream=None):
         p = self.plan
-        dev = p.descs.device
+        dev = self.counts.device
         if (not select.is_cuda or select.device != dev or select.dtype != torch.int32
-                or not select.is_contiguous() or select.numel() < p.count):
-            raise ECF8Error(f"select must be a contiguous int32 tensor of >= {p.count} flags on {dev}")
+                or not select.is_contiguous() or select.numel() < p.n_blocks):
+            raise ECF8Error(f"select must be a contiguous int32 tensor of >= {p.n_blocks} "
+                            f"flags on {dev}")
+        for args, t in p.singles:
+            decode_into(*args, table=t, threads_per_block=p.threads_per_block, stream=stream)
+        if not p.count:
+            return
+        flags = select
+        if self.index is not None:
+            s = torch.cuda.current_stream(dev) if stream is None else stream
+            with torch.cuda.stream(s):
+                flags = select.index_select(0, self.index)
         with torch.cuda.device(dev):
-            check(lib().ecf8_decode_batched_select(p.descs.data_ptr(), p.count, select.data_ptr(),
+            check(lib().ecf8_decode_batched_select(p.descs.data_ptr(), p.count, flags.data_ptr(),
                                                    self.work.data_ptr(), self.counts.data_ptr(),
                                                    p.blocks_per_task, p.cap, p.threads_per_block,
                                                    _stream_handle(dev, stream)),

@@ -34,8 +34,10 @@ def _synthetic(rows, cols, sigma, seed):
 
 
 def _fibonacci_block(seed):
-    # exponent counts 1,1,2,3,5,... force a caterpillar tree whose longest
-    # code exceeds 16 bits, so the length limiter (utils.py:251-265) runs
+    # exponent counts 1,1,2,3,5,... give a caterpillar tree: with EOF that is
+    # 17 leaves, so the longest code is exactly 16 bits, the format's limit
+    # (the length limiter of utils.py:251-265 does not fire for 16
+    # exponents plus EOF; its test uses a larger alphabet)
     rng = np.random.default_rng(seed)
     counts = [1, 1]
     while len(counts) < 16:

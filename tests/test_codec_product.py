@@ -168,3 +168,26 @@ def test_encoder_rejects_symbol_without_code():
     codec = HuffmanCodec.from_frequencies({3: 10, 4: 5})
     with pytest.raises(ECF8Error):
         encode_exponents_for_cuda(np.array([3, 4, 5], np.uint8), codec)
+
+
+def test_product_length_limiter_equals_the_oracle_on_a_large_alphabet():
+    """The product's limiter (dfloat/huffman.py, utils.py:249-265) never
+    fires for 4-bit exponents: 16 symbols plus EOF are 17 leaves, so no code
+    exceeds 16 bits.  It is generic over the alphabet, so it is checked on
+    20 Fibonacci-weighted symbols (an unlimited tree 19 deep): same code
+    table and same clamped counter as the oracle, longest code <= 16."""
+    from dfloat.huffman import HuffmanCodec
+    from dfloat.utils import get_nbit_codec
+
+    counts = [1, 1]
+    while len(counts) < 20:
+        counts.append(counts[-1] + counts[-2])
+    counter = {s: c for s, c in enumerate(counts)}
+    unlimited = HuffmanCodec.from_frequencies(counter).get_code_table()
+    assert max(b for b, _ in unlimited.values()) > 16
+    codec, used, table = get_nbit_codec(counter, 16)
+    _, ref_used, ref_table = oc.get_nbit_codec(counter, 16)
+    assert max(b for b, _ in table.values()) <= 16
+    assert {str(k): v for k, v in table.items()} == {str(k): v for k, v in ref_table.items()}
+    assert dict(used) == dict(ref_used)
+    assert codec.get_code_table() is table

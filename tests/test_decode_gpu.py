@@ -699,3 +699,61 @@ def test_batched_select_replays_in_a_graph_with_new_flags(cuda_device):
         g.replay()
         torch.cuda.synchronize()
         _check_selected(flats, bufs, f)
+
+
+def test_batched_select_with_blocks_outside_the_batched_kernel(cuda_device):
+    """Flags are per block in the order given to prepare_batch, also when
+    some blocks (a multi-symbol table, a tiny block) are not in the batched
+    launch: the batched blocks follow their flags, the others are decoded on
+    every call.  Eager and graph-replayed."""
+    from ecf8_amd.decode import BatchSelect, build_table, prepare_batch
+
+    _say("batched select with singles")
+    flats = [_random_block(s) for s in (30, 31, 32, 33, 34, 35, 36, 37, 39, 44, 49)]
+    flats.insert(3, np.array([0x41, 0xC2, 0x33, 0x0A], np.uint8))  # too small to batch
+    blocks = [_dev_block(_compress(f), cuda_device) for f in flats]
+    tables = [build_table(b["luts"]) for b in blocks]
+    bufs = [torch.full((f.size + 32,), 0x3C, dtype=torch.uint8, device=cuda_device) for f in flats]
+    plan = prepare_batch(blocks, [b[: f.size] for b, f in zip(bufs, flats)], tables,
+                         blocks_per_task=2)
+    single = [i for i in range(len(flats)) if i not in plan.desc_blocks]
+    assert plan.singles and plan.count and 3 in single
+    assert any(tables[i].kind == MULTI for i in single)
+    sel = BatchSelect(plan)
+    flags_dev = torch.zeros(len(flats), dtype=torch.int32, device=cuda_device)
+
+    def check(f):
+        for i, (buf, flat) in enumerate(zip(bufs, flats)):
+            got = buf.cpu().numpy()
+            if f[i] or i in single:
+                assert np.array_equal(got[: flat.size], flat), f"block {i}"
+            else:
+                assert (got[: flat.size] == 0x3C).all(), f"unselected block {i} was written"
+            assert (got[flat.size:] == 0x3C).all(), f"block {i} wrote past its end"
+
+    rng = np.random.default_rng(8)
+    draws = [(rng.random(len(flats)) < 0.5).astype(np.int32) for _ in range(3)]
+    for f in draws:
+        for b in bufs:
+            b.fill_(0x3C)
+        flags_dev.copy_(torch.from_numpy(f).to(cuda_device))
+        sel(flags_dev)
+        torch.cuda.synchronize()
+        check(f)
+    s = torch.cuda.Stream(cuda_device)
+    s.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(s):
+        sel(flags_dev)
+    torch.cuda.current_stream(cuda_device).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sel(flags_dev)
+    for f in draws[::-1]:
+        for b in bufs:
+            b.fill_(0x3C)
+        flags_dev.copy_(torch.from_numpy(f).to(cuda_device))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        check(f)

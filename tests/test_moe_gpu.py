@@ -17,6 +17,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 FP8 = torch.float8_e4m3fn
+MULTI = 0  # ECF8_TABLE_MULTI
 
 
 def _rand_fp8(shape, gen, dev):
@@ -280,3 +281,43 @@ def test_moe_block_matches_a_torch_restatement(small_moe_models, cuda_device):
     # routing agrees with the fp64 choice
     assert torch.equal(torch.sort(r.route.topk_idx[:B].cpu().long(), -1).values,
                        torch.sort(idx, -1).values)
+
+
+def test_moe_with_a_multi_symbol_expert_matches_uncompressed(cuda_device):
+    """An expert whose exponents are dominated by one value gets a 1-bit
+    code, so its block needs the multi-symbol table and stays outside the
+    batched launch: the routed decode still covers it, and the compressed
+    model gives the FP8 model's tokens and logits, eager and graph-replayed."""
+    from dfloat.run.run import TensorManager
+    from ecf8_amd.decode import build_table
+    from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, random_moe_model
+
+    cfg = Qwen3MoeConfig(**dict(SMALL_MOE, layers=1))
+    plain, drawn = random_moe_model(cfg, cuda_device, seed=6)
+    comp, _ = random_moe_model(cfg, cuda_device, seed=6)
+    rng = np.random.default_rng(0)
+    for name, (w, s) in drawn[0]["experts"][3].items():
+        b = w.view(torch.uint8).numpy()
+        skew = rng.random(b.shape) < 0.8
+        b[skew] = (b[skew] & 0x87) | (11 << 3)  # exponent 11, sign and mantissa kept
+        plain.model.layers[0].mlp.experts[3].get_submodule(name).weight.data.copy_(
+            w.to(cuda_device))
+    compress_moe_layers(comp, drawn)
+    ex = comp.model.layers[0].mlp.experts[3]
+    assert build_table(ex.luts).kind == MULTI
+    B, T, new = 4, 24, 5
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(4))
+    results = {}
+    for name, model in (("fp8", plain), ("ecf8", comp)):
+        for graph in (False, True):
+            print(f"[moe multi] {name} graph={graph}", flush=True)
+            TensorManager.clear_device()
+            r = Qwen3MoeRunner(model, B, T, T + new, cuda_device)
+            if graph:
+                r.capture()
+            toks = r.generate(prompt, new).cpu()
+            results[(name, graph)] = (toks, r.logits.float().cpu())
+    base_t, base_l = results[("fp8", False)]
+    for key, (t, l) in results.items():
+        assert torch.equal(t, base_t), key
+        assert torch.equal(l, base_l), key
