@@ -14,9 +14,14 @@ attention block plus 128 expert blocks each compressed on its own, decoded
 by ONE batched launch (ecf8_decode_batched) per step.
 
 Prints ONE JSON line: decode GB/s of algorithmic bytes
-(compressed bytes read + FP8 bytes written), the roofline of the decode
-kernel against the 8 TB/s HBM peak, and the CPU decode baseline (the C
-restatement of the decode rule in oracle/) timed on this host.
+(compressed bytes read + FP8 bytes written) over the K timed steps, the
+roofline of the decode kernel against the 8 TB/s HBM peak from the
+per-launch duration (launches timed one by one), the CPU decode baseline
+(the C restatement of the decode rule in oracle/) timed on this host, and
+-- for the default workload -- the end-to-end half of the metric in an
+``e2e`` object: tokens/s and peak HBM of the Qwen3-8B-shaped model at batch
+16 (128 + 1024 tokens) and of the Qwen3-30B-A3B-shaped MoE (128 + 512),
+FP8 resident vs ECF8, each run in a child process after the timed region.
 """
 
 from __future__ import annotations
@@ -366,9 +371,7 @@ def e2e_generate(args):
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,
     }
-    print(json.dumps(line), flush=True)
-    if not same:
-        sys.exit(1)
+    return line
 
 
 def moe_generate(args):
@@ -464,9 +467,7 @@ def moe_generate(args):
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,
     }
-    print(json.dumps(line), flush=True)
-    if not same:
-        sys.exit(1)
+    return line
 
 
 def dit_generate(args):
@@ -553,12 +554,42 @@ def dit_generate(args):
         sys.exit(1)
 
 
+def e2e_child(workload: str, seed: int, timeout_s: float):
+    """Run an end-to-end workload of this script in a child process (its own
+    HIP context, so its kernels stay out of this process's profile and its
+    memory is returned when it ends) and return the summary of its JSON
+    line, or the reason it has none."""
+    import subprocess
+
+    cmd = [sys.executable, os.path.abspath(__file__), "--workload", workload, "--seed", str(seed)]
+    t0 = time.perf_counter()
+    print(f"[bench] e2e child: {' '.join(cmd[1:])}", file=sys.stderr, flush=True)
+    try:
+        res = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        return {"error": f"timed out after {timeout_s:.0f} s"}
+    sys.stderr.write(res.stderr)
+    lines = [ln for ln in res.stdout.splitlines() if ln.startswith("{")]
+    if not lines:
+        return {"error": f"exit status {res.returncode}, no result line"}
+    full = json.loads(lines[-1])
+    keep = ("uncompressed_fp8", "ecf8", "ecf8_mode", "ratio_vs_uncompressed", "identical_tokens",
+            "experts_routed_last_step")
+    out = {"workload": full["config"]["workload"], "unit": full["unit"],
+           "batch": full["config"]["batch"], "prompt_len": full["config"]["prompt_len"],
+           "new_tokens": full["config"]["new_tokens"],
+           "ecf8_decode": full["config"]["ecf8_decode"]}
+    out.update({k: full[k] for k in keep if k in full})
+    out["wall_s"] = round(time.perf_counter() - t0, 1)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--copies", type=int, default=4, help="rotated input/output sets")
+    ap.add_argument("--copies", type=int, default=10, help="rotated input/output sets")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "qwen3-8b-generate",
@@ -582,6 +613,13 @@ def main():
                          "CUs free)")
     ap.add_argument("--distinct-layers", type=int, default=2,
                     help="generate: layers drawn independently (the rest copy them)")
+    ap.add_argument("--e2e", choices=("all", "dense", "none"), default="all",
+                    help="qwen3-8b-layer: also run the end-to-end generate workloads (dense "
+                         "Qwen3-8B bs16, and the MoE) in child processes and report them in "
+                         "the line's e2e object")
+    ap.add_argument("--single-launches", type=int, default=10,
+                    help="launches timed one by one (an event pair each) for the per-launch "
+                         "kernel duration")
     ap.add_argument("--mode", choices=("decode", "copy"), default="decode",
                     help="copy: time a plain 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -591,12 +629,15 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         return copy_calibration(args.steps, args.warmup)
-    if args.workload == "qwen3-8b-generate":
-        if args.new_tokens is None:
-            args.new_tokens = 1024
-        return e2e_generate(args)
-    if args.workload == "qwen3-moe-generate":
-        return moe_generate(args)
+    if args.workload in ("qwen3-8b-generate", "qwen3-moe-generate"):
+        if args.workload == "qwen3-8b-generate":
+            if args.new_tokens is None:
+                args.new_tokens = 1024
+            line = e2e_generate(args)
+        else:
+            line = moe_generate(args)
+        print(json.dumps(line), flush=True)
+        sys.exit(0 if line["identical_tokens"] else 1)
     if args.workload == "flux-dit-generate":
         return dit_generate(args)
 
@@ -638,14 +679,32 @@ def main():
     wall = time.perf_counter() - t_wall
     total_ms = start.elapsed_time(end)
     ms_per_step = total_ms / args.steps
-    avg_launch_ms = ms_per_step
     gbps = alg / (ms_per_step * 1e-3) / 1e9
+    # Per-launch duration: launches one at a time, each between its own event
+    # pair on the launch stream (back to back, consecutive launches overlap
+    # their tail and head, so K launches take less than K durations).
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(args.single_launches)]
+    for i, (a, b) in enumerate(pairs):
+        a.record(stream)
+        step(args.steps + i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    launch_ms = [a.elapsed_time(b) for a, b in pairs]
+    avg_launch_ms = sum(launch_ms) / len(launch_ms) if launch_ms else ms_per_step
     kernel_gbps = alg / (avg_launch_ms * 1e-3) / 1e9
 
     cpu = enc = None
     if not args.no_cpu_baseline and cpu_case is not None:
         cpu = cpu_baseline(cpu_case[0], cpu_case[1], alg)
         enc = cpu_encode(cpu_case[2])
+    e2e = None
+    if args.workload == "qwen3-8b-layer" and args.e2e != "none":
+        del calls, cpu_case
+        torch.cuda.empty_cache()
+        e2e = {"qwen3_8b_bs16": e2e_child("qwen3-8b-generate", args.seed, 420)}
+        if args.e2e == "all":
+            e2e["qwen3_30b_a3b_bs16"] = e2e_child("qwen3-moe-generate", args.seed, 480)
     line = {
         "metric": "ECF8 decode GB/s + % HBM roofline; e2e tokens/s, Qwen3-8B-shape bs16",
         "value": round(gbps, 1),
@@ -654,6 +713,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "kernel_ms_per_launch": round(avg_launch_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -670,6 +730,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "cpu_encode": enc,
+        "e2e": e2e,
         "wall_s_timed": round(wall, 4),
         "bit_exact": ok,
     }
