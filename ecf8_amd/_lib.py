@@ -51,6 +51,12 @@ _SIGNATURES = {
         [_vp, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, ctypes.c_char_p, ctypes.c_size_t],
         _i32,
     ),
+    # include/ecf8_tile.h: the tiled execution layout
+    "ecf8_code_from_luts": ([_vp, _i32, _vp, _vp], _i32),
+    "ecf8_tile_sizes": ([_vp, _i64, _i64, _vp, _vp, _vp], _i32),
+    "ecf8_tile_encode": ([_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32], _i32),
+    "ecf8_tile_linear": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _i32, _vp], _i32),
+    "ecf8_tile_decode": ([_vp, _i64, _vp, _vp, _vp], _i32),
     # include/ecf8_llm.h: the consumer kernels
     "ecf8_fp8_linear": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp], _i32),
     "ecf8_rmsnorm": ([_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp, _vp], _i32),

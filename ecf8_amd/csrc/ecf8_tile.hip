@@ -1,0 +1,402 @@
+// Kernels over the tiled execution layout ECF8-T (ecf8_tile_layout.h).
+//
+// tile_linear16_kernel: the small-M (M <= 16, a decode step) block-scaled
+//   FP8 linear with its weight operands decoded on the fly: each wave
+//   decodes one 2048-symbol segment -- the B operands of its four MFMAs of
+//   one 128-column group -- into a wave-private LDS staging area, reads its
+//   lane's 32 exponents back, merges them with the sign/mantissa nibbles and
+//   runs v_mfma_f32_16x16x32_fp8_fp8.  No FP8 weight reaches HBM.  The K
+//   groups go to the waves, the products are scaled and summed, and the
+//   waves' partial sums are reduced, in exactly the order of the FP8
+//   linear (fp8_linear16_kernel / fp8_linear16p_kernel in ecf8_llm.hip) with
+//   the same wave count, so both give bit-identical outputs.
+// tile_decode_kernel: the same per-wave decode, written out as row-major
+//   FP8 bytes (the prompt's large-M linears read those).
+//
+// A wave's decode needs no workgroup barrier: its 64 lanes decode the
+// segment's 12-byte chunks with the byte automaton (12 lookups, plus the
+// code open at the chunk end), a wave64 prefix sum places each lane's
+// symbols, and the lanes OR them into the wave's staging area.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ecf8.h"
+#include "ecf8_dev.h"
+#include "ecf8_layout.h"
+#include "ecf8_llm.h"
+#include "ecf8_tile.h"
+#include "ecf8_tile_layout.h"
+
+namespace {
+
+using namespace ecf8;
+using namespace ecf8::dev;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kGroup = 128;
+constexpr int kStageDw = kTileSegSymbols / 8;           // 256 dwords of nibbles
+constexpr int kWaveStageDw = kStageDw + 8;              // + spill for symbols past 2048
+static_assert(4 * 64 <= kWaveStageDw, "a wave's staging area holds its 4x64 partial sums");
+
+// One weight operand of a (possibly fused) tiled linear.
+struct TileOperand {
+  const uint8_t *stream;
+  const uint32_t *seg_off;
+  const uint32_t *gaps;
+  const uint8_t *other;
+  const float *ws;  // weight_scale_inv [n/128, K/128]
+};
+
+struct TileSegs {
+  TileOperand op[ECF8_LINEAR_MAX_SEGS];
+  int n_end[ECF8_LINEAR_MAX_SEGS];  // cumulative output columns
+  int col[ECF8_LINEAR_MAX_SEGS];    // first output column
+  int count;
+};
+
+__device__ __forceinline__ float bf16_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// fp32 -> bf16, round to nearest even (as the FP8 linear does)
+__device__ __forceinline__ uint32_t f32_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// The loads one segment needs, issued before its decode.
+struct SegLoad {
+  uint32_t d0, d1, d2, d3;  // 16 bytes from the lane's chunk start (12 + look-ahead)
+  uint32_t gapw;            // the gap word holding the lane's nibble
+  uint4 oth;                // the lane's 32 sign/mantissa nibbles
+  int n_chunks;             // wave-uniform
+};
+
+__device__ __forceinline__ SegLoad seg_load(const TileOperand &t, uint32_t s, int lane) {
+  SegLoad r;
+  const uint32_t off = t.seg_off[s], end = t.seg_off[s + 1];  // uniform: scalar loads
+  r.n_chunks = (int)((end - off + kTileChunkBytes - 1) / kTileChunkBytes);
+  // lanes past the segment's chunks re-read its first one (in bounds; unused)
+  const uint32_t b = off + (lane < r.n_chunks ? (uint32_t)(kTileChunkBytes * lane) : 0u);
+  const u32x4_a4 v = *reinterpret_cast<const u32x4_a4 *>(t.stream + b);
+  r.d0 = v.x;
+  r.d1 = v.y;
+  r.d2 = v.z;
+  r.d3 = v.w;
+  r.gapw = t.gaps[(size_t)s * kTileGapWords + (lane >> 3)];
+  const u32x4 o = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4 *>(t.other + (size_t)s * kTileOtherBytes + 16 * lane));
+  r.oth = make_uint4(o.x, o.y, o.z, o.w);
+  return r;
+}
+
+// Byte i (0..15) of the lane's chunk window, shifted into a table offset
+// (byte << 2), from its little-endian dwords.
+template <int i>
+__device__ __forceinline__ uint32_t byte_off(const SegLoad &c) {
+  const uint32_t d = i < 4 ? c.d0 : i < 8 ? c.d1 : i < 12 ? c.d2 : c.d3;
+  constexpr int sh = 8 * (i & 3);
+  return sh >= 2 ? (d >> (sh - 2)) & 0x3FCu : (d << 2) & 0x3FCu;
+}
+
+// Decode one segment into the wave's staging area and return the lane's 32
+// exponents (symbol 32 lane + k in bits 4(k%8).. of component k/8).  The
+// staging area is all zero on entry and on return (each lane clears the
+// four dwords it read; symbols past 2048 go to the spill dwords, which are
+// never read).
+__device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t *s_dfa,
+                                                uint32_t *stage, int lane) {
+  const uint32_t gap = (c.gapw >> (4 * (lane & 7))) & 0xFu;
+  const uint32_t a0 = gap < 8 ? ((gap << 10) | byte_off<0>(c))
+                              : (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
+  const uint32_t e0 = dfa_at(s_dfa, a0);
+  const uint32_t e1 = dfa_at(s_dfa, (e0 & kDfaRowMask) | byte_off<1>(c));
+  const uint32_t e2 = dfa_at(s_dfa, (e1 & kDfaRowMask) | byte_off<2>(c));
+  const uint32_t e3 = dfa_at(s_dfa, (e2 & kDfaRowMask) | byte_off<3>(c));
+  const uint32_t e4 = dfa_at(s_dfa, (e3 & kDfaRowMask) | byte_off<4>(c));
+  const uint32_t e5 = dfa_at(s_dfa, (e4 & kDfaRowMask) | byte_off<5>(c));
+  const uint32_t e6 = dfa_at(s_dfa, (e5 & kDfaRowMask) | byte_off<6>(c));
+  const uint32_t e7 = dfa_at(s_dfa, (e6 & kDfaRowMask) | byte_off<7>(c));
+  const uint32_t e8 = dfa_at(s_dfa, (e7 & kDfaRowMask) | byte_off<8>(c));
+  const uint32_t e9 = dfa_at(s_dfa, (e8 & kDfaRowMask) | byte_off<9>(c));
+  const uint32_t e10 = dfa_at(s_dfa, (e9 & kDfaRowMask) | byte_off<10>(c));
+  const uint32_t e11 = dfa_at(s_dfa, (e10 & kDfaRowMask) | byte_off<11>(c));
+  // a code still open at the chunk's end started in it: the chunk owns it,
+  // and its symbol is the first one completed in look-ahead byte 12 or 13
+  const uint32_t row11 = e11 & kDfaRowMask;
+  const bool open = row11 >= ((uint32_t)kDfaFirstPendingRow << 10);
+  uint32_t e12 = dfa_at(s_dfa, row11 | byte_off<12>(c));
+  if (__builtin_amdgcn_ballot_w64(open && (e12 & 0xFFu) == 0)) {
+    const uint32_t e13 = dfa_at(s_dfa, (e12 & kDfaRowMask) | byte_off<13>(c));
+    if ((e12 & 0xFFu) == 0) e12 = e13;
+  }
+  const uint32_t et = open ? ((e12 & 0xF0000u) | 4u) : 0u;
+  const bool live = lane < c.n_chunks;
+  int cnt4 = (int)((e0 & 0xFFu) + (e1 & 0xFFu) + (e2 & 0xFFu) + (e3 & 0xFFu) + (e4 & 0xFFu) +
+                   (e5 & 0xFFu) + (e6 & 0xFFu) + (e7 & 0xFFu) + (e8 & 0xFFu) + (e9 & 0xFFu) +
+                   (e10 & 0xFFu) + (e11 & 0xFFu) + (et & 0xFFu));
+  if (!live) cnt4 = 0;
+  const int incl = wave_inclusive_scan(cnt4);
+  // a start past the real symbols (garbage decoded from the bytes after the
+  // segment) is clamped to the spill dwords' start; 12 entries of <= 16 bits
+  // plus 4 stay within them
+  uint32_t pos4 = min((uint32_t)(incl - cnt4), (uint32_t)kStageDw << 5);
+  auto put = [&](uint32_t syms, uint32_t n4) {
+    const uint64_t v = (uint64_t)syms << (pos4 & 31u);
+    uint32_t *const q = stage + (pos4 >> 5);
+    atomicOr(q, (uint32_t)v);
+    atomicOr(q + 1, (uint32_t)(v >> 32));
+    pos4 += n4;
+  };
+  auto put2 = [&](uint32_t ea, uint32_t eb) {
+    uint32_t t, syms;
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+        "src1_sel:WORD_1"
+        : "=v"(t) : "v"(ea), "v"(eb));
+    asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+        "src1_sel:WORD_1"
+        : "=v"(syms) : "v"(t), "v"(ea));
+    put(syms, (ea & 0xFFu) + (eb & 0xFFu));
+  };
+  if (live) {
+    put2(e0, e1);
+    put2(e2, e3);
+    put2(e4, e5);
+    put2(e6, e7);
+    put2(e8, e9);
+    put2(e10, e11);
+    put(et >> 16, 0u);
+  }
+  // the wave's own ORs complete before its lanes read the staged symbols
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  uint4 *const mine = reinterpret_cast<uint4 *>(stage) + lane;
+  const uint4 ex = *mine;
+  *mine = make_uint4(0u, 0u, 0u, 0u);
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  return ex;
+}
+
+// Operand address of the panel `panel` (16 output columns) of the fused
+// segments: its operand, the panel index inside it, its output column.
+__device__ __forceinline__ void panel_of(const TileSegs &segs, int panel, TileOperand &op,
+                                         int &p, int &col) {
+  int n0 = panel * 16, start = 0, k = 0;
+#pragma unroll
+  for (int s = 1; s < ECF8_LINEAR_MAX_SEGS; ++s)
+    if (s < segs.count && n0 >= segs.n_end[s - 1]) {
+      k = s;
+      start = segs.n_end[s - 1];
+    }
+  op = segs.op[k];
+  col = segs.col[k];
+  p = (n0 - start) / 16;
+}
+
+// out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
+// for M <= 16, persistent over the 16-column panels.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
+    const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, TileSegs segs,
+    const uint32_t *__restrict__ table, uint16_t *__restrict__ out, int ldo, int n_panels) {
+  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kgroups = K / kGroup;
+  if ((int)blockIdx.x >= n_panels) return;  // uniform, before any barrier
+
+  load_dfa_batched<WAVES * 64>(s_dfa, table, threadIdx.x);
+  uint32_t *const stage = s_stage[wave];
+  for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
+
+  const int r = lane & 15, g = lane >> 4;
+  const bool row_ok = r < M;
+  const uint8_t *arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+  bool srow_ok[4];
+  const float *srow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    srow_ok[i] = 4 * g + i < M;
+    srow[i] = as + (size_t)(srow_ok[i] ? 4 * g + i : 0) * kgroups;
+  }
+  __syncthreads();
+
+  for (int panel = blockIdx.x; panel < n_panels; panel += gridDim.x) {
+    TileOperand op;
+    int p, col;
+    panel_of(segs, panel, op, p, col);
+    const float *wsrow = op.ws + (size_t)(p * 16 / kGroup) * kgroups;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int kg = wave; kg < kgroups; kg += WAVES) {
+      const uint32_t s = (uint32_t)p * (uint32_t)kgroups + (uint32_t)kg;
+      const SegLoad c = seg_load(op, s, lane);
+      uint4 av0 = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
+      uint4 av1 = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+      const float wsv = wsrow[kg];
+      float sav[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sav[i] = srow[i][kg];
+      const uint4 ex = decode_segment(c, s_dfa, stage, lane);
+      if (!row_ok) av0 = av1 = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sav[i] = srow_ok[i] ? sav[i] : 0.f;
+      const uint2 w0 = merge8(ex.x, c.oth.x), w1 = merge8(ex.y, c.oth.y);
+      const uint2 w2 = merge8(ex.z, c.oth.z), w3 = merge8(ex.w, c.oth.w);
+      v4f d = {0.f, 0.f, 0.f, 0.f};
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
+          0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av0.w << 32) | av0.z), (long)(((uint64_t)w1.y << 32) | w1.x), d, 0,
+          0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av1.y << 32) | av1.x), (long)(((uint64_t)w2.y << 32) | w2.x), d, 0,
+          0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+          (long)(((uint64_t)av1.w << 32) | av1.z), (long)(((uint64_t)w3.y << 32) | w3.x), d, 0,
+          0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * wsv, acc[i]);
+    }
+    // the waves' partial sums through their (now zero) staging areas, summed
+    // in wave order as the FP8 linear sums them
+    float *const red = reinterpret_cast<float *>(stage);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[i * 64 + lane] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int i = threadIdx.x >> 6, l = threadIdx.x & 63;
+      float sum = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv) sum += reinterpret_cast<const float *>(s_stage[wv])[i * 64 + l];
+      const int m = 4 * (l >> 4) + i;
+      if (m < M) out[(size_t)m * ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
+    }
+    __syncthreads();
+    for (int i = lane; i < 4 * 64; i += 64) stage[i] = 0u;  // staging is zero again
+  }
+}
+
+// Row-major FP8 bytes of one tiled operand W[n, K]: every wave decodes
+// segments wave_id, + total waves, ... and stores each lane's two 16-byte
+// runs.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
+    TileOperand op, const uint32_t *__restrict__ table, uint8_t *__restrict__ out, int K,
+    uint32_t n_seg) {
+  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  load_dfa_batched<WAVES * 64>(s_dfa, table, threadIdx.x);
+  uint32_t *const stage = s_stage[wave];
+  for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
+  __syncthreads();
+  const uint32_t kgroups = (uint32_t)K / kGroup;
+  const int r = lane & 15, g = lane >> 4;
+  for (uint32_t s = blockIdx.x * WAVES + wave; s < n_seg; s += gridDim.x * WAVES) {
+    const SegLoad c = seg_load(op, s, lane);
+    const uint4 ex = decode_segment(c, s_dfa, stage, lane);
+    const uint2 w0 = merge8(ex.x, c.oth.x), w1 = merge8(ex.y, c.oth.y);
+    const uint2 w2 = merge8(ex.z, c.oth.z), w3 = merge8(ex.w, c.oth.w);
+    const uint32_t p = s / kgroups, kg = s % kgroups;
+    uint8_t *const row = out + (size_t)(p * 16 + r) * K + kg * kGroup + 16 * g;
+    __builtin_nontemporal_store(u32x4{w0.x, w0.y, w1.x, w1.y}, reinterpret_cast<u32x4 *>(row));
+    __builtin_nontemporal_store(u32x4{w2.x, w2.y, w3.x, w3.y},
+                                reinterpret_cast<u32x4 *>(row + 64));
+  }
+}
+
+inline hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+template <class Kernel>
+int resident_grid(Kernel kernel, int threads, int64_t work, int *grid) {
+  int dev = 0, cus = 0, occ = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(kernel),
+                                                    threads, 0) != hipSuccess)
+    return ECF8_ERR_HIP;
+  const int64_t g = (int64_t)cus * (occ > 0 ? occ : 1);
+  *grid = (int)(g < work ? g : work);
+  return ECF8_OK;
+}
+
+int check_operand(const ecf8_tile_operand &t) {
+  if (!t.stream || !t.seg_off || !t.gaps || !t.other || !t.weight_scale) return ECF8_ERR_INVALID_ARG;
+  if (!aligned(t.stream, 4) || !aligned(t.seg_off, 4) || !aligned(t.gaps, 4) ||
+      !aligned(t.other, 16) || !aligned(t.weight_scale, 4))
+    return ECF8_ERR_MISALIGNED;
+  return ECF8_OK;
+}
+
+}  // namespace
+
+extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int64_t K,
+                                const ecf8_tile_operand *ops, int n_ops, const uint32_t *table,
+                                void *out, int64_t ldo, int waves, void *stream) {
+  if (!aq || !as || !ops || !table || !out || M <= 0 || K <= 0 || n_ops < 1 ||
+      n_ops > ECF8_LINEAR_MAX_SEGS)
+    return ECF8_ERR_INVALID_ARG;
+  if (M > 16 || K % kGroup || K > (1 << 20) || (waves != 8 && waves != 16))
+    return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(aq, 16) || !aligned(out, 4) || !aligned(as, 4) || !aligned(table, 4))
+    return ECF8_ERR_MISALIGNED;
+  TileSegs s{};
+  int64_t n_total = 0;
+  for (int i = 0; i < n_ops; ++i) {
+    const ecf8_tile_operand &t = ops[i];
+    const int rc = check_operand(t);
+    if (rc != ECF8_OK) return rc;
+    if (t.n <= 0 || t.out_col < 0) return ECF8_ERR_INVALID_ARG;
+    if (t.n % kGroup) return ECF8_ERR_UNSUPPORTED;
+    if (t.out_col + t.n > ldo) return ECF8_ERR_CAPACITY;
+    n_total += t.n;
+    s.op[i] = TileOperand{static_cast<const uint8_t *>(t.stream), t.seg_off, t.gaps,
+                          static_cast<const uint8_t *>(t.other), t.weight_scale};
+    s.n_end[i] = (int)n_total;
+    s.col[i] = (int)t.out_col;
+  }
+  if (n_total > (1 << 24)) return ECF8_ERR_UNSUPPORTED;
+  s.count = n_ops;
+  const int n_panels = (int)(n_total / 16);
+  const auto *a = static_cast<const uint8_t *>(aq);
+  auto *o = static_cast<uint16_t *>(out);
+  int grid = 0, rc;
+  if (waves == 16) {
+    rc = resident_grid(tile_linear16_kernel<16>, 1024, n_panels, &grid);
+    if (rc != ECF8_OK) return rc;
+    tile_linear16_kernel<16><<<(unsigned)grid, 1024, 0, as_stream(stream)>>>(
+        a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels);
+  } else {
+    rc = resident_grid(tile_linear16_kernel<8>, 512, n_panels, &grid);
+    if (rc != ECF8_OK) return rc;
+    tile_linear16_kernel<8><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(
+        a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels);
+  }
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
+extern "C" int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *table,
+                                void *out, void *stream) {
+  if (!op || !table || !out || K <= 0) return ECF8_ERR_INVALID_ARG;
+  const int rc0 = check_operand(*op);
+  if (rc0 != ECF8_OK) return rc0;
+  if (op->n <= 0 || op->n % 16 || K % kGroup) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(out, 16) || !aligned(table, 4)) return ECF8_ERR_MISALIGNED;
+  if ((int64_t)op->n * K >= ((int64_t)1 << 40)) return ECF8_ERR_UNSUPPORTED;
+  const int64_t n_seg = (int64_t)(op->n / 16) * (K / kGroup);
+  if (n_seg > (int64_t)UINT32_MAX / 2) return ECF8_ERR_UNSUPPORTED;
+  const TileOperand t{static_cast<const uint8_t *>(op->stream), op->seg_off, op->gaps,
+                      static_cast<const uint8_t *>(op->other), op->weight_scale};
+  int grid = 0;
+  const int rc = resident_grid(tile_decode_kernel<8>, 512, (n_seg + 7) / 8, &grid);
+  if (rc != ECF8_OK) return rc;
+  tile_decode_kernel<8><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(
+      t, table, static_cast<uint8_t *>(out), (int)K, (uint32_t)n_seg);
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}

@@ -1,0 +1,197 @@
+// Host side of the tiled execution layout (ECF8-T; layout in
+// ecf8_tile_layout.h): recovering a block's Huffman code from its LUT stack,
+// and re-encoding one FP8 Linear into MFMA-order segments under that code.
+// No reference counterpart: the reference decodes each block into FP8
+// before its GEMM (dfloat/run/run.py:84-155); this layout lets the small-M
+// linear decode the exponents itself (ecf8_tile_linear), with the block's
+// own code, so the compressed size is the reference layout's.
+
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "ecf8.h"
+#include "ecf8_tile.h"
+#include "ecf8_tile_layout.h"
+
+using namespace ecf8;
+
+namespace {
+
+// Element (row, column) of symbol i of segment (panel p, group kg).
+inline void tile_element(int64_t p, int64_t kg, int i, int64_t *row, int64_t *col) {
+  const int lane = i / kTileLaneSymbols, j = i % kTileLaneSymbols;
+  const int r = lane & 15, q = lane >> 4;
+  *row = p * kTileRows + r;
+  *col = kg * kTileGroup + (j < 16 ? 16 * q + j : 64 + 16 * q + (j - 16));
+}
+
+inline int exponent_of(uint8_t b) { return (b >> 3) & 0xF; }
+inline int other_of(uint8_t b) { return ((b >> 4) & 0x8) | (b & 0x7); }
+
+// Bits of one segment under the code lengths.
+int64_t segment_bits(const uint8_t *w, int64_t k, int64_t p, int64_t kg, const uint8_t *code_bits,
+                     bool *missing) {
+  int64_t bits = 0;
+  for (int i = 0; i < kTileSegSymbols; ++i) {
+    int64_t row, col;
+    tile_element(p, kg, i, &row, &col);
+    const int e = exponent_of(w[row * k + col]);
+    if (code_bits[e] == 0) *missing = true;
+    bits += code_bits[e];
+  }
+  return bits;
+}
+
+// Write one segment: codes MSB-first from the segment's first byte, chunk
+// gaps, sign/mantissa nibbles.  `out` holds the segment's bytes (zeroed).
+void write_segment(const uint8_t *w, int64_t k, int64_t p, int64_t kg, const uint8_t *code_bits,
+                   const uint32_t *code_vals, uint8_t *out, uint32_t *gaps, uint8_t *other) {
+  uint64_t acc = 0;  // pending bits, right-aligned
+  int nacc = 0;
+  int64_t nbyte = 0, pos = 0;
+  int next_chunk = 0;  // first chunk whose gap is not yet recorded
+  memset(gaps, 0, kTileGapWords * 4);
+  for (int i = 0; i < kTileSegSymbols; ++i) {
+    int64_t row, col;
+    tile_element(p, kg, i, &row, &col);
+    const uint8_t b = w[row * k + col];
+    const int e = exponent_of(b), len = code_bits[e];
+    // the first code starting in each chunk: its offset in the chunk
+    while (next_chunk < kTileLanes && pos >= (int64_t)next_chunk * kTileChunkBits) {
+      const int64_t gap = pos - (int64_t)next_chunk * kTileChunkBits;
+      if (gap < kTileChunkBits) gaps[next_chunk >> 3] |= (uint32_t)gap << (4 * (next_chunk & 7));
+      ++next_chunk;
+    }
+    acc = (acc << len) | code_vals[e];
+    nacc += len;
+    pos += len;
+    while (nacc >= 8) {
+      out[nbyte++] = (uint8_t)(acc >> (nacc - 8));
+      nacc -= 8;
+    }
+    const int o = other_of(b);
+    uint8_t &ob = other[i >> 1];
+    ob = (uint8_t)((i & 1) ? (ob | o) : (o << 4));
+  }
+  if (nacc) out[nbyte++] = (uint8_t)(acc << (8 - nacc));
+}
+
+}  // namespace
+
+extern "C" int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *code_bits,
+                                   uint32_t *code_vals) {
+  if (!luts || !code_bits || !code_vals) return ECF8_ERR_INVALID_ARG;
+  if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
+  const uint8_t *len_row = luts + 256 * (n_luts - 1);
+  memset(code_bits, 0, 16);
+  memset(code_vals, 0, 16 * sizeof(uint32_t));
+  // each symbol's code is the first 16-bit window (in increasing order)
+  // that the reference rule (dfloat/run/decode.cu:85-91) decodes to it
+  bool seen[16] = {false};
+  for (uint32_t w = 0; w < 65536; ++w) {
+    int v = luts[w >> 8];
+    if (v >= 240) {
+      const int row = 256 - v;
+      if (row > n_luts - 2) return ECF8_ERR_FORMAT;
+      v = luts[row * 256 + (w & 0xFF)];
+    }
+    if (v > 15) return ECF8_ERR_FORMAT;
+    const int len = len_row[v];
+    if (len < 1 || len > 16) return ECF8_ERR_FORMAT;
+    if (!seen[v]) {
+      seen[v] = true;
+      code_bits[v] = (uint8_t)len;
+      code_vals[v] = w >> (16 - len);
+    }
+  }
+  // a prefix code: every window starting with a symbol's code decodes to it
+  for (int s = 0; s < 16; ++s) {
+    if (!seen[s]) continue;
+    const uint32_t lo = code_vals[s] << (16 - code_bits[s]);
+    const uint32_t hi = lo + (1u << (16 - code_bits[s]));
+    for (uint32_t w = lo; w < hi; ++w) {
+      int v = luts[w >> 8];
+      if (v >= 240) v = luts[(256 - v) * 256 + (w & 0xFF)];
+      if (v != s) return ECF8_ERR_FORMAT;
+    }
+  }
+  return ECF8_OK;
+}
+
+extern "C" int ecf8_tile_sizes(const uint8_t *weight, int64_t n_rows, int64_t k,
+                               const uint8_t *code_bits, int64_t *stream_bytes,
+                               int64_t *n_segments) {
+  if (!weight || !code_bits || !stream_bytes || !n_segments || n_rows <= 0 || k <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (n_rows % kTileRows || k % kTileGroup) return ECF8_ERR_UNSUPPORTED;
+  const int64_t panels = n_rows / kTileRows, groups = k / kTileGroup;
+  int64_t total = 0;
+  bool missing = false;
+  for (int64_t p = 0; p < panels; ++p) {
+    for (int64_t kg = 0; kg < groups; ++kg) {
+      const int64_t bytes = tile_segment_bytes(segment_bits(weight, k, p, kg, code_bits, &missing));
+      if (bytes > kTileMaxSegBytes) return ECF8_ERR_CAPACITY;
+      total += bytes;
+    }
+  }
+  if (missing) return ECF8_ERR_FORMAT;  // an exponent without a code
+  if (total + kTilePadBytes > (int64_t)UINT32_MAX) return ECF8_ERR_UNSUPPORTED;
+  *stream_bytes = total + kTilePadBytes;
+  *n_segments = panels * groups;
+  return ECF8_OK;
+}
+
+extern "C" int ecf8_tile_encode(const uint8_t *weight, int64_t n_rows, int64_t k,
+                                const uint8_t *code_bits, const uint32_t *code_vals,
+                                uint8_t *stream, int64_t stream_capacity, uint32_t *seg_off,
+                                uint32_t *gaps, uint8_t *other, int n_threads) {
+  if (!weight || !code_bits || !code_vals || !stream || !seg_off || !gaps || !other ||
+      n_rows <= 0 || k <= 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (n_rows % kTileRows || k % kTileGroup) return ECF8_ERR_UNSUPPORTED;
+  for (int s = 0; s < 16; ++s)
+    if (code_bits[s] > 16 || (code_bits[s] && code_vals[s] >> code_bits[s])) return ECF8_ERR_FORMAT;
+  const int64_t panels = n_rows / kTileRows, groups = k / kTileGroup, n_seg = panels * groups;
+  const int nt = std::max(1, std::min(n_threads, 64));
+  // pass 1: segment sizes (parallel), then offsets
+  std::vector<int64_t> bytes(n_seg);
+  std::vector<int> bad(nt, 0);
+  auto run = [&](auto &&body) {
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; ++t)
+      th.emplace_back([&, t] {
+        for (int64_t s = t; s < n_seg; s += nt) body(t, s);
+      });
+    for (auto &x : th) x.join();
+  };
+  run([&](int t, int64_t s) {
+    bool missing = false;
+    bytes[s] = tile_segment_bytes(segment_bits(weight, k, s / groups, s % groups, code_bits,
+                                               &missing));
+    if (missing) bad[t] |= 1;
+    if (bytes[s] > kTileMaxSegBytes) bad[t] |= 2;
+  });
+  int any_bad = 0;
+  for (int b : bad) any_bad |= b;
+  if (any_bad & 1) return ECF8_ERR_FORMAT;
+  if (any_bad & 2) return ECF8_ERR_CAPACITY;
+  int64_t off = 0;
+  for (int64_t s = 0; s < n_seg; ++s) {
+    if (off > (int64_t)UINT32_MAX) return ECF8_ERR_UNSUPPORTED;
+    seg_off[s] = (uint32_t)off;
+    off += bytes[s];
+  }
+  if (off + kTilePadBytes > stream_capacity || off > (int64_t)UINT32_MAX) return ECF8_ERR_CAPACITY;
+  seg_off[n_seg] = (uint32_t)off;
+  memset(stream, 0, (size_t)(off + kTilePadBytes));
+  // pass 2: the segments (parallel; disjoint outputs)
+  run([&](int, int64_t s) {
+    write_segment(weight, k, s / groups, s % groups, code_bits, code_vals, stream + seg_off[s],
+                  gaps + s * kTileGapWords, other + s * kTileOtherBytes);
+  });
+  return ECF8_OK;
+}

@@ -1,0 +1,193 @@
+"""The tiled execution layout ECF8-T (include/ecf8_tile.h) from Python.
+
+A compressed block (one layer, the reference's layout) is re-tiled at load
+time, Linear by Linear, under the block's own Huffman code: the symbols of
+each 16-row x 128-column tile are reordered into the lanes' MFMA operand
+order and cut into 2048-symbol segments.  The decode step's small-M linears
+then decode their weight operands themselves (``TileLinearPlan``, the C ABI
+``ecf8_tile_linear``), bit-identical to decoding the block and running the
+FP8 linear, without writing or re-reading an FP8 copy; the prompt's
+large-M linears decode a tiled Linear to row-major FP8 first
+(``tile_decode``).
+
+No reference counterpart: the reference decodes every block before its
+GEMMs (dfloat/run/run.py:84-155).  The checkpoint and hook layout stays the
+reference's; this layout is derived from it in device memory.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+from ._lib import ECF8Error, check, lib
+
+__all__ = ["code_from_luts", "tile_encode", "TiledOperand", "tile_decode", "TileLinearPlan",
+           "linear_waves", "SEG_SYMBOLS"]
+
+SEG_SYMBOLS = 2048
+_GROUP = 128
+
+
+class _TileOp(ctypes.Structure):
+    _fields_ = [("stream", ctypes.c_void_p), ("seg_off", ctypes.c_void_p),
+                ("gaps", ctypes.c_void_p), ("other", ctypes.c_void_p),
+                ("weight_scale", ctypes.c_void_p), ("n", ctypes.c_int64),
+                ("out_col", ctypes.c_int64)]
+
+
+def _vp(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def code_from_luts(luts) -> tuple[np.ndarray, np.ndarray]:
+    """(code_bits u8[16], code_vals u32[16]) of a block's Huffman code, read
+    off its LUT stack (ecf8_code_from_luts)."""
+    lut = np.ascontiguousarray(torch.as_tensor(luts).detach().cpu().numpy(), dtype=np.uint8)
+    if lut.size % 256:
+        raise ECF8Error("luts size is not a multiple of 256")
+    bits = np.zeros(16, np.uint8)
+    vals = np.zeros(16, np.uint32)
+    check(lib().ecf8_code_from_luts(_vp(lut), lut.size // 256, _vp(bits), _vp(vals)),
+          "ecf8_code_from_luts")
+    return bits, vals
+
+
+def tile_encode(weight, code_bits, code_vals, n_threads: int | None = None) -> dict:
+    """ECF8-T encoding of one FP8 Linear (e4m3fn or uint8 [n, K], any device;
+    encoded on the host): {stream, seg_off, gaps, other} as CPU tensors."""
+    w = weight.detach()
+    if w.dtype == torch.float8_e4m3fn:
+        w = w.view(torch.uint8)
+    if w.dtype != torch.uint8 or w.dim() != 2:
+        raise ECF8Error("weight must be a 2-D e4m3fn or uint8 tensor")
+    wn = np.ascontiguousarray(w.cpu().numpy())
+    n, k = wn.shape
+    bits = np.ascontiguousarray(code_bits, dtype=np.uint8)
+    vals = np.ascontiguousarray(code_vals, dtype=np.uint32)
+    L = lib()
+    nb, ns = ctypes.c_int64(), ctypes.c_int64()
+    check(L.ecf8_tile_sizes(_vp(wn), n, k, _vp(bits), ctypes.byref(nb), ctypes.byref(ns)),
+          "ecf8_tile_sizes")
+    stream = np.empty(nb.value, np.uint8)
+    seg_off = np.empty(ns.value + 1, np.uint32)
+    gaps = np.empty(ns.value * 8, np.uint32)
+    other = np.empty(ns.value * 1024, np.uint8)
+    threads = n_threads or min(os.cpu_count() or 1, 16)
+    check(L.ecf8_tile_encode(_vp(wn), n, k, _vp(bits), _vp(vals), _vp(stream), nb.value,
+                             _vp(seg_off), _vp(gaps), _vp(other), threads), "ecf8_tile_encode")
+    return {"stream": torch.from_numpy(stream), "seg_off": torch.from_numpy(seg_off.view(np.int32)),
+            "gaps": torch.from_numpy(gaps.view(np.int32)), "other": torch.from_numpy(other)}
+
+
+class TiledOperand:
+    """One tiled Linear on a device: its ECF8-T tensors, its weight scales
+    and shape."""
+
+    def __init__(self, enc: dict, weight_scale: torch.Tensor, n: int, k: int, device=None):
+        dev = torch.device(device) if device is not None else weight_scale.device
+        self.stream = enc["stream"].to(dev)
+        self.seg_off = enc["seg_off"].to(dev)
+        self.gaps = enc["gaps"].to(dev)
+        self.other = enc["other"].to(dev)
+        self.weight_scale = weight_scale.to(dev).contiguous()
+        self.n, self.k = int(n), int(k)
+        if self.n % _GROUP or self.k % _GROUP:
+            raise ECF8Error("tiled Linears need 128-multiples")
+        if tuple(self.weight_scale.shape) != (self.n // _GROUP, self.k // _GROUP):
+            raise ECF8Error("weight_scale does not match the Linear's shape")
+        n_seg = (self.n // 16) * (self.k // _GROUP)
+        if (self.seg_off.numel() != n_seg + 1 or self.gaps.numel() != 8 * n_seg
+                or self.other.numel() != 1024 * n_seg):
+            raise ECF8Error("tiled tensors do not match the Linear's shape")
+        self.device = dev
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in
+                   (self.stream, self.seg_off, self.gaps, self.other))
+
+    def c_struct(self, out_col: int = 0) -> _TileOp:
+        return _TileOp(self.stream.data_ptr(), self.seg_off.data_ptr(), self.gaps.data_ptr(),
+                       self.other.data_ptr(), self.weight_scale.data_ptr(), self.n, out_col)
+
+
+def _table_ptr(table, dev):
+    data = getattr(table, "data", table)
+    if not data.is_cuda or data.device != dev:
+        raise ECF8Error(f"the decode table must be on {dev}")
+    if getattr(table, "kind", 1) not in (1,):
+        raise ECF8Error("tiled decoding needs the block's automaton (ECF8_TABLE_DFA) table")
+    return data.data_ptr()
+
+
+def tile_decode(op: TiledOperand, table, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Row-major e4m3fn [n, K] of a tiled Linear (into ``out`` if given)."""
+    dev = op.device
+    if out is None:
+        out = torch.empty(op.n, op.k, dtype=torch.float8_e4m3fn, device=dev)
+    if (not out.is_cuda or out.device != dev or out.numel() < op.n * op.k
+            or not out.is_contiguous() or out.dtype not in (torch.uint8, torch.float8_e4m3fn)):
+        raise ECF8Error("out must be a contiguous e4m3fn/uint8 tensor of n*K elements on the device")
+    s = op.c_struct()
+    with torch.cuda.device(dev):
+        check(lib().ecf8_tile_decode(ctypes.byref(s), op.k, _table_ptr(table, dev), out.data_ptr(),
+                                     torch.cuda.current_stream(dev).cuda_stream), "ecf8_tile_decode")
+    return out
+
+
+def linear_waves(n_total: int, k: int, device) -> int:
+    """The wave count the FP8 linear uses for M <= 16 at this shape (16 for
+    K >= 64 groups or the persistent K = 4096 form, else 8): the tiled
+    linear must use the same one to sum in the same order."""
+    if k // _GROUP >= 64:
+        return 16
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    if k == 4096 and n_total // 16 > 2 * cus:
+        return 16
+    return 8
+
+
+class TileLinearPlan:
+    """A (possibly fused) small-M linear over tiled operands written side by
+    side into ``out`` (bf16 [rows, ldo]) -- the tiled counterpart of
+    llm_kernels.LinearPlan."""
+
+    def __init__(self, ops, table, out: torch.Tensor, waves: int | None = None):
+        if not 1 <= len(ops) <= 3:
+            raise ECF8Error("1..3 operands per linear")
+        dev = out.device
+        if out.dtype != torch.bfloat16 or not out.is_cuda or not out.is_contiguous():
+            raise ECF8Error("out must be a contiguous bf16 CUDA tensor")
+        K = ops[0].k
+        arr = (_TileOp * len(ops))()
+        col = 0
+        for i, op in enumerate(ops):
+            if op.k != K or op.device != dev:
+                raise ECF8Error("operands differ in K or device")
+            arr[i] = op.c_struct(col)
+            col += op.n
+        if out.shape[-1] < col:
+            raise ECF8Error(f"out has {out.shape[-1]} columns, {col} needed")
+        self.ops, self.arr, self.K, self.N, self.out = list(ops), arr, K, col, out
+        self.ldo = out.shape[-1]
+        self.table_ptr = _table_ptr(table, dev)
+        self._table = table
+        self.waves = waves if waves is not None else linear_waves(col, K, dev)
+
+    def __call__(self, aq: torch.Tensor, a_scale: torch.Tensor, M: int):
+        dev = self.out.device
+        if (aq.dtype != torch.float8_e4m3fn or a_scale.dtype != torch.float32 or aq.device != dev
+                or aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < M
+                or tuple(a_scale.shape[1:]) != (self.K // _GROUP,) or a_scale.shape[0] < M
+                or not aq.is_contiguous() or not a_scale.is_contiguous()):
+            raise ECF8Error("activation shape does not match the linear")
+        if not 1 <= M <= 16 or self.out.shape[0] < M:
+            raise ECF8Error("the tiled linear runs 1..16 rows")
+        check(lib().ecf8_tile_linear(aq.data_ptr(), a_scale.data_ptr(), M, self.K, self.arr,
+                                     len(self.ops), self.table_ptr, self.out.data_ptr(), self.ldo,
+                                     self.waves, torch.cuda.current_stream(dev).cuda_stream),
+              "ecf8_tile_linear")
+        return self.out

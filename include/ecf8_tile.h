@@ -1,0 +1,106 @@
+/*
+ * ecf8_tile.h -- the tiled execution layout ECF8-T of libecf8.so: one
+ * compressed FP8 Linear re-encoded, under its block's own Huffman code, so
+ * that the small-M linear of a decode step decodes its weight operands
+ * itself instead of reading a decoded FP8 copy from HBM.
+ *
+ * No reference counterpart.  The reference decodes each block into FP8
+ * before its GEMMs (dfloat/run/run.py:84-155, one decode per forward-pre-
+ * hook); its on-disk layout (dfloat/utils.py:373-530) stays the checkpoint
+ * format and the hook path's input, and a loader may re-tile a block's
+ * Linears from it at load time (decode once, ecf8_tile_encode).
+ *
+ * Layout (N a multiple of 16, K of 128): segment s = p * (K/128) + kg holds
+ * the 16 x 128 tile of rows 16p.., columns 128kg.. in MFMA lane order --
+ * symbol 32 l + j is row 16p + (l & 15), column 128kg + 16 (l >> 4) + j
+ * (j < 16) or 128kg + 64 + 16 (l >> 4) + (j - 16) (j >= 16).
+ *   stream   u8       each segment's codes, MSB-first, 4-byte aligned,
+ *                     then 16 padding bytes
+ *   seg_off  u32[S+1] segment byte offsets; seg_off[S] = end of the codes
+ *   gaps     u32[8 S] bit offset of the first code in each 12-byte chunk
+ *                     (4 bits per chunk, chunk c in bits 4(c%8) of word c/8)
+ *   other    u8[1024 S] sign/mantissa nibbles in symbol order, even
+ *                     symbol high (the reference's packed_other_4bits rule)
+ * A segment holds at most 64 chunks (768 bytes).
+ */
+#ifndef ECF8_TILE_H
+#define ECF8_TILE_H
+
+#include <stdint.h>
+
+#include "ecf8.h"
+#include "ecf8_llm.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ host */
+
+/*
+ * The block's Huffman code recovered from its LUT stack: for each exponent
+ * s with a code, code_bits[s] = its length and code_vals[s] its value (the
+ * first 16-bit window the reference rule, dfloat/run/decode.cu:85-91,
+ * decodes to s).  Checks that every window starting with a symbol's code
+ * decodes to it (a prefix code); ECF8_ERR_FORMAT otherwise.
+ */
+int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *code_bits, uint32_t *code_vals);
+
+/*
+ * Sizes of the ECF8-T encoding of weight (e4m3fn bytes, row-major
+ * [n_rows, k], host memory) under code_bits: stream bytes (padding
+ * included) and segment count.  ECF8_ERR_CAPACITY when a segment exceeds
+ * 768 bytes; ECF8_ERR_FORMAT when an exponent has no code.
+ */
+int ecf8_tile_sizes(const uint8_t *weight, int64_t n_rows, int64_t k, const uint8_t *code_bits,
+                    int64_t *stream_bytes, int64_t *n_segments);
+
+/*
+ * Encode weight into the layout above (host memory; seg_off holds S+1
+ * entries, gaps 8 S words, other 1024 S bytes), on up to n_threads host
+ * threads.
+ */
+int ecf8_tile_encode(const uint8_t *weight, int64_t n_rows, int64_t k, const uint8_t *code_bits,
+                     const uint32_t *code_vals, uint8_t *stream, int64_t stream_capacity,
+                     uint32_t *seg_off, uint32_t *gaps, uint8_t *other, int n_threads);
+
+/* ---------------------------------------------------------------- device */
+
+/* One tiled weight operand (device memory) of a linear. */
+typedef struct ecf8_tile_operand {
+  const void *stream;        /* 4-byte aligned */
+  const uint32_t *seg_off;
+  const uint32_t *gaps;
+  const void *other;         /* 16-byte aligned */
+  const float *weight_scale; /* weight_scale_inv f32 [n/128, K/128] */
+  int64_t n;                 /* output columns (rows of W), multiple of 128 */
+  int64_t out_col;           /* first output column of this operand */
+} ecf8_tile_operand;
+
+/*
+ * The small-M (M <= 16) block-scaled FP8 linear of ecf8_fp8_linear with
+ * its weight operands decoded on the fly from ECF8-T:
+ *   out[m, out_col + n] = sum_g (sum_{k in g} aq[m,k] W[n,k]) as[m,g] ws[n/128,g]
+ * `table`: the ECF8_TABLE_DFA table of the block's LUTs (all operands
+ * share the block's code).  `waves` (8 or 16) must be the wave count
+ * ecf8_fp8_linear uses for the same shape -- 16 when K/128 >= 64 or when
+ * K = 4096 has more than 2 x CUs 16-column tiles, else 8 -- and the result
+ * is then bit-identical to decoding W and calling ecf8_fp8_linear.
+ * aq: 16-byte aligned; out: bf16, ldo elements per row.
+ */
+int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int64_t K,
+                     const ecf8_tile_operand *ops, int n_ops, const uint32_t *table, void *out,
+                     int64_t ldo, int waves, void *stream);
+
+/*
+ * Decode one tiled operand into row-major e4m3fn bytes out[n, K]
+ * (16-byte aligned) with the DFA table of its block.
+ */
+int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *table, void *out,
+                     void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ECF8_TILE_H */
