@@ -309,7 +309,8 @@ def e2e_generate(args):
     decode step) and must produce identical tokens."""
     import torch
 
-    from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model, timed_generate
+    from ecf8_amd.llm import (Qwen3Config, Qwen3Runner, compress_layers, random_model,
+                              retile_layers, timed_generate)
     from ecf8_amd.prefetch import LayerPrefetcher
     from dfloat.run.run import TensorManager
 
@@ -322,15 +323,25 @@ def e2e_generate(args):
     g = torch.Generator().manual_seed(args.seed + 7)
     prompt = torch.randint(0, cfg.vocab, (B, T), generator=g)
     results = {}
-    for mode in ("fp8", "ecf8", "ecf8_prefetch"):
+    prefetcher = None
+    for mode in ("fp8", "ecf8", "ecf8_prefetch", "ecf8_fused"):
         if mode == "ecf8":
             t0 = time.time()
             compress_layers(model, drawn)
             torch.cuda.synchronize()
             print(f"[bench] layers compressed in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
         if mode == "ecf8_prefetch":
-            LayerPrefetcher(model.model.layers, dev,
-                            workgroups_per_cu=args.prefetch_workgroups).install()
+            prefetcher = LayerPrefetcher(model.model.layers, dev,
+                                         workgroups_per_cu=args.prefetch_workgroups).install()
+        if mode == "ecf8_fused":
+            prefetcher.uninstall()
+            prefetcher = None
+            TensorManager.clear_device()
+            torch.cuda.empty_cache()
+            t0 = time.time()
+            retile_layers(model, drawn)
+            torch.cuda.synchronize()
+            print(f"[bench] layers re-tiled in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
         TensorManager.clear_device()
         torch.cuda.empty_cache()
         runner = Qwen3Runner(model, B, T, T + new, dev)
@@ -341,11 +352,16 @@ def e2e_generate(args):
               f"peak {r['peak_mib']:.0f} MiB", file=sys.stderr, flush=True)
         r["weights_mib"] = sum(t.numel() * t.element_size() for t in
                                list(model.parameters()) + list(model.buffers())) / 2**20
+        if mode == "ecf8_fused":
+            r["weights_mib"] += sum(op.nbytes() for layer in model.model.layers
+                                    for op in layer._ecf8_tiles.values()) / 2**20
         results[mode] = r
         del runner
-    same = all(torch.equal(results["fp8"]["tokens"], results[m]["tokens"])
-               for m in ("ecf8", "ecf8_prefetch"))
-    fp8, ecf8 = results["fp8"], results["ecf8_prefetch"]
+    ecf8_modes = ("ecf8", "ecf8_prefetch", "ecf8_fused")
+    same = all(torch.equal(results["fp8"]["tokens"], results[m]["tokens"]) for m in ecf8_modes)
+    fp8 = results["fp8"]
+    best = max(ecf8_modes, key=lambda m: results[m]["tokens_per_s"])
+    ecf8 = results[best]
 
     def summary(r):
         return {"tokens_per_s": round(r["tokens_per_s"], 1), "latency_s": round(r["latency_s"], 4),
@@ -364,10 +380,15 @@ def e2e_generate(args):
                    "intermediate": cfg.intermediate, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
                    "vocab": cfg.vocab, "batch": B, "prompt_len": T, "new_tokens": new,
                    "distinct_layer_weights": args.distinct_layers, "decoding": "greedy",
-                   "ecf8_decode": "next layer decoded on a side stream (double-buffered)"},
+                   "ecf8_decode": {
+                       "ecf8": "each layer decoded in its forward-pre-hook, then FP8 GEMMs",
+                       "ecf8_prefetch": "next layer decoded on a side stream (double-buffered)",
+                       "ecf8_fused": "layers re-tiled at load (ECF8-T); decode-step linears "
+                                     "decode their weight operands into the MFMAs"}[best]},
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
-        "ecf8_in_hook": summary(results["ecf8"]),
+        "ecf8_mode": best,
+        "ecf8_modes": {m: summary(results[m]) for m in ecf8_modes},
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,
     }
@@ -573,8 +594,8 @@ def e2e_child(workload: str, seed: int, timeout_s: float):
     if not lines:
         return {"error": f"exit status {res.returncode}, no result line"}
     full = json.loads(lines[-1])
-    keep = ("uncompressed_fp8", "ecf8", "ecf8_mode", "ratio_vs_uncompressed", "identical_tokens",
-            "experts_routed_last_step")
+    keep = ("uncompressed_fp8", "ecf8", "ecf8_mode", "ecf8_modes", "ratio_vs_uncompressed",
+            "identical_tokens", "experts_routed_last_step")
     out = {"workload": full["config"]["workload"], "unit": full["unit"],
            "batch": full["config"]["batch"], "prompt_len": full["config"]["prompt_len"],
            "new_tokens": full["config"]["new_tokens"],

@@ -30,6 +30,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import llm_kernels as K
+from . import tiled
 from ._lib import ECF8Error
 
 LINEAR_NAMES = ("mlp.down_proj", "mlp.gate_proj", "mlp.up_proj", "self_attn.k_proj",
@@ -284,6 +285,42 @@ class Qwen3Runner(_GreedyRunner):
 
     # ------------------------------------------------------------ layer
 
+    def _linear(self, layer, index, which, names, out, M):
+        """The linear `which` of a layer: an FP8 plan over the layer's (hook
+        injected) weights, or -- for a re-tiled layer -- the tiled linear
+        that decodes its weight operands itself (M <= 16) or, for the
+        prompt, its Linears decoded into the decode buffer first."""
+        tiles = getattr(layer, "_ecf8_tiles", None)
+        if tiles is None:
+            mods = [layer.get_submodule(n) for n in names]
+            return self._plan(layer, index, which, [(x.weight, x.weight_scale_inv) for x in mods],
+                              out)
+        if M <= 16:
+            key = (index, which, "tiled")
+            p = self._plans.get(key)
+            if p is None:
+                p = tiled.TileLinearPlan([tiles[n] for n in names], layer._ecf8_tile_table, out)
+                self._plans[key] = p
+            return p
+        weights = []
+        for n in names:
+            op = tiles[n]
+            buf = self._tile_scratch(op.n * op.k, n)
+            tiled.tile_decode(op, layer._ecf8_tile_table, buf)
+            weights.append((buf.view(op.n, op.k), op.weight_scale))
+        return K.LinearPlan(weights, out)
+
+    def _tile_scratch(self, numel, name):
+        """Prompt-time FP8 buffers for re-tiled Linears, one per Linear name
+        (reused by every layer: layers run one after another)."""
+        if not hasattr(self, "_tile_bufs"):
+            self._tile_bufs = {}
+        buf = self._tile_bufs.get(name)
+        if buf is None or buf.numel() < numel:
+            buf = torch.empty(numel, dtype=torch.float8_e4m3fn, device=self.dev)
+            self._tile_bufs[name] = buf
+        return buf[:numel]
+
     def layer(self, layer: DecoderLayer, index: int, x_prev, prefill: bool):
         cfg = self.cfg
         B, T = self.B, (self.T if prefill else 1)
@@ -293,10 +330,8 @@ class Qwen3Runner(_GreedyRunner):
         aqH, asH = self.aq[H], self.as_[H]
         K.rmsnorm(self.res, layer.input_layernorm.weight, cfg.eps, M, x=x_prev, out_q=aqH,
                   out_scale=asH)
-        self._plan(layer, index, "qkv", [(a.q_proj.weight, a.q_proj.weight_scale_inv),
-                                         (a.k_proj.weight, a.k_proj.weight_scale_inv),
-                                         (a.v_proj.weight, a.v_proj.weight_scale_inv)],
-                   self.qkv)(aqH, asH, M)
+        self._linear(layer, index, "qkv", ("self_attn.q_proj", "self_attn.k_proj",
+                                           "self_attn.v_proj"), self.qkv, M)(aqH, asH, M)
         aqA, asA = self.aq[Hq * 128], self.as_[Hq * 128]
         if prefill:
             K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
@@ -307,17 +342,14 @@ class Qwen3Runner(_GreedyRunner):
             K.decode_attention_fused(self.qkv, B, Hq, Hkv, a.q_norm.weight, a.k_norm.weight,
                                      cfg.eps, self.cos, self.sin, self.pos, self.kc[index],
                                      self.vc[index], self.work, aqA, asA)
-        self._plan(layer, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
-                   self.o)(aqA, asA, M)
+        self._linear(layer, index, "o", ("self_attn.o_proj",), self.o, M)(aqA, asA, M)
         K.rmsnorm(self.res, layer.post_attention_layernorm.weight, cfg.eps, M, x=self.o,
                   out_q=aqH, out_scale=asH)
-        self._plan(layer, index, "gu", [(m.gate_proj.weight, m.gate_proj.weight_scale_inv),
-                                        (m.up_proj.weight, m.up_proj.weight_scale_inv)],
-                   self.gu)(aqH, asH, M)
+        self._linear(layer, index, "gu", ("mlp.gate_proj", "mlp.up_proj"), self.gu, M)(aqH, asH,
+                                                                                       M)
         aqI, asI = self.aq[I], self.as_[I]
         K.silu_mul_quant(self.gu, M, aqI, asI)
-        self._plan(layer, index, "down", [(m.down_proj.weight, m.down_proj.weight_scale_inv)],
-                   self.down)(aqI, asI, M)
+        self._linear(layer, index, "down", ("mlp.down_proj",), self.down, M)(aqI, asI, M)
         return self.down
 
 
@@ -387,6 +419,55 @@ def compress_layers(model: Qwen3ForCausalLM, drawn=None, threads_per_block: int 
             value = comp[attr] if attr == "split_positions" else comp[attr].to(dev).clone()
             _process_compressed_tensor(layer, attr, value, f"model.layers.{i}.{attr}", pattern,
                                        threads_per_block, bytes_per_thread)
+    return model
+
+
+def retile_layers(model: Qwen3ForCausalLM, drawn=None, n_threads: int | None = None):
+    """Re-tile every compressed layer for the fused decode + linear
+    (ecf8_amd.tiled): each layer's block is decoded once on its device, each
+    of its seven Linears re-encoded under the block's own code into the
+    tiled layout, and the block's reference-layout buffers and decode hook
+    removed -- the decode step's linears then decode their weight operands
+    themselves.  ``drawn`` (from random_model) lets layers that hold copies
+    of one block share one encoding; each layer keeps its own device copy."""
+    from ecf8_amd.decode import build_table, decode
+
+    cache = {}
+    for i, layer in enumerate(model.model.layers):
+        if not hasattr(layer, "encoded"):
+            raise ECF8Error(f"layer {i} holds no compressed block")
+        dev = layer.encoded.device
+        key = i % len(drawn) if drawn is not None else None
+        enc = cache.get(key) if key is not None else None
+        if enc is None:
+            flat = decode(layer.luts, layer.encoded, layer.packed_other_4bits,
+                          layer.output_positions, layer.gaps).cpu()
+            bits, vals = tiled.code_from_luts(layer.luts)
+            parts = torch.tensor_split(flat, layer.split_positions)
+            enc = {}
+            for mod, part in zip(layer.weight_injection_modules, parts):
+                name = next(n for n in LINEAR_NAMES if layer.get_submodule(n) is mod)
+                enc[name] = tiled.tile_encode(part.view(mod.out_features, mod.in_features), bits,
+                                              vals, n_threads)
+            if key is not None:
+                cache[key] = enc
+        layer._ecf8_tiles = {
+            n: tiled.TiledOperand(enc[n], layer.get_submodule(n).weight_scale_inv,
+                                  layer.get_submodule(n).out_features,
+                                  layer.get_submodule(n).in_features, dev)
+            for n in LINEAR_NAMES}
+        table = build_table(layer.luts.contiguous())
+        if table.kind != 1:
+            raise ECF8Error(f"layer {i}: the tiled linear needs LUTs without a 1-bit code")
+        layer._ecf8_tile_table = table
+        layer._forward_pre_hooks.clear()
+        for n in LINEAR_NAMES:  # weight views a decode hook injected earlier
+            layer.get_submodule(n).__dict__.pop("weight", None)
+        for attr in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
+                     "split_positions"):
+            if attr in layer._buffers:
+                del layer._buffers[attr]
+        layer.__dict__.pop("_ecf8_state", None)
     return model
 
 

@@ -7,8 +7,8 @@
 * Qwen3-8B-shaped model (36 layers, hidden 4096, vocab 151,936): every
   layer's forward-pre-hook injects bit-exact weights, and a batch-16 greedy
   generate from 128-token prompts gives the FP8 model's tokens and logits,
-  eager and graph-replayed, with the decode in the hook and on the side
-  stream.
+  eager and graph-replayed, with the decode in the hook, on the side
+  stream, and fused into the decode step's linears (re-tiled layers).
 * FLUX.1-dev-shaped DiT (19 double + 38 single blocks, hidden 3072): every
   block injects bit-exact weights, and one denoising step at 4096 image +
   512 text tokens gives the FP8 pipeline's latents.
@@ -110,7 +110,7 @@ def test_moe_layer_routed_selection(moe_layer, cuda_device):
 
 def test_qwen3_8b_model_bs16_matches_fp8(cuda_device):
     from dfloat.run.run import TensorManager
-    from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model
+    from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model, retile_layers
     from ecf8_amd.prefetch import LayerPrefetcher
 
     cfg = Qwen3Config()
@@ -148,6 +148,10 @@ def test_qwen3_8b_model_bs16_matches_fp8(cuda_device):
     pf = LayerPrefetcher(model.model.layers, cuda_device).install()
     run("ecf8_prefetch", True)
     pf.uninstall()
+    _say("[full] Qwen3-8B: re-tiling")
+    retile_layers(model, drawn)
+    for graph in (False, True):
+        run("ecf8_fused", graph)
     base_t, base_l = results[("fp8", False)]
     assert len(set(base_t.reshape(-1).tolist())) > 1
     for key, (t, l) in results.items():

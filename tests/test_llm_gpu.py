@@ -419,6 +419,22 @@ def test_compressed_model_matches_uncompressed_exactly(small_models, cuda_device
                 results[("ecf8_prefetch", wpc, graph, rep)] = (toks, r.logits.float().cpu())
             del r
         pf.uninstall()
+    # re-tiled: the decode-step linears decode their weight operands
+    # themselves (ECF8-T), the prompt decodes each tiled Linear first
+    from ecf8_amd.llm import retile_layers
+
+    retile_layers(comp)
+    assert not hasattr(comp.model.layers[0], "encoded")
+    for graph in (False, True):
+        _say(f"[llm] e2e ecf8 fused graph={graph}")
+        TensorManager.clear_device()
+        r = Qwen3Runner(comp, B, T, T + new, cuda_device)
+        if graph:
+            r.capture()
+        for rep in range(2):
+            toks = r.generate(prompt, new).cpu()
+            results[("ecf8_fused", graph, rep)] = (toks, r.logits.float().cpu())
+        del r
     base_t, base_l = results[("fp8", False)]
     for key, (t, l) in results.items():
         assert torch.equal(t, base_t), key
