@@ -67,17 +67,18 @@ __device__ __forceinline__ uint32_t f32_bf16(float f) {
   return u >> 16;
 }
 
-// The loads one segment needs, issued before its decode.
+// A segment's code window: 16 bytes from the lane's chunk start (12 + look-
+// ahead) and the gap word holding the lane's nibble.
 struct SegLoad {
-  uint32_t d0, d1, d2, d3;  // 16 bytes from the lane's chunk start (12 + look-ahead)
-  uint32_t gapw;            // the gap word holding the lane's nibble
-  uint4 oth;                // the lane's 32 sign/mantissa nibbles
-  int n_chunks;             // wave-uniform
+  uint32_t d0, d1, d2, d3;
+  uint32_t gapw;
+  int n_chunks;  // wave-uniform
 };
 
-__device__ __forceinline__ SegLoad seg_load(const TileOperand &t, uint32_t s, int lane) {
+// The window of segment s, whose codes occupy bytes [off, end) of the stream.
+__device__ __forceinline__ SegLoad seg_window(const TileOperand &t, uint32_t s, uint32_t off,
+                                              uint32_t end, int lane) {
   SegLoad r;
-  const uint32_t off = t.seg_off[s], end = t.seg_off[s + 1];  // uniform: scalar loads
   r.n_chunks = (int)((end - off + kTileChunkBytes - 1) / kTileChunkBytes);
   // lanes past the segment's chunks re-read its first one (in bounds; unused)
   const uint32_t b = off + (lane < r.n_chunks ? (uint32_t)(kTileChunkBytes * lane) : 0u);
@@ -87,10 +88,13 @@ __device__ __forceinline__ SegLoad seg_load(const TileOperand &t, uint32_t s, in
   r.d2 = v.z;
   r.d3 = v.w;
   r.gapw = t.gaps[(size_t)s * kTileGapWords + (lane >> 3)];
-  const u32x4 o = __builtin_nontemporal_load(
-      reinterpret_cast<const u32x4 *>(t.other + (size_t)s * kTileOtherBytes + 16 * lane));
-  r.oth = make_uint4(o.x, o.y, o.z, o.w);
   return r;
+}
+
+// The lane's 32 sign/mantissa nibbles of segment s (read once: streamed).
+__device__ __forceinline__ u32x4 seg_other(const TileOperand &t, uint32_t s, int lane) {
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4 *>(t.other + (size_t)s * kTileOtherBytes + 16 * lane));
 }
 
 // Byte i (0..15) of the lane's chunk window, shifted into a table offset
@@ -110,8 +114,11 @@ __device__ __forceinline__ uint32_t byte_off(const SegLoad &c) {
 __device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t *s_dfa,
                                                 uint32_t *stage, int lane) {
   const uint32_t gap = (c.gapw >> (4 * (lane & 7))) & 0xFu;
-  const uint32_t a0 = gap < 8 ? ((gap << 10) | byte_off<0>(c))
-                              : (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
+  // start row: skip `gap` bits of byte 0, or (gap >= 8) take the entry that
+  // skips byte 0 into row gap - 8 (both computed, one selected)
+  const uint32_t a_in = (gap << 10) | byte_off<0>(c);
+  const uint32_t a_skip = (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
+  const uint32_t a0 = gap < 8 ? a_in : a_skip;
   const uint32_t e0 = dfa_at(s_dfa, a0);
   const uint32_t e1 = dfa_at(s_dfa, (e0 & kDfaRowMask) | byte_off<1>(c));
   const uint32_t e2 = dfa_at(s_dfa, (e1 & kDfaRowMask) | byte_off<2>(c));
@@ -135,9 +142,12 @@ __device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t
   }
   const uint32_t et = open ? ((e12 & 0xF0000u) | 4u) : 0u;
   const bool live = lane < c.n_chunks;
-  int cnt4 = (int)((e0 & 0xFFu) + (e1 & 0xFFu) + (e2 & 0xFFu) + (e3 & 0xFFu) + (e4 & 0xFFu) +
-                   (e5 & 0xFFu) + (e6 & 0xFFu) + (e7 & 0xFFu) + (e8 & 0xFFu) + (e9 & 0xFFu) +
-                   (e10 & 0xFFu) + (e11 & 0xFFu) + (et & 0xFFu));
+  // the count fields (bits 0..7, at most 16 each, bits 8..9 clear) summed
+  // by adding whole entries: 13 of them stay below 256, so the low byte of
+  // the sum is exact
+  const uint32_t s01 = e0 + e1, s23 = e2 + e3, s45 = e4 + e5, s67 = e6 + e7;
+  const uint32_t s89 = e8 + e9, sab = e10 + e11;
+  int cnt4 = (int)((s01 + s23 + s45 + s67 + s89 + sab + et) & 0xFFu);
   if (!live) cnt4 = 0;
   const int incl = wave_inclusive_scan(cnt4);
   // a start past the real symbols (garbage decoded from the bytes after the
@@ -151,7 +161,7 @@ __device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t
     atomicOr(q + 1, (uint32_t)(v >> 32));
     pos4 += n4;
   };
-  auto put2 = [&](uint32_t ea, uint32_t eb) {
+  auto put2 = [&](uint32_t ea, uint32_t eb, uint32_t sum) {
     uint32_t t, syms;
     asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
         "src1_sel:WORD_1"
@@ -159,15 +169,15 @@ __device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t
     asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
         "src1_sel:WORD_1"
         : "=v"(syms) : "v"(t), "v"(ea));
-    put(syms, (ea & 0xFFu) + (eb & 0xFFu));
+    put(syms, sum & 0xFFu);
   };
   if (live) {
-    put2(e0, e1);
-    put2(e2, e3);
-    put2(e4, e5);
-    put2(e6, e7);
-    put2(e8, e9);
-    put2(e10, e11);
+    put2(e0, e1, s01);
+    put2(e2, e3, s23);
+    put2(e4, e5, s45);
+    put2(e6, e7, s67);
+    put2(e8, e9, s89);
+    put2(e10, e11, sab);
     put(et >> 16, 0u);
   }
   // the wave's own ORs complete before its lanes read the staged symbols
@@ -197,15 +207,72 @@ __device__ __forceinline__ void panel_of(const TileSegs &segs, int panel, TileOp
   p = (n0 - start) / 16;
 }
 
+// Compiler barrier: memory operations keep their order across it, so loads
+// issue in the order their waits are counted in (vmcnt retires in order).
+__device__ __forceinline__ void issue_order() { asm volatile("" ::: "memory"); }
+
+// LDS-only workgroup barrier: outstanding global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One step of a wave's walk: panel blockIdx.x + j * gridDim.x (j = 0..),
+// group kg = wave + u * WAVES (u = 0..ng-1, the same ng for every wave; a
+// step past the last group or panel computes nothing and reads in-bounds
+// clamped addresses).  Wave-uniform.
+struct Step {
+  TileOperand op;
+  int p, col;   // panel index inside the operand, its first output column
+  int kg;       // group, 0 when past the last one
+  bool valid;   // a real panel and group: decoded and multiplied
+  bool closes;  // the last step of a real panel: its partial sums are parked
+};
+
+__device__ __forceinline__ Step step_at(const TileSegs &segs, int panel, int u, int wave,
+                                        int waves, int kgroups, int n_panels) {
+  Step st;
+  const int kg = wave + u * waves;
+  st.valid = panel < n_panels && kg < kgroups;
+  st.closes = panel < n_panels && (u + 1) * waves >= kgroups;
+  panel_of(segs, panel < n_panels ? panel : n_panels - 1, st.op, st.p, st.col);
+  st.kg = kg < kgroups ? kg : 0;
+  return st;
+}
+
+// The step's offsets and weight scale by one vector load: lane 0 the
+// segment's first byte, lane 1 its end, the other lanes its weight scale.
+__device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int lane) {
+  const uint32_t s = (uint32_t)st.p * (uint32_t)kgroups + (uint32_t)st.kg;
+  const uint32_t *a =
+      lane < 2 ? st.op.seg_off + s + lane
+               : reinterpret_cast<const uint32_t *>(st.op.ws) + (size_t)(st.p >> 3) * kgroups + st.kg;
+  return *a;
+}
+
+constexpr int kRedPanels = 4;  // panels whose partial sums wait for one reduction
+
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
+//
+// Each wave walks its steps (segments) as a software pipeline: while it
+// decodes step t it has step t+1's code window and nibbles and step t+2's
+// offsets in flight, with every load unconditional (clamped addresses) and
+// issued in a fixed order, so the waits before a decode never cover the
+// next step's loads.  The loop is unrolled by two so no in-flight register
+// is copied.  Partial sums of up to kRedPanels panels wait in LDS and are
+// reduced together, in wave order as the FP8 linear sums them, behind a
+// barrier that fences LDS only.
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
     const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, TileSegs segs,
     const uint32_t *__restrict__ table, uint16_t *__restrict__ out, int ldo, int n_panels) {
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) float s_part[kRedPanels][WAVES][256];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kgroups = K / kGroup;
   if ((int)blockIdx.x >= n_panels) return;  // uniform, before any barrier
 
@@ -213,39 +280,108 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
   uint32_t *const stage = s_stage[wave];
   for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
 
+  // the lane's A-operand row and the 4 output rows whose scales it applies;
+  // rows past M read row 0 and are zeroed before use
   const int r = lane & 15, g = lane >> 4;
   const bool row_ok = r < M;
-  const uint8_t *arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+  const uint8_t *const arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+  uint32_t srow[4];
   bool srow_ok[4];
-  const float *srow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     srow_ok[i] = 4 * g + i < M;
-    srow[i] = as + (size_t)(srow_ok[i] ? 4 * g + i : 0) * kgroups;
+    srow[i] = (uint32_t)(srow_ok[i] ? 4 * g + i : 0) * (uint32_t)kgroups;
   }
+  const int ng = (kgroups + WAVES - 1) / WAVES;
+  const int n_mine = (n_panels - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+  // an even number of steps (a trailing one past the last panel computes
+  // nothing), so the unrolled loop's back edge always follows a second step
+  const int n_steps = (n_mine * ng + 1) & ~1;
   __syncthreads();
 
-  for (int panel = blockIdx.x; panel < n_panels; panel += gridDim.x) {
-    TileOperand op;
-    int p, col;
-    panel_of(segs, panel, op, p, col);
-    const float *wsrow = op.ws + (size_t)(p * 16 / kGroup) * kgroups;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int kg = wave; kg < kgroups; kg += WAVES) {
-      const uint32_t s = (uint32_t)p * (uint32_t)kgroups + (uint32_t)kg;
-      const SegLoad c = seg_load(op, s, lane);
-      uint4 av0 = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
-      uint4 av1 = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
-      const float wsv = wsrow[kg];
-      float sav[4];
+  // cursors of steps t+1 and t+2 (panel, u)
+  int pan1 = blockIdx.x, u1 = 0, pan2 = blockIdx.x, u2 = 0;
+  auto advance = [&](int &pan, int &u) {
+    if (++u == ng) {
+      u = 0;
+      pan += gridDim.x;
+    }
+  };
+  // prologue: step 0's offsets and window, step 1's offsets
+  Step cur = step_at(segs, pan1, u1, wave, WAVES, kgroups, n_panels);
+  advance(pan1, u1);
+  advance(pan2, u2);
+  advance(pan2, u2);
+  const uint32_t m0 = step_meta(cur, kgroups, lane);
+  Step nx1 = step_at(segs, pan1, u1, wave, WAVES, kgroups, n_panels);
+  uint32_t mA = step_meta(nx1, kgroups, lane), mB = 0;
+  issue_order();
+  const uint32_t s_cur0 = (uint32_t)cur.p * (uint32_t)kgroups + (uint32_t)cur.kg;
+  SegLoad wA = seg_window(cur.op, s_cur0, __builtin_amdgcn_readlane(m0, 0),
+                          __builtin_amdgcn_readlane(m0, 1), lane);
+  u32x4 oA = seg_other(cur.op, s_cur0, lane);
+  float ws_cur = __int_as_float(__builtin_amdgcn_readlane(m0, 2));
+  SegLoad wB;
+  u32x4 oB;
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int pending = 0, first_pending = 0;  // panels waiting in s_part, ordinal of the first
+
+  auto reduce = [&]() {
+    lds_barrier();
+    // wave w sums accumulator i = w % 4 of panel j (wave-uniform: the panel's
+    // operand and columns come from scalar loads); unrolled, as a loop around
+    // the store would make the compiler drain the prefetched loads first
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sav[i] = srow[i][kg];
-      const uint4 ex = decode_segment(c, s_dfa, stage, lane);
+    for (int k = 0; k < (4 * kRedPanels + WAVES - 1) / WAVES; ++k) {
+      const int jw = wave + k * WAVES;
+      if (jw >= 4 * pending) break;
+      const int j = jw >> 2, i = jw & 3, l = lane;
+      float sum = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv) sum += s_part[j][wv][i * 64 + l];
+      TileOperand op;
+      int p, col;
+      panel_of(segs, (int)blockIdx.x + (first_pending + j) * (int)gridDim.x, op, p, col);
+      const int m = 4 * (l >> 4) + i;
+      if (m < M) out[(size_t)m * ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
+    }
+    lds_barrier();
+    first_pending += pending;
+    pending = 0;
+  };
+
+  // step t: compute `cur` from (w, o), load step t+1's window into (wn, on)
+  // from its offsets m_next, and step t+2's offsets into m_issue
+  auto step = [&](int t, SegLoad &w, u32x4 &o, SegLoad &wn, u32x4 &on, uint32_t &m_next,
+                  uint32_t &m_issue) {
+    // activations of this step (L2-resident), issued first
+    issue_order();
+    uint4 av0 = *reinterpret_cast<const uint4 *>(arow + cur.kg * kGroup);
+    uint4 av1 = *reinterpret_cast<const uint4 *>(arow + cur.kg * kGroup + 64);
+    float sav[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sav[i] = as[srow[i] + (uint32_t)cur.kg];
+    issue_order();
+    // step t+2's offsets and weight scale
+    const Step nx2 = step_at(segs, pan2, u2, wave, WAVES, kgroups, n_panels);
+    m_issue = step_meta(nx2, kgroups, lane);
+    issue_order();
+    // step t+1's window and nibbles
+    const uint32_t off1 = __builtin_amdgcn_readlane(m_next, 0);
+    const uint32_t end1 = __builtin_amdgcn_readlane(m_next, 1);
+    const float ws1 = __int_as_float(__builtin_amdgcn_readlane(m_next, 2));
+    const uint32_t s1 = (uint32_t)nx1.p * (uint32_t)kgroups + (uint32_t)nx1.kg;
+    wn = seg_window(nx1.op, s1, off1, end1, lane);
+    on = seg_other(nx1.op, s1, lane);
+    issue_order();
+    if (cur.valid) {
+      const uint4 ex = decode_segment(w, s_dfa, stage, lane);
       if (!row_ok) av0 = av1 = make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) sav[i] = srow_ok[i] ? sav[i] : 0.f;
-      const uint2 w0 = merge8(ex.x, c.oth.x), w1 = merge8(ex.y, c.oth.y);
-      const uint2 w2 = merge8(ex.z, c.oth.z), w3 = merge8(ex.w, c.oth.w);
+      const uint2 w0 = merge8(ex.x, o.x), w1 = merge8(ex.y, o.y);
+      const uint2 w2 = merge8(ex.z, o.z), w3 = merge8(ex.w, o.w);
       v4f d = {0.f, 0.f, 0.f, 0.f};
       d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
           (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
@@ -260,24 +396,26 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
           (long)(((uint64_t)av1.w << 32) | av1.z), (long)(((uint64_t)w3.y << 32) | w3.x), d, 0,
           0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * wsv, acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * ws_cur, acc[i]);
     }
-    // the waves' partial sums through their (now zero) staging areas, summed
-    // in wave order as the FP8 linear sums them
-    float *const red = reinterpret_cast<float *>(stage);
+    if (cur.closes) {  // the panel's last step: park its partial sums
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[i * 64 + lane] = acc[i];
-    __syncthreads();
-    if (threadIdx.x < 256) {
-      const int i = threadIdx.x >> 6, l = threadIdx.x & 63;
-      float sum = 0.f;
-#pragma unroll
-      for (int wv = 0; wv < WAVES; ++wv) sum += reinterpret_cast<const float *>(s_stage[wv])[i * 64 + l];
-      const int m = 4 * (l >> 4) + i;
-      if (m < M) out[(size_t)m * ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
+      for (int i = 0; i < 4; ++i) {
+        s_part[pending][wave][i * 64 + lane] = acc[i];
+        acc[i] = 0.f;
+      }
+      ++pending;
+      if (pending == kRedPanels || t + 2 >= n_steps) reduce();
     }
-    __syncthreads();
-    for (int i = lane; i < 4 * 64; i += 64) stage[i] = 0u;  // staging is zero again
+    cur = nx1;
+    ws_cur = ws1;
+    nx1 = nx2;
+    advance(pan2, u2);
+  };
+
+  for (int t = 0; t < n_steps; t += 2) {
+    step(t, wA, oA, wB, oB, mA, mB);
+    step(t + 1, wB, oB, wA, oA, mB, mA);
   }
 }
 
@@ -298,10 +436,11 @@ __global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
   const uint32_t kgroups = (uint32_t)K / kGroup;
   const int r = lane & 15, g = lane >> 4;
   for (uint32_t s = blockIdx.x * WAVES + wave; s < n_seg; s += gridDim.x * WAVES) {
-    const SegLoad c = seg_load(op, s, lane);
+    const SegLoad c = seg_window(op, s, op.seg_off[s], op.seg_off[s + 1], lane);
+    const u32x4 oth = seg_other(op, s, lane);
     const uint4 ex = decode_segment(c, s_dfa, stage, lane);
-    const uint2 w0 = merge8(ex.x, c.oth.x), w1 = merge8(ex.y, c.oth.y);
-    const uint2 w2 = merge8(ex.z, c.oth.z), w3 = merge8(ex.w, c.oth.w);
+    const uint2 w0 = merge8(ex.x, oth.x), w1 = merge8(ex.y, oth.y);
+    const uint2 w2 = merge8(ex.z, oth.z), w3 = merge8(ex.w, oth.w);
     const uint32_t p = s / kgroups, kg = s % kgroups;
     uint8_t *const row = out + (size_t)(p * 16 + r) * K + kg * kGroup + 16 * g;
     __builtin_nontemporal_store(u32x4{w0.x, w0.y, w1.x, w1.y}, reinterpret_cast<u32x4 *>(row));
