@@ -99,6 +99,28 @@ __device__ __forceinline__ void load_dfa_batched(uint32_t *s_dfa,
   }
 }
 
+// The table in two halves -- loads into registers, then LDS stores -- so a
+// kernel can issue other loads in between and overlap their round trips.
+template <int kThreads>
+struct DfaLoad {
+  static constexpr int kIters = (kDfaEntries + kThreads - 1) / kThreads;
+  uint32_t v[kIters];
+  __device__ __forceinline__ void load(const uint32_t *__restrict__ table, int tid) {
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+      const int i = tid + j * kThreads;
+      v[j] = i < kDfaEntries ? table[i] : 0u;
+    }
+  }
+  __device__ __forceinline__ void store(uint32_t *s_dfa, int tid) const {
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+      const int i = tid + j * kThreads;
+      if (i < kDfaEntries) s_dfa[i] = dfa_entry_in_range(v[j]);
+    }
+  }
+};
+
 }  // namespace dev
 }  // namespace ecf8
 

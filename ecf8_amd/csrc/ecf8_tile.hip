@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "ecf8.h"
 #include "ecf8_dev.h"
 #include "ecf8_layout.h"
@@ -253,21 +255,33 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 
 constexpr int kRedPanels = 4;  // panels whose partial sums wait for one reduction
 
+// Steps whose loads are in flight during a decode.  One suffices: a step's
+// decode outlasts the memory round trip, and on MI355X distances 2 and 3
+// measured slower (Qwen3-8B layer at M = 16: 81.0 us at 1, 90.2 at 2,
+// 89.3 at 3) -- more registers and code for no latency left to hide.
+#ifndef ECF8_TILE_PREFETCH
+#define ECF8_TILE_PREFETCH 1
+#endif
+constexpr int kPrefetch = ECF8_TILE_PREFETCH;
+static_assert(kPrefetch >= 1 && kPrefetch <= 3, "prefetch distance");
+
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
 //
 // Each wave walks its steps (segments) as a software pipeline: while it
-// decodes step t it has step t+1's code window and nibbles and step t+2's
-// offsets in flight, with every load unconditional (clamped addresses) and
-// issued in a fixed order, so the waits before a decode never cover the
-// next step's loads.  The loop is unrolled by two so no in-flight register
-// is copied.  Partial sums of up to kRedPanels panels wait in LDS and are
+// decodes step t, the code windows and nibbles of steps t+1..t+P (P =
+// kPrefetch) and the offsets of step t+P+1 are in flight -- every load
+// unconditional (clamped addresses) and issued in a fixed order, so the wait
+// before a decode never covers a later step's loads.  The loop is unrolled
+// by P+1 and the buffers rotate by name, so no in-flight register is
+// copied.  Partial sums of up to kRedPanels panels wait in LDS and are
 // reduced together, in wave order as the FP8 linear sums them, behind a
 // barrier that fences LDS only.
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
     const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, TileSegs segs,
     const uint32_t *__restrict__ table, uint16_t *__restrict__ out, int ldo, int n_panels) {
+  constexpr int P = kPrefetch, NB = kPrefetch + 1;
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
   __shared__ __attribute__((aligned(16))) float s_part[kRedPanels][WAVES][256];
@@ -275,10 +289,7 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kgroups = K / kGroup;
   if ((int)blockIdx.x >= n_panels) return;  // uniform, before any barrier
-
-  load_dfa_batched<WAVES * 64>(s_dfa, table, threadIdx.x);
   uint32_t *const stage = s_stage[wave];
-  for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
 
   // the lane's A-operand row and the 4 output rows whose scales it applies;
   // rows past M read row 0 and are zeroed before use
@@ -294,35 +305,50 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
   }
   const int ng = (kgroups + WAVES - 1) / WAVES;
   const int n_mine = (n_panels - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
-  // an even number of steps (a trailing one past the last panel computes
-  // nothing), so the unrolled loop's back edge always follows a second step
-  const int n_steps = (n_mine * ng + 1) & ~1;
-  __syncthreads();
+  const int n_real = n_mine * ng;
+  // a multiple of NB steps (trailing ones past the last panel compute
+  // nothing), so the unrolled loop's back edge always follows its last copy
+  const int n_steps = (n_real + NB - 1) / NB * NB;
 
-  // cursors of steps t+1 and t+2 (panel, u)
-  int pan1 = blockIdx.x, u1 = 0, pan2 = blockIdx.x, u2 = 0;
-  auto advance = [&](int &pan, int &u) {
+  // steps t .. t+P+1: sc[0] is the step being computed
+  Step sc[P + 2];
+  int pan = blockIdx.x, u = 0;  // cursor of the step after the last in sc
+  auto next_step = [&]() {
+    const Step st = step_at(segs, pan, u, wave, WAVES, kgroups, n_panels);
     if (++u == ng) {
       u = 0;
       pan += gridDim.x;
     }
+    return st;
   };
-  // prologue: step 0's offsets and window, step 1's offsets
-  Step cur = step_at(segs, pan1, u1, wave, WAVES, kgroups, n_panels);
-  advance(pan1, u1);
-  advance(pan2, u2);
-  advance(pan2, u2);
-  const uint32_t m0 = step_meta(cur, kgroups, lane);
-  Step nx1 = step_at(segs, pan1, u1, wave, WAVES, kgroups, n_panels);
-  uint32_t mA = step_meta(nx1, kgroups, lane), mB = 0;
+#pragma unroll
+  for (int i = 0; i < P + 1; ++i) sc[i] = next_step();
+
+  // prologue: offsets of steps 0..P, the automaton table, then the windows
+  // and nibbles of steps 0..P-1 -- issued in that order so their round trips
+  // overlap
+  uint32_t m[NB];
+  SegLoad w[NB];
+  u32x4 o[NB];
+  float wsv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) m[i] = step_meta(sc[i], kgroups, lane);
   issue_order();
-  const uint32_t s_cur0 = (uint32_t)cur.p * (uint32_t)kgroups + (uint32_t)cur.kg;
-  SegLoad wA = seg_window(cur.op, s_cur0, __builtin_amdgcn_readlane(m0, 0),
-                          __builtin_amdgcn_readlane(m0, 1), lane);
-  u32x4 oA = seg_other(cur.op, s_cur0, lane);
-  float ws_cur = __int_as_float(__builtin_amdgcn_readlane(m0, 2));
-  SegLoad wB;
-  u32x4 oB;
+  DfaLoad<WAVES * 64> dfa;
+  dfa.load(table, threadIdx.x);
+  issue_order();
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const uint32_t si = (uint32_t)sc[i].p * (uint32_t)kgroups + (uint32_t)sc[i].kg;
+    w[i] = seg_window(sc[i].op, si, __builtin_amdgcn_readlane(m[i], 0),
+                      __builtin_amdgcn_readlane(m[i], 1), lane);
+    o[i] = seg_other(sc[i].op, si, lane);
+    wsv[i] = __int_as_float(__builtin_amdgcn_readlane(m[i], 2));
+  }
+  issue_order();
+  dfa.store(s_dfa, threadIdx.x);
+  for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
+  lds_barrier();
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   int pending = 0, first_pending = 0;  // panels waiting in s_part, ordinal of the first
@@ -343,45 +369,47 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
       TileOperand op;
       int p, col;
       panel_of(segs, (int)blockIdx.x + (first_pending + j) * (int)gridDim.x, op, p, col);
-      const int m = 4 * (l >> 4) + i;
-      if (m < M) out[(size_t)m * ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
+      const int mm = 4 * (l >> 4) + i;
+      if (mm < M) out[(size_t)mm * ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
     }
     lds_barrier();
     first_pending += pending;
     pending = 0;
   };
 
-  // step t: compute `cur` from (w, o), load step t+1's window into (wn, on)
-  // from its offsets m_next, and step t+2's offsets into m_issue
-  auto step = [&](int t, SegLoad &w, u32x4 &o, SegLoad &wn, u32x4 &on, uint32_t &m_next,
-                  uint32_t &m_issue) {
+  // step t, the k-th copy in the unrolled loop (k = t mod NB): compute from
+  // buffer k, load step t+P's window into buffer (k+P) mod NB from its
+  // offsets m[(k+P) mod NB], and step t+P+1's offsets into m[(k+P+1) mod NB]
+  auto step = [&](int t, auto kc) {
+    constexpr int k = decltype(kc)::value;
+    constexpr int kl = (k + P) % NB, km = (k + P + 1) % NB;
     // activations of this step (L2-resident), issued first
     issue_order();
-    uint4 av0 = *reinterpret_cast<const uint4 *>(arow + cur.kg * kGroup);
-    uint4 av1 = *reinterpret_cast<const uint4 *>(arow + cur.kg * kGroup + 64);
+    uint4 av0 = *reinterpret_cast<const uint4 *>(arow + sc[0].kg * kGroup);
+    uint4 av1 = *reinterpret_cast<const uint4 *>(arow + sc[0].kg * kGroup + 64);
     float sav[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sav[i] = as[srow[i] + (uint32_t)cur.kg];
+    for (int i = 0; i < 4; ++i) sav[i] = as[srow[i] + (uint32_t)sc[0].kg];
     issue_order();
-    // step t+2's offsets and weight scale
-    const Step nx2 = step_at(segs, pan2, u2, wave, WAVES, kgroups, n_panels);
-    m_issue = step_meta(nx2, kgroups, lane);
+    sc[P + 1] = next_step();
+    m[km] = step_meta(sc[P + 1], kgroups, lane);
     issue_order();
-    // step t+1's window and nibbles
-    const uint32_t off1 = __builtin_amdgcn_readlane(m_next, 0);
-    const uint32_t end1 = __builtin_amdgcn_readlane(m_next, 1);
-    const float ws1 = __int_as_float(__builtin_amdgcn_readlane(m_next, 2));
-    const uint32_t s1 = (uint32_t)nx1.p * (uint32_t)kgroups + (uint32_t)nx1.kg;
-    wn = seg_window(nx1.op, s1, off1, end1, lane);
-    on = seg_other(nx1.op, s1, lane);
+    {
+      const Step &sl = sc[P];
+      const uint32_t sl_s = (uint32_t)sl.p * (uint32_t)kgroups + (uint32_t)sl.kg;
+      w[kl] = seg_window(sl.op, sl_s, __builtin_amdgcn_readlane(m[kl], 0),
+                         __builtin_amdgcn_readlane(m[kl], 1), lane);
+      o[kl] = seg_other(sl.op, sl_s, lane);
+      wsv[kl] = __int_as_float(__builtin_amdgcn_readlane(m[kl], 2));
+    }
     issue_order();
-    if (cur.valid) {
-      const uint4 ex = decode_segment(w, s_dfa, stage, lane);
+    if (sc[0].valid) {
+      const uint4 ex = decode_segment(w[k], s_dfa, stage, lane);
       if (!row_ok) av0 = av1 = make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) sav[i] = srow_ok[i] ? sav[i] : 0.f;
-      const uint2 w0 = merge8(ex.x, o.x), w1 = merge8(ex.y, o.y);
-      const uint2 w2 = merge8(ex.z, o.z), w3 = merge8(ex.w, o.w);
+      const uint2 w0 = merge8(ex.x, o[k].x), w1 = merge8(ex.y, o[k].y);
+      const uint2 w2 = merge8(ex.z, o[k].z), w3 = merge8(ex.w, o[k].w);
       v4f d = {0.f, 0.f, 0.f, 0.f};
       d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
           (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
@@ -396,26 +424,26 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
           (long)(((uint64_t)av1.w << 32) | av1.z), (long)(((uint64_t)w3.y << 32) | w3.x), d, 0,
           0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * ws_cur, acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * wsv[k], acc[i]);
     }
-    if (cur.closes) {  // the panel's last step: park its partial sums
+    if (sc[0].closes) {  // the panel's last step: park its partial sums
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         s_part[pending][wave][i * 64 + lane] = acc[i];
         acc[i] = 0.f;
       }
       ++pending;
-      if (pending == kRedPanels || t + 2 >= n_steps) reduce();
+      if (pending == kRedPanels || t == n_real - 1) reduce();
     }
-    cur = nx1;
-    ws_cur = ws1;
-    nx1 = nx2;
-    advance(pan2, u2);
+#pragma unroll
+    for (int i = 0; i < P + 1; ++i) sc[i] = sc[i + 1];
   };
 
-  for (int t = 0; t < n_steps; t += 2) {
-    step(t, wA, oA, wB, oB, mA, mB);
-    step(t + 1, wB, oB, wA, oA, mB, mA);
+  for (int t = 0; t < n_steps; t += NB) {
+    step(t, std::integral_constant<int, 0>{});
+    if constexpr (NB > 1) step(t + 1, std::integral_constant<int, 1 % NB>{});
+    if constexpr (NB > 2) step(t + 2, std::integral_constant<int, 2 % NB>{});
+    if constexpr (NB > 3) step(t + 3, std::integral_constant<int, 3 % NB>{});
   }
 }
 
