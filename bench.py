@@ -368,7 +368,8 @@ def e2e_generate(args):
                 "peak_mib": round(r["peak_mib"], 1), "weights_mib": round(r["weights_mib"], 1)}
 
     line = {
-        "metric": "e2e tokens/s, Qwen3-8B-shape bs16 (ECF8-compressed, per-layer decode before the FP8 GEMMs)",
+        "metric": "e2e tokens/s, Qwen3-8B-shape bs16 (ECF8-compressed layers, fastest decode "
+                  "mode; config.ecf8_decode names it)",
         "value": round(ecf8["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -402,15 +403,19 @@ def moe_generate(args):
     embedding and lm_head), batch 16, random prompts of 128 tokens, greedy
     decoding of --new-tokens (default 512) tokens: first with the FP8
     weights resident, then with every attention block and expert
-    ECF8-compressed.  The attention block is decoded by its forward-pre-hook.
-    Per decode step, only the experts the router picked are decoded, in one
-    batched launch per layer, selected on the device.  Both runs use the same
-    engine (eager prefill, one HIP graph replay per decode step) and must
-    produce identical tokens."""
+    ECF8-compressed -- decoded by the attention block's forward-pre-hook and,
+    per decode step, only the experts the router picked in one batched
+    launch per layer (selected on the device), with the next layer's
+    attention block on a side stream, and finally re-tiled (ECF8-T), the
+    decode step's attention and grouped expert linears decoding their
+    weight operands themselves.  Every run uses the same engine (eager
+    prefill, one HIP graph replay per decode step) and must produce
+    identical tokens."""
     import torch
 
     from ecf8_amd.llm import timed_generate
-    from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, random_moe_model
+    from ecf8_amd.moe import (Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers,
+                              random_moe_model, retile_moe_layers)
     from ecf8_amd.prefetch import LayerPrefetcher
     from dfloat.run.run import TensorManager
 
@@ -424,7 +429,8 @@ def moe_generate(args):
     g = torch.Generator().manual_seed(args.seed + 7)
     prompt = torch.randint(0, cfg.vocab, (B, T), generator=g)
     results = {}
-    for mode in ("fp8", "ecf8", "ecf8_prefetch"):
+    prefetcher = None
+    for mode in ("fp8", "ecf8", "ecf8_prefetch", "ecf8_fused"):
         if mode == "ecf8":
             t0 = time.time()
             compress_moe_layers(model, drawn)
@@ -433,8 +439,18 @@ def moe_generate(args):
                   flush=True)
         if mode == "ecf8_prefetch":
             # the next layer's attention block decoded on a side stream
-            LayerPrefetcher([layer.self_attn for layer in model.model.layers], dev,
-                            workgroups_per_cu=args.prefetch_workgroups).install()
+            prefetcher = LayerPrefetcher([layer.self_attn for layer in model.model.layers], dev,
+                                         workgroups_per_cu=args.prefetch_workgroups).install()
+        if mode == "ecf8_fused":
+            prefetcher.uninstall()
+            prefetcher = None
+            TensorManager.clear_device()
+            torch.cuda.empty_cache()
+            t0 = time.time()
+            retile_moe_layers(model, drawn)
+            torch.cuda.synchronize()
+            print(f"[bench] blocks re-tiled in {time.time() - t0:.1f}s", file=sys.stderr,
+                  flush=True)
         TensorManager.clear_device()
         torch.cuda.empty_cache()
         t0 = time.time()
@@ -450,12 +466,15 @@ def moe_generate(args):
               f"peak {r['peak_mib']:.0f} MiB", file=sys.stderr, flush=True)
         r["weights_mib"] = sum(t.numel() * t.element_size() for t in
                                list(model.parameters()) + list(model.buffers())) / 2**20
+        if mode == "ecf8_fused":
+            r["weights_mib"] += sum(op.nbytes() for mod in model.modules()
+                                    for op in getattr(mod, "_ecf8_tiles", {}).values()) / 2**20
         results[mode] = r
         del runner
-    same = all(torch.equal(results["fp8"]["tokens"], results[m]["tokens"])
-               for m in ("ecf8", "ecf8_prefetch"))
+    ecf8_modes = ("ecf8", "ecf8_prefetch", "ecf8_fused")
+    same = all(torch.equal(results["fp8"]["tokens"], results[m]["tokens"]) for m in ecf8_modes)
     fp8 = results["fp8"]
-    best = max(("ecf8", "ecf8_prefetch"), key=lambda m: results[m]["tokens_per_s"])
+    best = max(ecf8_modes, key=lambda m: results[m]["tokens_per_s"])
     ecf8 = results[best]
 
     def summary(r):
@@ -464,7 +483,7 @@ def moe_generate(args):
 
     line = {
         "metric": "e2e tokens/s, Qwen3-30B-A3B-shape MoE bs16 (ECF8 attention blocks and "
-                  "experts; routed experts decoded in one batched launch per layer)",
+                  "experts, fastest decode mode; config.ecf8_decode names it)",
         "value": round(ecf8["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -477,13 +496,18 @@ def moe_generate(args):
                    "top_k": cfg.top_k, "moe_intermediate": cfg.moe_intermediate,
                    "vocab": cfg.vocab, "batch": B, "prompt_len": T, "new_tokens": new,
                    "distinct_layer_weights": args.distinct_layers, "decoding": "greedy",
-                   "ecf8_decode": "attention block in its hook; routed experts per step "
-                                  "(device-side selection, one batched launch per layer)"},
+                   "ecf8_decode": {
+                       "ecf8": "attention block in its hook; routed experts per step "
+                               "(device-side selection, one batched launch per layer)",
+                       "ecf8_prefetch": "next layer's attention block on a side stream; routed "
+                                        "experts per step (one batched launch per layer)",
+                       "ecf8_fused": "blocks re-tiled at load (ECF8-T); decode-step attention "
+                                     "and routed-expert linears decode their weight operands "
+                                     "into the MFMAs"}[best]},
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
         "ecf8_mode": best,
-        "ecf8_attention_in_hook": summary(results["ecf8"]),
-        "ecf8_attention_prefetched": summary(results["ecf8_prefetch"]),
+        "ecf8_modes": {m: summary(results[m]) for m in ecf8_modes},
         "experts_routed_last_step": ecf8["experts_routed_last_step"],
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,

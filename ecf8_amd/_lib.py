@@ -57,6 +57,9 @@ _SIGNATURES = {
     "ecf8_tile_encode": ([_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32], _i32),
     "ecf8_tile_linear": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _vp, _i64, _i32, _vp], _i32),
     "ecf8_tile_decode": ([_vp, _i64, _vp, _vp, _vp], _i32),
+    "ecf8_tile_moe_linear": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64,
+                              _vp, _i64, _i32, _vp], _i32),
+    "ecf8_tile_decode_batch": ([_vp, _vp, _vp, _i32, _i64, _i64, _vp], _i32),
     # include/ecf8_llm.h: the consumer kernels
     "ecf8_fp8_linear": ([_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp], _i32),
     "ecf8_rmsnorm": ([_vp, _vp, _vp, _f32, _i64, _i64, _vp, _vp, _vp, _vp], _i32),

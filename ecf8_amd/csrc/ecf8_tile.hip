@@ -209,6 +209,64 @@ __device__ __forceinline__ void panel_of(const TileSegs &segs, int panel, TileOp
   p = (n0 - start) / 16;
 }
 
+// The panels of a dense linear's workgroup walk: its fused operands.
+struct DenseWalk {
+  const TileSegs *segs;  // the kernel argument itself: indexed in place, never copied
+  __device__ __forceinline__ void at(int panel, TileOperand &op, int &p, int &col) const {
+    panel_of(*segs, panel, op, p, col);
+  }
+};
+
+// A value known to be wave-uniform, moved to scalar registers.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// A global-memory pointer known to be wave-uniform: scalar registers, and
+// the global address space restated so its loads stay global (not flat)
+// loads, which would share the wait counter of the LDS lookups.
+template <class T>
+__device__ __forceinline__ const T *uniform(const T *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  typedef const __attribute__((address_space(1))) T GlobalT;
+  return (const T *)(GlobalT *)(((uint64_t)hi << 32) | lo);
+}
+
+// The panels of one expert of a grouped linear: its n_segs (<= 3) operands
+// of seg_n columns each (e.g. gate, up), operand k at output column
+// k seg_n.  The operands are read once, into scalar registers.
+struct ExpertWalk {
+  TileOperand op[ECF8_LINEAR_MAX_SEGS];
+  int tiles_per_seg, seg_n, n_segs;
+  __device__ __forceinline__ void load(const ecf8_tile_operand *ops, int n, int sn) {
+    static_assert(ECF8_LINEAR_MAX_SEGS == 3, "three operands per expert");
+    n_segs = n;
+    seg_n = sn;
+    tiles_per_seg = sn / 16;
+#pragma unroll
+    for (int k = 0; k < ECF8_LINEAR_MAX_SEGS; ++k) {
+      const ecf8_tile_operand &t = ops[k < n ? k : 0];
+      op[k] = TileOperand{uniform(static_cast<const uint8_t *>(t.stream)), uniform(t.seg_off),
+                          uniform(t.gaps), uniform(static_cast<const uint8_t *>(t.other)),
+                          uniform(t.weight_scale)};
+    }
+  }
+  template <class T>
+  static __device__ __forceinline__ T pick(bool c, T x, T y) {  // by value: a select, not an address
+    return c ? x : y;
+  }
+  __device__ __forceinline__ void at(int panel, TileOperand &o, int &p, int &col) const {
+    const bool k1 = panel >= tiles_per_seg, k2 = n_segs > 2 && panel >= 2 * tiles_per_seg;
+    o.stream = pick(k2, op[2].stream, pick(k1, op[1].stream, op[0].stream));
+    o.seg_off = pick(k2, op[2].seg_off, pick(k1, op[1].seg_off, op[0].seg_off));
+    o.gaps = pick(k2, op[2].gaps, pick(k1, op[1].gaps, op[0].gaps));
+    o.other = pick(k2, op[2].other, pick(k1, op[1].other, op[0].other));
+    o.ws = pick(k2, op[2].ws, pick(k1, op[1].ws, op[0].ws));
+    const int k = (k1 ? 1 : 0) + (k2 ? 1 : 0);
+    p = panel - k * tiles_per_seg;
+    col = k * seg_n;
+  }
+};
+
 // Compiler barrier: memory operations keep their order across it, so loads
 // issue in the order their waits are counted in (vmcnt retires in order).
 __device__ __forceinline__ void issue_order() { asm volatile("" ::: "memory"); }
@@ -232,13 +290,14 @@ struct Step {
   bool closes;  // the last step of a real panel: its partial sums are parked
 };
 
-__device__ __forceinline__ Step step_at(const TileSegs &segs, int panel, int u, int wave,
+template <class Walk>
+__device__ __forceinline__ Step step_at(const Walk &walk, int panel, int u, int wave,
                                         int waves, int kgroups, int n_panels) {
   Step st;
   const int kg = wave + u * waves;
   st.valid = panel < n_panels && kg < kgroups;
   st.closes = panel < n_panels && (u + 1) * waves >= kgroups;
-  panel_of(segs, panel < n_panels ? panel : n_panels - 1, st.op, st.p, st.col);
+  walk.at(panel < n_panels ? panel : n_panels - 1, st.op, st.p, st.col);
   st.kg = kg < kgroups ? kg : 0;
   return st;
 }
@@ -277,31 +336,84 @@ static_assert(kPrefetch >= 1 && kPrefetch <= 3, "prefetch distance");
 // copied.  Partial sums of up to kRedPanels panels wait in LDS and are
 // reduced together, in wave order as the FP8 linear sums them, behind a
 // barrier that fences LDS only.
-template <int WAVES>
+// Arguments of the dense linear (one fused set of operands, rows 0..M-1)
+// and of the grouped expert linear (workgroup (split, slot) takes expert
+// active[slot], its rows offsets[e].. of the sorted pairs, gathered from
+// aq rows row_of[q] when row_of is set).
+struct TileDenseArgs {
+  const uint8_t *aq;
+  const float *as;
+  int M, K;
+  TileSegs segs;
+  const uint32_t *table;
+  uint16_t *out;
+  int ldo, n_panels;
+};
+
+struct TileMoeArgs {
+  const uint8_t *aq;
+  const float *as;
+  const int *row_of;
+  const int *offsets;
+  const int *active;
+  const int *n_active;
+  const ecf8_tile_operand *ops;   // [E * n_segs]
+  const uint32_t *const *tables;  // [E]
+  uint16_t *out;
+  int K, ldo, n_segs, seg_n;
+};
+
+template <int WAVES, bool kMoe>
 __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
-    const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, TileSegs segs,
-    const uint32_t *__restrict__ table, uint16_t *__restrict__ out, int ldo, int n_panels) {
+    typename std::conditional<kMoe, TileMoeArgs, TileDenseArgs>::type a) {
   constexpr int P = kPrefetch, NB = kPrefetch + 1;
+  using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
   __shared__ __attribute__((aligned(16))) float s_part[kRedPanels][WAVES][256];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kgroups = K / kGroup;
-  if ((int)blockIdx.x >= n_panels) return;  // uniform, before any barrier
+  const int K = a.K, kgroups = K / kGroup;
+  // the workgroup's rows, operands and table (uniform)
+  int M, row0 = 0, n_panels;
+  const uint32_t *table;
+  Walk walk;
+  if constexpr (kMoe) {
+    const int slot = blockIdx.y;
+    if (slot >= uniform(a.n_active[0])) return;  // uniform, before any barrier
+    const int e = uniform(a.active[slot]);
+    row0 = uniform(a.offsets[e]);
+    // an expert holds at most one pair per routed token: <= 16 rows
+    M = min(uniform(a.offsets[e + 1]) - row0, 16);
+    table = uniform(a.tables[e]);
+    walk.load(a.ops + (size_t)e * a.n_segs, a.n_segs, a.seg_n);
+    n_panels = a.n_segs * (a.seg_n / 16);
+  } else {
+    M = a.M;
+    table = a.table;
+    walk = DenseWalk{&a.segs};
+    n_panels = a.n_panels;
+  }
+  if (M <= 0 || (int)blockIdx.x >= n_panels) return;  // uniform, before any barrier
   uint32_t *const stage = s_stage[wave];
+  const float *const as = a.as;
 
   // the lane's A-operand row and the 4 output rows whose scales it applies;
-  // rows past M read row 0 and are zeroed before use
+  // rows past M read the first row and are zeroed before use
+  auto a_row = [&](int rr) -> uint32_t {
+    const int q = row0 + (rr < M ? rr : 0);
+    if constexpr (kMoe) return (uint32_t)(a.row_of ? a.row_of[q] : q);
+    return (uint32_t)q;
+  };
   const int r = lane & 15, g = lane >> 4;
   const bool row_ok = r < M;
-  const uint8_t *const arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+  const uint8_t *const arow = a.aq + (size_t)a_row(r) * K + 16 * g;
   uint32_t srow[4];
   bool srow_ok[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     srow_ok[i] = 4 * g + i < M;
-    srow[i] = (uint32_t)(srow_ok[i] ? 4 * g + i : 0) * (uint32_t)kgroups;
+    srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
   }
   const int ng = (kgroups + WAVES - 1) / WAVES;
   const int n_mine = (n_panels - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
@@ -314,7 +426,7 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
   Step sc[P + 2];
   int pan = blockIdx.x, u = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
-    const Step st = step_at(segs, pan, u, wave, WAVES, kgroups, n_panels);
+    const Step st = step_at(walk, pan, u, wave, WAVES, kgroups, n_panels);
     if (++u == ng) {
       u = 0;
       pan += gridDim.x;
@@ -368,9 +480,10 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
       for (int wv = 0; wv < WAVES; ++wv) sum += s_part[j][wv][i * 64 + l];
       TileOperand op;
       int p, col;
-      panel_of(segs, (int)blockIdx.x + (first_pending + j) * (int)gridDim.x, op, p, col);
+      walk.at((int)blockIdx.x + (first_pending + j) * (int)gridDim.x, op, p, col);
       const int mm = 4 * (l >> 4) + i;
-      if (mm < M) out[(size_t)mm * ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
+      if (mm < M)
+        a.out[(size_t)(row0 + mm) * a.ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
     }
     lds_barrier();
     first_pending += pending;
@@ -447,16 +560,43 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
   }
 }
 
-// Row-major FP8 bytes of one tiled operand W[n, K]: every wave decodes
+// Row-major FP8 bytes of tiled operands W[n, K]: every wave decodes
 // segments wave_id, + total waves, ... and stores each lane's two 16-byte
-// runs.
-template <int WAVES>
+// runs.  One operand (kBatch false), or operand blockIdx.y of a device
+// array of same-shape operands, each with its own table and output.
+struct TileDecodeArgs {
+  TileOperand op;
+  const uint32_t *table;
+  uint8_t *out;
+};
+
+struct TileDecodeBatchArgs {
+  const ecf8_tile_operand *ops;
+  const uint32_t *const *tables;
+  uint8_t *const *outs;
+};
+
+template <int WAVES, bool kBatch>
 __global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
-    TileOperand op, const uint32_t *__restrict__ table, uint8_t *__restrict__ out, int K,
+    typename std::conditional<kBatch, TileDecodeBatchArgs, TileDecodeArgs>::type a, int K,
     uint32_t n_seg) {
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  TileOperand op;
+  const uint32_t *table;
+  uint8_t *out;
+  if constexpr (kBatch) {
+    const ecf8_tile_operand &t = a.ops[blockIdx.y];
+    op = TileOperand{static_cast<const uint8_t *>(t.stream), t.seg_off, t.gaps,
+                     static_cast<const uint8_t *>(t.other), t.weight_scale};
+    table = a.tables[blockIdx.y];
+    out = a.outs[blockIdx.y];
+  } else {
+    op = a.op;
+    table = a.table;
+    out = a.out;
+  }
   load_dfa_batched<WAVES * 64>(s_dfa, table, threadIdx.x);
   uint32_t *const stage = s_stage[wave];
   for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
@@ -480,15 +620,24 @@ __global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
 inline hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Workgroups of `kernel` resident on the device at once.
 template <class Kernel>
-int resident_grid(Kernel kernel, int threads, int64_t work, int *grid) {
+int resident_slots(Kernel kernel, int threads, int64_t *slots) {
   int dev = 0, cus = 0, occ = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(kernel),
                                                     threads, 0) != hipSuccess)
     return ECF8_ERR_HIP;
-  const int64_t g = (int64_t)cus * (occ > 0 ? occ : 1);
+  *slots = (int64_t)cus * (occ > 0 ? occ : 1);
+  return ECF8_OK;
+}
+
+template <class Kernel>
+int resident_grid(Kernel kernel, int threads, int64_t work, int *grid) {
+  int64_t g = 0;
+  const int rc = resident_slots(kernel, threads, &g);
+  if (rc != ECF8_OK) return rc;
   *grid = (int)(g < work ? g : work);
   return ECF8_OK;
 }
@@ -533,19 +682,57 @@ extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int6
   const int n_panels = (int)(n_total / 16);
   const auto *a = static_cast<const uint8_t *>(aq);
   auto *o = static_cast<uint16_t *>(out);
+  const TileDenseArgs args{a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels};
   int grid = 0, rc;
   if (waves == 16) {
-    rc = resident_grid(tile_linear16_kernel<16>, 1024, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<16, false>, 1024, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<16><<<(unsigned)grid, 1024, 0, as_stream(stream)>>>(
-        a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels);
+    tile_linear16_kernel<16, false><<<(unsigned)grid, 1024, 0, as_stream(stream)>>>(args);
   } else {
-    rc = resident_grid(tile_linear16_kernel<8>, 512, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<8, false>, 512, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<8><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(
-        a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels);
+    tile_linear16_kernel<8, false><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(args);
   }
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
+extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *row_of,
+                                    const int *offsets, const int *active, const int *n_active,
+                                    int n_experts, const ecf8_tile_operand *ops,
+                                    const uint32_t *const *tables, int n_segs, int64_t seg_n,
+                                    int64_t K, int64_t M, void *out, int64_t ldo, int splits,
+                                    void *stream) {
+  if (!aq || !as || !offsets || !active || !n_active || !ops || !tables || !out ||
+      n_experts <= 0 || n_segs < 1 || n_segs > ECF8_LINEAR_MAX_SEGS || seg_n <= 0 || K <= 0 ||
+      M <= 0 || splits < 0)
+    return ECF8_ERR_INVALID_ARG;
+  if (M > 16 || seg_n % kGroup || K % kGroup || K > (1 << 20) || n_segs * seg_n > (1 << 20) ||
+      n_experts > 65535)
+    return ECF8_ERR_UNSUPPORTED;
+  if (ldo < n_segs * seg_n) return ECF8_ERR_CAPACITY;
+  if (!aligned(aq, 16) || !aligned(as, 4) || !aligned(out, 4) || !aligned(ops, 8) ||
+      !aligned(tables, 8))
+    return ECF8_ERR_MISALIGNED;
+  const TileMoeArgs args{static_cast<const uint8_t *>(aq), as, row_of, offsets, active, n_active,
+                         ops, tables, static_cast<uint16_t *>(out), (int)K, (int)ldo, n_segs,
+                         (int)seg_n};
+  const int64_t n_tiles = n_segs * seg_n / 16;
+  // the FP8 grouped linear's wave count for this K (it sums in that order)
+  const bool eight = K / kGroup > 8;
+  auto launch = [&](auto kernel, int threads) {
+    int64_t g = splits;
+    if (g == 0) {  // about 1.4 workgroups per slot for the experts' share
+      int64_t slots = 0;
+      const int rc = resident_slots(kernel, threads, &slots);
+      if (rc != ECF8_OK) return rc;
+      g = (slots * 10 + 7 * n_experts - 1) / (7 * n_experts);
+    }
+    g = g < 1 ? 1 : g > n_tiles ? n_tiles : g;
+    kernel<<<dim3((unsigned)g, (unsigned)n_experts), threads, 0, as_stream(stream)>>>(args);
+    return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+  };
+  return eight ? launch(tile_linear16_kernel<8, true>, 512)
+               : launch(tile_linear16_kernel<4, true>, 256);
 }
 
 extern "C" int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *table,
@@ -558,12 +745,35 @@ extern "C" int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const ui
   if ((int64_t)op->n * K >= ((int64_t)1 << 40)) return ECF8_ERR_UNSUPPORTED;
   const int64_t n_seg = (int64_t)(op->n / 16) * (K / kGroup);
   if (n_seg > (int64_t)UINT32_MAX / 2) return ECF8_ERR_UNSUPPORTED;
-  const TileOperand t{static_cast<const uint8_t *>(op->stream), op->seg_off, op->gaps,
-                      static_cast<const uint8_t *>(op->other), op->weight_scale};
+  const TileDecodeArgs args{
+      TileOperand{static_cast<const uint8_t *>(op->stream), op->seg_off, op->gaps,
+                  static_cast<const uint8_t *>(op->other), op->weight_scale},
+      table, static_cast<uint8_t *>(out)};
   int grid = 0;
-  const int rc = resident_grid(tile_decode_kernel<8>, 512, (n_seg + 7) / 8, &grid);
+  const int rc = resident_grid(tile_decode_kernel<8, false>, 512, (n_seg + 7) / 8, &grid);
   if (rc != ECF8_OK) return rc;
-  tile_decode_kernel<8><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(
-      t, table, static_cast<uint8_t *>(out), (int)K, (uint32_t)n_seg);
+  tile_decode_kernel<8, false><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(args, (int)K,
+                                                                             (uint32_t)n_seg);
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
+extern "C" int ecf8_tile_decode_batch(const ecf8_tile_operand *ops, const uint32_t *const *tables,
+                                      void *const *outs, int n_ops, int64_t n, int64_t K,
+                                      void *stream) {
+  if (!ops || !tables || !outs || n_ops <= 0 || n <= 0 || K <= 0) return ECF8_ERR_INVALID_ARG;
+  if (n % 16 || K % kGroup || n_ops > 65535) return ECF8_ERR_UNSUPPORTED;
+  if (!aligned(ops, 8) || !aligned(tables, 8) || !aligned(outs, 8)) return ECF8_ERR_MISALIGNED;
+  if (n * K >= ((int64_t)1 << 40)) return ECF8_ERR_UNSUPPORTED;
+  const int64_t n_seg = (n / 16) * (K / kGroup);
+  if (n_seg > (int64_t)UINT32_MAX / 2) return ECF8_ERR_UNSUPPORTED;
+  const TileDecodeBatchArgs args{ops, tables, reinterpret_cast<uint8_t *const *>(outs)};
+  int64_t slots = 0;
+  const int rc = resident_slots(tile_decode_kernel<8, true>, 512, &slots);
+  if (rc != ECF8_OK) return rc;
+  // about two workgroups per resident slot over all operands
+  int64_t g = (2 * slots + n_ops - 1) / n_ops, need = (n_seg + 7) / 8;
+  g = g < 1 ? 1 : g > need ? need : g;
+  tile_decode_kernel<8, true><<<dim3((unsigned)g, (unsigned)n_ops), 512, 0, as_stream(stream)>>>(
+      args, (int)K, (uint32_t)n_seg);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }

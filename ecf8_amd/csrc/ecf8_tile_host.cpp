@@ -89,9 +89,9 @@ extern "C" int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *cod
   const uint8_t *len_row = luts + 256 * (n_luts - 1);
   memset(code_bits, 0, 16);
   memset(code_vals, 0, 16 * sizeof(uint32_t));
-  // each symbol's code is the first 16-bit window (in increasing order)
-  // that the reference rule (dfloat/run/decode.cu:85-91) decodes to it
-  bool seen[16] = {false};
+  // the symbol every 16-bit window decodes to under the reference rule
+  // (dfloat/run/decode.cu:85-91)
+  std::vector<uint8_t> sym(65536);
   for (uint32_t w = 0; w < 65536; ++w) {
     int v = luts[w >> 8];
     if (v >= 240) {
@@ -102,21 +102,27 @@ extern "C" int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *cod
     if (v > 15) return ECF8_ERR_FORMAT;
     const int len = len_row[v];
     if (len < 1 || len > 16) return ECF8_ERR_FORMAT;
-    if (!seen[v]) {
-      seen[v] = true;
-      code_bits[v] = (uint8_t)len;
-      code_vals[v] = w >> (16 - len);
-    }
+    sym[w] = (uint8_t)v;
   }
-  // a prefix code: every window starting with a symbol's code decodes to it
+  // A symbol's code of length L: the first aligned block of 2^(16-L)
+  // windows that all decode to it.  The rule decodes every window of such a
+  // block to the symbol and consumes L bits, so the block encodes the
+  // symbol whether or not it is the compressor's own code -- an incomplete
+  // code (Kraft sum below 1) leaves code-less windows that the LUT builder
+  // fills with some symbol, so "the first window decoding to s" is not a
+  // code in general.
   for (int s = 0; s < 16; ++s) {
-    if (!seen[s]) continue;
-    const uint32_t lo = code_vals[s] << (16 - code_bits[s]);
-    const uint32_t hi = lo + (1u << (16 - code_bits[s]));
-    for (uint32_t w = lo; w < hi; ++w) {
-      int v = luts[w >> 8];
-      if (v >= 240) v = luts[(256 - v) * 256 + (w & 0xFF)];
-      if (v != s) return ECF8_ERR_FORMAT;
+    const int len = len_row[s];
+    if (len < 1 || len > 16) continue;
+    const uint32_t span = 1u << (16 - len);
+    for (uint32_t lo = 0; lo < 65536; lo += span) {
+      bool all = true;
+      for (uint32_t w = lo; w < lo + span && all; ++w) all = sym[w] == s;
+      if (all) {
+        code_bits[s] = (uint8_t)len;
+        code_vals[s] = lo >> (16 - len);
+        break;
+      }
     }
   }
   return ECF8_OK;

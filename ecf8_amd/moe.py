@@ -31,6 +31,7 @@ import torch.nn as nn
 
 from . import decode as _dev
 from . import llm_kernels as K
+from . import tiled
 from ._lib import ECF8Error
 from .llm import FP8Linear, RMSNorm, _GreedyRunner, _rotary_tables
 from .synth import QWEN3_MOE_ATTN, QWEN3_MOE_EXPERT
@@ -131,13 +132,45 @@ class _LayerExperts:
     of (gate, up) and (down) per expert.  Compressed experts (buffers
     registered by the loader) decode into slot e of the shared expert
     buffer; ``decode_routed`` decodes the experts whose select flag is set,
-    ``decode_all`` every expert (the prompt, where nearly all are picked)."""
+    ``decode_all`` every expert (the prompt, where nearly all are picked).
+    Re-tiled experts (retile_moe_layers) run the decode step's grouped
+    linears on their tiled form (``tiled_gu`` / ``tiled_down``, which decode
+    the routed experts' weight operands themselves); ``decode_all`` writes
+    every expert's FP8 Linears into the buffer for the prompt."""
 
     def __init__(self, mlp: SparseMoeBlock, expert_buf, gu_out, down_out):
         experts = list(mlp.experts)
         self.compressed = hasattr(experts[0], "encoded")
+        self.tiled = hasattr(experts[0], "_ecf8_tiles")
         weights = []
-        if self.compressed:
+        if self.tiled:
+            n_e = sum(lin.out_features * lin.in_features
+                      for lin in (experts[0].gate_proj, experts[0].up_proj, experts[0].down_proj))
+            if expert_buf is None or expert_buf.numel() < n_e * len(experts):
+                raise ECF8Error("expert buffer too small for the layer's experts")
+            tables = [ex._ecf8_tile_table for ex in experts]
+            self._decoders = []
+            views = {name: [] for name in ("gate_proj", "up_proj", "down_proj")}
+            for e, ex in enumerate(experts):
+                off = e * n_e
+                for name in ("gate_proj", "up_proj", "down_proj"):
+                    lin = ex.get_submodule(name)
+                    n = lin.out_features * lin.in_features
+                    views[name].append(expert_buf[off:off + n].view(lin.out_features,
+                                                                    lin.in_features))
+                    off += n
+            for name in ("gate_proj", "up_proj", "down_proj"):
+                self._decoders.append(tiled.TileDecodeBatch(
+                    [ex._ecf8_tiles[name] for ex in experts], tables, views[name]))
+            for e, ex in enumerate(experts):
+                weights.append(tuple((views[name][e], ex.get_submodule(name).weight_scale_inv)
+                                     for name in ("gate_proj", "up_proj", "down_proj")))
+            self.tiled_gu = tiled.TileMoePlan(
+                [[ex._ecf8_tiles["gate_proj"], ex._ecf8_tiles["up_proj"]] for ex in experts],
+                tables, gu_out)
+            self.tiled_down = tiled.TileMoePlan([[ex._ecf8_tiles["down_proj"]] for ex in experts],
+                                                tables, down_out)
+        elif self.compressed:
             n_e = experts[0].packed_other_4bits.numel() * 2
             if expert_buf is None or expert_buf.numel() < n_e * len(experts):
                 raise ECF8Error("expert buffer too small for the layer's experts")
@@ -172,7 +205,11 @@ class _LayerExperts:
         self.select(flags)
 
     def decode_all(self):
-        _dev.decode_batched(self.plan)
+        if self.tiled:
+            for dec in self._decoders:
+                dec()
+        else:
+            _dev.decode_batched(self.plan)
 
 
 class Qwen3MoeRunner(_GreedyRunner):
@@ -226,10 +263,11 @@ class Qwen3MoeRunner(_GreedyRunner):
         self.hs = torch.empty(P, I // 128, dtype=torch.float32, device=dev)
         self.down = torch.empty(P, H, **bf)
         layers = list(model.model.layers)
-        compressed = hasattr(layers[0].mlp.experts[0], "encoded")
+        ex0 = layers[0].mlp.experts[0]
         self.expert_buf = None
-        if compressed:
-            n_e = layers[0].mlp.experts[0].packed_other_4bits.numel() * 2
+        if hasattr(ex0, "encoded") or hasattr(ex0, "_ecf8_tiles"):
+            n_e = sum(lin.out_features * lin.in_features
+                      for lin in (ex0.gate_proj, ex0.up_proj, ex0.down_proj))
             self.expert_buf = torch.empty(n_e * E, dtype=torch.float8_e4m3fn, device=dev)
         self.experts = [_LayerExperts(layer.mlp, self.expert_buf, self.gu, self.down)
                         for layer in layers]
@@ -239,15 +277,45 @@ class Qwen3MoeRunner(_GreedyRunner):
         self.logits = None
         self._plans = {}
 
+    def _attn_linear(self, a: MoeAttention, index: int, which, names, out, M):
+        """An FP8 plan over the attention block's (hook injected) weights, or
+        for a re-tiled block the tiled linear (M <= 16) or its Linears
+        decoded into prompt buffers first."""
+        tiles = getattr(a, "_ecf8_tiles", None)
+        if tiles is None:
+            mods = [a.get_submodule(n) for n in names]
+            return self._plan(a, index, which, [(x.weight, x.weight_scale_inv) for x in mods], out)
+        if M <= 16:
+            key = (index, which, "tiled")
+            p = self._plans.get(key)
+            if p is None:
+                p = tiled.TileLinearPlan([tiles[n] for n in names], a._ecf8_tile_table, out)
+                self._plans[key] = p
+            return p
+        weights = []
+        for n in names:
+            op = tiles[n]
+            buf = self._tile_scratch(op.n * op.k, n)
+            tiled.tile_decode(op, a._ecf8_tile_table, buf)
+            weights.append((buf.view(op.n, op.k), op.weight_scale))
+        return K.LinearPlan(weights, out)
+
+    def _tile_scratch(self, numel, name):
+        if not hasattr(self, "_tile_bufs"):
+            self._tile_bufs = {}
+        buf = self._tile_bufs.get(name)
+        if buf is None or buf.numel() < numel:
+            buf = torch.empty(numel, dtype=torch.float8_e4m3fn, device=self.dev)
+            self._tile_bufs[name] = buf
+        return buf[:numel]
+
     def attention(self, a: MoeAttention, index: int, prefill: bool):
         cfg = self.cfg
         B, T = self.B, (self.T if prefill else 1)
         M = B * T
         Hq, Hkv = cfg.heads, cfg.kv_heads
-        self._plan(a, index, "qkv", [(a.q_proj.weight, a.q_proj.weight_scale_inv),
-                                     (a.k_proj.weight, a.k_proj.weight_scale_inv),
-                                     (a.v_proj.weight, a.v_proj.weight_scale_inv)],
-                   self.qkv)(self.aqH, self.asH, M)
+        self._attn_linear(a, index, "qkv", ("q_proj", "k_proj", "v_proj"), self.qkv,
+                          M)(self.aqH, self.asH, M)
         if prefill:
             K.qk_norm_rope(self.qkv, B, T, Hq, Hkv, a.q_norm.weight, a.k_norm.weight, cfg.eps,
                            self.cos, self.sin, self.pos, self.q, self.kc[index], self.vc[index])
@@ -257,8 +325,7 @@ class Qwen3MoeRunner(_GreedyRunner):
             K.decode_attention_fused(self.qkv, B, Hq, Hkv, a.q_norm.weight, a.k_norm.weight,
                                      cfg.eps, self.cos, self.sin, self.pos, self.kc[index],
                                      self.vc[index], self.work, self.aqA, self.asA)
-        self._plan(a, index, "o", [(a.o_proj.weight, a.o_proj.weight_scale_inv)],
-                   self.o)(self.aqA, self.asA, M)
+        self._attn_linear(a, index, "o", ("o_proj",), self.o, M)(self.aqA, self.asA, M)
 
     def _moe(self, mlp: SparseMoeBlock, index: int, M: int, prefill: bool,
              quantized: bool = False):
@@ -267,7 +334,8 @@ class Qwen3MoeRunner(_GreedyRunner):
         cfg, r, ex = self.cfg, self.route, self.experts[index]
         if not quantized:
             K.act_quant(self.hb, M, self.aqH, self.asH)  # the experts' input
-        if prefill and ex.compressed:
+        fused = ex.tiled and not prefill and M <= 16
+        if (prefill or ex.tiled) and (ex.compressed or ex.tiled) and not fused:
             ex.decode_all()
         step = self.chunk if prefill else M
         for c0 in range(0, M, step):
@@ -276,9 +344,10 @@ class Qwen3MoeRunner(_GreedyRunner):
             K.moe_group(r, m)
             if ex.compressed and not prefill:
                 ex.decode_routed(r.select)
-            ex.gu(self.aqH[c0:c0 + m], self.asH[c0:c0 + m], r, gather=True, M=m)
+            gu, down = (ex.tiled_gu, ex.tiled_down) if fused else (ex.gu, ex.down)
+            gu(self.aqH[c0:c0 + m], self.asH[c0:c0 + m], r, gather=True, M=m)
             K.silu_mul_quant(self.gu, m * cfg.top_k, self.hq, self.hs)
-            ex.down(self.hq, self.hs, r, gather=False, M=m)
+            down(self.hq, self.hs, r, gather=False, M=m)
             K.moe_combine(self.down, r, m, self.y[c0:c0 + m])
 
     def layer(self, layer: MoeDecoderLayer, index: int, x_prev, prefill: bool):
@@ -378,4 +447,66 @@ def compress_moe_layers(model: Qwen3MoeForCausalLM, drawn=None, threads_per_bloc
                     {n: ex.get_submodule(n).weight.detach().cpu() for n in EXPERT_LINEARS})
             register(ex, f"model.layers.{i}.mlp.experts.{e}", {EXPERT_REGEX: list(EXPERT_LINEARS)},
                      comp_of(None if key is None else (key, e), w_ex))
+    return model
+
+
+def retile_moe_layers(model: Qwen3MoeForCausalLM, drawn=None, n_threads: int | None = None):
+    """Re-tile every compressed attention block and expert for the fused
+    decode step (ecf8_amd.tiled): each block is decoded once on its device,
+    its Linears re-encoded under the block's own code into the tiled layout,
+    and its reference-layout buffers and decode hook removed.  The decode
+    step's attention linears and grouped expert linears then decode their
+    weight operands themselves; the prompt decodes the tiled Linears first.
+    ``drawn`` (from random_moe_model) lets layers that hold copies of one
+    block share one encoding; each layer keeps its own device copy."""
+    from .decode import build_table, decode
+
+    cache = {}
+
+    def encode(key, mod, names):
+        enc = cache.get(key) if key is not None else None
+        if enc is None:
+            flat = decode(mod.luts, mod.encoded, mod.packed_other_4bits, mod.output_positions,
+                          mod.gaps).cpu()
+            bits, vals = tiled.code_from_luts(mod.luts)
+            parts = torch.tensor_split(flat, mod.split_positions)
+            enc = {}
+            for sub, part in zip(mod.weight_injection_modules, parts):
+                name = next(n for n in names if mod.get_submodule(n) is sub)
+                enc[name] = tiled.tile_encode(part.view(sub.out_features, sub.in_features), bits,
+                                              vals, n_threads)
+            if key is not None:
+                cache[key] = enc
+        return enc
+
+    def install(mod, names, enc, where):
+        dev = mod.encoded.device
+        table = build_table(mod.luts.contiguous())
+        if table.kind != 1:
+            raise ECF8Error(f"{where}: the tiled linears need LUTs without a 1-bit code")
+        mod._ecf8_tiles = {
+            n: tiled.TiledOperand(enc[n], mod.get_submodule(n).weight_scale_inv,
+                                  mod.get_submodule(n).out_features,
+                                  mod.get_submodule(n).in_features, dev)
+            for n in names}
+        mod._ecf8_tile_table = table
+        mod._forward_pre_hooks.clear()
+        for n in names:  # weight views a decode hook injected earlier
+            mod.get_submodule(n).__dict__.pop("weight", None)
+        for attr in (*_KEYS, "split_positions"):
+            if attr in mod._buffers:
+                del mod._buffers[attr]
+        mod.__dict__.pop("_ecf8_state", None)
+
+    for i, layer in enumerate(model.model.layers):
+        if not hasattr(layer.self_attn, "encoded"):
+            raise ECF8Error(f"layer {i} holds no compressed blocks")
+        key = i % len(drawn) if drawn is not None else None
+        install(layer.self_attn, ATTN_LINEARS,
+                encode(None if key is None else (key, "attn"), layer.self_attn, ATTN_LINEARS),
+                f"layer {i} attention")
+        for e, ex in enumerate(layer.mlp.experts):
+            install(ex, EXPERT_LINEARS,
+                    encode(None if key is None else (key, e), ex, EXPERT_LINEARS),
+                    f"layer {i} expert {e}")
     return model

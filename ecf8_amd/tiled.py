@@ -26,7 +26,7 @@ import torch
 from ._lib import ECF8Error, check, lib
 
 __all__ = ["code_from_luts", "tile_encode", "TiledOperand", "tile_decode", "TileLinearPlan",
-           "linear_waves", "SEG_SYMBOLS"]
+           "linear_waves", "TileMoePlan", "TileDecodeBatch", "SEG_SYMBOLS"]
 
 SEG_SYMBOLS = 2048
 _GROUP = 128
@@ -191,3 +191,100 @@ class TileLinearPlan:
                                      self.waves, torch.cuda.current_stream(dev).cuda_stream),
               "ecf8_tile_linear")
         return self.out
+
+
+def _device_structs(structs, dev) -> torch.Tensor:
+    """A ctypes struct array copied to device memory (8-byte aligned)."""
+    raw = ctypes.string_at(ctypes.addressof(structs), ctypes.sizeof(structs))
+    return torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
+
+
+def _device_ptrs(ptrs, dev) -> torch.Tensor:
+    return torch.tensor(list(ptrs), dtype=torch.int64).to(dev)
+
+
+class TileMoePlan:
+    """The grouped expert linear over tiled experts (``ecf8_tile_moe_linear``):
+    the tiled counterpart of llm_kernels.MoeLinearPlan.  ``experts`` is a
+    list (one per expert) of 1..3 TiledOperands of one shape [seg_n, K]
+    (e.g. gate, up); ``tables`` one automaton table per expert (its block's
+    code)."""
+
+    def __init__(self, experts, tables, out: torch.Tensor, splits: int = 0):
+        dev = out.device
+        if out.dtype != torch.bfloat16 or not out.is_cuda or not out.is_contiguous():
+            raise ECF8Error("out must be a contiguous bf16 CUDA tensor")
+        n_segs = len(experts[0])
+        if not 1 <= n_segs <= 3 or any(len(e) != n_segs for e in experts):
+            raise ECF8Error("every expert needs the same 1..3 operands")
+        if len(tables) != len(experts):
+            raise ECF8Error("one table per expert")
+        seg_n, K = experts[0][0].n, experts[0][0].k
+        arr = (_TileOp * (len(experts) * n_segs))()
+        for e, ops in enumerate(experts):
+            for j, op in enumerate(ops):
+                if (op.n, op.k) != (seg_n, K) or op.device != dev:
+                    raise ECF8Error("expert operands differ in shape or device")
+                arr[e * n_segs + j] = op.c_struct(j * seg_n)
+        if out.shape[-1] < n_segs * seg_n:
+            raise ECF8Error(f"out has {out.shape[-1]} columns, {n_segs * seg_n} needed")
+        self.ops_dev = _device_structs(arr, dev)
+        self.tables_dev = _device_ptrs((_table_ptr(t, dev) for t in tables), dev)
+        self._keep = (list(experts), list(tables))
+        self.E, self.n_segs, self.seg_n, self.K, self.out = len(experts), n_segs, seg_n, K, out
+        self.splits = int(splits)
+
+    def __call__(self, aq, a_scale, r, gather: bool, M: int | None = None):
+        """As MoeLinearPlan: ``gather``: activation rows are tokens, else one
+        row per sorted pair; M (<= 16): the tokens routed into ``r``."""
+        dev = self.out.device
+        M = r.M if M is None else M
+        if not 1 <= M <= min(r.M, 16):
+            raise ECF8Error("the tiled grouped linear runs 1..16 routed tokens")
+        rows = M if gather else M * r.top_k
+        if (aq.dtype != torch.float8_e4m3fn or a_scale.dtype != torch.float32 or aq.device != dev
+                or aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < rows
+                or tuple(a_scale.shape[1:]) != (self.K // _GROUP,) or a_scale.shape[0] < rows
+                or not aq.is_contiguous() or not a_scale.is_contiguous()
+                or self.out.shape[0] < r.M * r.top_k or r.E != self.E):
+            raise ECF8Error("activation / output shape does not match the grouped linear")
+        check(lib().ecf8_tile_moe_linear(
+            aq.data_ptr(), a_scale.data_ptr(), r.pair_tok.data_ptr() if gather else None,
+            r.offsets.data_ptr(), r.active.data_ptr(), r.n_active.data_ptr(), self.E,
+            self.ops_dev.data_ptr(), self.tables_dev.data_ptr(), self.n_segs, self.seg_n, self.K, M,
+            self.out.data_ptr(), self.out.shape[-1], self.splits,
+            torch.cuda.current_stream(dev).cuda_stream), "ecf8_tile_moe_linear")
+        return self.out
+
+
+class TileDecodeBatch:
+    """``ecf8_tile_decode_batch``: same-shape tiled operands (e.g. one
+    projection of every expert) decoded into their row-major FP8 outputs
+    in one launch."""
+
+    def __init__(self, ops, tables, outs):
+        if not ops or len(tables) != len(ops) or len(outs) != len(ops):
+            raise ECF8Error("one table and one output per operand")
+        dev = ops[0].device
+        n, k = ops[0].n, ops[0].k
+        arr = (_TileOp * len(ops))()
+        for i, (op, o) in enumerate(zip(ops, outs)):
+            if (op.n, op.k) != (n, k) or op.device != dev:
+                raise ECF8Error("operands differ in shape or device")
+            if (not o.is_cuda or o.device != dev or o.numel() < n * k or not o.is_contiguous()
+                    or o.dtype not in (torch.uint8, torch.float8_e4m3fn) or o.data_ptr() % 16):
+                raise ECF8Error("each output must be a contiguous, 16-byte aligned e4m3fn/uint8 "
+                                "tensor of n*K elements on the device")
+            arr[i] = op.c_struct()
+        self.ops_dev = _device_structs(arr, dev)
+        self.tables_dev = _device_ptrs((_table_ptr(t, dev) for t in tables), dev)
+        self.outs_dev = _device_ptrs((o.data_ptr() for o in outs), dev)
+        self._keep = (list(ops), list(tables), list(outs))
+        self.n_ops, self.n, self.k, self.device = len(ops), n, k, dev
+
+    def __call__(self):
+        with torch.cuda.device(self.device):
+            check(lib().ecf8_tile_decode_batch(
+                self.ops_dev.data_ptr(), self.tables_dev.data_ptr(), self.outs_dev.data_ptr(),
+                self.n_ops, self.n, self.k, torch.cuda.current_stream(self.device).cuda_stream),
+                "ecf8_tile_decode_batch")

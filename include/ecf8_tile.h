@@ -38,11 +38,15 @@ extern "C" {
 /* ------------------------------------------------------------------ host */
 
 /*
- * The block's Huffman code recovered from its LUT stack: for each exponent
- * s with a code, code_bits[s] = its length and code_vals[s] its value (the
- * first 16-bit window the reference rule, dfloat/run/decode.cu:85-91,
- * decodes to s).  Checks that every window starting with a symbol's code
- * decodes to it (a prefix code); ECF8_ERR_FORMAT otherwise.
+ * A Huffman code for the block's exponents recovered from its LUT stack:
+ * for each exponent s of code length L (the stack's length row), the first
+ * aligned block of 2^(16-L) 16-bit windows that the reference rule
+ * (dfloat/run/decode.cu:85-91) decodes entirely to s gives code_bits[s] = L
+ * and code_vals[s] = the block's L-bit prefix; code_bits[s] = 0 when no
+ * such block exists.  Every code so recovered decodes to its symbol under
+ * the rule (the compressor's own code, except where code-less windows of an
+ * incomplete code form an earlier such block).  ECF8_ERR_FORMAT when a
+ * window decodes to no symbol.
  */
 int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *code_bits, uint32_t *code_vals);
 
@@ -98,6 +102,37 @@ int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int64_t K,
  */
 int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *table, void *out,
                      void *stream);
+
+/*
+ * The grouped expert linear of ecf8_moe_linear (include/ecf8_llm.h) with
+ * its weight operands decoded on the fly from ECF8-T, for a decode step of
+ * M <= 16 routed tokens (so an expert holds at most 16 sorted pairs):
+ *   out[q, s * seg_n + j] = linear(aq[row(q)], ops[e * n_segs + s])[j]
+ * for every sorted position q of expert e.  ops: device array of
+ * n_experts * n_segs operands (each [seg_n, K], its own out_col unused);
+ * tables: device array of n_experts ECF8_TABLE_DFA tables (each expert's
+ * block).  The wave count is ecf8_moe_linear's for this K (8 when K/128 >
+ * 8, else 4), so the result is bit-identical to decoding the experts and
+ * calling ecf8_moe_linear.  Workgroup (split, slot) takes the 16-column
+ * tiles split, split + splits, ... of expert active[slot]; splits = 0
+ * picks about 1.4 resident workgroups per expert slot.  Idle slots exit, so
+ * the launch can be captured in a graph.  The device arrays are trusted:
+ * their pointers must satisfy ecf8_tile_linear's alignment rules.
+ */
+int ecf8_tile_moe_linear(const void *aq, const float *as, const int *row_of, const int *offsets,
+                         const int *active, const int *n_active, int n_experts,
+                         const ecf8_tile_operand *ops, const uint32_t *const *tables, int n_segs,
+                         int64_t seg_n, int64_t K, int64_t M, void *out, int64_t ldo, int splits,
+                         void *stream);
+
+/*
+ * ecf8_tile_decode over n_ops operands of one shape [n, K] in one launch:
+ * ops, tables and outs are device arrays (operand i decodes with tables[i]
+ * into outs[i], 16-byte aligned), e.g. one projection of every expert of a
+ * layer.
+ */
+int ecf8_tile_decode_batch(const ecf8_tile_operand *ops, const uint32_t *const *tables,
+                           void *const *outs, int n_ops, int64_t n, int64_t K, void *stream);
 
 #ifdef __cplusplus
 }

@@ -125,12 +125,15 @@ def test_encoder_equals_a_python_restatement(n, k, seed):
 
 
 def test_segments_decode_under_the_reference_rule():
+    _check_segments(_weights(64, 512, 7), _compressed)
+
+
+def _check_segments(w, compressed):
     from ecf8_amd.tiled import code_from_luts, tile_encode
 
-    n, k = 64, 512
-    w = _weights(n, k, 7)
+    n, k = w.shape
     wb = w.view(torch.uint8).numpy()
-    res = _compressed(w)
+    res = compressed(w)
     luts = res["luts"].numpy()
     bits, vals = code_from_luts(luts)
     enc = tile_encode(w, bits, vals)
@@ -165,6 +168,39 @@ def test_segments_decode_under_the_reference_rule():
             first = next(x for x in starts + [10 ** 9] if x >= 96 * c)
             if first < 96 * c + 96:
                 assert first == 96 * c + g, (s, c)
+
+
+def test_code_recovery_from_an_incomplete_code():
+    """A Qwen3-MoE-shaped expert block (intermediate 256) whose Huffman code
+    leaves 4 of the 65536 16-bit windows without a code (Kraft sum
+    1 - 2^-14): the LUT builder fills them with exponent 0, ahead of
+    exponent 0's real 13-bit code.  Every recovered code has the
+    compressor's length and decodes to its symbol under the reference rule,
+    and a Linear of the block encodes and decodes segment by segment."""
+    from dfloat.compress import compress_flat
+    from ecf8_amd.synth import flat_block, synthetic_block
+    from ecf8_amd.tiled import code_from_luts
+
+    shapes = {"gate_proj": (256, 2048, 0.02), "up_proj": (256, 2048, 0.02),
+              "down_proj": (2048, 256, 0.02)}
+    weights = synthetic_block(shapes, seed=400016)
+    flat, _ = flat_block(weights)
+    res = compress_flat(flat)
+    table = {s: v for s, v in res["table"].items() if isinstance(s, (int, np.integer))}
+    assert sum(2.0 ** -nb for nb, _ in table.values()) < 1.0  # incomplete
+    luts = res["luts"].numpy()
+    bits, vals = code_from_luts(luts)
+    for sym, (nb, _) in table.items():
+        assert bits[sym] == nb, sym
+        lo = int(vals[sym]) << (16 - nb)
+        for wnd in range(lo, lo + (1 << (16 - nb))):
+            assert oc.lut_decode_one(luts, wnd) == (sym, nb), (sym, wnd)
+    # the compressor's code of exponent 0 differs from the first window
+    # decoding to 0: the case a first-window rule gets wrong
+    nb0, val0 = table[0]
+    first0 = next(wnd for wnd in range(65536) if oc.lut_decode_one(luts, wnd)[0] == 0)
+    assert first0 >> (16 - nb0) != val0
+    _check_segments(weights["gate_proj"][0][:32].contiguous(), lambda _w: res)
 
 
 def test_layout_refusals():

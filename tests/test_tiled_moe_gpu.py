@@ -1,0 +1,182 @@
+"""The tiled execution layout's grouped expert linear on the GPU
+(include/ecf8_tile.h: ecf8_tile_moe_linear, ecf8_tile_decode_batch), on
+Qwen3-30B-A3B-shaped experts (hidden 2048, intermediate 768), each expert
+compressed as its own block and re-tiled under its own code:
+
+* ecf8_tile_decode_batch writes every expert's original FP8 bytes;
+* ecf8_tile_moe_linear -- routed experts decoding their weight operands on
+  the fly -- is bit-identical to ecf8_moe_linear over the decoded experts,
+  for gate/up (token rows gathered, 8 waves) and down (one row per sorted
+  pair, 4 waves), 1, 5 and 16 routed tokens, any workgroup split;
+* a re-tiled small MoE model generates the FP8 model's tokens and logits,
+  eager and graph-replayed;
+* it refuses what it cannot run.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+E, H, I, TOP_K = 16, 2048, 768, 8
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def experts(cuda_device):
+    from dfloat.compress import compress_flat
+    from ecf8_amd.decode import build_table
+    from ecf8_amd.synth import flat_block, synthetic_block
+    from ecf8_amd.tiled import TiledOperand, code_from_luts, tile_encode
+
+    shapes = {"gate_proj": (I, H, 0.02), "up_proj": (I, H, 0.02), "down_proj": (H, I, 0.02)}
+    dense, ops, tables = [], [], []
+    _say(f"[tiled-moe] encoding {E} experts")
+    for e in range(E):
+        w = synthetic_block(shapes, seed=500 + e)
+        flat, _ = flat_block(w)
+        res = compress_flat(flat)
+        table = build_table(res["luts"].contiguous().to(cuda_device))
+        assert table.kind == 1
+        bits, vals = code_from_luts(res["luts"])
+        ops.append({n: TiledOperand(tile_encode(wt, bits, vals), s, wt.shape[0], wt.shape[1],
+                                    cuda_device) for n, (wt, s) in w.items()})
+        dense.append({n: (wt.to(cuda_device), s.to(cuda_device)) for n, (wt, s) in w.items()})
+        tables.append(table)
+    return dense, ops, tables
+
+
+def test_tile_decode_batch_writes_the_original_bytes(experts, cuda_device):
+    from ecf8_amd.tiled import TileDecodeBatch
+
+    dense, ops, tables = experts
+    for name in ("gate_proj", "down_proj"):
+        n, k = ops[0][name].n, ops[0][name].k
+        buf = torch.full((E, n * k + 64), 0x5A, dtype=torch.uint8, device=cuda_device)
+        TileDecodeBatch([o[name] for o in ops], tables, [buf[e, :n * k] for e in range(E)])()
+        torch.cuda.synchronize()
+        for e in range(E):
+            assert torch.equal(buf[e, :n * k].view(n, k), dense[e][name][0].view(torch.uint8)), \
+                (name, e)
+        assert bool((buf[:, n * k:] == 0x5A).all())
+
+
+def _routing(M, seed, dev):
+    """Router state for M tokens with top-k distinct random experts, grouped
+    by ecf8_moe_group."""
+    from ecf8_amd import llm_kernels as K
+
+    g = torch.Generator().manual_seed(seed)
+    r = K.MoeRouting(16, TOP_K, E, dev)
+    idx = torch.stack([torch.randperm(E, generator=g)[:TOP_K] for _ in range(M)])
+    r.topk_idx[:M] = idx.to(torch.int32).to(dev)
+    r.topk_w[:M] = torch.rand(M, TOP_K, generator=g).to(dev)
+    K.moe_group(r, M)
+    return r
+
+
+def _acts(rows, K, seed, dev):
+    from ecf8_amd.llm_kernels import act_quant
+
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, K, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    aq = torch.empty(rows, K, dtype=torch.float8_e4m3fn, device=dev)
+    as_ = torch.empty(rows, K // 128, dtype=torch.float32, device=dev)
+    act_quant(x, rows, aq, as_)
+    return aq, as_
+
+
+@pytest.mark.parametrize("splits", [0, 1, 5])
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_tile_moe_linear_is_bit_identical_to_the_fp8_grouped_linear(experts, cuda_device, which,
+                                                                       M, splits):
+    from ecf8_amd.llm_kernels import MoeLinearPlan
+    from ecf8_amd.tiled import TileMoePlan
+
+    dense, ops, tables = experts
+    names = ["gate_proj", "up_proj"] if which == "gate_up" else ["down_proj"]
+    gather = which == "gate_up"
+    K = H if gather else I
+    N = sum(ops[0][n].n for n in names)
+    r = _routing(M, 7 + M, cuda_device)
+    P = 16 * TOP_K
+    aq, as_ = _acts(16 if gather else P, K, 3 + M, cuda_device)
+    ref = torch.full((P, N + 8), 7.0, dtype=torch.bfloat16, device=cuda_device)
+    got = ref.clone()
+    MoeLinearPlan([[dense[e][n] for n in names] for e in range(E)], ref)(aq, as_, r, gather, M=M)
+    plan = TileMoePlan([[ops[e][n] for n in names] for e in range(E)], tables, got, splits=splits)
+    _say(f"[tiled-moe] {which} M={M} splits={splits}")
+    plan(aq, as_, r, gather, M=M)
+    torch.cuda.synchronize()
+    rows = M * TOP_K
+    assert torch.equal(got[:rows], ref[:rows]), which
+    assert bool((got[rows:] == 7.0).all()) and bool((got[:, N:] == 7.0).all())
+    assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
+
+
+def test_tile_moe_linear_refusals(experts, cuda_device):
+    from ecf8_amd._lib import ECF8Error
+    from ecf8_amd import llm_kernels as K
+    from ecf8_amd.tiled import TileMoePlan
+
+    dense, ops, tables = experts
+    out = torch.empty(32 * TOP_K, 2 * I, dtype=torch.bfloat16, device=cuda_device)
+    plan = TileMoePlan([[o["gate_proj"], o["up_proj"]] for o in ops], tables, out)
+    r = K.MoeRouting(32, TOP_K, E, cuda_device)
+    aq, as_ = _acts(32, H, 1, cuda_device)
+    with pytest.raises(ECF8Error):
+        plan(aq, as_, r, True, M=17)  # more than 16 routed tokens
+    with pytest.raises(ECF8Error):
+        TileMoePlan([[o["gate_proj"], o["down_proj"]] for o in ops], tables, out)  # shapes differ
+    with pytest.raises(ECF8Error):
+        TileMoePlan([[o["gate_proj"]] for o in ops], tables[:-1], out)  # a table missing
+
+
+SMALL_MOE = dict(hidden=2048, layers=2, heads=16, kv_heads=2, experts=16, top_k=4,
+                 moe_intermediate=256, vocab=1024)
+
+
+def test_retiled_moe_model_matches_fp8_exactly(cuda_device):
+    """Attention blocks and experts re-tiled: the decode step's attention
+    linears and grouped expert linears decode their weight operands
+    themselves, the prompt decodes the tiled Linears first; eager and
+    graph-replayed, the FP8 model's tokens and logits."""
+    from dfloat.run.run import TensorManager
+    from ecf8_amd.moe import (Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers,
+                              random_moe_model, retile_moe_layers)
+
+    cfg = Qwen3MoeConfig(**SMALL_MOE)
+    plain, drawn = random_moe_model(cfg, cuda_device, seed=4)
+    tiled_model, _ = random_moe_model(cfg, cuda_device, seed=4)
+    compress_moe_layers(tiled_model, drawn)
+    retile_moe_layers(tiled_model, drawn)
+    assert not hasattr(tiled_model.model.layers[0].mlp.experts[0], "encoded")
+    B, T, new = 4, 40, 6
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(5))
+    results = {}
+    for name, model in (("fp8", plain), ("fused", tiled_model)):
+        for graph in (False, True):
+            _say(f"[tiled-moe] e2e {name} graph={graph}")
+            TensorManager.clear_device()
+            r = Qwen3MoeRunner(model, B, T, T + new, cuda_device,
+                               prefill_chunk=512 if graph else 24)
+            if graph:
+                r.capture()
+            for rep in range(2):
+                toks = r.generate(prompt, new).cpu()
+                results[(name, graph, rep)] = (toks, r.logits.float().cpu())
+            del r
+    base_t, base_l = results[("fp8", False, 0)]
+    for key, (t, l) in results.items():
+        assert torch.equal(t, base_t), key
+        assert torch.equal(l, base_l), key
+    assert len(set(base_t.reshape(-1).tolist())) > 1
