@@ -287,7 +287,7 @@ struct Step {
   int p, col;   // panel index inside the operand, its first output column
   int kg;       // group, 0 when past the last one
   bool valid;   // a real panel and group: decoded and multiplied
-  bool closes;  // the last step of a real panel: its partial sums are parked
+  bool closes;  // the panel's last step (u = ng - 1): its partial sums are parked
 };
 
 template <class Walk>
@@ -296,7 +296,7 @@ __device__ __forceinline__ Step step_at(const Walk &walk, int panel, int u, int 
   Step st;
   const int kg = wave + u * waves;
   st.valid = panel < n_panels && kg < kgroups;
-  st.closes = panel < n_panels && (u + 1) * waves >= kgroups;
+  st.closes = (u + 1) * waves >= kgroups;
   walk.at(panel < n_panels ? panel : n_panels - 1, st.op, st.p, st.col);
   st.kg = kg < kgroups ? kg : 0;
   return st;
@@ -312,7 +312,25 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
   return *a;
 }
 
-constexpr int kRedPanels = 4;  // panels whose partial sums wait for one reduction
+// Launch shapes: panels of partial sums per reduction (RED) and FP8
+// workgroups per workgroup (G), chosen for waves per CU (LDS: automaton
+// 24.6 KB + 1 KB staging per wave + RED x waves KB of partial sums; MI355X,
+// Qwen3-30B-A3B experts at 16 tokens: down 58.2 us at G = 1, RED = 4 and
+// 51.7 us at G = 2, RED = 2).
+#ifndef ECF8_TILE_DENSE8_RED
+#define ECF8_TILE_DENSE8_RED 2
+#endif
+#ifndef ECF8_TILE_MOE_RED
+#define ECF8_TILE_MOE_RED 2
+#endif
+#ifndef ECF8_TILE_MOE8_GROUPS
+#define ECF8_TILE_MOE8_GROUPS 1
+#endif
+#ifndef ECF8_TILE_MOE4_GROUPS
+#define ECF8_TILE_MOE4_GROUPS 2
+#endif
+constexpr int kDense8Red = ECF8_TILE_DENSE8_RED, kMoeRed = ECF8_TILE_MOE_RED;
+constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_GROUPS;
 
 // Steps whose loads are in flight during a decode.  One suffices: a step's
 // decode outlasts the memory round trip, and on MI355X distances 2 and 3
@@ -327,15 +345,24 @@ static_assert(kPrefetch >= 1 && kPrefetch <= 3, "prefetch distance");
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
 //
+// A workgroup runs G groups of WAVES waves; group g is the FP8 linear's
+// workgroup number blockIdx.x * G + g of a grid G times larger: it takes
+// those panels and sums each in that workgroup's wave order, so the result
+// does not depend on G (more waves per CU for shapes whose FP8 workgroup is
+// small).  The groups walk in lockstep (a group out of panels walks empty
+// steps), so every wave reaches the same barriers.
+//
 // Each wave walks its steps (segments) as a software pipeline: while it
 // decodes step t, the code windows and nibbles of steps t+1..t+P (P =
 // kPrefetch) and the offsets of step t+P+1 are in flight -- every load
 // unconditional (clamped addresses) and issued in a fixed order, so the wait
 // before a decode never covers a later step's loads.  The loop is unrolled
 // by P+1 and the buffers rotate by name, so no in-flight register is
-// copied.  Partial sums of up to kRedPanels panels wait in LDS and are
+// copied.  Partial sums of up to RED panels per group wait in LDS and are
 // reduced together, in wave order as the FP8 linear sums them, behind a
-// barrier that fences LDS only.
+// barrier that fences LDS only.  (A barrier-free scheme -- the last wave in
+// sums each panel -- measured slower on MI355X: it hands the summing to the
+// slowest wave.)
 // Arguments of the dense linear (one fused set of operands, rows 0..M-1)
 // and of the grouped expert linear (workgroup (split, slot) takes expert
 // active[slot], its rows offsets[e].. of the sorted pairs, gathered from
@@ -363,16 +390,17 @@ struct TileMoeArgs {
   int K, ldo, n_segs, seg_n;
 };
 
-template <int WAVES, bool kMoe>
-__global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
+template <int WAVES, int G, int RED, bool kMoe>
+__global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
     typename std::conditional<kMoe, TileMoeArgs, TileDenseArgs>::type a) {
-  constexpr int P = kPrefetch, NB = kPrefetch + 1;
+  constexpr int P = kPrefetch, NB = kPrefetch + 1, HW = WAVES * G;
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
   __shared__ uint32_t s_dfa[kDfaEntries];
-  __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
-  __shared__ __attribute__((aligned(16))) float s_part[kRedPanels][WAVES][256];
+  __shared__ __attribute__((aligned(16))) uint32_t s_stage[HW][kWaveStageDw];
+  __shared__ __attribute__((aligned(16))) float s_part[RED][G][WAVES][256];
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int group = hw / WAVES, wave = hw % WAVES;
   const int K = a.K, kgroups = K / kGroup;
   // the workgroup's rows, operands and table (uniform)
   int M, row0 = 0, n_panels;
@@ -394,8 +422,11 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
     walk = DenseWalk{&a.segs};
     n_panels = a.n_panels;
   }
-  if (M <= 0 || (int)blockIdx.x >= n_panels) return;  // uniform, before any barrier
-  uint32_t *const stage = s_stage[wave];
+  // this group's panels: vwg, vwg + vgrid, ...
+  const int vwg = (int)blockIdx.x * G + group, vgrid = (int)gridDim.x * G;
+  const int vwg0 = (int)blockIdx.x * G;  // the workgroup's first group: the most panels
+  if (M <= 0 || vwg0 >= n_panels) return;  // uniform, before any barrier
+  uint32_t *const stage = s_stage[hw];
   const float *const as = a.as;
 
   // the lane's A-operand row and the 4 output rows whose scales it applies;
@@ -416,20 +447,19 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
     srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
   }
   const int ng = (kgroups + WAVES - 1) / WAVES;
-  const int n_mine = (n_panels - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
-  const int n_real = n_mine * ng;
+  const int n_real = ((n_panels - 1 - vwg0) / vgrid + 1) * ng;  // the first group's steps
   // a multiple of NB steps (trailing ones past the last panel compute
   // nothing), so the unrolled loop's back edge always follows its last copy
   const int n_steps = (n_real + NB - 1) / NB * NB;
 
   // steps t .. t+P+1: sc[0] is the step being computed
   Step sc[P + 2];
-  int pan = blockIdx.x, u = 0;  // cursor of the step after the last in sc
+  int pan = vwg, u = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
     const Step st = step_at(walk, pan, u, wave, WAVES, kgroups, n_panels);
     if (++u == ng) {
       u = 0;
-      pan += gridDim.x;
+      pan += vgrid;
     }
     return st;
   };
@@ -446,7 +476,7 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
 #pragma unroll
   for (int i = 0; i < NB; ++i) m[i] = step_meta(sc[i], kgroups, lane);
   issue_order();
-  DfaLoad<WAVES * 64> dfa;
+  DfaLoad<HW * 64> dfa;
   dfa.load(table, threadIdx.x);
   issue_order();
 #pragma unroll
@@ -463,24 +493,30 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
   lds_barrier();
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  int pending = 0, first_pending = 0;  // panels waiting in s_part, ordinal of the first
+  // panels per group waiting in s_part (the same count in every group), and
+  // the ordinal of the first
+  int pending = 0, first_pending = 0;
 
   auto reduce = [&]() {
     lds_barrier();
-    // wave w sums accumulator i = w % 4 of panel j (wave-uniform: the panel's
-    // operand and columns come from scalar loads); unrolled, as a loop around
-    // the store would make the compiler drain the prefetched loads first
+    // item (group gg, panel j, accumulator i) -> one wave (wave-uniform: the
+    // panel's operand and columns come from scalar loads); unrolled, as a
+    // loop around the store would make the compiler drain the prefetched
+    // loads first
+    const int per_group = 4 * pending;
 #pragma unroll
-    for (int k = 0; k < (4 * kRedPanels + WAVES - 1) / WAVES; ++k) {
-      const int jw = wave + k * WAVES;
-      if (jw >= 4 * pending) break;
-      const int j = jw >> 2, i = jw & 3, l = lane;
+    for (int k = 0; k < (4 * RED * G + HW - 1) / HW; ++k) {
+      const int jw = hw + k * HW;
+      if (jw >= G * per_group) break;
+      const int gg = jw / per_group, j = (jw % per_group) >> 2, i = jw & 3, l = lane;
+      const int panel = vwg0 + gg + (first_pending + j) * vgrid;
+      if (panel >= n_panels) continue;  // a group out of panels
       float sum = 0.f;
 #pragma unroll
-      for (int wv = 0; wv < WAVES; ++wv) sum += s_part[j][wv][i * 64 + l];
+      for (int wv = 0; wv < WAVES; ++wv) sum += s_part[j][gg][wv][i * 64 + l];
       TileOperand op;
       int p, col;
-      walk.at((int)blockIdx.x + (first_pending + j) * (int)gridDim.x, op, p, col);
+      walk.at(panel, op, p, col);
       const int mm = 4 * (l >> 4) + i;
       if (mm < M)
         a.out[(size_t)(row0 + mm) * a.ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
@@ -539,14 +575,14 @@ __global__ __launch_bounds__(WAVES * 64) void tile_linear16_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * wsv[k], acc[i]);
     }
-    if (sc[0].closes) {  // the panel's last step: park its partial sums
+    if (sc[0].closes) {  // the panel's last step (all groups at once): park its partial sums
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s_part[pending][wave][i * 64 + lane] = acc[i];
+        s_part[pending][group][wave][i * 64 + lane] = acc[i];
         acc[i] = 0.f;
       }
       ++pending;
-      if (pending == kRedPanels || t == n_real - 1) reduce();
+      if (pending == RED || t == n_real - 1) reduce();
     }
 #pragma unroll
     for (int i = 0; i < P + 1; ++i) sc[i] = sc[i + 1];
@@ -685,13 +721,14 @@ extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int6
   const TileDenseArgs args{a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels};
   int grid = 0, rc;
   if (waves == 16) {
-    rc = resident_grid(tile_linear16_kernel<16, false>, 1024, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<16, 1, 4, false>, 1024, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<16, false><<<(unsigned)grid, 1024, 0, as_stream(stream)>>>(args);
+    tile_linear16_kernel<16, 1, 4, false><<<(unsigned)grid, 1024, 0, as_stream(stream)>>>(args);
   } else {
-    rc = resident_grid(tile_linear16_kernel<8, false>, 512, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<8, 1, kDense8Red, false>, 512, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<8, false><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(args);
+    tile_linear16_kernel<8, 1, kDense8Red, false><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(
+        args);
   }
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
@@ -719,20 +756,24 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
   const int64_t n_tiles = n_segs * seg_n / 16;
   // the FP8 grouped linear's wave count for this K (it sums in that order)
   const bool eight = K / kGroup > 8;
-  auto launch = [&](auto kernel, int threads) {
+  // groups: G FP8 workgroups per workgroup (splits counts FP8 workgroups)
+  auto launch = [&](auto kernel, int threads, int groups) {
     int64_t g = splits;
     if (g == 0) {  // about 1.4 workgroups per slot for the experts' share
       int64_t slots = 0;
       const int rc = resident_slots(kernel, threads, &slots);
       if (rc != ECF8_OK) return rc;
-      g = (slots * 10 + 7 * n_experts - 1) / (7 * n_experts);
+      g = (slots * groups * 10 + 7 * n_experts - 1) / (7 * n_experts);
     }
     g = g < 1 ? 1 : g > n_tiles ? n_tiles : g;
-    kernel<<<dim3((unsigned)g, (unsigned)n_experts), threads, 0, as_stream(stream)>>>(args);
+    const int64_t wgs = (g + groups - 1) / groups;
+    kernel<<<dim3((unsigned)wgs, (unsigned)n_experts), threads, 0, as_stream(stream)>>>(args);
     return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
   };
-  return eight ? launch(tile_linear16_kernel<8, true>, 512)
-               : launch(tile_linear16_kernel<4, true>, 256);
+  return eight ? launch(tile_linear16_kernel<8, kMoe8Groups, kMoeRed, true>, 512 * kMoe8Groups,
+                        kMoe8Groups)
+               : launch(tile_linear16_kernel<4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
+                        kMoe4Groups);
 }
 
 extern "C" int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *table,
