@@ -308,10 +308,14 @@ struct BlockArgs {
 //
 // kChecked: tensors too small for the clamped vector loads (fewer than 12
 // bitstream bytes or 16 elements) use byte-wise loads throughout.
+//
+// load_table (optional): a table to load into s_dfa first -- after the
+// first block's loads are issued, so the two round trips overlap.
 template <int kThreads, bool kChecked, bool kPrio = true>
-__device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s_dfa,
+__device__ __forceinline__ void dfa_blocks(const BlockArgs &a, uint32_t *s_dfa,
                                            int *s_wave_sum, uint32_t *s_edge, uint32_t *s_dyn,
-                                           int stage_cap, int fb, int fb_step, int fb_end) {
+                                           int stage_cap, int fb, int fb_step, int fb_end,
+                                           const uint32_t *load_table = nullptr) {
   constexpr int kWaves = kThreads / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -355,6 +359,7 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, const uint32_t *s
   uint32_t op_lo, op_hi;
   {
     const uint32_t opv = op32[2 * (fb + (lane & 1))];
+    if (load_table) load_dfa_rounds<kThreads, 7>(s_dfa, load_table, tid);
     op_lo = __builtin_amdgcn_readlane(opv, 0);
     op_hi = __builtin_amdgcn_readlane(opv, 1);
   }
@@ -581,13 +586,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     const int fb_first = contiguous ? r * blocks_per_task : r;
     const int fb_step = contiguous ? 1 : tasks;
     const int fb_last = contiguous ? min(n_fb, (r + 1) * blocks_per_task) : n_fb;
-    // the previous task ended with a barrier: no wave still reads s_dfa
-    load_dfa<kThreads>(s_dfa, d.table, tid);
-    const BlockArgs a{d.luts, d.n_luts, d.encoded, n_bytes, d.packed_other_4bits,
-                      reinterpret_cast<const uint32_t *>(d.output_positions), d.gaps,
-                      d.outputs, (uint32_t)d.n_elements};
+    // the previous task ended with a barrier: no wave still reads s_dfa.
+    // The table loads in dfa_blocks, seven per lane in flight (two round
+    // trips instead of thirteen), overlapped with the first block's.
+    const BlockArgs a{as_global(d.luts), d.n_luts, as_global(d.encoded), n_bytes,
+                      as_global(d.packed_other_4bits),
+                      as_global(reinterpret_cast<const uint32_t *>(d.output_positions)),
+                      as_global(d.gaps), as_global(d.outputs), (uint32_t)d.n_elements};
     dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, fb_first,
-                                fb_step, fb_last);
+                                fb_step, fb_last, as_global(d.table));
   }
 }
 

@@ -99,6 +99,39 @@ __device__ __forceinline__ void load_dfa_batched(uint32_t *s_dfa,
   }
 }
 
+// A pointer read out of memory (a descriptor) to global memory: the
+// address space restated, so its loads and stores are global, not flat,
+// operations -- flat ones also count on the LDS wait counter, so every LDS
+// wait would wait for them too.
+template <class T>
+__device__ __forceinline__ T *as_global(T *p) {
+  typedef __attribute__((address_space(1))) T GlobalT;
+  return (T *)(GlobalT *)reinterpret_cast<uint64_t>(p);
+}
+
+// load_dfa_batched in rounds of kBatch loads per lane, from a table address
+// read out of memory (a descriptor): the global address space is restated
+// so the loads are global, not flat, loads.
+template <int kThreads, int kBatch>
+__device__ __forceinline__ void load_dfa_rounds(uint32_t *s_dfa, const uint32_t *table, int tid) {
+  const uint32_t *const t = as_global(table);
+  constexpr int kIters = (kDfaEntries + kThreads - 1) / kThreads;
+#pragma unroll
+  for (int j0 = 0; j0 < kIters; j0 += kBatch) {
+    uint32_t v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int i = tid + (j0 + j) * kThreads;
+      v[j] = (j0 + j < kIters && i < kDfaEntries) ? t[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int i = tid + (j0 + j) * kThreads;
+      if (j0 + j < kIters && i < kDfaEntries) s_dfa[i] = dfa_entry_in_range(v[j]);
+    }
+  }
+}
+
 // The table in two halves -- loads into registers, then LDS stores -- so a
 // kernel can issue other loads in between and overlap their round trips.
 template <int kThreads>
