@@ -556,7 +556,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   const int tid = threadIdx.x;
   if (tid < kEdgeDwords) s_edge[tid] = 0u;
   constexpr uint32_t kBlockBytes = (uint32_t)kThreads * kChunkBytes;
-  for (int task = blockIdx.x; task < n_tasks; task += gridDim.x) {
+  // Task order.  Several tensors: the workgroups of XCD x (workgroups are
+  // dealt to the 8 XCDs round robin) take the x-th eighth of the task list,
+  // strided over them, so a tensor's tasks share one XCD's L2 and its table
+  // is fetched from HBM about once instead of once per XCD.  One tensor, or
+  // a grid that is not a multiple of 8: tasks strided over the whole grid.
+  constexpr int kXcds = 8;
+  int task = blockIdx.x, task_end = n_tasks, task_step = gridDim.x;
+  if (count > 1 && gridDim.x % kXcds == 0) {
+    const int x = blockIdx.x % kXcds, per = gridDim.x / kXcds;
+    task = (int)(((int64_t)x * n_tasks) / kXcds) + (int)(blockIdx.x / kXcds);
+    task_end = (int)(((int64_t)(x + 1) * n_tasks) / kXcds);
+    task_step = per;
+  }
+  for (; task < task_end; task += task_step) {
     // the tensor of this task: the last descriptor whose first task is <= it
     int lo = 0, hi = count - 1;
     while (lo < hi) {
