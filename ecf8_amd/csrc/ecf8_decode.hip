@@ -586,19 +586,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
       continue;
     const uint32_t n_bytes = (uint32_t)d.n_bytes;
     const int n_fb = (int)((n_bytes + kBlockBytes - 1) / kBlockBytes);
-    // One tensor: its tasks interleave the format-blocks (task r takes r,
-    // r + tasks, ...), so the workgroups running at the same time sweep the
-    // bytes in order, as the one-tensor kernel does.  Several tensors (an
-    // MoE layer): task r takes a contiguous run of blocks instead.
-    // Measured on MI355X: a whole MoE layer 263 -> 253 us contiguous, while
-    // one Qwen3-8B layer on the side stream loses 3 % contiguous.
+    // A tensor's tasks interleave its format-blocks (task r takes r,
+    // r + tasks, ...): its tasks run at the same time on one XCD (the order
+    // above), so together they sweep the tensor's bytes in order, as the
+    // one-tensor kernel's grid does.  Measured on MI355X, a whole
+    // Qwen3-30B-A3B layer (two rotated sets): 245.5 us with contiguous runs
+    // of blocks per task, 238.6 us interleaved.
     const int tasks = (n_fb + blocks_per_task - 1) / blocks_per_task;
     const int r = task - d.task_begin;
     if (r >= tasks) continue;
-    const bool contiguous = count > 1;  // uniform
-    const int fb_first = contiguous ? r * blocks_per_task : r;
-    const int fb_step = contiguous ? 1 : tasks;
-    const int fb_last = contiguous ? min(n_fb, (r + 1) * blocks_per_task) : n_fb;
     // the previous task ended with a barrier: no wave still reads s_dfa.
     // The table loads in dfa_blocks, seven per lane in flight (two round
     // trips instead of thirteen), overlapped with the first block's.
@@ -606,8 +602,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
                       as_global(d.packed_other_4bits),
                       as_global(reinterpret_cast<const uint32_t *>(d.output_positions)),
                       as_global(d.gaps), as_global(d.outputs), (uint32_t)d.n_elements};
-    dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, fb_first,
-                                fb_step, fb_last, as_global(d.table));
+    dfa_blocks<kThreads, false>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap, r, tasks, n_fb,
+                                as_global(d.table));
   }
 }
 

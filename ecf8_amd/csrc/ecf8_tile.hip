@@ -100,97 +100,121 @@ __device__ __forceinline__ u32x4 seg_other(const TileOperand &t, uint32_t s, int
 }
 
 // Byte i (0..15) of the lane's chunk window, shifted into a table offset
-// (byte << 2), from its little-endian dwords.
-template <int i>
-__device__ __forceinline__ uint32_t byte_off(const SegLoad &c) {
+// (byte << 2), from its little-endian dwords (i a constant after unrolling).
+__device__ __forceinline__ uint32_t byte_off(const SegLoad &c, int i) {
   const uint32_t d = i < 4 ? c.d0 : i < 8 ? c.d1 : i < 12 ? c.d2 : c.d3;
-  constexpr int sh = 8 * (i & 3);
+  const int sh = 8 * (i & 3);
   return sh >= 2 ? (d >> (sh - 2)) & 0x3FCu : (d << 2) & 0x3FCu;
 }
 
-// Decode one segment into the wave's staging area and return the lane's 32
-// exponents (symbol 32 lane + k in bits 4(k%8).. of component k/8).  The
-// staging area is all zero on entry and on return (each lane clears the
-// four dwords it read; symbols past 2048 go to the spill dwords, which are
-// never read).
-__device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t *s_dfa,
-                                                uint32_t *stage, int lane) {
-  const uint32_t gap = (c.gapw >> (4 * (lane & 7))) & 0xFu;
-  // start row: skip `gap` bits of byte 0, or (gap >= 8) take the entry that
-  // skips byte 0 into row gap - 8 (both computed, one selected)
-  const uint32_t a_in = (gap << 10) | byte_off<0>(c);
-  const uint32_t a_skip = (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
-  const uint32_t a0 = gap < 8 ? a_in : a_skip;
-  const uint32_t e0 = dfa_at(s_dfa, a0);
-  const uint32_t e1 = dfa_at(s_dfa, (e0 & kDfaRowMask) | byte_off<1>(c));
-  const uint32_t e2 = dfa_at(s_dfa, (e1 & kDfaRowMask) | byte_off<2>(c));
-  const uint32_t e3 = dfa_at(s_dfa, (e2 & kDfaRowMask) | byte_off<3>(c));
-  const uint32_t e4 = dfa_at(s_dfa, (e3 & kDfaRowMask) | byte_off<4>(c));
-  const uint32_t e5 = dfa_at(s_dfa, (e4 & kDfaRowMask) | byte_off<5>(c));
-  const uint32_t e6 = dfa_at(s_dfa, (e5 & kDfaRowMask) | byte_off<6>(c));
-  const uint32_t e7 = dfa_at(s_dfa, (e6 & kDfaRowMask) | byte_off<7>(c));
-  const uint32_t e8 = dfa_at(s_dfa, (e7 & kDfaRowMask) | byte_off<8>(c));
-  const uint32_t e9 = dfa_at(s_dfa, (e8 & kDfaRowMask) | byte_off<9>(c));
-  const uint32_t e10 = dfa_at(s_dfa, (e9 & kDfaRowMask) | byte_off<10>(c));
-  const uint32_t e11 = dfa_at(s_dfa, (e10 & kDfaRowMask) | byte_off<11>(c));
+// Decode N segments at once, segment j into the staging area stage + j *
+// kWaveStageDw, and return each lane's 32 exponents of each (symbol 32 lane
+// + k in bits 4(k%8).. of component k/8).  The N automaton walks are
+// independent chains of LDS lookups: issued interleaved, each one's round
+// trips hide the other's.  The staging areas are all zero on entry and on
+// return (each lane clears the four dwords it read; symbols past 2048 go to
+// the spill dwords, which are never read).
+template <int N>
+__device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uint32_t *s_dfa,
+                                                uint32_t *stage, int lane, uint4 (&ex)[N]) {
+  uint32_t e[N][12];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const uint32_t gap = (c[j].gapw >> (4 * (lane & 7))) & 0xFu;
+    // start row: skip `gap` bits of byte 0, or (gap >= 8) take the entry
+    // that skips byte 0 into row gap - 8 (both computed, one selected)
+    const uint32_t a_in = (gap << 10) | byte_off(c[j], 0);
+    const uint32_t a_skip = (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
+    e[j][0] = dfa_at(s_dfa, gap < 8 ? a_in : a_skip);
+  }
+#pragma unroll
+  for (int i = 1; i < 12; ++i)
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      e[j][i] = dfa_at(s_dfa, (e[j][i - 1] & kDfaRowMask) | byte_off(c[j], i));
   // a code still open at the chunk's end started in it: the chunk owns it,
   // and its symbol is the first one completed in look-ahead byte 12 or 13
-  const uint32_t row11 = e11 & kDfaRowMask;
-  const bool open = row11 >= ((uint32_t)kDfaFirstPendingRow << 10);
-  uint32_t e12 = dfa_at(s_dfa, row11 | byte_off<12>(c));
-  if (__builtin_amdgcn_ballot_w64(open && (e12 & 0xFFu) == 0)) {
-    const uint32_t e13 = dfa_at(s_dfa, (e12 & kDfaRowMask) | byte_off<13>(c));
-    if ((e12 & 0xFFu) == 0) e12 = e13;
+  uint32_t e12[N];
+  bool open[N], late = false;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const uint32_t row11 = e[j][11] & kDfaRowMask;
+    open[j] = row11 >= ((uint32_t)kDfaFirstPendingRow << 10);
+    e12[j] = dfa_at(s_dfa, row11 | byte_off(c[j], 12));
+    late = late || (open[j] && (e12[j] & 0xFFu) == 0);
   }
-  const uint32_t et = open ? ((e12 & 0xF0000u) | 4u) : 0u;
-  const bool live = lane < c.n_chunks;
-  // the count fields (bits 0..7, at most 16 each, bits 8..9 clear) summed
-  // by adding whole entries: 13 of them stay below 256, so the low byte of
-  // the sum is exact
-  const uint32_t s01 = e0 + e1, s23 = e2 + e3, s45 = e4 + e5, s67 = e6 + e7;
-  const uint32_t s89 = e8 + e9, sab = e10 + e11;
-  int cnt4 = (int)((s01 + s23 + s45 + s67 + s89 + sab + et) & 0xFFu);
-  if (!live) cnt4 = 0;
-  const int incl = wave_inclusive_scan(cnt4);
-  // a start past the real symbols (garbage decoded from the bytes after the
-  // segment) is clamped to the spill dwords' start; 12 entries of <= 16 bits
-  // plus 4 stay within them
-  uint32_t pos4 = min((uint32_t)(incl - cnt4), (uint32_t)kStageDw << 5);
-  auto put = [&](uint32_t syms, uint32_t n4) {
-    const uint64_t v = (uint64_t)syms << (pos4 & 31u);
-    uint32_t *const q = stage + (pos4 >> 5);
-    atomicOr(q, (uint32_t)v);
-    atomicOr(q + 1, (uint32_t)(v >> 32));
-    pos4 += n4;
-  };
-  auto put2 = [&](uint32_t ea, uint32_t eb, uint32_t sum) {
-    uint32_t t, syms;
-    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
-        "src1_sel:WORD_1"
-        : "=v"(t) : "v"(ea), "v"(eb));
-    asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
-        "src1_sel:WORD_1"
-        : "=v"(syms) : "v"(t), "v"(ea));
-    put(syms, sum & 0xFFu);
-  };
-  if (live) {
-    put2(e0, e1, s01);
-    put2(e2, e3, s23);
-    put2(e4, e5, s45);
-    put2(e6, e7, s67);
-    put2(e8, e9, s89);
-    put2(e10, e11, sab);
-    put(et >> 16, 0u);
+  if (__builtin_amdgcn_ballot_w64(late)) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const uint32_t e13 = dfa_at(s_dfa, (e12[j] & kDfaRowMask) | byte_off(c[j], 13));
+      if ((e12[j] & 0xFFu) == 0) e12[j] = e13;
+    }
+  }
+  int cnt4[N];
+  uint32_t et[N], s2[N][6];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    et[j] = open[j] ? ((e12[j] & 0xF0000u) | 4u) : 0u;
+    // the count fields (bits 0..7, at most 16 each, bits 8..9 clear) summed
+    // by adding whole entries: 13 of them stay below 256, so the low byte
+    // of the sum is exact
+#pragma unroll
+    for (int i = 0; i < 6; ++i) s2[j][i] = e[j][2 * i] + e[j][2 * i + 1];
+    const uint32_t sum = s2[j][0] + s2[j][1] + s2[j][2] + s2[j][3] + s2[j][4] + s2[j][5] + et[j];
+    cnt4[j] = lane < c[j].n_chunks ? (int)(sum & 0xFFu) : 0;
+  }
+  int incl[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) incl[j] = wave_inclusive_scan(cnt4[j]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    uint32_t *const st = stage + j * kWaveStageDw;
+    // a start past the real symbols (garbage decoded from the bytes after
+    // the segment) is clamped to the spill dwords' start; 12 entries of <=
+    // 16 bits plus 4 stay within them
+    uint32_t pos4 = min((uint32_t)(incl[j] - cnt4[j]), (uint32_t)kStageDw << 5);
+    auto put = [&](uint32_t syms, uint32_t n4) {
+      const uint64_t v = (uint64_t)syms << (pos4 & 31u);
+      uint32_t *const q = st + (pos4 >> 5);
+      atomicOr(q, (uint32_t)v);
+      atomicOr(q + 1, (uint32_t)(v >> 32));
+      pos4 += n4;
+    };
+    auto put2 = [&](uint32_t ea, uint32_t eb, uint32_t sum) {
+      uint32_t t, syms;
+      asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:WORD_1"
+          : "=v"(t) : "v"(ea), "v"(eb));
+      asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:WORD_1"
+          : "=v"(syms) : "v"(t), "v"(ea));
+      put(syms, sum & 0xFFu);
+    };
+    if (lane < c[j].n_chunks) {
+#pragma unroll
+      for (int i = 0; i < 6; ++i) put2(e[j][2 * i], e[j][2 * i + 1], s2[j][i]);
+      put(et[j] >> 16, 0u);
+    }
   }
   // the wave's own ORs complete before its lanes read the staged symbols
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  uint4 *const mine = reinterpret_cast<uint4 *>(stage) + lane;
-  const uint4 ex = *mine;
-  *mine = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    uint4 *const mine = reinterpret_cast<uint4 *>(stage + j * kWaveStageDw) + lane;
+    ex[j] = *mine;
+    *mine = make_uint4(0u, 0u, 0u, 0u);
+  }
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  return ex;
+}
+
+__device__ __forceinline__ uint4 decode_segment(const SegLoad &c, const uint32_t *s_dfa,
+                                                uint32_t *stage, int lane) {
+  const SegLoad cs[1] = {c};
+  uint4 ex[1];
+  decode_segments<1>(cs, s_dfa, stage, lane, ex);
+  return ex[0];
 }
 
 // Operand address of the panel `panel` (16 output columns) of the fused
@@ -317,6 +341,9 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 // 24.6 KB + 1 KB staging per wave + RED x waves KB of partial sums; MI355X,
 // Qwen3-30B-A3B experts at 16 tokens: down 58.2 us at G = 1, RED = 4 and
 // 51.7 us at G = 2, RED = 2).
+#ifndef ECF8_TILE_DENSE16_RED
+#define ECF8_TILE_DENSE16_RED 4
+#endif
 #ifndef ECF8_TILE_DENSE8_RED
 #define ECF8_TILE_DENSE8_RED 2
 #endif
@@ -329,6 +356,7 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 #ifndef ECF8_TILE_MOE4_GROUPS
 #define ECF8_TILE_MOE4_GROUPS 2
 #endif
+constexpr int kDense16Red = ECF8_TILE_DENSE16_RED;
 constexpr int kDense8Red = ECF8_TILE_DENSE8_RED, kMoeRed = ECF8_TILE_MOE_RED;
 constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_GROUPS;
 
@@ -341,6 +369,17 @@ constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_
 #endif
 constexpr int kPrefetch = ECF8_TILE_PREFETCH;
 static_assert(kPrefetch >= 1 && kPrefetch <= 3, "prefetch distance");
+// Steps a wave decodes at once (interleaved automaton walks), then
+// multiplies one after the other in step order.  One: on MI355X two
+// measured slower (Qwen3-8B layer at M = 16: 81.9 us at 1, 92.8 at 2;
+// Qwen3-30B-A3B down projection 52.3 vs 67.9 us) -- the same VALU work per
+// step, 120+ VGPRs (6 -> 4 waves per SIMD where LDS allowed 6) and scalar
+// registers spilled to VGPR lanes, for no latency left to hide.
+#ifndef ECF8_TILE_PAIR
+#define ECF8_TILE_PAIR 1
+#endif
+constexpr int kPair = ECF8_TILE_PAIR;
+static_assert(kPair == 1 || kPair == 2, "steps per pass");
 
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
@@ -393,10 +432,10 @@ struct TileMoeArgs {
 template <int WAVES, int G, int RED, bool kMoe>
 __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
     typename std::conditional<kMoe, TileMoeArgs, TileDenseArgs>::type a) {
-  constexpr int P = kPrefetch, NB = kPrefetch + 1, HW = WAVES * G;
+  constexpr int P = kPrefetch, NB = kPrefetch + 1, HW = WAVES * G, S = kPair;
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
   __shared__ uint32_t s_dfa[kDfaEntries];
-  __shared__ __attribute__((aligned(16))) uint32_t s_stage[HW][kWaveStageDw];
+  __shared__ __attribute__((aligned(16))) uint32_t s_stage[HW][S * kWaveStageDw];
   __shared__ __attribute__((aligned(16))) float s_part[RED][G][WAVES][256];
   const int lane = threadIdx.x & 63;
   const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -448,12 +487,13 @@ __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
   }
   const int ng = (kgroups + WAVES - 1) / WAVES;
   const int n_real = ((n_panels - 1 - vwg0) / vgrid + 1) * ng;  // the first group's steps
-  // a multiple of NB steps (trailing ones past the last panel compute
-  // nothing), so the unrolled loop's back edge always follows its last copy
-  const int n_steps = (n_real + NB - 1) / NB * NB;
+  // a multiple of NB passes of S steps (trailing ones past the last panel
+  // compute nothing), so the unrolled loop's back edge always follows its
+  // last copy
+  const int n_steps = (n_real + NB * S - 1) / (NB * S) * (NB * S);
 
-  // steps t .. t+P+1: sc[0] is the step being computed
-  Step sc[P + 2];
+  // passes t .. t+P+1 (S steps each): sc[0..S-1] is the pass being computed
+  Step sc[(P + 2) * S];
   int pan = vwg, u = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
     const Step st = step_at(walk, pan, u, wave, WAVES, kgroups, n_panels);
@@ -464,32 +504,37 @@ __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
     return st;
   };
 #pragma unroll
-  for (int i = 0; i < P + 1; ++i) sc[i] = next_step();
+  for (int i = 0; i < (P + 1) * S; ++i) sc[i] = next_step();
 
-  // prologue: offsets of steps 0..P, the automaton table, then the windows
-  // and nibbles of steps 0..P-1 -- issued in that order so their round trips
-  // overlap
-  uint32_t m[NB];
-  SegLoad w[NB];
-  u32x4 o[NB];
-  float wsv[NB];
+  // prologue: offsets of passes 0..P, the automaton table, then the windows
+  // and nibbles of passes 0..P-1 -- issued in that order so their round
+  // trips overlap
+  uint32_t m[NB][S];
+  SegLoad w[NB][S];
+  u32x4 o[NB][S];
+  float wsv[NB][S];
 #pragma unroll
-  for (int i = 0; i < NB; ++i) m[i] = step_meta(sc[i], kgroups, lane);
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < S; ++j) m[i][j] = step_meta(sc[i * S + j], kgroups, lane);
   issue_order();
   DfaLoad<HW * 64> dfa;
   dfa.load(table, threadIdx.x);
   issue_order();
+  auto issue_window = [&](const Step &sl, uint32_t mv, SegLoad &wv, u32x4 &ov, float &sv) {
+    const uint32_t si = (uint32_t)sl.p * (uint32_t)kgroups + (uint32_t)sl.kg;
+    wv = seg_window(sl.op, si, __builtin_amdgcn_readlane(mv, 0), __builtin_amdgcn_readlane(mv, 1),
+                    lane);
+    ov = seg_other(sl.op, si, lane);
+    sv = __int_as_float(__builtin_amdgcn_readlane(mv, 2));
+  };
 #pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const uint32_t si = (uint32_t)sc[i].p * (uint32_t)kgroups + (uint32_t)sc[i].kg;
-    w[i] = seg_window(sc[i].op, si, __builtin_amdgcn_readlane(m[i], 0),
-                      __builtin_amdgcn_readlane(m[i], 1), lane);
-    o[i] = seg_other(sc[i].op, si, lane);
-    wsv[i] = __int_as_float(__builtin_amdgcn_readlane(m[i], 2));
-  }
+  for (int i = 0; i < P; ++i)
+#pragma unroll
+    for (int j = 0; j < S; ++j) issue_window(sc[i * S + j], m[i][j], w[i][j], o[i][j], wsv[i][j]);
   issue_order();
   dfa.store(s_dfa, threadIdx.x);
-  for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
+  for (int i = lane; i < S * kWaveStageDw; i += 64) stage[i] = 0u;
   lds_barrier();
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -526,73 +571,85 @@ __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
     pending = 0;
   };
 
-  // step t, the k-th copy in the unrolled loop (k = t mod NB): compute from
-  // buffer k, load step t+P's window into buffer (k+P) mod NB from its
-  // offsets m[(k+P) mod NB], and step t+P+1's offsets into m[(k+P+1) mod NB]
-  auto step = [&](int t, auto kc) {
+  // pass t (steps t..t+S-1), the k-th copy in the unrolled loop: decode
+  // from buffer k, load pass t+P's windows into buffer (k+P) mod NB from
+  // their offsets m[(k+P) mod NB], and pass t+P+1's offsets into
+  // m[(k+P+1) mod NB]; then the steps' products, in step order
+  auto pass = [&](int t, auto kc) {
     constexpr int k = decltype(kc)::value;
     constexpr int kl = (k + P) % NB, km = (k + P + 1) % NB;
-    // activations of this step (L2-resident), issued first
+    // activations of this pass (L2-resident), issued first
     issue_order();
-    uint4 av0 = *reinterpret_cast<const uint4 *>(arow + sc[0].kg * kGroup);
-    uint4 av1 = *reinterpret_cast<const uint4 *>(arow + sc[0].kg * kGroup + 64);
-    float sav[4];
+    uint4 av[S][2];
+    float sav[S][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sav[i] = as[srow[i] + (uint32_t)sc[0].kg];
-    issue_order();
-    sc[P + 1] = next_step();
-    m[km] = step_meta(sc[P + 1], kgroups, lane);
-    issue_order();
-    {
-      const Step &sl = sc[P];
-      const uint32_t sl_s = (uint32_t)sl.p * (uint32_t)kgroups + (uint32_t)sl.kg;
-      w[kl] = seg_window(sl.op, sl_s, __builtin_amdgcn_readlane(m[kl], 0),
-                         __builtin_amdgcn_readlane(m[kl], 1), lane);
-      o[kl] = seg_other(sl.op, sl_s, lane);
-      wsv[kl] = __int_as_float(__builtin_amdgcn_readlane(m[kl], 2));
+    for (int j = 0; j < S; ++j) {
+      av[j][0] = *reinterpret_cast<const uint4 *>(arow + sc[j].kg * kGroup);
+      av[j][1] = *reinterpret_cast<const uint4 *>(arow + sc[j].kg * kGroup + 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sav[j][i] = as[srow[i] + (uint32_t)sc[j].kg];
     }
     issue_order();
-    if (sc[0].valid) {
-      const uint4 ex = decode_segment(w[k], s_dfa, stage, lane);
-      if (!row_ok) av0 = av1 = make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sav[i] = srow_ok[i] ? sav[i] : 0.f;
-      const uint2 w0 = merge8(ex.x, o[k].x), w1 = merge8(ex.y, o[k].y);
-      const uint2 w2 = merge8(ex.z, o[k].z), w3 = merge8(ex.w, o[k].w);
-      v4f d = {0.f, 0.f, 0.f, 0.f};
-      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-          (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
-          0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-          (long)(((uint64_t)av0.w << 32) | av0.z), (long)(((uint64_t)w1.y << 32) | w1.x), d, 0,
-          0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-          (long)(((uint64_t)av1.y << 32) | av1.x), (long)(((uint64_t)w2.y << 32) | w2.x), d, 0,
-          0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-          (long)(((uint64_t)av1.w << 32) | av1.z), (long)(((uint64_t)w3.y << 32) | w3.x), d, 0,
-          0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[i] * wsv[k], acc[i]);
+    for (int j = 0; j < S; ++j) {
+      sc[(P + 1) * S + j] = next_step();
+      m[km][j] = step_meta(sc[(P + 1) * S + j], kgroups, lane);
     }
-    if (sc[0].closes) {  // the panel's last step (all groups at once): park its partial sums
+    issue_order();
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s_part[pending][group][wave][i * 64 + lane] = acc[i];
-        acc[i] = 0.f;
+    for (int j = 0; j < S; ++j)
+      issue_window(sc[P * S + j], m[kl][j], w[kl][j], o[kl][j], wsv[kl][j]);
+    issue_order();
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < S; ++j) any = any || sc[j].valid;
+    uint4 ex[S];
+    if (any) decode_segments<S>(w[k], s_dfa, stage, lane, ex);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      if (sc[j].valid) {
+        uint4 av0 = av[j][0], av1 = av[j][1];
+        if (!row_ok) av0 = av1 = make_uint4(0, 0, 0, 0);
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = srow_ok[i] ? sav[j][i] : 0.f;
+        const uint2 w0 = merge8(ex[j].x, o[k][j].x), w1 = merge8(ex[j].y, o[k][j].y);
+        const uint2 w2 = merge8(ex[j].z, o[k][j].z), w3 = merge8(ex[j].w, o[k][j].w);
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
+            0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av0.w << 32) | av0.z), (long)(((uint64_t)w1.y << 32) | w1.x), d, 0,
+            0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av1.y << 32) | av1.x), (long)(((uint64_t)w2.y << 32) | w2.x), d, 0,
+            0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            (long)(((uint64_t)av1.w << 32) | av1.z), (long)(((uint64_t)w3.y << 32) | w3.x), d, 0,
+            0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sv[i] * wsv[k][j], acc[i]);
       }
-      ++pending;
-      if (pending == RED || t == n_real - 1) reduce();
+      if (sc[j].closes) {  // the panel's last step (all groups at once): park its partial sums
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s_part[pending][group][wave][i * 64 + lane] = acc[i];
+          acc[i] = 0.f;
+        }
+        ++pending;
+        if (pending == RED || t + j == n_real - 1) reduce();
+      }
     }
 #pragma unroll
-    for (int i = 0; i < P + 1; ++i) sc[i] = sc[i + 1];
+    for (int i = 0; i < (P + 1) * S; ++i) sc[i] = sc[i + S];
   };
 
-  for (int t = 0; t < n_steps; t += NB) {
-    step(t, std::integral_constant<int, 0>{});
-    if constexpr (NB > 1) step(t + 1, std::integral_constant<int, 1 % NB>{});
-    if constexpr (NB > 2) step(t + 2, std::integral_constant<int, 2 % NB>{});
-    if constexpr (NB > 3) step(t + 3, std::integral_constant<int, 3 % NB>{});
+  for (int t = 0; t < n_steps; t += NB * S) {
+    pass(t, std::integral_constant<int, 0>{});
+    if constexpr (NB > 1) pass(t + S, std::integral_constant<int, 1 % NB>{});
+    if constexpr (NB > 2) pass(t + 2 * S, std::integral_constant<int, 2 % NB>{});
+    if constexpr (NB > 3) pass(t + 3 * S, std::integral_constant<int, 3 % NB>{});
   }
 }
 
@@ -721,9 +778,10 @@ extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int6
   const TileDenseArgs args{a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels};
   int grid = 0, rc;
   if (waves == 16) {
-    rc = resident_grid(tile_linear16_kernel<16, 1, 4, false>, 1024, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<16, 1, kDense16Red, false>, 1024, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<16, 1, 4, false><<<(unsigned)grid, 1024, 0, as_stream(stream)>>>(args);
+    tile_linear16_kernel<16, 1, kDense16Red, false><<<(unsigned)grid, 1024, 0,
+                                                      as_stream(stream)>>>(args);
   } else {
     rc = resident_grid(tile_linear16_kernel<8, 1, kDense8Red, false>, 512, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
