@@ -302,25 +302,30 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// One step of a wave's walk: panel blockIdx.x + j * gridDim.x (j = 0..),
-// group kg = wave + u * WAVES (u = 0..ng-1, the same ng for every wave; a
-// step past the last group or panel computes nothing and reads in-bounds
-// clamped addresses).  Wave-uniform.
+// One step of a hardware wave's walk: a panel of the group's walk and one
+// K group of it, kg = v + u * WAVES -- step u of virtual wave v, the wave
+// of the FP8 linear that sums group kg (a step past the last group or
+// panel computes nothing and reads in-bounds clamped addresses).
+// Wave-uniform.
 struct Step {
   TileOperand op;
-  int p, col;   // panel index inside the operand, its first output column
-  int kg;       // group, 0 when past the last one
-  bool valid;   // a real panel and group: decoded and multiplied
-  bool closes;  // the panel's last step (u = ng - 1): its partial sums are parked
+  int p, col;    // panel index inside the operand, its first output column
+  int kg;        // group, 0 when past the last one
+  int v;         // virtual wave whose partial sums this step adds to
+  bool valid;    // a real panel and group: decoded and multiplied
+  bool vcloses;  // v's last step of the panel: its partial sums are parked
+  bool closes;   // the hardware wave's last step of the panel
 };
 
 template <class Walk>
-__device__ __forceinline__ Step step_at(const Walk &walk, int panel, int u, int wave,
-                                        int waves, int kgroups, int n_panels) {
+__device__ __forceinline__ Step step_at(const Walk &walk, int panel, int v, int u, int waves,
+                                        int kgroups, int n_panels, bool vcloses, bool closes) {
   Step st;
-  const int kg = wave + u * waves;
+  const int kg = v + u * waves;
   st.valid = panel < n_panels && kg < kgroups;
-  st.closes = (u + 1) * waves >= kgroups;
+  st.v = v;
+  st.vcloses = vcloses;
+  st.closes = closes;
   walk.at(panel < n_panels ? panel : n_panels - 1, st.op, st.p, st.col);
   st.kg = kg < kgroups ? kg : 0;
   return st;
@@ -356,7 +361,15 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 #ifndef ECF8_TILE_MOE4_GROUPS
 #define ECF8_TILE_MOE4_GROUPS 2
 #endif
-constexpr int kDense16Red = ECF8_TILE_DENSE16_RED;
+// Packed four-wave shape (three hardware waves per FP8 workgroup): G = 4,
+// twelve waves -- a multiple of the CU's four SIMDs.  On MI355X,
+// Qwen3-30B-A3B down projection at 16 tokens: 49.1 us packed at G = 4
+// against 52.9 unpacked; 71.4 at G = 2 and 74.9 at G = 3 (six and nine
+// waves per workgroup load the SIMDs unevenly).
+#ifndef ECF8_TILE_MOE4P_GROUPS
+#define ECF8_TILE_MOE4P_GROUPS 4
+#endif
+constexpr int kDense16Red = ECF8_TILE_DENSE16_RED, kMoe4PGroups = ECF8_TILE_MOE4P_GROUPS;
 constexpr int kDense8Red = ECF8_TILE_DENSE8_RED, kMoeRed = ECF8_TILE_MOE_RED;
 constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_GROUPS;
 
@@ -384,12 +397,22 @@ static_assert(kPair == 1 || kPair == 2, "steps per pass");
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
 //
-// A workgroup runs G groups of WAVES waves; group g is the FP8 linear's
-// workgroup number blockIdx.x * G + g of a grid G times larger: it takes
-// those panels and sums each in that workgroup's wave order, so the result
-// does not depend on G (more waves per CU for shapes whose FP8 workgroup is
-// small).  The groups walk in lockstep (a group out of panels walks empty
-// steps), so every wave reaches the same barriers.
+// A workgroup runs G groups of HWW hardware waves; group g is the FP8
+// linear's workgroup number blockIdx.x * G + g of a grid G times larger: it
+// takes those panels and sums each in the order of that workgroup's WAVES
+// waves, so the result does not depend on G (more waves per CU for shapes
+// whose FP8 workgroup is small).  The groups walk in lockstep (a group out
+// of panels walks empty steps), so every wave reaches the same barriers.
+//
+// HWW = WAVES: hardware wave w is the FP8 linear's wave w (groups w,
+// w + WAVES, ...; when WAVES does not divide the groups, the last step of
+// some waves is empty).  HWW < WAVES (packed): the FP8 waves' steps, wave
+// by wave, are dealt to the hardware waves in equal runs that never split
+// a wave's steps (the host checks), so a hardware wave may run several FP8
+// waves one after the other, each from a zero sum, parking each one's
+// partial sums in its own slot: the same products, sums and reduction --
+// e.g. K = 768, six groups over four FP8 waves (two, two, one, one) -- run
+// on three hardware waves of two steps each with no empty step.
 //
 // Each wave walks its steps (segments) as a software pipeline: while it
 // decodes step t, the code windows and nibbles of steps t+1..t+P (P =
@@ -429,17 +452,19 @@ struct TileMoeArgs {
   int K, ldo, n_segs, seg_n;
 };
 
-template <int WAVES, int G, int RED, bool kMoe>
-__global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
+template <int WAVES, int HWW, int G, int RED, bool kMoe>
+__global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
     typename std::conditional<kMoe, TileMoeArgs, TileDenseArgs>::type a) {
-  constexpr int P = kPrefetch, NB = kPrefetch + 1, HW = WAVES * G, S = kPair;
+  constexpr int P = kPrefetch, NB = kPrefetch + 1, HW = HWW * G, S = kPair;
+  constexpr bool kPacked = HWW != WAVES;
+  static_assert(HWW <= WAVES, "at most one hardware wave per FP8 wave");
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
   __shared__ uint32_t s_dfa[kDfaEntries];
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[HW][S * kWaveStageDw];
   __shared__ __attribute__((aligned(16))) float s_part[RED][G][WAVES][256];
   const int lane = threadIdx.x & 63;
   const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int group = hw / WAVES, wave = hw % WAVES;
+  const int group = hw / HWW, hwave = hw % HWW;
   const int K = a.K, kgroups = K / kGroup;
   // the workgroup's rows, operands and table (uniform)
   int M, row0 = 0, n_panels;
@@ -486,7 +511,30 @@ __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
     srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
   }
   const int ng = (kgroups + WAVES - 1) / WAVES;
-  const int n_real = ((n_panels - 1 - vwg0) / vgrid + 1) * ng;  // the first group's steps
+  // steps per panel of each hardware wave, and (packed) step q's FP8 wave
+  // and its step in that wave: position hwave * spw + q of the FP8 waves'
+  // steps listed wave by wave (the first `full` waves have ng steps, the
+  // others ng - 1)
+  const int spw = kPacked ? kgroups / HWW : ng;
+  constexpr int kMaxSpw = kPacked ? 2 : 1;
+  int pv[kMaxSpw], pu[kMaxSpw];
+  bool pvc[kMaxSpw];
+  if constexpr (kPacked) {
+    const int full = kgroups % WAVES ? kgroups % WAVES : WAVES;
+#pragma unroll
+    for (int q = 0; q < kMaxSpw; ++q) {
+      const int sp = hwave * spw + q;
+      const bool long_wave = sp < full * ng;
+      const int n_v = long_wave ? ng : ng - 1;
+      const int base = long_wave ? 0 : full * ng;
+      const int v0 = long_wave ? 0 : full;
+      const int d = n_v > 0 ? n_v : 1;
+      pv[q] = v0 + (sp - base) / d;
+      pu[q] = (sp - base) % d;
+      pvc[q] = pu[q] == n_v - 1;
+    }
+  }
+  const int n_real = ((n_panels - 1 - vwg0) / vgrid + 1) * spw;  // the first group's steps
   // a multiple of NB passes of S steps (trailing ones past the last panel
   // compute nothing), so the unrolled loop's back edge always follows its
   // last copy
@@ -494,11 +542,19 @@ __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
 
   // passes t .. t+P+1 (S steps each): sc[0..S-1] is the pass being computed
   Step sc[(P + 2) * S];
-  int pan = vwg, u = 0;  // cursor of the step after the last in sc
+  int pan = vwg, q = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
-    const Step st = step_at(walk, pan, u, wave, WAVES, kgroups, n_panels);
-    if (++u == ng) {
-      u = 0;
+    const bool last = q == spw - 1;
+    Step st;
+    if constexpr (kPacked) {
+      const bool q1 = q > 0;  // spw <= 2
+      st = step_at(walk, pan, q1 ? pv[1] : pv[0], q1 ? pu[1] : pu[0], WAVES, kgroups, n_panels,
+                   q1 ? pvc[1] : pvc[0], last);
+    } else {
+      st = step_at(walk, pan, hwave, q, WAVES, kgroups, n_panels, last, last);
+    }
+    if (++q == spw) {
+      q = 0;
       pan += vgrid;
     }
     return st;
@@ -631,12 +687,14 @@ __global__ __launch_bounds__(WAVES * G * 64) void tile_linear16_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sv[i] * wsv[k][j], acc[i]);
       }
-      if (sc[j].closes) {  // the panel's last step (all groups at once): park its partial sums
+      if (sc[j].vcloses) {  // the FP8 wave's last step of the panel: park its partial sums
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          s_part[pending][group][wave][i * 64 + lane] = acc[i];
+          s_part[pending][group][sc[j].v][i * 64 + lane] = acc[i];
           acc[i] = 0.f;
         }
+      }
+      if (sc[j].closes) {  // the panel's last step (all groups at once)
         ++pending;
         if (pending == RED || t + j == n_real - 1) reduce();
       }
@@ -735,6 +793,24 @@ int resident_grid(Kernel kernel, int threads, int64_t work, int *grid) {
   return ECF8_OK;
 }
 
+// Whether the steps of `waves` FP8 waves over `kgroups` groups (wave v
+// takes groups v, v + waves, ...), listed wave by wave, deal to `hw`
+// hardware waves in equal runs of at most two steps that split no wave's
+// steps, every wave having at least one.
+bool packs(int waves, int hw, int kgroups) {
+  if (hw <= 0 || kgroups < waves || kgroups % hw || kgroups / hw > 2) return false;
+  const int spw = kgroups / hw, ng = (kgroups + waves - 1) / waves;
+  const int full = kgroups % waves ? kgroups % waves : waves;
+  int first = 0;  // position of wave v's first step
+  for (int v = 0; v < waves; ++v) {
+    const int n_v = v < full ? ng : ng - 1;
+    for (int b = first + 1; b < first + n_v; ++b)
+      if (b % spw == 0) return false;  // a run would start inside wave v's steps
+    first += n_v;
+  }
+  return true;
+}
+
 int check_operand(const ecf8_tile_operand &t) {
   if (!t.stream || !t.seg_off || !t.gaps || !t.other || !t.weight_scale) return ECF8_ERR_INVALID_ARG;
   if (!aligned(t.stream, 4) || !aligned(t.seg_off, 4) || !aligned(t.gaps, 4) ||
@@ -778,15 +854,15 @@ extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int6
   const TileDenseArgs args{a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels};
   int grid = 0, rc;
   if (waves == 16) {
-    rc = resident_grid(tile_linear16_kernel<16, 1, kDense16Red, false>, 1024, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<16, 16, 1, kDense16Red, false>, 1024, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<16, 1, kDense16Red, false><<<(unsigned)grid, 1024, 0,
-                                                      as_stream(stream)>>>(args);
+    tile_linear16_kernel<16, 16, 1, kDense16Red, false><<<(unsigned)grid, 1024, 0,
+                                                          as_stream(stream)>>>(args);
   } else {
-    rc = resident_grid(tile_linear16_kernel<8, 1, kDense8Red, false>, 512, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<8, 8, 1, kDense8Red, false>, 512, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<8, 1, kDense8Red, false><<<(unsigned)grid, 512, 0, as_stream(stream)>>>(
-        args);
+    tile_linear16_kernel<8, 8, 1, kDense8Red, false><<<(unsigned)grid, 512, 0,
+                                                       as_stream(stream)>>>(args);
   }
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
@@ -828,10 +904,15 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
     kernel<<<dim3((unsigned)wgs, (unsigned)n_experts), threads, 0, as_stream(stream)>>>(args);
     return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
   };
-  return eight ? launch(tile_linear16_kernel<8, kMoe8Groups, kMoeRed, true>, 512 * kMoe8Groups,
-                        kMoe8Groups)
-               : launch(tile_linear16_kernel<4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
-                        kMoe4Groups);
+  if (eight)
+    return launch(tile_linear16_kernel<8, 8, kMoe8Groups, kMoeRed, true>, 512 * kMoe8Groups,
+                  kMoe8Groups);
+  // four FP8 waves whose steps pack onto three hardware waves (K = 768)
+  if (packs(4, 3, (int)(K / kGroup)))
+    return launch(tile_linear16_kernel<4, 3, kMoe4PGroups, kMoeRed, true>, 192 * kMoe4PGroups,
+                  kMoe4PGroups);
+  return launch(tile_linear16_kernel<4, 4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
+                kMoe4Groups);
 }
 
 extern "C" int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *table,
