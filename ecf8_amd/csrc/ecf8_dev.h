@@ -14,13 +14,17 @@ namespace dev {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// (a & m) | (b & ~m) as one v_bfi_b32.  Written out, the compiler expands
-// it to two ANDs and an OR when m is a constant (gfx9 VOP3 takes no literal
-// operand, so the mask comes from an SGPR).
-__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
-  return r;
+// (a & M) | (b & ~M) as one v_bfi_b32.  The constant mask reaches the
+// compiler as an opaque SGPR value (one s_mov): with a visible constant it
+// expands the expression to ANDs and an OR.  The v_bfi_b32 itself is the
+// compiler's own instruction, not inline asm, so the hazard recognizer sees
+// its VGPR write -- an MFMA that reads a VGPR right after a VALU op wrote it
+// needs wait states the recognizer inserts only for instructions it knows.
+template <uint32_t M>
+__device__ __forceinline__ uint32_t bfi(uint32_t a, uint32_t b) {
+  uint32_t m;
+  asm("s_mov_b32 %0, %1" : "=s"(m) : "i"(M));
+  return (a & m) | (b & ~m);
 }
 
 // 8 FP8 bytes from 8 exponent nibbles (E, element k in bits 4k..4k+3) and
@@ -28,10 +32,10 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint2 merge8(uint32_t e, uint32_t o) {
   // even elements 2j: sign = O_j bit 7, exponent = E_j low nibble,
   // mantissa = O_j bits 4..6
-  const uint32_t h = bfi(0x80808080u, o, bfi(0x78787878u, e << 3, o >> 4));
+  const uint32_t h = bfi<0x80808080u>(o, bfi<0x78787878u>(e << 3, o >> 4));
   // odd elements 2j+1: sign = O_j bit 3, exponent = E_j high nibble,
   // mantissa = O_j bits 0..2
-  const uint32_t l = bfi(0x80808080u, o << 4, bfi(0x78787878u, e >> 1, o));
+  const uint32_t l = bfi<0x80808080u>(o << 4, bfi<0x78787878u>(e >> 1, o));
   uint2 r;
   r.x = __builtin_amdgcn_perm(h, l, 0x01050004u);  // h0 l0 h1 l1
   r.y = __builtin_amdgcn_perm(h, l, 0x03070206u);  // h2 l2 h3 l3

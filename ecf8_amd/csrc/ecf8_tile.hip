@@ -69,6 +69,18 @@ __device__ __forceinline__ uint32_t f32_bf16(float f) {
   return u >> 16;
 }
 
+// 8 FP8 bytes -- operand elements 8r..8r+7 of a lane, as two dwords of 4
+// -- from its staged exponent dword E (elements 0..3 in the even nibbles,
+// 4..7 in the odd ones) and nibble dword O (byte j = o_j << 4 | o_{j+4},
+// o = sign << 3 | mantissa): the run order of the layout needs no byte
+// interleave.
+__device__ __forceinline__ uint2 merge8_runs(uint32_t e, uint32_t o) {
+  uint2 r;
+  r.x = bfi<0x80808080u>(o, bfi<0x78787878u>(e << 3, o >> 4));
+  r.y = bfi<0x80808080u>(o << 4, bfi<0x78787878u>(e >> 1, o));
+  return r;
+}
+
 // A segment's code window: 16 bytes from the lane's chunk start (12 + look-
 // ahead) and the gap word holding the lane's nibble.
 struct SegLoad {
@@ -100,11 +112,37 @@ __device__ __forceinline__ u32x4 seg_other(const TileOperand &t, uint32_t s, int
 }
 
 // Byte i (0..15) of the lane's chunk window, shifted into a table offset
-// (byte << 2), from its little-endian dwords (i a constant after unrolling).
+// (byte << 2), from its little-endian dwords (i a constant after
+// unrolling): one SDWA shift that selects the byte.
 __device__ __forceinline__ uint32_t byte_off(const SegLoad &c, int i) {
   const uint32_t d = i < 4 ? c.d0 : i < 8 ? c.d1 : i < 12 ? c.d2 : c.d3;
-  const int sh = 8 * (i & 3);
-  return sh >= 2 ? (d >> (sh - 2)) & 0x3FCu : (d << 2) & 0x3FCu;
+  uint32_t r;
+  switch (i & 3) {
+    case 0:
+      asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:BYTE_0" : "=v"(r) : "v"(d));
+      break;
+    case 1:
+      asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:BYTE_1" : "=v"(r) : "v"(d));
+      break;
+    case 2:
+      asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:BYTE_2" : "=v"(r) : "v"(d));
+      break;
+    default:
+      asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+          "src1_sel:BYTE_3" : "=v"(r) : "v"(d));
+      break;
+  }
+  return r;
+}
+
+// The automaton entry after `e` on the byte at table offset `off`: the
+// entry's next row (bits 10..14) and the offset (bits 2..9) merged by one
+// v_bfi_b32 -- the only VALU op between two lookups of a walk.
+__device__ __forceinline__ uint32_t dfa_next(const uint32_t *s_dfa, uint32_t e, uint32_t off) {
+  return dfa_at(s_dfa, bfi<kDfaRowMask>(e, off));
 }
 
 // Decode N segments at once, segment j into the staging area stage + j *
@@ -131,7 +169,7 @@ __device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uin
   for (int i = 1; i < 12; ++i)
 #pragma unroll
     for (int j = 0; j < N; ++j)
-      e[j][i] = dfa_at(s_dfa, (e[j][i - 1] & kDfaRowMask) | byte_off(c[j], i));
+      e[j][i] = dfa_next(s_dfa, e[j][i - 1], byte_off(c[j], i));
   // a code still open at the chunk's end started in it: the chunk owns it,
   // and its symbol is the first one completed in look-ahead byte 12 or 13
   uint32_t e12[N];
@@ -140,13 +178,13 @@ __device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uin
   for (int j = 0; j < N; ++j) {
     const uint32_t row11 = e[j][11] & kDfaRowMask;
     open[j] = row11 >= ((uint32_t)kDfaFirstPendingRow << 10);
-    e12[j] = dfa_at(s_dfa, row11 | byte_off(c[j], 12));
+    e12[j] = dfa_next(s_dfa, e[j][11], byte_off(c[j], 12));
     late = late || (open[j] && (e12[j] & 0xFFu) == 0);
   }
   if (__builtin_amdgcn_ballot_w64(late)) {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-      const uint32_t e13 = dfa_at(s_dfa, (e12[j] & kDfaRowMask) | byte_off(c[j], 13));
+      const uint32_t e13 = dfa_next(s_dfa, e12[j], byte_off(c[j], 13));
       if ((e12[j] & 0xFFu) == 0) e12[j] = e13;
     }
   }
@@ -168,17 +206,21 @@ __device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uin
   for (int j = 0; j < N; ++j) incl[j] = wave_inclusive_scan(cnt4[j]);
 #pragma unroll
   for (int j = 0; j < N; ++j) {
-    uint32_t *const st = stage + j * kWaveStageDw;
-    // a start past the real symbols (garbage decoded from the bytes after
-    // the segment) is clamped to the spill dwords' start; 12 entries of <=
-    // 16 bits plus 4 stay within them
-    uint32_t pos4 = min((uint32_t)(incl[j] - cnt4[j]), (uint32_t)kStageDw << 5);
+    // the staging area's LDS byte address x 8, plus the lane's first bit:
+    // a bit address, whose dword is (bit >> 3) & ~3 (the area is dword
+    // aligned).  A start past the real symbols (garbage decoded from the
+    // bytes after the segment) is clamped to the spill dwords' start; 12
+    // entries of <= 16 bits plus 4 stay within them
+    typedef __attribute__((address_space(3))) uint32_t LdsU32;
+    const uint32_t st_bits =
+        (uint32_t)(uintptr_t)(LdsU32 *)(stage + j * kWaveStageDw) << 3;
+    uint32_t bit = st_bits + min((uint32_t)(incl[j] - cnt4[j]), (uint32_t)kStageDw << 5);
     auto put = [&](uint32_t syms, uint32_t n4) {
-      const uint64_t v = (uint64_t)syms << (pos4 & 31u);
-      uint32_t *const q = st + (pos4 >> 5);
+      const uint64_t v = (uint64_t)syms << (bit & 31u);
+      uint32_t *const q = (uint32_t *)(LdsU32 *)(uintptr_t)((bit >> 3) & ~3u);
       atomicOr(q, (uint32_t)v);
       atomicOr(q + 1, (uint32_t)(v >> 32));
-      pos4 += n4;
+      bit += n4;
     };
     auto put2 = [&](uint32_t ea, uint32_t eb, uint32_t sum) {
       uint32_t t, syms;
@@ -669,8 +711,10 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
         float sv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[i] = srow_ok[i] ? sav[j][i] : 0.f;
-        const uint2 w0 = merge8(ex[j].x, o[k][j].x), w1 = merge8(ex[j].y, o[k][j].y);
-        const uint2 w2 = merge8(ex[j].z, o[k][j].z), w3 = merge8(ex[j].w, o[k][j].w);
+        const uint2 w0 = merge8_runs(ex[j].x, o[k][j].x);
+        const uint2 w1 = merge8_runs(ex[j].y, o[k][j].y);
+        const uint2 w2 = merge8_runs(ex[j].z, o[k][j].z);
+        const uint2 w3 = merge8_runs(ex[j].w, o[k][j].w);
         v4f d = {0.f, 0.f, 0.f, 0.f};
         d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
             (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
@@ -758,8 +802,8 @@ __global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
     const SegLoad c = seg_window(op, s, op.seg_off[s], op.seg_off[s + 1], lane);
     const u32x4 oth = seg_other(op, s, lane);
     const uint4 ex = decode_segment(c, s_dfa, stage, lane);
-    const uint2 w0 = merge8(ex.x, oth.x), w1 = merge8(ex.y, oth.y);
-    const uint2 w2 = merge8(ex.z, oth.z), w3 = merge8(ex.w, oth.w);
+    const uint2 w0 = merge8_runs(ex.x, oth.x), w1 = merge8_runs(ex.y, oth.y);
+    const uint2 w2 = merge8_runs(ex.z, oth.z), w3 = merge8_runs(ex.w, oth.w);
     const uint32_t p = s / kgroups, kg = s % kgroups;
     uint8_t *const row = out + (size_t)(p * 16 + r) * K + kg * kGroup + 16 * g;
     __builtin_nontemporal_store(u32x4{w0.x, w0.y, w1.x, w1.y}, reinterpret_cast<u32x4 *>(row));

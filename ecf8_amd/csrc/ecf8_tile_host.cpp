@@ -21,12 +21,13 @@ using namespace ecf8;
 
 namespace {
 
-// Element (row, column) of symbol i of segment (panel p, group kg).
+// Element (row, column) of symbol i of segment (panel p, group kg): lane
+// i / 32's operand element m = tile_operand_elem(i % 32).
 inline void tile_element(int64_t p, int64_t kg, int i, int64_t *row, int64_t *col) {
-  const int lane = i / kTileLaneSymbols, j = i % kTileLaneSymbols;
+  const int lane = i / kTileLaneSymbols, m = tile_operand_elem(i % kTileLaneSymbols);
   const int r = lane & 15, q = lane >> 4;
   *row = p * kTileRows + r;
-  *col = kg * kTileGroup + (j < 16 ? 16 * q + j : 64 + 16 * q + (j - 16));
+  *col = kg * kTileGroup + (m < 16 ? 16 * q + m : 64 + 16 * q + (m - 16));
 }
 
 inline int exponent_of(uint8_t b) { return (b >> 3) & 0xF; }

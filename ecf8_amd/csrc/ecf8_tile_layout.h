@@ -6,10 +6,16 @@
 // framing change, so that one wave decodes exactly the B operands of the
 // MFMAs it runs.  Segment s = p * (K / 128) + kg holds the 2048 elements of
 // the 16 x 128 tile (rows 16p.., columns 128kg..) in MFMA lane order: symbol
-// 32 l + j is row 16p + (l & 15), column 128kg + c(j) with
-// c(j) = 16 (l >> 4) + j for j < 16 and 64 + 16 (l >> 4) + (j - 16) for
-// j >= 16 -- lane l's operands of v_mfma_f32_16x16x32_fp8_fp8 for the four
-// K32 slices of the group, in the order the FP8 linear feeds them.
+// 32 l + j is lane l's operand element m = tile_operand_elem(j), row
+// 16p + (l & 15), column 128kg + c(m) with c(m) = 16 (l >> 4) + m for
+// m < 16 and 64 + 16 (l >> 4) + (m - 16) for m >= 16 -- lane l's operands
+// of v_mfma_f32_16x16x32_fp8_fp8 for the four K32 slices of the group, in
+// the order the FP8 linear feeds them.  Within each run of 8 symbols the
+// elements come in the order 0, 4, 1, 5, 2, 6, 3, 7: the lane's staged
+// exponent dword then holds elements 0..3 in its even nibbles and 4..7 in
+// its odd ones, and each nibble byte holds elements j and j + 4, so two
+// shift-and-insert pairs place them straight into the operand's two dwords
+// (no byte interleave).
 //
 //   stream  u8     segment s's codes (MSB-first, as the reference's
 //                  bitstream) at byte seg_off[s], 4-byte aligned, then 16
@@ -42,6 +48,10 @@ constexpr int kTileMaxSegBytes = kTileLanes * kTileChunkBytes;  // 768
 constexpr int kTileGapWords = kTileLanes / 8;                   // 8
 constexpr int kTileOtherBytes = kTileSegSymbols / 2;            // 1024
 constexpr int kTilePadBytes = 16;
+
+// Operand element (0..31) of a lane's symbol j (0..31): runs of 8 in the
+// order 0, 4, 1, 5, 2, 6, 3, 7.
+constexpr int tile_operand_elem(int j) { return (j & ~7) | ((j & 1) << 2) | ((j & 7) >> 1); }
 
 // Bytes a segment of `bits` code bits occupies (4-byte aligned).
 inline int64_t tile_segment_bytes(int64_t bits) { return (((bits + 7) >> 3) + 3) & ~int64_t(3); }

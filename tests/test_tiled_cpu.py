@@ -22,10 +22,15 @@ from oracle import codec as oc
 ROWS, GROUP, LANES, LANE_SYMS, CHUNK = 16, 128, 64, 32, 12
 
 
+# a lane's symbols, in runs of 8, are its operand elements 0, 4, 1, 5, 2, 6, 3, 7
+_RUN = (0, 4, 1, 5, 2, 6, 3, 7)
+
+
 def _element(p, kg, i):
     lane, j = divmod(i, LANE_SYMS)
+    m = 8 * (j // 8) + _RUN[j % 8]
     r, q = lane & 15, lane >> 4
-    col = kg * GROUP + (16 * q + j if j < 16 else 64 + 16 * q + (j - 16))
+    col = kg * GROUP + (16 * q + m if m < 16 else 64 + 16 * q + (m - 16))
     return p * ROWS + r, col
 
 
