@@ -165,11 +165,28 @@ __device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uin
     const uint32_t a_skip = (uint32_t)(kDfaSkipByte * 4) + ((gap - 8) << 2);
     e[j][0] = dfa_at(s_dfa, gap < 8 ? a_in : a_skip);
   }
+  // each pair of entries, once both are in: its symbols (entry b's after
+  // entry a's count) and its count field sum, so the pair's two entries
+  // need not stay live until the staging
+  uint32_t sy[N][6], s2[N][6];
+  auto pair = [&](int j, int i) {
+    const uint32_t ea = e[j][2 * i], eb = e[j][2 * i + 1];
+    uint32_t t;
+    asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+        "src1_sel:WORD_1"
+        : "=v"(t) : "v"(ea), "v"(eb));
+    asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+        "src1_sel:WORD_1"
+        : "=v"(sy[j][i]) : "v"(t), "v"(ea));
+    s2[j][i] = ea + eb;
+  };
 #pragma unroll
   for (int i = 1; i < 12; ++i)
 #pragma unroll
-    for (int j = 0; j < N; ++j)
+    for (int j = 0; j < N; ++j) {
       e[j][i] = dfa_next(s_dfa, e[j][i - 1], byte_off(c[j], i));
+      if (i & 1) pair(j, i >> 1);
+    }
   // a code still open at the chunk's end started in it: the chunk owns it,
   // and its symbol is the first one completed in look-ahead byte 12 or 13
   uint32_t e12[N];
@@ -189,15 +206,13 @@ __device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uin
     }
   }
   int cnt4[N];
-  uint32_t et[N], s2[N][6];
+  uint32_t et[N];
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     et[j] = open[j] ? ((e12[j] & 0xF0000u) | 4u) : 0u;
     // the count fields (bits 0..7, at most 16 each, bits 8..9 clear) summed
     // by adding whole entries: 13 of them stay below 256, so the low byte
     // of the sum is exact
-#pragma unroll
-    for (int i = 0; i < 6; ++i) s2[j][i] = e[j][2 * i] + e[j][2 * i + 1];
     const uint32_t sum = s2[j][0] + s2[j][1] + s2[j][2] + s2[j][3] + s2[j][4] + s2[j][5] + et[j];
     cnt4[j] = lane < c[j].n_chunks ? (int)(sum & 0xFFu) : 0;
   }
@@ -222,19 +237,9 @@ __device__ __forceinline__ void decode_segments(const SegLoad (&c)[N], const uin
       atomicOr(q + 1, (uint32_t)(v >> 32));
       bit += n4;
     };
-    auto put2 = [&](uint32_t ea, uint32_t eb, uint32_t sum) {
-      uint32_t t, syms;
-      asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
-          "src1_sel:WORD_1"
-          : "=v"(t) : "v"(ea), "v"(eb));
-      asm("v_or_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
-          "src1_sel:WORD_1"
-          : "=v"(syms) : "v"(t), "v"(ea));
-      put(syms, sum & 0xFFu);
-    };
     if (lane < c[j].n_chunks) {
 #pragma unroll
-      for (int i = 0; i < 6; ++i) put2(e[j][2 * i], e[j][2 * i + 1], s2[j][i]);
+      for (int i = 0; i < 6; ++i) put(sy[j][i], s2[j][i] & 0xFFu);
       put(et[j] >> 16, 0u);
     }
   }
@@ -387,9 +392,10 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 // workgroups per workgroup (G), chosen for waves per CU (LDS: automaton
 // 24.6 KB + 1 KB staging per wave + RED x waves KB of partial sums; MI355X,
 // Qwen3-30B-A3B experts at 16 tokens: down 58.2 us at G = 1, RED = 4 and
-// 51.7 us at G = 2, RED = 2).
+// 51.7 us at G = 2, RED = 2).  The sixteen-wave dense shape takes RED = 2:
+// 74 KB, two workgroups per CU.
 #ifndef ECF8_TILE_DENSE16_RED
-#define ECF8_TILE_DENSE16_RED 4
+#define ECF8_TILE_DENSE16_RED 2
 #endif
 #ifndef ECF8_TILE_DENSE8_RED
 #define ECF8_TILE_DENSE8_RED 2
@@ -415,15 +421,25 @@ constexpr int kDense16Red = ECF8_TILE_DENSE16_RED, kMoe4PGroups = ECF8_TILE_MOE4
 constexpr int kDense8Red = ECF8_TILE_DENSE8_RED, kMoeRed = ECF8_TILE_MOE_RED;
 constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_GROUPS;
 
-// Steps whose loads are in flight during a decode.  One suffices: a step's
-// decode outlasts the memory round trip, and on MI355X distances 2 and 3
-// measured slower (Qwen3-8B layer at M = 16: 81.0 us at 1, 90.2 at 2,
-// 89.3 at 3) -- more registers and code for no latency left to hide.
+// Steps ahead a wave loads a segment's window and nibbles (P) and its
+// offsets (at least P + 1).  None and one: the kernel fits 64 VGPRs, so
+// the sixteen-wave dense shape runs two workgroups (eight waves per SIMD)
+// per CU and the waves hide each other's round trips; the decode is then
+// mostly VALU-bound (counters on the Qwen3-8B gate/up at M = 16: VALU busy
+// 66 % at four waves per SIMD with a step of prefetch, 74 % at eight
+// without).  MI355X, Qwen3-8B layer at M = 16: 77.2 us against 78.5 with a
+// step of prefetch (75 VGPRs, four waves per SIMD); offsets two steps ahead
+// spill at 64 VGPRs (92.6 us); prefetch distances 2 and 3 at four waves
+// per SIMD measured slower still (90.2 and 89.3 us against 81.0 at 1).
 #ifndef ECF8_TILE_PREFETCH
-#define ECF8_TILE_PREFETCH 1
+#define ECF8_TILE_PREFETCH 0
 #endif
 constexpr int kPrefetch = ECF8_TILE_PREFETCH;
-static_assert(kPrefetch >= 1 && kPrefetch <= 3, "prefetch distance");
+#ifndef ECF8_TILE_META_AHEAD
+#define ECF8_TILE_META_AHEAD 1
+#endif
+constexpr int kMetaAhead = ECF8_TILE_META_AHEAD;
+static_assert(kPrefetch >= 0 && kPrefetch <= 3, "prefetch distance");
 // Steps a wave decodes at once (interleaved automaton walks), then
 // multiplies one after the other in step order.  One: on MI355X two
 // measured slower (Qwen3-8B layer at M = 16: 81.9 us at 1, 92.8 at 2;
@@ -435,6 +451,12 @@ static_assert(kPrefetch >= 1 && kPrefetch <= 3, "prefetch distance");
 #endif
 constexpr int kPair = ECF8_TILE_PAIR;
 static_assert(kPair == 1 || kPair == 2, "steps per pass");
+// The sign/mantissa nibbles of a step loaded with its activations, at the
+// step itself (1), or a step ahead with its code window (0).
+#ifndef ECF8_TILE_OTH_NOW
+#define ECF8_TILE_OTH_NOW 0
+#endif
+constexpr bool kOthNow = ECF8_TILE_OTH_NOW;
 
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
@@ -494,10 +516,22 @@ struct TileMoeArgs {
   int K, ldo, n_segs, seg_n;
 };
 
+// Waves per SIMD the register allocation targets: eight (64 VGPRs), so
+// LDS alone bounds the workgroups per CU.
+#ifndef ECF8_TILE_WPE
+#define ECF8_TILE_WPE 8
+#endif
 template <int WAVES, int HWW, int G, int RED, bool kMoe>
-__global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
+__global__ __launch_bounds__(HWW * G * 64) __attribute__((amdgpu_waves_per_eu(ECF8_TILE_WPE)))
+void tile_linear16_kernel(
     typename std::conditional<kMoe, TileMoeArgs, TileDenseArgs>::type a) {
-  constexpr int P = kPrefetch, NB = kPrefetch + 1, HW = HWW * G, S = kPair;
+  // P: passes ahead a window is loaded; MD: passes ahead its offsets are
+  // (two would keep the offsets a pass reads from being the youngest load,
+  // whose wait also waits for the previous pass's output stores, but costs
+  // the registers of a second ring entry); NB: buffers of each ring and
+  // copies of the unrolled loop
+  constexpr int P = kPrefetch, MD = kPrefetch + 1 > kMetaAhead ? kPrefetch + 1 : kMetaAhead;
+  constexpr int NB = MD, HW = HWW * G, S = kPair;
   constexpr bool kPacked = HWW != WAVES;
   static_assert(HWW <= WAVES, "at most one hardware wave per FP8 wave");
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
@@ -536,22 +570,18 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
   const float *const as = a.as;
 
   // the lane's A-operand row and the 4 output rows whose scales it applies;
-  // rows past M read the first row and are zeroed before use
+  // rows past M read the first row: an MFMA output row depends on its own A
+  // row only, and rows past M are never stored, so they need no masking
   auto a_row = [&](int rr) -> uint32_t {
     const int q = row0 + (rr < M ? rr : 0);
     if constexpr (kMoe) return (uint32_t)(a.row_of ? a.row_of[q] : q);
     return (uint32_t)q;
   };
   const int r = lane & 15, g = lane >> 4;
-  const bool row_ok = r < M;
   const uint8_t *const arow = a.aq + (size_t)a_row(r) * K + 16 * g;
   uint32_t srow[4];
-  bool srow_ok[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    srow_ok[i] = 4 * g + i < M;
-    srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
-  }
+  for (int i = 0; i < 4; ++i) srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
   const int ng = (kgroups + WAVES - 1) / WAVES;
   // steps per panel of each hardware wave, and (packed) step q's FP8 wave
   // and its step in that wave: position hwave * spw + q of the FP8 waves'
@@ -582,8 +612,8 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
   // last copy
   const int n_steps = (n_real + NB * S - 1) / (NB * S) * (NB * S);
 
-  // passes t .. t+P+1 (S steps each): sc[0..S-1] is the pass being computed
-  Step sc[(P + 2) * S];
+  // passes t .. t+MD (S steps each): sc[0..S-1] is the pass being computed
+  Step sc[(MD + 1) * S];
   int pan = vwg, q = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
     const bool last = q == spw - 1;
@@ -602,11 +632,11 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
     return st;
   };
 #pragma unroll
-  for (int i = 0; i < (P + 1) * S; ++i) sc[i] = next_step();
+  for (int i = 0; i < MD * S; ++i) sc[i] = next_step();
 
-  // prologue: offsets of passes 0..P, the automaton table, then the windows
-  // and nibbles of passes 0..P-1 -- issued in that order so their round
-  // trips overlap
+  // prologue: offsets of passes 0..MD-1, the automaton table, then the
+  // windows and nibbles of passes 0..P-1 -- issued in that order so their
+  // round trips overlap
   uint32_t m[NB][S];
   SegLoad w[NB][S];
   u32x4 o[NB][S];
@@ -623,7 +653,7 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
     const uint32_t si = (uint32_t)sl.p * (uint32_t)kgroups + (uint32_t)sl.kg;
     wv = seg_window(sl.op, si, __builtin_amdgcn_readlane(mv, 0), __builtin_amdgcn_readlane(mv, 1),
                     lane);
-    ov = seg_other(sl.op, si, lane);
+    if constexpr (!kOthNow) ov = seg_other(sl.op, si, lane);
     sv = __int_as_float(__builtin_amdgcn_readlane(mv, 2));
   };
 #pragma unroll
@@ -675,13 +705,24 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
   // m[(k+P+1) mod NB]; then the steps' products, in step order
   auto pass = [&](int t, auto kc) {
     constexpr int k = decltype(kc)::value;
-    constexpr int kl = (k + P) % NB, km = (k + P + 1) % NB;
-    // activations of this pass (L2-resident), issued first
+    constexpr int kl = (k + P) % NB, km = (k + MD) % NB;
     issue_order();
+    if constexpr (P == 0) {
+      // no prefetch: this pass's windows first, from offsets loaded a pass
+      // ago (read into scalars here, before m is reused below)
+#pragma unroll
+      for (int j = 0; j < S; ++j) issue_window(sc[j], m[k][j], w[k][j], o[k][j], wsv[k][j]);
+      issue_order();
+    }
+    // activations of this pass (L2-resident)
     uint4 av[S][2];
     float sav[S][4];
+    u32x4 on[S];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
+      if constexpr (kOthNow)
+        on[j] = seg_other(sc[j].op, (uint32_t)sc[j].p * (uint32_t)kgroups + (uint32_t)sc[j].kg,
+                          lane);
       av[j][0] = *reinterpret_cast<const uint4 *>(arow + sc[j].kg * kGroup);
       av[j][1] = *reinterpret_cast<const uint4 *>(arow + sc[j].kg * kGroup + 64);
 #pragma unroll
@@ -690,13 +731,15 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
     issue_order();
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      sc[(P + 1) * S + j] = next_step();
-      m[km][j] = step_meta(sc[(P + 1) * S + j], kgroups, lane);
+      sc[MD * S + j] = next_step();
+      m[km][j] = step_meta(sc[MD * S + j], kgroups, lane);
     }
     issue_order();
+    if constexpr (P > 0) {
 #pragma unroll
-    for (int j = 0; j < S; ++j)
-      issue_window(sc[P * S + j], m[kl][j], w[kl][j], o[kl][j], wsv[kl][j]);
+      for (int j = 0; j < S; ++j)
+        issue_window(sc[P * S + j], m[kl][j], w[kl][j], o[kl][j], wsv[kl][j]);
+    }
     issue_order();
     bool any = false;
 #pragma unroll
@@ -706,15 +749,10 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (sc[j].valid) {
-        uint4 av0 = av[j][0], av1 = av[j][1];
-        if (!row_ok) av0 = av1 = make_uint4(0, 0, 0, 0);
-        float sv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = srow_ok[i] ? sav[j][i] : 0.f;
-        const uint2 w0 = merge8_runs(ex[j].x, o[k][j].x);
-        const uint2 w1 = merge8_runs(ex[j].y, o[k][j].y);
-        const uint2 w2 = merge8_runs(ex[j].z, o[k][j].z);
-        const uint2 w3 = merge8_runs(ex[j].w, o[k][j].w);
+        const uint4 av0 = av[j][0], av1 = av[j][1];
+        const u32x4 ok = kOthNow ? on[j] : o[k][j];
+        const uint2 w0 = merge8_runs(ex[j].x, ok.x), w1 = merge8_runs(ex[j].y, ok.y);
+        const uint2 w2 = merge8_runs(ex[j].z, ok.z), w3 = merge8_runs(ex[j].w, ok.w);
         v4f d = {0.f, 0.f, 0.f, 0.f};
         d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
             (long)(((uint64_t)av0.y << 32) | av0.x), (long)(((uint64_t)w0.y << 32) | w0.x), d, 0,
@@ -729,7 +767,7 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
             (long)(((uint64_t)av1.w << 32) | av1.z), (long)(((uint64_t)w3.y << 32) | w3.x), d, 0,
             0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sv[i] * wsv[k][j], acc[i]);
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[i], sav[j][i] * wsv[k][j], acc[i]);
       }
       if (sc[j].vcloses) {  // the FP8 wave's last step of the panel: park its partial sums
 #pragma unroll
@@ -744,7 +782,7 @@ __global__ __launch_bounds__(HWW * G * 64) void tile_linear16_kernel(
       }
     }
 #pragma unroll
-    for (int i = 0; i < (P + 1) * S; ++i) sc[i] = sc[i + S];
+    for (int i = 0; i < MD * S; ++i) sc[i] = sc[i + S];
   };
 
   for (int t = 0; t < n_steps; t += NB * S) {
