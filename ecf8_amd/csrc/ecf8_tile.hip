@@ -439,6 +439,17 @@ constexpr int kPrefetch = ECF8_TILE_PREFETCH;
 #define ECF8_TILE_META_AHEAD 1
 #endif
 constexpr int kMetaAhead = ECF8_TILE_META_AHEAD;
+// Without prefetch, each pass issues the next pass's window right after its
+// own decode (it then overlaps the MFMAs and the reduction, and is not live
+// across a decode), and the prologue the first one, behind the automaton's
+// loads.  MI355X, same-box alternation: Qwen3-8B layer at M = 16 75.1-75.3
+// us against 76.1-76.3 with each window issued at its own step; grouped
+// down projection 43.4 against 44.3 us (the sixteen-wave shape spills 12
+// bytes per lane around the MFMAs and is still faster).
+#ifndef ECF8_TILE_LATE
+#define ECF8_TILE_LATE 1
+#endif
+constexpr bool kLateWindow = ECF8_TILE_LATE;
 static_assert(kPrefetch >= 0 && kPrefetch <= 3, "prefetch distance");
 // Steps a wave decodes at once (interleaved automaton walks), then
 // multiplies one after the other in step order.  One: on MI355X two
@@ -531,7 +542,8 @@ void tile_linear16_kernel(
   // the registers of a second ring entry); NB: buffers of each ring and
   // copies of the unrolled loop
   constexpr int P = kPrefetch, MD = kPrefetch + 1 > kMetaAhead ? kPrefetch + 1 : kMetaAhead;
-  constexpr int NB = MD, HW = HWW * G, S = kPair;
+  constexpr bool kLate = P == 0 && kLateWindow;
+  constexpr int NB = kLate ? 2 : MD, HW = HWW * G, S = kPair;
   constexpr bool kPacked = HWW != WAVES;
   static_assert(HWW <= WAVES, "at most one hardware wave per FP8 wave");
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
@@ -642,7 +654,7 @@ void tile_linear16_kernel(
   u32x4 o[NB][S];
   float wsv[NB][S];
 #pragma unroll
-  for (int i = 0; i < NB; ++i)
+  for (int i = 0; i < MD; ++i)
 #pragma unroll
     for (int j = 0; j < S; ++j) m[i][j] = step_meta(sc[i * S + j], kgroups, lane);
   issue_order();
@@ -660,6 +672,10 @@ void tile_linear16_kernel(
   for (int i = 0; i < P; ++i)
 #pragma unroll
     for (int j = 0; j < S; ++j) issue_window(sc[i * S + j], m[i][j], w[i][j], o[i][j], wsv[i][j]);
+  if constexpr (kLate) {
+#pragma unroll
+    for (int j = 0; j < S; ++j) issue_window(sc[j], m[0][j], w[0][j], o[0][j], wsv[0][j]);
+  }
   issue_order();
   dfa.store(s_dfa, threadIdx.x);
   for (int i = lane; i < S * kWaveStageDw; i += 64) stage[i] = 0u;
@@ -707,7 +723,7 @@ void tile_linear16_kernel(
     constexpr int k = decltype(kc)::value;
     constexpr int kl = (k + P) % NB, km = (k + MD) % NB;
     issue_order();
-    if constexpr (P == 0) {
+    if constexpr (P == 0 && !kLate) {
       // no prefetch: this pass's windows first, from offsets loaded a pass
       // ago (read into scalars here, before m is reused below)
 #pragma unroll
@@ -746,6 +762,16 @@ void tile_linear16_kernel(
     for (int j = 0; j < S; ++j) any = any || sc[j].valid;
     uint4 ex[S];
     if (any) decode_segments<S>(w[k], s_dfa, stage, lane, ex);
+    if constexpr (kLate) {
+      // the next pass's windows, into the other buffer: in flight during
+      // this pass's MFMAs and reduction
+      constexpr int kn = (k + 1) % NB;
+      issue_order();
+#pragma unroll
+      for (int j = 0; j < S; ++j)
+        issue_window(sc[MD * S + j], m[kn][j], w[kn][j], o[kn][j], wsv[kn][j]);
+      issue_order();
+    }
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (sc[j].valid) {
