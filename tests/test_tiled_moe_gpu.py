@@ -7,7 +7,8 @@ compressed as its own block and re-tiled under its own code:
 * ecf8_tile_moe_linear -- routed experts decoding their weight operands on
   the fly -- is bit-identical to ecf8_moe_linear over the decoded experts,
   for gate/up (token rows gathered, 8 waves) and down (one row per sorted
-  pair, 4 waves), 1, 5 and 16 routed tokens, any workgroup split;
+  pair, 4 waves: packed on three hardware waves at K = 768, unpacked at
+  K = 1024), 1, 5 and 16 routed tokens, any workgroup split;
 * a re-tiled small MoE model generates the FP8 model's tokens and logits,
   eager and graph-replayed;
 * it refuses what it cannot run.
@@ -120,6 +121,58 @@ def test_tile_moe_linear_is_bit_identical_to_the_fp8_grouped_linear(experts, cud
     rows = M * TOP_K
     assert torch.equal(got[:rows], ref[:rows]), which
     assert bool((got[rows:] == 7.0).all()) and bool((got[:, N:] == 7.0).all())
+    assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
+
+
+@pytest.fixture(scope="module")
+def wide_experts(cuda_device):
+    """Eight experts of intermediate 1024: the down projection's K = 1024
+    gives the FP8 grouped linear four waves of two groups each, which run
+    unpacked (K = 768's six groups run packed on three hardware waves)."""
+    from dfloat.compress import compress_flat
+    from ecf8_amd.decode import build_table
+    from ecf8_amd.synth import flat_block, synthetic_block
+    from ecf8_amd.tiled import TiledOperand, code_from_luts, tile_encode
+
+    inter = 1024
+    dense, ops, tables = [], [], []
+    for e in range(8):
+        w = synthetic_block({"down_proj": (H, inter, 0.02)}, seed=700 + e)
+        res = compress_flat(flat_block(w)[0])
+        tables.append(build_table(res["luts"].contiguous().to(cuda_device)))
+        bits, vals = code_from_luts(res["luts"])
+        wt, sc = w["down_proj"]
+        ops.append(TiledOperand(tile_encode(wt, bits, vals), sc, wt.shape[0], wt.shape[1],
+                                cuda_device))
+        dense.append((wt.to(cuda_device), sc.to(cuda_device)))
+    return dense, ops, tables, inter
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_unpacked_four_wave_down_projection_is_bit_identical(wide_experts, cuda_device, M):
+    from ecf8_amd import llm_kernels as K
+    from ecf8_amd.llm_kernels import MoeLinearPlan
+    from ecf8_amd.tiled import TileMoePlan
+
+    dense, ops, tables, inter = wide_experts
+    n_exp, top_k = len(ops), 4
+    g = torch.Generator().manual_seed(90 + M)
+    r = K.MoeRouting(16, top_k, n_exp, cuda_device)
+    r.topk_idx[:M] = torch.stack([torch.randperm(n_exp, generator=g)[:top_k]
+                                  for _ in range(M)]).to(torch.int32).to(cuda_device)
+    r.topk_w[:M] = torch.rand(M, top_k, generator=g).to(cuda_device)
+    K.moe_group(r, M)
+    P = 16 * top_k
+    aq, as_ = _acts(P, inter, 40 + M, cuda_device)
+    ref = torch.full((P, H + 8), 7.0, dtype=torch.bfloat16, device=cuda_device)
+    got = ref.clone()
+    MoeLinearPlan([[d] for d in dense], ref)(aq, as_, r, False, M=M)
+    _say(f"[tiled-moe] unpacked down K={inter} M={M}")
+    TileMoePlan([[o] for o in ops], tables, got)(aq, as_, r, False, M=M)
+    torch.cuda.synchronize()
+    rows = M * top_k
+    assert torch.equal(got[:rows], ref[:rows])
+    assert bool((got[rows:] == 7.0).all()) and bool((got[:, H:] == 7.0).all())
     assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
 
 
