@@ -12,8 +12,11 @@
  *
  * Layout (N a multiple of 16, K of 128): segment s = p * (K/128) + kg holds
  * the 16 x 128 tile of rows 16p.., columns 128kg.. in MFMA lane order --
- * symbol 32 l + j is row 16p + (l & 15), column 128kg + 16 (l >> 4) + j
- * (j < 16) or 128kg + 64 + 16 (l >> 4) + (j - 16) (j >= 16).
+ * symbol 32 l + j is lane l's operand element m, row 16p + (l & 15),
+ * column 128kg + 16 (l >> 4) + m (m < 16) or 128kg + 64 + 16 (l >> 4) +
+ * (m - 16) (m >= 16), where m runs 0, 4, 1, 5, 2, 6, 3, 7 within each
+ * run of 8 symbols (m = (j & ~7) | (j & 1) << 2 | (j & 7) >> 1): each
+ * nibble byte then holds operand elements j and j + 4 of its run.
  *   stream   u8       each segment's codes, MSB-first, 4-byte aligned,
  *                     then 16 padding bytes
  *   seg_off  u32[S+1] segment byte offsets; seg_off[S] = end of the codes
