@@ -520,11 +520,13 @@ def dit_generate(args):
     one 1024x1024 image: 4096 latent tokens of 64 channels and 512 text
     tokens of 4096, embedded guidance 3.5, --dit-steps Euler steps at batch
     1; first with the FP8 weights resident, then with every block
-    ECF8-compressed and decoded by its forward-pre-hook.  Both runs must
+    ECF8-compressed and decoded by its forward-pre-hook, then with each
+    block's decode on a side stream one block ahead.  Every run must
     produce identical latents."""
     import torch
 
-    from ecf8_amd.dit import FluxConfig, compress_blocks, random_pipeline, timed_generate
+    from ecf8_amd.dit import (FluxConfig, compress_blocks, prefetch_blocks, random_pipeline,
+                              timed_generate)
     from dfloat.run.run import TensorManager
 
     dev = torch.device("cuda", 0)
@@ -537,12 +539,15 @@ def dit_generate(args):
     txt = torch.randn(1, 512, cfg.txt_dim, generator=g).to(torch.bfloat16).to(dev)
     pooled = torch.randn(1, cfg.pooled_dim, generator=g).to(torch.bfloat16).to(dev)
     results = {}
-    for mode in ("fp8", "ecf8"):
+    weights_exact = True
+    for mode in ("fp8", "ecf8", "ecf8_prefetch"):
         if mode == "ecf8":
             t0 = time.time()
             compress_blocks(pipe, drawn)
             torch.cuda.synchronize()
             print(f"[bench] blocks compressed in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+        if mode == "ecf8_prefetch":
+            prefetch_blocks(pipe, dev, workgroups_per_cu=args.prefetch_workgroups)
         TensorManager.clear_device()
         torch.cuda.empty_cache()
         timed_generate(pipe, lat, txt, pooled, 1, (64, 64))  # warm-up
@@ -552,27 +557,32 @@ def dit_generate(args):
         print(f"[bench] {mode}: {r['seconds']:.3f} s/image, peak {r['peak_mib']:.0f} MiB",
               file=sys.stderr, flush=True)
         results[mode] = r
-    same = torch.equal(results["fp8"]["latents"].view(torch.int16),
-                       results["ecf8"]["latents"].view(torch.int16))
-    diff = (results["fp8"]["latents"].float() - results["ecf8"]["latents"].float()).abs().max().item()
-    # the decode path's own claim, checked directly: every block's hook
-    # injects exactly its original FP8 weights
-    weights_exact = True
-    for blocks, dr in ((pipe.dit.blocks, drawn[0]), (pipe.dit.single_blocks, drawn[1])):
-        for i, blk in enumerate(blocks):
-            for hook in blk._forward_pre_hooks.values():
-                hook(blk, None)
-            for name, (w, _) in dr[i % len(dr)].items():
-                got = blk.get_submodule(name).weight.view(torch.uint8)
-                weights_exact &= torch.equal(got, w.view(torch.uint8).to(dev))
-    fp8, ecf8 = results["fp8"], results["ecf8"]
+        if mode == "ecf8":
+            # the decode path's own claim, checked directly: every block's
+            # hook injects exactly its original FP8 weights
+            for blocks, dr in ((pipe.dit.blocks, drawn[0]), (pipe.dit.single_blocks, drawn[1])):
+                for i, blk in enumerate(blocks):
+                    for hook in blk._forward_pre_hooks.values():
+                        hook(blk, None)
+                    for name, (w, _) in dr[i % len(dr)].items():
+                        got = blk.get_submodule(name).weight.view(torch.uint8)
+                        weights_exact &= torch.equal(got, w.view(torch.uint8).to(dev))
+    ecf8_modes = ("ecf8", "ecf8_prefetch")
+    fp8 = results["fp8"]
+    same = all(torch.equal(fp8["latents"].view(torch.int16), results[m]["latents"].view(torch.int16))
+               for m in ecf8_modes)
+    diff = max((fp8["latents"].float() - results[m]["latents"].float()).abs().max().item()
+               for m in ecf8_modes)
+    best = min(ecf8_modes, key=lambda m: results[m]["seconds"])
+    ecf8 = results[best]
 
     def summary(r):
         return {"seconds_per_image": round(r["seconds"], 3), "peak_mib": round(r["peak_mib"], 1),
                 "weights_mib": round(r["weights_mib"], 1)}
 
     line = {
-        "metric": "DiT s/image, FLUX.1-dev-shape 1024x1024 (ECF8-compressed blocks)",
+        "metric": "DiT s/image, FLUX.1-dev-shape 1024x1024 (ECF8-compressed blocks, fastest "
+                  "decode mode; config.ecf8_decode names it)",
         "value": round(ecf8["seconds"], 3),
         "unit": "s/image",
         "n_gpus": 1,
@@ -586,9 +596,15 @@ def dit_generate(args):
                    "steps": args.dit_steps, "guidance": 3.5,
                    "distinct_block_weights": args.distinct_layers,
                    "linears": "FP8 weights dequantized to bf16 per call + library bf16 GEMM",
-                   "attention": "bf16 operands, fp32 accumulation"},
+                   "attention": "bf16 operands, fp32 accumulation",
+                   "ecf8_decode": {
+                       "ecf8": "each block decoded in its forward-pre-hook",
+                       "ecf8_prefetch": "next block decoded on a side stream (two buffers, "
+                                        "a third for the last of an odd count)"}[best]},
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
+        "ecf8_mode": best,
+        "ecf8_modes": {m: summary(results[m]) for m in ecf8_modes},
         "ratio_vs_uncompressed": round(fp8["seconds"] / ecf8["seconds"], 4),
         "weights_bit_exact": bool(weights_exact),
         "identical_latents": same,
@@ -632,8 +648,8 @@ def e2e_child(workload: str, seed: int, timeout_s: float):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--copies", type=int, default=10, help="rotated input/output sets")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -700,13 +716,14 @@ def main():
         if rc:
             raise RuntimeError(f"decode failed with status {rc}")
 
+    # Warm-up straight into the timed region: the only gap between them is
+    # the synchronization.  The outputs are verified after timing (so they
+    # are the timed launches' own): verifying in between left the GPU idle
+    # for the host copy and compare, and the timed launches then paid its
+    # return from idle clocks (measured on MI355X: 72.5-73.3 us per launch
+    # instead of 68).
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    ok = verify()
-    if not ok:
-        print("[bench] decoded weights differ from the original FP8 bytes", file=sys.stderr)
-        sys.exit(1)
 
     # One event pair around the K back-to-back launches on the launch stream:
     # a step is exactly one decode kernel, so the average launch duration is
@@ -739,6 +756,10 @@ def main():
     torch.cuda.synchronize()
     launch_ms = [a.elapsed_time(b) for a, b in pairs]
     avg_launch_ms = sum(launch_ms) / len(launch_ms) if launch_ms else ms_per_step
+    ok = verify()
+    if not ok:
+        print("[bench] decoded weights differ from the original FP8 bytes", file=sys.stderr)
+        sys.exit(1)
 
     cpu = enc = None
     if not args.no_cpu_baseline and cpu_case is not None:
