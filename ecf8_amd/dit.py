@@ -377,6 +377,18 @@ def compress_blocks(pipe: FluxPipeline, drawn=None, threads_per_block: int = 512
     return pipe
 
 
+def prefetch_blocks(pipe: FluxPipeline, device=None, workgroups_per_cu: float = 2):
+    """Replace the compressed blocks' decode hooks by side-stream prefetch
+    (ecf8_amd/prefetch.py) over the blocks in forward order: the 19 double
+    blocks, then the 38 single blocks.  A block's decode (an HBM-bound
+    pass) then runs while the previous block's matrix-bound GEMMs and
+    attention run, instead of between them."""
+    from .prefetch import LayerPrefetcher
+
+    blocks = list(pipe.dit.blocks) + list(pipe.dit.single_blocks)
+    return LayerPrefetcher(blocks, device, workgroups_per_cu=workgroups_per_cu).install()
+
+
 def timed_generate(pipe, latents, txt, pooled, steps, grid):
     dev = latents.device
     torch.cuda.synchronize(dev)

@@ -7,11 +7,14 @@ compute of a layer (small-M FP8 GEMMs, norms, attention) leaves most of the
 HBM bandwidth idle, so the decode of layer i+1 runs on a second HIP stream
 while layer i computes:
 
-* two decode buffers; layer i reads buffer i % 2;
+* two decode buffers; layer i reads buffer i % 2, except that with an odd
+  layer count the last layer reads a third buffer, so that the decode of
+  layer 0 for the next pass (buffer 0) never overwrites the running layer;
 * layer i's pre-hook makes the compute stream wait for layer i's decode,
-  injects its weight views, then has the side stream wait until layer i-1
-  has released buffer (i+1) % 2 and decode layer i+1 into it;
-* layer i's post-hook records that buffer i % 2 is free again;
+  injects its weight views, then has the side stream wait until the layer
+  that last read layer i+1's buffer has released it and decode layer i+1
+  into it;
+* layer i's post-hook records that its buffer is free again;
 * the last layer's pre-hook decodes layer 0 for the next forward pass, and
   its post-hook joins the side stream back into the compute stream, so a
   forward pass (and a HIP graph captured from one) starts and ends with
@@ -37,13 +40,18 @@ class LayerPrefetcher:
     def __init__(self, layers, device=None, workgroups_per_cu: float = 2,
                  threads_per_block: int = 512):
         layers = list(layers)
-        if len(layers) < 2 or len(layers) % 2:
-            raise ValueError("the prefetcher pairs layers over two buffers: give an even count >= 2")
+        if len(layers) < 2:
+            raise ValueError("the prefetcher alternates layers over buffers: give at least two layers")
         self.layers = layers
         self.dev = torch.device(device) if device is not None else layers[0].encoded.device
         sizes = [m.packed_other_4bits.numel() * 2 for m in layers]
-        self.bufs = [torch.empty(max(sizes), dtype=torch.float8_e4m3fn, device=self.dev)
-                     for _ in range(2)]
+        self.slot = [i % 2 for i in range(len(layers))]
+        if len(layers) % 2:
+            self.slot[-1] = 2
+        n_bufs = max(self.slot) + 1
+        self.bufs = [torch.empty(max(n for n, b in zip(sizes, self.slot) if b == k),
+                                 dtype=torch.float8_e4m3fn, device=self.dev)
+                     for k in range(n_bufs)]
         self.side = torch.cuda.Stream(self.dev)
         cus = torch.cuda.get_device_properties(self.dev).multi_processor_count
         # fractions below 1 leave some CUs without a decode workgroup
@@ -52,7 +60,7 @@ class LayerPrefetcher:
         for i, (m, n) in enumerate(zip(layers, sizes)):
             m.__dict__["_ecf8_tpb"] = threads_per_block
             table, max_block, _ = _module_state(m)
-            out = self.bufs[i % 2][:n]
+            out = self.bufs[self.slot[i]][:n]
             n_fb = _dev.n_format_blocks(m.encoded.numel(), threads_per_block, 8)
             bpt = max(1, -(-n_fb // slots))
             plan = _dev.prepare_batch([{k: getattr(m, k) for k in _KEYS}], [out], [table],
@@ -61,8 +69,8 @@ class LayerPrefetcher:
             self.plans.append(plan)
             self.views.append(out)
         self.ready = [torch.cuda.Event() for _ in layers]
-        self.free = [torch.cuda.Event() for _ in range(2)]
-        self._released = [False, False]
+        self.free = [torch.cuda.Event() for _ in range(n_bufs)]
+        self._released = [False] * n_bufs
         self._handles = []
         self.primed = False
 
@@ -70,7 +78,7 @@ class LayerPrefetcher:
         """Queue layer i's decode on the side stream, after the buffer it
         writes has been released by the compute stream."""
         main = torch.cuda.current_stream(self.dev)
-        b = i % 2
+        b = self.slot[i]
         if self._released[b]:
             self.side.wait_event(self.free[b])
         else:
@@ -82,7 +90,7 @@ class LayerPrefetcher:
     def prime(self):
         """Decode layer 0 before the first forward pass (joined into the
         compute stream, as at the end of every pass)."""
-        self._released = [False, False]
+        self._released = [False] * len(self.bufs)
         self._decode(0)
         torch.cuda.current_stream(self.dev).wait_stream(self.side)
         self.primed = True
@@ -100,11 +108,11 @@ class LayerPrefetcher:
     def _post(self, i: int):
         def hook(module, _args, _out):
             main = torch.cuda.current_stream(self.dev)
-            self.free[i % 2].record(main)
-            self._released[i % 2] = True
+            self.free[self.slot[i]].record(main)
+            self._released[self.slot[i]] = True
             if i == len(self.layers) - 1:
                 main.wait_stream(self.side)  # join: layer 0 is decoded for the next pass
-                self._released = [False, False]
+                self._released = [False] * len(self.bufs)
         return hook
 
     def install(self):

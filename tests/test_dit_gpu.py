@@ -1,7 +1,8 @@
 """GPU checks of the FLUX-shaped DiT flow (ecf8_amd/dit.py): the FP8 block
 dequantization is bit-exact against torch's fp32 product rounded to bf16,
 and sampling with ECF8-compressed blocks (decoded by the forward-pre-hook)
-gives exactly the latents of the same pipeline kept in FP8."""
+gives exactly the latents of the same pipeline kept in FP8, also with the
+blocks decoded on a side stream one block ahead."""
 
 from __future__ import annotations
 
@@ -46,3 +47,30 @@ def test_compressed_dit_samples_exactly_like_fp8(cuda_device):
     assert torch.isfinite(a.float()).all()
     assert not torch.equal(a, lat)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_prefetched_dit_samples_exactly_like_fp8(cuda_device):
+    """Five blocks (an odd count: the last block takes the prefetcher's
+    third buffer), decoded one block ahead on a side stream, over three
+    sampling steps: each step's first block was decoded by the previous
+    step's last pre-hook."""
+    from ecf8_amd.dit import FluxConfig, compress_blocks, generate, prefetch_blocks, random_pipeline
+    from dfloat.run.run import TensorManager
+
+    cfg = FluxConfig(**dict(SMALL, single=3))
+    plain, drawn = random_pipeline(cfg, cuda_device, seed=5)
+    comp, _ = random_pipeline(cfg, cuda_device, seed=5)
+    compress_blocks(comp, drawn)
+    pf = prefetch_blocks(comp, cuda_device)
+    assert pf.slot == [0, 1, 0, 1, 2]
+    g = torch.Generator().manual_seed(6)
+    lat = torch.randn(1, 64, cfg.in_channels, generator=g).to(torch.bfloat16).to(cuda_device)
+    txt = torch.randn(1, 16, cfg.txt_dim, generator=g).to(torch.bfloat16).to(cuda_device)
+    pooled = torch.randn(1, cfg.pooled_dim, generator=g).to(torch.bfloat16).to(cuda_device)
+    TensorManager.clear_device()
+    a = generate(plain, lat, txt, pooled, steps=3, grid=(8, 8))
+    for _ in range(2):
+        b = generate(comp, lat, txt, pooled, steps=3, grid=(8, 8))
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert not torch.equal(a, lat)
+    pf.uninstall()
