@@ -521,12 +521,13 @@ def dit_generate(args):
     tokens of 4096, embedded guidance 3.5, --dit-steps Euler steps at batch
     1; first with the FP8 weights resident, then with every block
     ECF8-compressed and decoded by its forward-pre-hook, then with each
-    block's decode on a side stream one block ahead.  Every run must
-    produce identical latents."""
+    block's decode on a side stream one block ahead, then with each block
+    decoded straight into its Linears' bf16 weights (no FP8 pass, no
+    per-call dequantization).  Every run must produce identical latents."""
     import torch
 
-    from ecf8_amd.dit import (FluxConfig, compress_blocks, prefetch_blocks, random_pipeline,
-                              timed_generate)
+    from ecf8_amd.dit import (FluxConfig, compress_blocks, fuse_dequant_blocks, prefetch_blocks,
+                              random_pipeline, timed_generate)
     from dfloat.run.run import TensorManager
 
     dev = torch.device("cuda", 0)
@@ -540,14 +541,19 @@ def dit_generate(args):
     pooled = torch.randn(1, cfg.pooled_dim, generator=g).to(torch.bfloat16).to(dev)
     results = {}
     weights_exact = True
-    for mode in ("fp8", "ecf8", "ecf8_prefetch"):
+    prefetcher = None
+    for mode in ("fp8", "ecf8", "ecf8_prefetch", "ecf8_fused"):
         if mode == "ecf8":
             t0 = time.time()
             compress_blocks(pipe, drawn)
             torch.cuda.synchronize()
             print(f"[bench] blocks compressed in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
         if mode == "ecf8_prefetch":
-            prefetch_blocks(pipe, dev, workgroups_per_cu=args.prefetch_workgroups)
+            prefetcher = prefetch_blocks(pipe, dev, workgroups_per_cu=args.prefetch_workgroups)
+        if mode == "ecf8_fused":
+            prefetcher.uninstall()
+            prefetcher = None
+            fuse_dequant_blocks(pipe)
         TensorManager.clear_device()
         torch.cuda.empty_cache()
         timed_generate(pipe, lat, txt, pooled, 1, (64, 64))  # warm-up
@@ -567,7 +573,7 @@ def dit_generate(args):
                     for name, (w, _) in dr[i % len(dr)].items():
                         got = blk.get_submodule(name).weight.view(torch.uint8)
                         weights_exact &= torch.equal(got, w.view(torch.uint8).to(dev))
-    ecf8_modes = ("ecf8", "ecf8_prefetch")
+    ecf8_modes = ("ecf8", "ecf8_prefetch", "ecf8_fused")
     fp8 = results["fp8"]
     same = all(torch.equal(fp8["latents"].view(torch.int16), results[m]["latents"].view(torch.int16))
                for m in ecf8_modes)
@@ -600,7 +606,9 @@ def dit_generate(args):
                    "ecf8_decode": {
                        "ecf8": "each block decoded in its forward-pre-hook",
                        "ecf8_prefetch": "next block decoded on a side stream (two buffers, "
-                                        "a third for the last of an odd count)"}[best]},
+                                        "a third for the last of an odd count)",
+                       "ecf8_fused": "each block decoded straight into its Linears' bf16 "
+                                     "weights (FP8 x block scale, one pass)"}[best]},
         "uncompressed_fp8": summary(fp8),
         "ecf8": summary(ecf8),
         "ecf8_mode": best,

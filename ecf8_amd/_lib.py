@@ -42,6 +42,8 @@ _SIGNATURES = {
                      _i32, _vp], _i32),
     "ecf8_decode_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp],
                             _i32),
+    "ecf8_decode_bf16": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _i32, _vp, _i32,
+                          _i32, _i32, _vp], _i32),
     "ecf8_encoded_sizes": ([_vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp], _i32),
     "ecf8_encode_exponents": (
         [_vp, _i64, _vp, _vp, _i32, _u32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _i64],

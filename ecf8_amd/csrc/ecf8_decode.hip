@@ -247,6 +247,108 @@ __device__ __forceinline__ void flush_edges(uint32_t *s_edge, uint8_t *__restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Scaled bf16 output (ecf8_decode_bf16)
+// ---------------------------------------------------------------------------
+
+// One Linear of the block: elements [start, start + rows * cols) are its
+// row-major weight.  The row of element q is (q - start) / cols, computed as
+// umulhi(q - start, magic) >> shift (exact for q - start < 2^31: magic =
+// ceil(2^(31 + s) / cols), shift = s - 1, s = ceil(log2 cols)).
+struct ScalePart {
+  uint32_t start, cols, magic, shift;
+  const float *scale;  // [rows / 128][cols / 128]
+};
+struct ScaleParts {
+  ScalePart p[ECF8_MAX_SCALED_PARTS];
+  int n;
+};
+
+// Block scale of the 16-element segment at gpos (gpos < n_elements; a
+// segment never straddles a row or a part: both are multiples of 16).
+__device__ __forceinline__ float segment_scale(const ScalePart *s_parts, int n_parts,
+                                               uint32_t gpos) {
+  int k = 0;
+  for (int j = 1; j < n_parts; ++j) k += gpos >= s_parts[j].start ? 1 : 0;
+  const uint32_t idx = gpos - s_parts[k].start;
+  const uint32_t cols = s_parts[k].cols;
+  const uint32_t row = __umulhi(idx, s_parts[k].magic) >> s_parts[k].shift;
+  const uint32_t col = idx - row * cols;
+  return as_global(s_parts[k].scale)[(row >> 7) * (cols >> 7) + (col >> 7)];
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Four FP8 bytes (element order) -> four bf16 of fp8 x sc: exact FP8 -> f32
+// conversions, one f32 product each, round to nearest even to bf16.
+__device__ __forceinline__ uint2 fp8x4_scaled_bf16(uint32_t w, float sc) {
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false) * sc;
+  const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true) * sc;
+  return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(a, bf16x2)),
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector(b, bf16x2)));
+}
+
+// write_block for scaled bf16 output: the same merge, then each segment's
+// 16 FP8 bytes become 32 bytes of bf16 (two 128-bit stores).  sc0/sc1: the
+// scales of this lane's first two segments, looked up during the staging
+// phase; further segments look theirs up here.  An edge slot also keeps
+// the segment's scale (dword 7).
+template <int kThreads>
+__device__ __forceinline__ void write_block_bf16(const uint32_t *stage, const BlockRange &br,
+                                                 uint2 pre0, uint2 pre1,
+                                                 const uint8_t *__restrict__ packed,
+                                                 uint32_t n_elements, uint16_t *__restrict__ out16,
+                                                 uint32_t *s_edge, int tid, float sc0, float sc1,
+                                                 const ScalePart *s_parts, int n_parts) {
+  for (int s = tid, k = 0; s < br.nseg; s += kThreads, ++k) {
+    const uint2 ev = reinterpret_cast<const uint2 *>(stage)[s];
+    const uint32_t gpos = br.base + 16u * (uint32_t)s;
+    uint2 ov = k == 0 ? pre0 : pre1;
+    if (k > 1 || gpos + 16 > n_elements) ov = load_nibbles_checked(packed, n_elements, gpos);
+    const float sc = k == 0 ? sc0 : k == 1 ? sc1 : segment_scale(s_parts, n_parts, gpos);
+    const uint2 lo = merge8(ev.x, ov.x);
+    const uint2 hi8 = merge8(ev.y, ov.y);
+    if (gpos >= br.start && gpos + 16 <= br.end) {
+      const uint2 b0 = fp8x4_scaled_bf16(lo.x, sc), b1 = fp8x4_scaled_bf16(lo.y, sc);
+      const uint2 b2 = fp8x4_scaled_bf16(hi8.x, sc), b3 = fp8x4_scaled_bf16(hi8.y, sc);
+      u32x4 *const o = reinterpret_cast<u32x4 *>(out16 + gpos);
+      __builtin_nontemporal_store(u32x4{b0.x, b0.y, b1.x, b1.y}, o);
+      __builtin_nontemporal_store(u32x4{b2.x, b2.y, b3.x, b3.y}, o + 1);
+    } else {  // only the first and the last segment can be partial
+      uint32_t *const e = s_edge + (s == 0 ? 0 : kEdgeSlotDwords);
+      *reinterpret_cast<uint4 *>(e) = make_uint4(lo.x, lo.y, hi8.x, hi8.y);
+      e[4] = gpos;
+      e[5] = br.start;
+      e[6] = br.end;
+      e[7] = __float_as_uint(sc);
+    }
+  }
+}
+
+// flush_edges for scaled bf16 output: one element per lane, 16-bit stores.
+__device__ __forceinline__ void flush_edges_bf16(uint32_t *s_edge, uint16_t *__restrict__ out16,
+                                                 int tid, int first) {
+  const int t = tid - first;
+  if ((unsigned)t < 32u) {
+    uint32_t *const e = s_edge + (t >> 4) * kEdgeSlotDwords;
+    const uint32_t i = (uint32_t)t & 15u;
+    const uint4 meta = *reinterpret_cast<const uint4 *>(e + 4);  // gpos, start, end, scale
+    uint32_t w = e[i >> 2];
+    asm volatile("" : "+v"(w));  // both reads before the range test: one LDS round trip
+    const uint32_t q = meta.x + i;
+    const uint32_t b = (w >> (8 * (i & 3))) & 0xFFu;
+    const f32x2 v = f32x2{__builtin_amdgcn_cvt_f32_fp8((int)b, 0), 0.f} * __uint_as_float(meta.w);
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    const bool in_range = q >= meta.y && q < meta.z;
+    if (in_range) out16[q] = (uint16_t)(h & 0xFFFFu);
+    if (i == 0) {
+      e[5] = 0u;
+      e[6] = 0u;
+    }
+  }
+}
+
 // ===========================================================================
 // DFA kernel (tables of kind ECF8_TABLE_DFA)
 // ===========================================================================
@@ -299,6 +401,10 @@ struct BlockArgs {
   const uint8_t *gaps;
   uint8_t *out;
   uint32_t n_elements;
+  // scaled bf16 output instead of out (ecf8_decode_bf16)
+  uint16_t *out16 = nullptr;
+  const ScalePart *parts = nullptr;  // LDS copy of the part table
+  int n_parts = 0;
 };
 
 // Decode format-blocks fb, fb + fb_step, ... below fb_end (fb < fb_end) of
@@ -311,7 +417,7 @@ struct BlockArgs {
 //
 // load_table (optional): a table to load into s_dfa first -- after the
 // first block's loads are issued, so the two round trips overlap.
-template <int kThreads, bool kChecked, bool kPrio = true>
+template <int kThreads, bool kChecked, bool kPrio = true, bool kBf16 = false>
 __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, uint32_t *s_dfa,
                                            int *s_wave_sum, uint32_t *s_edge, uint32_t *s_dyn,
                                            int stage_cap, int fb, int fb_step, int fb_end,
@@ -433,7 +539,18 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, uint32_t *s_dfa,
     __syncthreads();
     const int excl4 = incl - cnt4 + waves_before<kWaves>(s_wave_sum, lane, wave);
     // the previous block's edge segments (parked before the barrier above)
-    flush_edges(s_edge, out, tid, kThreads - 64);
+    if constexpr (kBf16) flush_edges_bf16(s_edge, a.out16, tid, kThreads - 64);
+    else flush_edges(s_edge, out, tid, kThreads - 64);
+    // bf16 output: the scales of this lane's first two segments, loaded
+    // while the staging ORs run (positions clamped into the tensor, so every
+    // lookup is in bounds; lanes past the block's segments discard theirs)
+    float sc0 = 0.f, sc1 = 0.f;
+    if constexpr (kBf16) {
+      const uint32_t last_seg = n_elements - 16u;
+      sc0 = segment_scale(a.parts, a.n_parts, min(br.base + 16u * (uint32_t)tid, last_seg));
+      sc1 = segment_scale(a.parts, a.n_parts,
+                          min(br.base + 16u * (uint32_t)(tid + kThreads), last_seg));
+    }
 
     // ---- 3. OR the exponents into the staging buffer at their positions,
     // two automaton entries (at most 8 symbols, 32 bits) per 64-bit OR.
@@ -476,7 +593,12 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, uint32_t *s_dfa,
 
     // ---- 4. merge with the sign/mantissa nibbles and store FP8 bytes
     if (kPrio) __builtin_amdgcn_s_setprio(2);
-    write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, s_edge, tid);
+    if constexpr (kBf16)
+      write_block_bf16<kThreads>(stage, br, pre0, pre1, packed, n_elements, a.out16, s_edge, tid,
+                                 sc0, sc1, a.parts, a.n_parts);
+    else
+      write_block<kThreads, kChecked>(stage, br, pre0, pre1, packed, n_elements, out, s_edge,
+                                      tid);
     if (kPrio) __builtin_amdgcn_s_setprio(0);
     // the next iteration writes the other staging buffer; its barrier after
     // the scan orders this sweep before any reuse of this one
@@ -495,7 +617,8 @@ __device__ __forceinline__ void dfa_blocks(const BlockArgs &a, uint32_t *s_dfa,
     fb = fb_next;
   }
   __syncthreads();
-  flush_edges(s_edge, out, tid, kThreads - 64);
+  if constexpr (kBf16) flush_edges_bf16(s_edge, a.out16, tid, kThreads - 64);
+  else flush_edges(s_edge, out, tid, kThreads - 64);
 }
 
 // One tensor: the persistent grid strides over its format-blocks.
@@ -529,6 +652,38 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
                     reinterpret_cast<const uint32_t *>(op), gaps, out, n_elements};
   dfa_blocks<kThreads, kChecked>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap,
                                  (int)blockIdx.x, (int)gridDim.x, n_fb);
+}
+
+// One tensor decoded into scaled bf16 (ecf8_decode_bf16): the DFA kernel's
+// grid and phases, with each 16-element segment converted by its part's
+// block scale before the store.  The part table is copied into LDS (parts.n
+// <= ECF8_MAX_SCALED_PARTS entries, checked on the host).
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_bf16_kernel(
+    const uint8_t *__restrict__ luts, int n_luts, const uint32_t *__restrict__ table,
+    const uint8_t *__restrict__ encoded, uint32_t n_bytes,
+    const uint8_t *__restrict__ packed, const uint64_t *__restrict__ op,
+    const uint8_t *__restrict__ gaps, uint16_t *__restrict__ out16, uint32_t n_elements,
+    int n_fb, int stage_cap, const ScaleParts parts) {
+  constexpr int kWaves = kThreads / 64;
+  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ int s_wave_sum[kWaves];
+  __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
+  __shared__ ScalePart s_parts[ECF8_MAX_SCALED_PARTS];
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
+
+  const int tid = threadIdx.x;
+  load_dfa_batched<kThreads>(s_dfa, table, tid);
+  if (tid < kEdgeDwords) s_edge[tid] = 0u;
+  if (tid < parts.n) s_parts[tid] = parts.p[tid];
+  if ((int)blockIdx.x >= n_fb) return;  // uniform per workgroup, before any barrier
+  BlockArgs a{luts, n_luts, encoded, n_bytes, packed,
+              reinterpret_cast<const uint32_t *>(op), gaps, nullptr, n_elements};
+  a.out16 = out16;
+  a.parts = s_parts;
+  a.n_parts = parts.n;
+  dfa_blocks<kThreads, false, true, true>(a, s_dfa, s_wave_sum, s_edge, s_dyn, stage_cap,
+                                          (int)blockIdx.x, (int)gridDim.x, n_fb);
 }
 
 // Many tensors in one launch (e.g. the routed experts of an MoE layer): the
@@ -923,8 +1078,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
 // Per device: CU count, and per kernel variant the occupancy at the last
 // dynamic LDS size it was launched with.
 // {DFA, MULTI} x 4 block sizes x {unchecked, checked} (slots 0-15), batched
-// DFA x 4 (16-19), then the device-kind variants of DFA and MULTI (20-35)
-constexpr int kVariants = 36;
+// DFA x 4 (16-19), the device-kind variants of DFA and MULTI (20-35), then
+// the scaled-bf16 DFA kernel (36)
+constexpr int kVariants = 37;
 struct LaunchCache {
   int device = -1;
   int cus = 0;
@@ -1063,6 +1219,22 @@ int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
+int launch_dfa_bf16(const DecodeArgs &a, uint16_t *out16, const ScaleParts &parts) {
+  constexpr int kThreads = 512;
+  constexpr int kMaxSyms = kThreads * kChunkBits;
+  const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(a.cap) + kSpillDwords);
+  const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
+  auto kernel = decode_dfa_bf16_kernel<kThreads>;
+  int grid = 0;
+  const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
+                                 36, a.n_fb, &grid);
+  if (rc != ECF8_OK) return rc;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, a.stream, a.luts,
+                     a.n_luts, a.table, a.encoded, (uint32_t)a.n_bytes, a.packed, a.op, a.gaps,
+                     out16, (uint32_t)a.n_elements, (int)a.n_fb, a.cap, parts);
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
+}
+
 }  // namespace
 
 extern "C" int ecf8_decode_batched(const ecf8_block_desc *descs, int count, int n_tasks,
@@ -1191,6 +1363,58 @@ extern "C" int ecf8_decode(const uint8_t *luts, const uint8_t *encoded,
   return decode_checked(luts, encoded, packed_other_4bits, output_positions, gaps, outputs,
                         n_luts, n_bytes, n_elements, max_block_elements, min_code_bits, table,
                         table_kind, threads_per_block, bytes_per_thread, stream, true);
+}
+
+extern "C" int ecf8_decode_bf16(const uint8_t *luts, const uint8_t *encoded,
+                                const uint8_t *packed_other_4bits,
+                                const uint64_t *output_positions, const uint8_t *gaps,
+                                uint16_t *out_bf16, int n_luts, int64_t n_bytes,
+                                int64_t n_elements, int64_t max_block_elements,
+                                const uint32_t *table, int table_kind,
+                                const ecf8_scaled_part *parts, int n_parts,
+                                int threads_per_block, int bytes_per_thread, void *stream) {
+  // ecf8_decode's checks first (the output counted as its bytes: the same
+  // alignment), then this entry point's own
+  const int rc = decode_checked(luts, encoded, packed_other_4bits, output_positions, gaps,
+                                reinterpret_cast<uint8_t *>(out_bf16), n_luts, n_bytes,
+                                n_elements, max_block_elements, 0, table, table_kind,
+                                threads_per_block, bytes_per_thread, stream, false);
+  if (rc != ECF8_OK) return rc;
+  if (table_kind != ECF8_TABLE_DFA || threads_per_block != 512) return ECF8_ERR_UNSUPPORTED;
+  if (!parts || n_parts < 1 || n_parts > ECF8_MAX_SCALED_PARTS || !table)
+    return ECF8_ERR_INVALID_ARG;
+  ScaleParts sp{};
+  int64_t next = 0;
+  for (int j = 0; j < n_parts; ++j) {
+    const ecf8_scaled_part &p = parts[j];
+    if (!p.scale || p.rows <= 0 || p.cols <= 0 || p.rows % 128 || p.cols % 128 ||
+        p.start != next || p.rows > n_elements / p.cols)
+      return ECF8_ERR_INVALID_ARG;
+    if ((uintptr_t)p.scale & 3) return ECF8_ERR_MISALIGNED;
+    next += p.rows * p.cols;
+    const uint32_t cols = (uint32_t)p.cols;
+    int sh = 0;
+    while ((1ull << sh) < cols) ++sh;  // ceil(log2 cols) >= 7
+    sp.p[j].start = (uint32_t)p.start;
+    sp.p[j].cols = cols;
+    sp.p[j].magic = (uint32_t)(((1ull << (31 + sh)) + cols - 1) / cols);
+    sp.p[j].shift = (uint32_t)(sh - 1);
+    sp.p[j].scale = p.scale;
+  }
+  if (next != n_elements) return ECF8_ERR_INVALID_ARG;
+  // the kernel's clamped vector loads and its last-segment clamp
+  if (n_bytes < 12 || n_elements < 16) return ECF8_ERR_UNSUPPORTED;
+  sp.n = n_parts;
+  constexpr int kMaxSyms = 512 * kChunkBits;
+  const int64_t fb_bytes = 512 * (int64_t)kChunkBytes;
+  DecodeArgs a{luts,      n_luts, table,      encoded, n_bytes, packed_other_4bits,
+               output_positions, gaps, nullptr, n_elements, (n_bytes + fb_bytes - 1) / fb_bytes,
+               0, 0, (hipStream_t)stream};
+  const int cap = (max_block_elements <= 0 || max_block_elements > kMaxSyms)
+                      ? kMaxSyms
+                      : (int)max_block_elements;
+  a.cap = cap < 16 ? 16 : cap;
+  return launch_dfa_bf16(a, out_bf16, sp);
 }
 
 // ===========================================================================

@@ -180,6 +180,90 @@ def decode_into(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
     return out
 
 
+# ecf8_scaled_part (include/ecf8.h): scale pointer, start, rows, cols
+SCALED_PART_DTYPE = np.dtype([("scale", "<u8"), ("start", "<i8"), ("rows", "<i8"),
+                              ("cols", "<i8")])
+assert SCALED_PART_DTYPE.itemsize == 32
+MAX_SCALED_PARTS = 16
+
+
+class Bf16Decode:
+    """One block's ecf8_decode_bf16 call with every argument checked and
+    packed once (prepare_bf16); calling it launches the decode on the
+    current stream of the block's device, or on ``stream``.  Holds the
+    tensors it points to.  Valid while those tensors stay where they are."""
+
+    def __init__(self, dev, args, keep):
+        self.dev, self._args, self._keep = dev, args, keep
+        self._fn = lib().ecf8_decode_bf16
+
+    def __call__(self, stream=None):
+        rc = self._fn(*self._args, _stream_handle(self.dev, stream))
+        if rc:
+            check(rc, "ecf8_decode_bf16")
+
+
+def prepare_bf16(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
+                 packed_other_4bits: torch.Tensor, output_positions: torch.Tensor,
+                 gaps: torch.Tensor, parts, table: "DecodeTable | None" = None,
+                 max_block_elements: int = 0) -> Bf16Decode:
+    """Check and pack one ecf8_decode_bf16 call (see decode_bf16) for
+    repeated launches: a hook that decodes the same block every step pays
+    the checks once."""
+    dev = encoded.device
+    tensors = {"luts": luts, "encoded": encoded, "packed_other_4bits": packed_other_4bits,
+               "output_positions": output_positions, "gaps": gaps, "out": out}
+    for name, t in tensors.items():
+        if not t.is_cuda or t.device != dev:
+            raise ECF8Error(f"{name} must be on {dev}")
+        if not t.is_contiguous():
+            raise ECF8Error(f"{name} must be contiguous")
+    if out.dtype != torch.bfloat16:
+        raise ECF8Error(f"out must be bfloat16, got {out.dtype}")
+    n = packed_other_4bits.numel() * 2
+    if out.numel() < n:
+        raise ECF8Error(f"out holds {out.numel()} elements, {n} needed")
+    parts = list(parts)
+    if not 1 <= len(parts) <= MAX_SCALED_PARTS:
+        raise ECF8Error(f"1..{MAX_SCALED_PARTS} parts needed, got {len(parts)}")
+    rec = np.zeros(len(parts), dtype=SCALED_PART_DTYPE)
+    scales = []
+    for j, (start, rows, cols, scale) in enumerate(parts):
+        if scale.dtype != torch.float32 or not scale.is_contiguous() or scale.device != dev:
+            raise ECF8Error("each part's scale must be a contiguous float32 tensor on the device")
+        if tuple(scale.shape) != (int(rows) // 128, int(cols) // 128):
+            raise ECF8Error(f"part {j}: scale shape {tuple(scale.shape)} does not match "
+                            f"[{rows} / 128, {cols} / 128]")
+        rec[j] = (scale.data_ptr(), int(start), int(rows), int(cols))
+        scales.append(scale)
+    if table is None:
+        table = build_table(luts)
+    elif not isinstance(table, DecodeTable):
+        raise ECF8Error("table must be the DecodeTable returned by build_table")
+    args = (luts.data_ptr(), encoded.data_ptr(), packed_other_4bits.data_ptr(),
+            output_positions.data_ptr(), gaps.data_ptr(), out.data_ptr(), _n_luts(luts),
+            encoded.numel(), n, int(max_block_elements), table.data.data_ptr(), int(table.kind),
+            rec.ctypes.data, len(parts), 512, 8)
+    keep = (luts, encoded, packed_other_4bits, output_positions, gaps, out, table, rec, scales)
+    return Bf16Decode(dev, args, keep)
+
+
+def decode_bf16(out: torch.Tensor, luts: torch.Tensor, encoded: torch.Tensor,
+                packed_other_4bits: torch.Tensor, output_positions: torch.Tensor,
+                gaps: torch.Tensor, parts, table: "DecodeTable | None" = None,
+                max_block_elements: int = 0, stream=None) -> torch.Tensor:
+    """Decode one compressed block straight into the bf16 weights of its
+    block-scaled FP8 Linears (ecf8_decode_bf16): ``out`` (bfloat16, >= n
+    elements) receives bf16(fp8 x scale) for every element, the bytes
+    ecf8_decode followed by dequant_fp8_block on each Linear's view would
+    give.  ``parts``: (start, rows, cols, weight_scale_inv) per Linear, in
+    the block's element order (start = its split position).  Threads per
+    block 512, automaton tables only."""
+    prepare_bf16(out, luts, encoded, packed_other_4bits, output_positions, gaps, parts,
+                 table=table, max_block_elements=max_block_elements)(stream)
+    return out
+
+
 # ecf8_block_desc (include/ecf8.h): 7 device pointers, n_bytes, n_elements,
 # n_luts, task_begin
 BLOCK_DESC_DTYPE = np.dtype([

@@ -81,7 +81,11 @@ class _Lin(FP8Linear):
                                  requires_grad=False)
 
     def forward(self, x):
-        w = K.dequant_fp8_block(self.weight, self.weight_scale_inv)
+        # bf16 weights decoded by the block's hook (fuse_dequant_blocks), or
+        # the FP8 weight dequantized here
+        w = self.__dict__.get("_w_bf16")
+        if w is None:
+            w = K.dequant_fp8_block(self.weight, self.weight_scale_inv)
         return F.linear(x, w, self.bias)
 
 
@@ -387,6 +391,78 @@ def prefetch_blocks(pipe: FluxPipeline, device=None, workgroups_per_cu: float = 
 
     blocks = list(pipe.dit.blocks) + list(pipe.dit.single_blocks)
     return LayerPrefetcher(blocks, device, workgroups_per_cu=workgroups_per_cu).install()
+
+
+_BF16_BUFFERS: dict = {}
+
+
+def _bf16_buffer(device, n: int) -> torch.Tensor:
+    """One grow-only bf16 decode buffer per device, shared by every block
+    (as the loader's TensorManager shares its FP8 buffer)."""
+    buf = _BF16_BUFFERS.get(device)
+    if buf is None or buf.numel() < n:
+        _BF16_BUFFERS.pop(device, None)
+        buf = torch.empty(n, dtype=torch.bfloat16, device=device)
+        _BF16_BUFFERS[device] = buf
+    return buf
+
+
+def fuse_dequant_blocks(pipe: FluxPipeline):
+    """Replace each compressed block's decode hook by one that decodes the
+    block straight into its Linears' bf16 weights (ecf8_decode_bf16: the
+    FP8 bytes times their 128x128 block scales, never written as FP8), so
+    the Linears skip their own dequantization: the same bf16 weights as
+    decode + dequantize, in one pass over HBM instead of two.
+
+    All blocks decode into one shared bf16 buffer (as the loader's hooks
+    share TensorManager's FP8 buffer); each Linear gets its view of that
+    buffer here, once, and every call's arguments are checked and packed
+    here, so a hook is one launch (the DiT's step issues thousands of small
+    kernels, and host time spent in hooks shows up as GPU idle time).  Call
+    after the pipeline is on its device; the blocks' FP8 ``weight`` views
+    are no longer set."""
+    from dfloat.run.run import TensorManager, _module_state
+    from ._lib import ECF8_TABLE_DFA
+    from .decode import decode_into, prepare_bf16
+
+    blocks = list(pipe.dit.blocks) + list(pipe.dit.single_blocks)
+    if not blocks:
+        return pipe
+    dev = blocks[0].encoded.device
+    n_max = max(b.packed_other_4bits.numel() * 2 for b in blocks)
+    out = _bf16_buffer(dev, n_max)
+    for blk in blocks:
+        lins = list(blk.weight_injection_modules)
+        starts = [0] + list(blk.split_positions)
+        parts = [(st, lin.out_features, lin.in_features, lin.weight_scale_inv)
+                 for st, lin in zip(starts, lins)]
+        n = blk.packed_other_4bits.numel() * 2
+        if starts[-1] + lins[-1].out_features * lins[-1].in_features != n:
+            raise ValueError("the block's Linears do not cover its compressed elements")
+        for (st, rows, cols, _), lin in zip(parts, lins):
+            lin.__dict__["_w_bf16"] = out[st:st + rows * cols].view(rows, cols)
+        table, max_block, min_bits = _module_state(blk)
+        if table.kind == ECF8_TABLE_DFA:
+            call = prepare_bf16(out, blk.luts, blk.encoded, blk.packed_other_4bits,
+                                blk.output_positions, blk.gaps, parts, table=table,
+                                max_block_elements=max_block)
+
+            def hook(module, _args, call=call):
+                call()
+        else:  # LUTs the automaton cannot run: decode, then dequantize
+            def hook(module, _args, parts=parts, n=n, table=table, max_block=max_block,
+                     min_bits=min_bits):
+                fp8 = TensorManager.get_tensor(module.encoded.device, n)
+                decode_into(fp8, module.luts, module.encoded, module.packed_other_4bits,
+                            module.output_positions, module.gaps, table=table,
+                            max_block_elements=max_block, min_code_bits=min_bits)
+                for st, rows, cols, scale in parts:
+                    K.dequant_fp8_block(fp8[st:st + rows * cols].view(rows, cols), scale,
+                                        out=out[st:st + rows * cols])
+
+        blk._forward_pre_hooks.clear()
+        blk.register_forward_pre_hook(hook)
+    return pipe
 
 
 def timed_generate(pipe, latents, txt, pooled, steps, grid):

@@ -192,6 +192,52 @@ int ecf8_decode_batched_select(const ecf8_block_desc *descs, int count, const in
                                int blocks_per_task, int64_t max_block_elements,
                                int threads_per_block, void *stream);
 
+/*
+ * One Linear of a compressed block for ecf8_decode_bf16: elements
+ * [start, start + rows * cols) of the block's flat output are its row-major
+ * weight [rows, cols] (start = the block's split_positions entry,
+ * dfloat/utils.py:188-204), and `scale` its f32 block scales
+ * [rows / 128][cols / 128] (device memory, row-major, 4-byte aligned).
+ */
+typedef struct ecf8_scaled_part {
+  const float *scale;
+  int64_t start;
+  int64_t rows;
+  int64_t cols;
+} ecf8_scaled_part; /* 32 bytes */
+
+#define ECF8_MAX_SCALED_PARTS 16
+
+/*
+ * Decode one compressed block straight into the bf16 weights its FP8
+ * Linears compute with: output element q of part p is
+ * bf16(fp8(q) * p.scale[r / 128][c / 128]) (r, c = q's row and column in
+ * the part; f32 product, round to nearest even) -- the bytes that
+ * ecf8_decode followed by ecf8_dequant_fp8_block on each part's view give,
+ * in one pass that never writes the FP8 bytes.  No reference counterpart:
+ * the reference decodes FP8 (dfloat/run/decode.cu:15-26) and its consumer
+ * converts each Linear's weight per call; this serves consumers that run a
+ * bf16 GEMM on block-scaled FP8 weights (the DiT flow, whose reference
+ * hook is dfloat/run/run.py:84-155).
+ * Arguments as ecf8_decode, with outputs replaced by out_bf16 (device
+ * u16[n_elements], 16-byte aligned), and:
+ *   table_kind  must be ECF8_TABLE_DFA (ECF8_ERR_UNSUPPORTED otherwise:
+ *               decode with ecf8_decode and dequantize)
+ *   parts       host array of n_parts (1..ECF8_MAX_SCALED_PARTS) parts in
+ *               element order: parts[0].start = 0, each next start = the
+ *               previous start + rows * cols, the last part ending at
+ *               n_elements; rows and cols positive multiples of 128
+ *   threads_per_block must be 512, bytes_per_thread 8; the block needs at
+ *   least 12 bitstream bytes (ECF8_ERR_UNSUPPORTED otherwise).
+ * Every argument error is returned before anything is launched.
+ */
+int ecf8_decode_bf16(const uint8_t *luts, const uint8_t *encoded,
+                     const uint8_t *packed_other_4bits, const uint64_t *output_positions,
+                     const uint8_t *gaps, uint16_t *out_bf16, int n_luts, int64_t n_bytes,
+                     int64_t n_elements, int64_t max_block_elements, const uint32_t *table,
+                     int table_kind, const ecf8_scaled_part *parts, int n_parts,
+                     int threads_per_block, int bytes_per_thread, void *stream);
+
 /* ------------------------------------------------------------------ host */
 
 /*
