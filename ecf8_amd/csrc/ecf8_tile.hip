@@ -400,11 +400,25 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 #ifndef ECF8_TILE_DENSE8_RED
 #define ECF8_TILE_DENSE8_RED 2
 #endif
+#ifndef ECF8_TILE_DENSE8_GROUPS
+#define ECF8_TILE_DENSE8_GROUPS 1
+#endif
+#ifndef ECF8_TILE_MOE8_RED
+#define ECF8_TILE_MOE8_RED ECF8_TILE_MOE_RED
+#endif
 #ifndef ECF8_TILE_MOE_RED
 #define ECF8_TILE_MOE_RED 2
 #endif
+// The eight-wave shapes at G = 1 hold 49.4 KB of LDS: three workgroups per
+// CU, six waves per SIMD.  Two FP8 workgroups per workgroup (one automaton
+// copy, 74.3 KB) give two workgroups per CU and eight waves per SIMD.  On
+// MI355X, alternating builds: Qwen3-30B-A3B grouped gate/up at 16 tokens
+// 67.0 / 67.6 us at G = 2 against 69.1 / 71.0 at G = 1 (bit-identical),
+// e2e 1651 / 1650 against 1647 / 1646 tokens/s; the dense eight-wave shape
+// keeps G = 1: its smallest linear (o, 256 panels) would fill only 128 CUs
+// (11.8 -> 14.0 us).
 #ifndef ECF8_TILE_MOE8_GROUPS
-#define ECF8_TILE_MOE8_GROUPS 1
+#define ECF8_TILE_MOE8_GROUPS 2
 #endif
 #ifndef ECF8_TILE_MOE4_GROUPS
 #define ECF8_TILE_MOE4_GROUPS 2
@@ -420,6 +434,7 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 constexpr int kDense16Red = ECF8_TILE_DENSE16_RED, kMoe4PGroups = ECF8_TILE_MOE4P_GROUPS;
 constexpr int kDense8Red = ECF8_TILE_DENSE8_RED, kMoeRed = ECF8_TILE_MOE_RED;
 constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_GROUPS;
+constexpr int kDense8Groups = ECF8_TILE_DENSE8_GROUPS, kMoe8Red = ECF8_TILE_MOE8_RED;
 
 // Steps ahead a wave loads a segment's window and nibbles (P) and its
 // offsets (at least P + 1).  None and one: the kernel fits 64 VGPRs, so
@@ -967,9 +982,11 @@ extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int6
     tile_linear16_kernel<16, 16, 1, kDense16Red, false><<<(unsigned)grid, 1024, 0,
                                                           as_stream(stream)>>>(args);
   } else {
-    rc = resident_grid(tile_linear16_kernel<8, 8, 1, kDense8Red, false>, 512, n_panels, &grid);
+    constexpr int G = kDense8Groups;
+    rc = resident_grid(tile_linear16_kernel<8, 8, G, kDense8Red, false>, 512 * G,
+                       (n_panels + G - 1) / G, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<8, 8, 1, kDense8Red, false><<<(unsigned)grid, 512, 0,
+    tile_linear16_kernel<8, 8, G, kDense8Red, false><<<(unsigned)grid, 512 * G, 0,
                                                        as_stream(stream)>>>(args);
   }
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
@@ -1013,7 +1030,7 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
     return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
   };
   if (eight)
-    return launch(tile_linear16_kernel<8, 8, kMoe8Groups, kMoeRed, true>, 512 * kMoe8Groups,
+    return launch(tile_linear16_kernel<8, 8, kMoe8Groups, kMoe8Red, true>, 512 * kMoe8Groups,
                   kMoe8Groups);
   // four FP8 waves whose steps pack onto three hardware waves (K = 768)
   if (packs(4, 3, (int)(K / kGroup)))
