@@ -428,6 +428,12 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 // Qwen3-30B-A3B down projection at 16 tokens: 49.1 us packed at G = 4
 // against 52.9 unpacked; 71.4 at G = 2 and 74.9 at G = 3 (six and nine
 // waves per workgroup load the SIMDs unevenly).
+// ECF8_TILE_MOE_PACK 0 runs K = 768 unpacked instead (four hardware waves
+// per FP8 workgroup): at G = 4, sixteen waves and eight per SIMD, the same
+// down projection took 48.6-53.8 us against 43.9-44.8 packed.
+#ifndef ECF8_TILE_MOE_PACK
+#define ECF8_TILE_MOE_PACK 1
+#endif
 #ifndef ECF8_TILE_MOE4P_GROUPS
 #define ECF8_TILE_MOE4P_GROUPS 4
 #endif
@@ -1033,7 +1039,7 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
     return launch(tile_linear16_kernel<8, 8, kMoe8Groups, kMoe8Red, true>, 512 * kMoe8Groups,
                   kMoe8Groups);
   // four FP8 waves whose steps pack onto three hardware waves (K = 768)
-  if (packs(4, 3, (int)(K / kGroup)))
+  if (ECF8_TILE_MOE_PACK && packs(4, 3, (int)(K / kGroup)))
     return launch(tile_linear16_kernel<4, 3, kMoe4PGroups, kMoeRed, true>, 192 * kMoe4PGroups,
                   kMoe4PGroups);
   return launch(tile_linear16_kernel<4, 4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
