@@ -158,15 +158,43 @@ def _inject(module: nn.Module, reconstructed: torch.Tensor) -> None:
                 raise ValueError(f"Unsupported module type: {type(sub)}")
 
 
+def _injected(module: nn.Module):
+    """(module, weight tensor) pairs _inject set on this block."""
+    targets = [module] if isinstance(module, (nn.Linear, nn.Embedding)) else \
+        list(module.weight_injection_modules)
+    return [(t, t.__dict__.get("weight")) for t in targets]
+
+
 def get_hook(threads_per_block: int, bytes_per_thread: int):
     """Forward-pre-hook factory (dfloat/run/run.py:84-155): decode the
     module's compressed block on its device's current stream into the shared
-    TensorManager buffer, then inject the weight views."""
+    TensorManager buffer, then inject the weight views.
+
+    The first call checks every buffer (decode_into) and injects the views;
+    it keeps the packed launch arguments and the injected views, keyed by
+    the buffers' and the output's addresses.  A later call with the same
+    key makes that one launch, and injects again only if a view was
+    replaced in between: the views of an unchanged buffer are the same
+    views, and a block's host time here is GPU idle time in an eager
+    forward that issues thousands of small kernels."""
 
     def decode_hook(module, _):
         n_elements = module.packed_other_4bits.numel() * 2
         device = module.encoded.device
         reconstructed = TensorManager.get_tensor(device, n_elements)
+        key = (reconstructed.data_ptr(), module.luts.data_ptr(), module.encoded.data_ptr(),
+               module.packed_other_4bits.data_ptr(), module.output_positions.data_ptr(),
+               module.gaps.data_ptr(), n_elements)
+        fast = module.__dict__.get("_ecf8_launch")
+        if fast is not None and fast[0] == key:
+            _, fn, args, views, _table = fast
+            rc = fn(*args, torch.cuda.current_stream(device).cuda_stream)
+            if rc:
+                check(rc, "ecf8_decode")
+            if any(t.__dict__.get("weight") is not v for t, v in views):
+                _inject(module, reconstructed)
+                module.__dict__["_ecf8_launch"] = fast[:3] + (_injected(module), fast[4])
+            return
         module.__dict__["_ecf8_tpb"] = threads_per_block
         table, max_block, min_bits = _module_state(module)
         _dev.decode_into(reconstructed, module.luts, module.encoded, module.packed_other_4bits,
@@ -174,6 +202,12 @@ def get_hook(threads_per_block: int, bytes_per_thread: int):
                          threads_per_block=threads_per_block, bytes_per_thread=bytes_per_thread,
                          max_block_elements=max_block, min_code_bits=min_bits)
         _inject(module, reconstructed)
+        args = (module.luts.data_ptr(), module.encoded.data_ptr(),
+                module.packed_other_4bits.data_ptr(), module.output_positions.data_ptr(),
+                module.gaps.data_ptr(), reconstructed.data_ptr(), _dev._n_luts(module.luts),
+                module.encoded.numel(), n_elements, int(max_block), int(min_bits),
+                table.data.data_ptr(), int(table.kind), threads_per_block, bytes_per_thread)
+        module.__dict__["_ecf8_launch"] = (key, lib().ecf8_decode, args, _injected(module), table)
 
     return decode_hook
 
