@@ -197,6 +197,64 @@ def _qwen3_layer_workload(args, dev):
     return calls, verify, alg, n, config, (block, n, flat)
 
 
+def _flux_block_bf16_workload(args, dev):
+    """One FLUX.1-dev double block (8 Linears, 226.5 M elements) as one
+    compressed block, decoded straight into its Linears' bf16 weights
+    (ecf8_decode_bf16: fp8 x 128x128 block scale, round to nearest even)."""
+    import torch
+
+    from dfloat.compress import compress_flat
+    from ecf8_amd.decode import build_table, largest_block, prepare_bf16
+    from ecf8_amd.dit import FluxConfig
+    from ecf8_amd.synth import flat_block, synthetic_block
+
+    t0 = time.time()
+    weights = synthetic_block(FluxConfig().double_shapes(), seed=args.seed + 1)
+    flat, split = flat_block(weights)
+    block = compress_flat(flat)
+    n = flat.numel()
+    names = sorted(weights)
+    starts = [0] + list(split)
+    print(f"[bench] compressed FLUX double block: {n} elements -> {block['encoded'].numel()} "
+          f"bitstream bytes in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    n_luts = block["luts"].shape[0]
+    _, reads, _ = algorithmic_bytes(n, block["encoded"].numel(), n_luts)
+    scale_bytes = sum(weights[k][1].numel() * 4 for k in names)
+    alg = reads + scale_bytes + 2 * n  # bf16 written
+    keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
+    max_block = largest_block(block["output_positions"])
+    sets = []
+    for _ in range(args.copies):
+        d = {k: block[k].contiguous().to(dev) for k in keys}
+        d["table"] = build_table(d["luts"])
+        d["out"] = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        parts = [(st, weights[k][0].shape[0], weights[k][0].shape[1], weights[k][1].to(dev))
+                 for st, k in zip(starts, names)]
+        d["call"] = prepare_bf16(d["out"], *(d[k] for k in keys), parts, table=d["table"],
+                                 max_block_elements=max_block)
+        sets.append(d)
+    torch.cuda.synchronize()
+    calls = [(lambda c=d["call"]: (c(), 0)[1], ()) for d in sets]
+
+    def verify():
+        ref = torch.cat([(w.float() * s.repeat_interleave(128, 0).repeat_interleave(128, 1))
+                         .to(torch.bfloat16).reshape(-1) for w, s in (weights[k] for k in names)])
+        return torch.equal(sets[0]["out"].view(torch.int16).cpu(), ref.view(torch.int16))
+
+    config = {
+        "workload": "flux-double-block-bf16-decode",
+        "elements": n,
+        "linears": ", ".join(names) + " (one compressed block)",
+        "bitstream_bytes": block["encoded"].numel(),
+        "algorithmic_bytes": alg,
+        "rotated_copies": args.copies,
+        "threads_per_block": 512,
+        "bytes_per_thread": 8,
+        "output": "bf16 = fp8 x 128x128 block scale (the DiT Linears' weights)",
+    }
+    return calls, verify, alg, n, config, None
+
+
 def _qwen3_moe_layer_workload(args, dev):
     """One Qwen3-30B-A3B-shaped MoE layer: the attention block and all 128
     expert blocks (each compressed on its own, as the reference's qwen3moe
@@ -661,13 +719,16 @@ def main():
     ap.add_argument("--copies", type=int, default=10, help="rotated input/output sets")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "qwen3-8b-generate",
-                                           "qwen3-moe-generate", "flux-dit-generate"),
+    ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "flux-block-bf16",
+                                           "qwen3-8b-generate", "qwen3-moe-generate",
+                                           "flux-dit-generate"),
                     default="qwen3-8b-layer",
                     help="qwen3-moe-layer: attention + 128 experts in one batched launch; "
                          "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8; "
                          "qwen3-moe-generate: the same for the 30B-A3B-shaped MoE; "
-                         "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8")
+                         "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8; "
+                         "flux-block-bf16: one FLUX double block decoded straight into bf16 "
+                         "weights")
     ap.add_argument("--dit-steps", type=int, default=28)
     ap.add_argument("--routed-tokens", type=int, default=0,
                     help="qwen3-moe-layer: decode only the experts a top-k router picks for "
@@ -713,10 +774,13 @@ def main():
     import torch
 
     dev = torch.device("cuda", 0)
-    setup = _qwen3_layer_workload if args.workload == "qwen3-8b-layer" else _qwen3_moe_layer_workload
+    setup = {"qwen3-8b-layer": _qwen3_layer_workload, "qwen3-moe-layer": _qwen3_moe_layer_workload,
+             "flux-block-bf16": _flux_block_bf16_workload}[args.workload]
     calls, verify, alg, n, config, cpu_case = setup(args, dev)
     pmc_profile = {"qwen3-8b-layer-decode": "decode_qwen3_layer_pmc.md",
-                   "qwen3-moe-layer-decode": "decode_qwen3_moe_layer_pmc.md"}.get(config["workload"])
+                   "qwen3-moe-layer-decode": "decode_qwen3_moe_layer_pmc.md",
+                   "flux-double-block-bf16-decode": "decode_flux_block_bf16_pmc.md"}.get(
+                       config["workload"])
 
     def step(i):
         fn, cargs = calls[i % len(calls)]
@@ -792,7 +856,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8",
+        "dtype": "u8" if config["workload"] != "flux-double-block-bf16-decode" else "u8 + f32 scale",
         "data": "synthetic",
         "config": config,
         "roofline": {
