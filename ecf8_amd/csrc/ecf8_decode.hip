@@ -306,8 +306,13 @@ __device__ __forceinline__ uint2 fp8x4_scaled_bf16(uint32_t w, float sc) {
 // segments per lane, each store covers every other 16 bytes of twice the
 // span.  Measured on MI355X per FLUX double block (226.5 M elements):
 // 138.9 us with whole segments, 131.6 us with half-segments.
-constexpr int kHalfPrefetch = 4;  // half-segments per lane whose nibbles load at block start
-constexpr int kScalePrefetch = 2;  // of those, half-segments whose scale loads before the ORs
+// Half-segments per lane whose nibbles load at block start, and of those,
+// the ones whose scale loads before the staging ORs (the rest look theirs up
+// in the store phase).  All four prefetched, FLUX double block: 127.3 us
+// against 130.6 with two (3 rotated sets), 0.1409 against 0.1415 ms on the
+// bench line (10 sets, four rounds each).
+constexpr int kHalfPrefetch = 4;
+constexpr int kScalePrefetch = 4;
 
 // Sign/mantissa dwords of this lane's first kHalfPrefetch half-segments,
 // loaded at block start (non-temporal; only lanes that have the
