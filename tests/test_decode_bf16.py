@@ -104,6 +104,31 @@ def test_fused_bf16_every_fp8_code_and_extreme_scales(cuda_device):
 
 
 @pytest.mark.gpu
+def test_fused_bf16_sixteen_small_parts(cuda_device):
+    """ECF8_MAX_SCALED_PARTS Linears of 128 x 128 to 384 x 256 elements:
+    format-blocks (up to 14 K elements at these dense codes) start in one part
+    and end in the next, so each block's scale lookups move forward across
+    a part boundary."""
+    from ecf8_amd.decode import MAX_SCALED_PARTS
+
+    g = torch.Generator().manual_seed(5)
+    weights = []
+    for j in range(MAX_SCALED_PARTS):
+        rows, cols = 128 * (1 + j % 3), 128 * (1 + (j // 3) % 2)
+        # mostly four exponents (2-bit codes): many elements per format-block
+        e = torch.randint(6, 10, (rows, cols), generator=g)
+        e[torch.rand(rows, cols, generator=g) < 0.05] = 3
+        o = torch.randint(0, 16, (rows, cols), generator=g)
+        b = ((o & 8) << 4 | e << 3 | (o & 7)).to(torch.uint8)
+        sc = torch.rand(rows // 128, cols // 128, generator=g) * 1e-2 + 1e-4
+        weights.append((b.view(FP8), sc))
+    fused, two, ref, tail = _decode_both(weights, cuda_device)
+    assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(fused.view(torch.int16), two.view(torch.int16))
+    assert torch.isnan(tail.float()).all()
+
+
+@pytest.mark.gpu
 def test_fused_bf16_rejects_a_multi_symbol_table(cuda_device):
     from ecf8_amd._lib import ECF8_TABLE_MULTI, ECF8Error
     from ecf8_amd.decode import build_table, decode_bf16
