@@ -176,7 +176,10 @@ def get_hook(threads_per_block: int, bytes_per_thread: int):
     key makes that one launch, and injects again only if a view was
     replaced in between: the views of an unchanged buffer are the same
     views, and a block's host time here is GPU idle time in an eager
-    forward that issues thousands of small kernels."""
+    forward that issues thousands of small kernels.  Like the derived table,
+    the kept arguments assume a block's compressed buffers are not rewritten
+    in place: new weights loaded into the same storage need the module's
+    ``_ecf8_state`` and ``_ecf8_launch`` entries dropped first."""
 
     def decode_hook(module, _):
         n_elements = module.packed_other_4bits.numel() * 2
