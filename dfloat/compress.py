@@ -130,11 +130,34 @@ def validate_cuda_decoding_fp8(result, tensors, device) -> None:
 validate_gpu_decoding_fp8 = validate_cuda_decoding_fp8
 
 
+def compressible_linear_types() -> tuple:
+    """The module types whose e4m3fn ``weight`` a block contributes
+    (scripts/compress.py:519-528): ``nn.Linear``, transformers' ``FP8Linear``
+    (every quantized Linear of an HF FP8 checkpoint) and DiffSynth's
+    ``AutoWrappedLinear``, each when importable.  Matching is by exact type,
+    as the reference's finder does (dfloat/utils.py:165)."""
+    types = [torch.nn.Linear]
+    try:
+        from transformers.integrations.finegrained_fp8 import FP8Linear
+        types.append(FP8Linear)
+    except ImportError:
+        pass
+    try:
+        from diffsynth.core.vram.layers import AutoWrappedLinear
+        types.append(AutoWrappedLinear)
+    except ImportError:
+        pass
+    return tuple(types)
+
+
 def fp8_layers_by_block(model, fp8_regex) -> dict:
     """{block name: {layer name: module}} of the FP8 layers to compress
     (scripts/compress.py:515-536): with a list of block regexes, every FP8
-    Linear under each matching block; with a dict {regex: layer paths}, the
-    selected layers of each matching block."""
+    layer of a ``compressible_linear_types`` type under each matching block;
+    with a dict {regex: layer paths}, the selected layers of each matching
+    block.  A matching block without a single FP8 layer raises ValueError:
+    its checkpoint would be written as compressed while holding nothing
+    compressed."""
     from .utils import (find_layers_by_data_type_and_layer_type, find_layers_by_selection,
                         locate_block_by_regex)
 
@@ -144,10 +167,16 @@ def fp8_layers_by_block(model, fp8_regex) -> dict:
             for name, block in locate_block_by_regex(model, regex).items():
                 out[name] = find_layers_by_selection(block, selected, name=name)
     else:
+        layer_types = compressible_linear_types()
         for name, block in locate_block_by_regex(model, "|".join(fp8_regex)).items():
             out[name] = find_layers_by_data_type_and_layer_type(
-                block, target_dtype=torch.float8_e4m3fn, layers=(torch.nn.Linear,), name=name)
-    return {k: v for k, v in out.items() if v}
+                block, target_dtype=torch.float8_e4m3fn, layers=layer_types, name=name)
+    empty = [k for k, v in out.items() if not v]
+    if empty:
+        raise ValueError(f"{len(empty)} block(s) matching the FP8 patterns hold no float8_e4m3fn "
+                         f"layer of types {[t.__name__ for t in compressible_linear_types()]}: "
+                         f"{empty[:4]}")
+    return out
 
 
 def _layout(model, fp8_regex, layout: str) -> str:
@@ -203,6 +232,8 @@ def compress_model(model, fp8_regex, save_path: str, threads_per_block: int = 51
     info = {"save_path": save_path, "model_fp8_regex": regexes,
             "bytes_per_thread": bytes_per_thread, "threads_per_block": threads_per_block}
     items = list(fp8_layers_by_block(model, fp8_regex).items())
+    if not items:
+        raise ValueError(f"no module of the model matches the FP8 block patterns {regexes}")
     if n_workers > 1 and len(items) > 1:
         from concurrent.futures import ThreadPoolExecutor
 

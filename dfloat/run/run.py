@@ -29,6 +29,7 @@ import torch.nn as nn
 
 from ecf8_amd import decode as _dev
 from ecf8_amd._lib import ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8Error, check, lib
+from ecf8_amd.hf_fp8 import bind_fp8_linears
 
 __all__ = [
     "DFloatModel",
@@ -455,6 +456,9 @@ class DFloatModel:
                 raise ValueError('device_map should be "auto" if no specific device is provided.')
             model = _dispatch_auto(model, max_memory)
         _warn_if_on_cpu(model)
+        # transformers' FP8Linear modules (the quantized Linears of an HF FP8
+        # checkpoint, fed by the decode hooks) run on the engine's FP8 linear
+        bind_fp8_linears(model)
         return model
 
 
