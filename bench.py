@@ -181,7 +181,9 @@ def _qwen3_layer_workload(args, dev):
              for d in sets]
 
     def verify():
-        return torch.equal(sets[0]["out"].view(torch.uint8).cpu(), flat.view(torch.uint8))
+        # every rotated set: each decoded the timed launches' bytes
+        want = flat.view(torch.uint8).to(dev)
+        return all(torch.equal(d["out"].view(torch.uint8), want) for d in sets)
 
     config = {
         "workload": "qwen3-8b-layer-decode",
@@ -239,7 +241,8 @@ def _flux_block_bf16_workload(args, dev):
     def verify():
         ref = torch.cat([(w.float() * s.repeat_interleave(128, 0).repeat_interleave(128, 1))
                          .to(torch.bfloat16).reshape(-1) for w, s in (weights[k] for k in names)])
-        return torch.equal(sets[0]["out"].view(torch.int16).cpu(), ref.view(torch.int16))
+        want = ref.view(torch.int16).to(dev)
+        return all(torch.equal(d["out"].view(torch.int16), want) for d in sets)
 
     config = {
         "workload": "flux-double-block-bf16-decode",
@@ -277,13 +280,13 @@ def _qwen3_moe_layer_workload(args, dev):
     print(f"[bench] compressed moe layer: {len(flats)} blocks, {n} elements in "
           f"{time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     keys = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps")
-    plans, first_outs = [], None
+    plans, out_sets = [], []
     copies = max(1, min(args.copies, 2))
     for _ in range(copies):
         blocks = [{k: c[k].contiguous().to(dev) for k in keys} for c in comp]
         tables = [build_table(b["luts"]) for b in blocks]
         outs = [torch.empty(f.numel(), dtype=torch.float8_e4m3fn, device=dev) for f in flats]
-        first_outs = outs if first_outs is None else first_outs
+        out_sets.append(outs)
         plans.append(prepare_batch(blocks, outs, tables))
     torch.cuda.synchronize()
     assert all(not p.singles for p in plans)
@@ -322,21 +325,23 @@ def _qwen3_moe_layer_workload(args, dev):
                   "algorithmic_bytes_mean": alg}
 
     def verify():
+        wants = [f.view(torch.uint8).to(dev) for f in flats]
         if routed is not None:
-            # one routed call on sentinel-filled outputs: the selected blocks
-            # decode exactly, the others are untouched
-            for o in first_outs:
-                o.view(torch.uint8).fill_(0x3C)
-            sels[0](flag_sets[0])
-            torch.cuda.synchronize()
+            # one routed call per rotated set on sentinel-filled outputs: the
+            # selected blocks decode exactly, the others are untouched
             ok = True
-            for o, f, s_ in zip(first_outs, flats, flag_sets[0].tolist()):
-                got = o.view(torch.uint8)
-                ok &= (torch.equal(got.cpu(), f.view(torch.uint8)) if s_
-                       else bool((got == 0x3C).all()))
+            for i, (outs, sel) in enumerate(zip(out_sets, sels)):
+                for o in outs:
+                    o.view(torch.uint8).fill_(0x3C)
+                sel(flag_sets[i])
+                torch.cuda.synchronize()
+                for o, w, s_ in zip(outs, wants, flag_sets[i].tolist()):
+                    got = o.view(torch.uint8)
+                    ok &= torch.equal(got, w) if s_ else bool((got == 0x3C).all())
             return ok
-        return all(torch.equal(o.view(torch.uint8).cpu(), f.view(torch.uint8))
-                   for o, f in zip(first_outs, flats))
+        # every rotated set, each written by the timed launches
+        return all(torch.equal(o.view(torch.uint8), w)
+                   for outs in out_sets for o, w in zip(outs, wants))
 
     config = {
         "workload": "qwen3-moe-layer-decode",

@@ -4,6 +4,11 @@
   blocks decoded by ONE batched launch, bit-exact, nothing written past any
   block; then through the device-side selection with a top-8 routing of 16
   tokens (selected blocks bit-exact, the others untouched).
+* Qwen3-30B-A3B-shaped model (48 layers x 128 experts, 6,192 compressed
+  blocks): batch-16 greedy generate from 128-token prompts gives the FP8
+  model's tokens and logits with routed batched expert decode, side-stream
+  attention decode and fused (re-tiled) decode-step linears, eager and
+  graph-replayed.
 * Qwen3-8B-shaped model (36 layers, hidden 4096, vocab 151,936): every
   layer's forward-pre-hook injects bit-exact weights, and a batch-16 greedy
   generate from 128-token prompts gives the FP8 model's tokens and logits,
@@ -150,6 +155,73 @@ def test_qwen3_8b_model_bs16_matches_fp8(cuda_device):
     pf.uninstall()
     _say("[full] Qwen3-8B: re-tiling")
     retile_layers(model, drawn)
+    for graph in (False, True):
+        run("ecf8_fused", graph)
+    base_t, base_l = results[("fp8", False)]
+    assert len(set(base_t.reshape(-1).tolist())) > 1
+    for key, (t, l) in results.items():
+        assert torch.equal(t, base_t), key
+        assert torch.equal(l, base_l), key
+
+
+# ----------------------------------------------------- Qwen3-30B-A3B model
+
+
+def test_qwen3_moe_model_bs16_matches_fp8(cuda_device):
+    """The 48-layer, 128-expert model (6,192 compressed blocks): batch 16,
+    128-token prompts, greedy decode; the FP8 model's tokens and logits with
+    the attention blocks decoded by their hooks and the routed experts by
+    one batched launch per layer (eager and graph-replayed), with the next
+    attention block on a side stream, and re-tiled (fused decode-step
+    linears, eager and graph-replayed)."""
+    from dfloat.run.run import TensorManager
+    from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, \
+        random_moe_model, retile_moe_layers
+    from ecf8_amd.prefetch import LayerPrefetcher
+
+    cfg = Qwen3MoeConfig()
+    assert (cfg.layers, cfg.hidden, cfg.experts, cfg.top_k, cfg.moe_intermediate) == \
+        (48, 2048, 128, 8, 768)
+    _say("[full] Qwen3-30B-A3B: building")
+    model, drawn = random_moe_model(cfg, cuda_device, distinct_layers=2, seed=0)
+    B, T, new = 16, 128, 4
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(2))
+    results = {}
+
+    def run(tag, graph):
+        _say(f"[full] Qwen3-30B-A3B: {tag} graph={graph}")
+        TensorManager.clear_device()
+        r = Qwen3MoeRunner(model, B, T, T + new, cuda_device)
+        if graph:
+            r.capture()
+        toks = r.generate(prompt, new).cpu()
+        results[(tag, graph)] = (toks, r.logits.float().cpu())
+        del r
+        torch.cuda.empty_cache()
+
+    for graph in (False, True):
+        run("fp8", graph)
+    _say("[full] Qwen3-30B-A3B: compressing 6,192 blocks")
+    compress_moe_layers(model, drawn)
+    n_blocks = sum(1 for m in model.modules() if "encoded" in m._buffers)
+    assert n_blocks == cfg.layers * (cfg.experts + 1)
+    # spot-check injected weights: every expert of the first and last layer
+    for i in (0, cfg.layers - 1):
+        for e, ex in enumerate(model.model.layers[i].mlp.experts):
+            for hook in ex._forward_pre_hooks.values():
+                hook(ex, None)
+            for name, (w, _) in drawn[i % len(drawn)]["experts"][e].items():
+                got = ex.get_submodule(name).weight.view(torch.uint8)
+                assert torch.equal(got, w.view(torch.uint8).to(cuda_device)), (i, e, name)
+    for graph in (False, True):
+        run("ecf8", graph)
+    pf = LayerPrefetcher([layer.self_attn for layer in model.model.layers], cuda_device).install()
+    run("ecf8_prefetch", True)
+    pf.uninstall()
+    TensorManager.clear_device()
+    torch.cuda.empty_cache()
+    _say("[full] Qwen3-30B-A3B: re-tiling")
+    retile_moe_layers(model, drawn)
     for graph in (False, True):
         run("ecf8_fused", graph)
     base_t, base_l = results[("fp8", False)]
