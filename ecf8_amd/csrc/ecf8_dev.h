@@ -82,10 +82,13 @@ __device__ __forceinline__ void load_dfa(uint32_t *s_dfa, const uint32_t *__rest
 // Up to 13 loads per lane in flight before the first wait: at 512 lanes
 // the whole table arrives in one memory round trip instead of 13 (measured
 // on MI355X: ~3 us less per launch of the one-tensor kernel).
-template <int kThreads>
+// kWithKind: the table's kind word (index kDfaEntries) is copied unchanged
+// into s_dfa[kDfaEntries] (s_dfa then holds kDfaEntries + 1 words).
+template <int kThreads, bool kWithKind = false>
 __device__ __forceinline__ void load_dfa_batched(uint32_t *s_dfa,
                                                  const uint32_t *__restrict__ table, int tid) {
-  constexpr int kIters = (kDfaEntries + kThreads - 1) / kThreads;
+  constexpr int kWords = kDfaEntries + (kWithKind ? 1 : 0);
+  constexpr int kIters = (kWords + kThreads - 1) / kThreads;
   constexpr int kBatch = kIters < 13 ? kIters : 13;
 #pragma unroll
   for (int j0 = 0; j0 < kIters; j0 += kBatch) {
@@ -93,12 +96,13 @@ __device__ __forceinline__ void load_dfa_batched(uint32_t *s_dfa,
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int i = tid + (j0 + j) * kThreads;
-      v[j] = i < kDfaEntries ? table[i] : 0u;
+      v[j] = i < kWords ? table[i] : 0u;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int i = tid + (j0 + j) * kThreads;
       if (i < kDfaEntries) s_dfa[i] = dfa_entry_in_range(v[j]);
+      else if (kWithKind && i == kDfaEntries) s_dfa[i] = v[j];
     }
   }
 }
@@ -140,13 +144,15 @@ __device__ __forceinline__ void load_dfa_rounds(uint32_t *s_dfa, const uint32_t 
 // kernel can issue other loads in between and overlap their round trips.
 template <int kThreads>
 struct DfaLoad {
-  static constexpr int kIters = (kDfaEntries + kThreads - 1) / kThreads;
+  // the table's kind word (index kDfaEntries) rides with the entries: it
+  // lands in s_dfa[kDfaEntries] unchanged, so s_dfa holds kDfaEntries + 1
+  static constexpr int kIters = (kDfaEntries + 1 + kThreads - 1) / kThreads;
   uint32_t v[kIters];
   __device__ __forceinline__ void load(const uint32_t *__restrict__ table, int tid) {
 #pragma unroll
     for (int j = 0; j < kIters; ++j) {
       const int i = tid + j * kThreads;
-      v[j] = i < kDfaEntries ? table[i] : 0u;
+      v[j] = i <= kDfaEntries ? table[i] : 0u;
     }
   }
   __device__ __forceinline__ void store(uint32_t *s_dfa, int tid) const {
@@ -154,6 +160,7 @@ struct DfaLoad {
     for (int j = 0; j < kIters; ++j) {
       const int i = tid + j * kThreads;
       if (i < kDfaEntries) s_dfa[i] = dfa_entry_in_range(v[j]);
+      else if (i == kDfaEntries) s_dfa[i] = v[j];
     }
   }
 };

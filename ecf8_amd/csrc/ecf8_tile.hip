@@ -41,6 +41,9 @@ typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 constexpr int kGroup = 128;
 constexpr int kStageDw = kTileSegSymbols / 8;           // 256 dwords of nibbles
 constexpr int kWaveStageDw = kStageDw + 8;              // + spill for symbols past 2048
+// outputs of a tiled kernel handed a table that is not an automaton
+constexpr uint16_t kBf16Nan = 0x7FC0;
+constexpr uint32_t kFp8Nan4 = 0x7F7F7F7Fu;  // four e4m3fn NaNs
 static_assert(4 * 64 <= kWaveStageDw, "a wave's staging area holds its 4x64 partial sums");
 
 // One weight operand of a (possibly fused) tiled linear.
@@ -568,7 +571,7 @@ void tile_linear16_kernel(
   constexpr bool kPacked = HWW != WAVES;
   static_assert(HWW <= WAVES, "at most one hardware wave per FP8 wave");
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
-  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ uint32_t s_dfa[kDfaEntries + 1];  // + the table's kind word
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[HW][S * kWaveStageDw];
   __shared__ __attribute__((aligned(16))) float s_part[RED][G][WAVES][256];
   const int lane = threadIdx.x & 63;
@@ -701,6 +704,20 @@ void tile_linear16_kernel(
   dfa.store(s_dfa, threadIdx.x);
   for (int i = lane; i < S * kWaveStageDw; i += 64) stage[i] = 0u;
   lds_barrier();
+  if (s_dfa[kDfaEntries] != (uint32_t)ECF8_TABLE_DFA) {
+    // not an automaton table (the host cannot see the kind of a table built
+    // on the device): every output this group owns becomes a bf16 NaN
+    // instead of a product of misread weights.  Uniform, after the last
+    // barrier the workgroup passes.
+    for (int pnl = vwg; pnl < n_panels; pnl += vgrid) {
+      TileOperand op;
+      int p, col;
+      walk.at(pnl, op, p, col);
+      for (int i = hwave * 64 + lane; i < 16 * M; i += HWW * 64)
+        a.out[(size_t)(row0 + (i >> 4)) * a.ldo + col + p * 16 + (i & 15)] = kBf16Nan;
+    }
+    return;
+  }
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   // panels per group waiting in s_part (the same count in every group), and
@@ -860,7 +877,7 @@ template <int WAVES, bool kBatch>
 __global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
     typename std::conditional<kBatch, TileDecodeBatchArgs, TileDecodeArgs>::type a, int K,
     uint32_t n_seg) {
-  __shared__ uint32_t s_dfa[kDfaEntries];
+  __shared__ uint32_t s_dfa[kDfaEntries + 1];  // + the table's kind word
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[WAVES][kWaveStageDw];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   TileOperand op;
@@ -877,12 +894,23 @@ __global__ __launch_bounds__(WAVES * 64) void tile_decode_kernel(
     table = a.table;
     out = a.out;
   }
-  load_dfa_batched<WAVES * 64>(s_dfa, table, threadIdx.x);
+  load_dfa_batched<WAVES * 64, true>(s_dfa, table, threadIdx.x);
   uint32_t *const stage = s_stage[wave];
   for (int i = lane; i < kWaveStageDw; i += 64) stage[i] = 0u;
   __syncthreads();
   const uint32_t kgroups = (uint32_t)K / kGroup;
   const int r = lane & 15, g = lane >> 4;
+  if (s_dfa[kDfaEntries] != (uint32_t)ECF8_TABLE_DFA) {
+    // not an automaton table: the segments' bytes become e4m3fn NaNs
+    const u32x4 nan4 = {kFp8Nan4, kFp8Nan4, kFp8Nan4, kFp8Nan4};
+    for (uint32_t s = blockIdx.x * WAVES + wave; s < n_seg; s += gridDim.x * WAVES) {
+      const uint32_t p = s / kgroups, kg = s % kgroups;
+      uint8_t *const row = out + (size_t)(p * 16 + r) * K + kg * kGroup + 16 * g;
+      *reinterpret_cast<u32x4 *>(row) = nan4;
+      *reinterpret_cast<u32x4 *>(row + 64) = nan4;
+    }
+    return;
+  }
   for (uint32_t s = blockIdx.x * WAVES + wave; s < n_seg; s += gridDim.x * WAVES) {
     const SegLoad c = seg_window(op, s, op.seg_off[s], op.seg_off[s + 1], lane);
     const u32x4 oth = seg_other(op, s, lane);

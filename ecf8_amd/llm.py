@@ -429,45 +429,28 @@ def retile_layers(model: Qwen3ForCausalLM, drawn=None, n_threads: int | None = N
     tiled layout, and the block's reference-layout buffers and decode hook
     removed -- the decode step's linears then decode their weight operands
     themselves.  ``drawn`` (from random_model) lets layers that hold copies
-    of one block share one encoding; each layer keeps its own device copy."""
-    from ecf8_amd.decode import build_table, decode
+    of one block share one encoding; each layer keeps its own device copy.
 
-    cache = {}
+    A block the tiled layout cannot hold -- LUTs with a 1-bit code (no
+    automaton table) or a Linear with a 16x128 segment over 3 bits per
+    exponent -- stays as it is, compressed in the reference layout with its
+    decode hook, and its linears run decode-then-GEMM; the refused layers
+    and their reasons are returned in ``model._ecf8_untiled`` and printed
+    on stderr.  Every check of a block runs before any of it changes."""
     for i, layer in enumerate(model.model.layers):
         if not hasattr(layer, "encoded"):
             raise ECF8Error(f"layer {i} holds no compressed block")
-        dev = layer.encoded.device
+    cache = {}
+    untiled = []
+    for i, layer in enumerate(model.model.layers):
         key = i % len(drawn) if drawn is not None else None
-        enc = cache.get(key) if key is not None else None
-        if enc is None:
-            flat = decode(layer.luts, layer.encoded, layer.packed_other_4bits,
-                          layer.output_positions, layer.gaps).cpu()
-            bits, vals = tiled.code_from_luts(layer.luts)
-            parts = torch.tensor_split(flat, layer.split_positions)
-            enc = {}
-            for mod, part in zip(layer.weight_injection_modules, parts):
-                name = next(n for n in LINEAR_NAMES if layer.get_submodule(n) is mod)
-                enc[name] = tiled.tile_encode(part.view(mod.out_features, mod.in_features), bits,
-                                              vals, n_threads)
-            if key is not None:
-                cache[key] = enc
-        layer._ecf8_tiles = {
-            n: tiled.TiledOperand(enc[n], layer.get_submodule(n).weight_scale_inv,
-                                  layer.get_submodule(n).out_features,
-                                  layer.get_submodule(n).in_features, dev)
-            for n in LINEAR_NAMES}
-        table = build_table(layer.luts.contiguous())
-        if table.kind != 1:
-            raise ECF8Error(f"layer {i}: the tiled linear needs LUTs without a 1-bit code")
-        layer._ecf8_tile_table = table
-        layer._forward_pre_hooks.clear()
-        for n in LINEAR_NAMES:  # weight views a decode hook injected earlier
-            layer.get_submodule(n).__dict__.pop("weight", None)
-        for attr in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
-                     "split_positions"):
-            if attr in layer._buffers:
-                del layer._buffers[attr]
-        layer.__dict__.pop("_ecf8_state", None)
+        got = tiled.tile_block(layer, LINEAR_NAMES, cache, key, n_threads)
+        if isinstance(got, str):
+            untiled.append((f"model.layers.{i}", got))
+            continue
+        tiled.install_tiles(layer, LINEAR_NAMES, *got)
+    tiled.report_untiled(untiled)
+    model.__dict__["_ecf8_untiled"] = untiled
     return model
 
 

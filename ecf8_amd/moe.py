@@ -458,55 +458,46 @@ def retile_moe_layers(model: Qwen3MoeForCausalLM, drawn=None, n_threads: int | N
     step's attention linears and grouped expert linears then decode their
     weight operands themselves; the prompt decodes the tiled Linears first.
     ``drawn`` (from random_moe_model) lets layers that hold copies of one
-    block share one encoding; each layer keeps its own device copy."""
-    from .decode import build_table, decode
+    block share one encoding; each layer keeps its own device copy.
 
-    cache = {}
-
-    def encode(key, mod, names):
-        enc = cache.get(key) if key is not None else None
-        if enc is None:
-            flat = decode(mod.luts, mod.encoded, mod.packed_other_4bits, mod.output_positions,
-                          mod.gaps).cpu()
-            bits, vals = tiled.code_from_luts(mod.luts)
-            parts = torch.tensor_split(flat, mod.split_positions)
-            enc = {}
-            for sub, part in zip(mod.weight_injection_modules, parts):
-                name = next(n for n in names if mod.get_submodule(n) is sub)
-                enc[name] = tiled.tile_encode(part.view(sub.out_features, sub.in_features), bits,
-                                              vals, n_threads)
-            if key is not None:
-                cache[key] = enc
-        return enc
-
-    def install(mod, names, enc, where):
-        dev = mod.encoded.device
-        table = build_table(mod.luts.contiguous())
-        if table.kind != 1:
-            raise ECF8Error(f"{where}: the tiled linears need LUTs without a 1-bit code")
-        mod._ecf8_tiles = {
-            n: tiled.TiledOperand(enc[n], mod.get_submodule(n).weight_scale_inv,
-                                  mod.get_submodule(n).out_features,
-                                  mod.get_submodule(n).in_features, dev)
-            for n in names}
-        mod._ecf8_tile_table = table
-        mod._forward_pre_hooks.clear()
-        for n in names:  # weight views a decode hook injected earlier
-            mod.get_submodule(n).__dict__.pop("weight", None)
-        for attr in (*_KEYS, "split_positions"):
-            if attr in mod._buffers:
-                del mod._buffers[attr]
-        mod.__dict__.pop("_ecf8_state", None)
-
+    A block the tiled layout cannot hold (LUTs with a 1-bit code, or a
+    Linear over 3 bits per exponent in some 16x128 segment) stays compressed
+    in the reference layout: an attention block keeps its decode hook, and
+    since one grouped launch serves all of a layer's experts, one refused
+    expert keeps every expert of its layer on the routed batched decode
+    followed by the FP8 grouped linear.  The refused blocks and their reasons
+    are returned in ``model._ecf8_untiled`` and printed on stderr; every
+    check of a block (or of a layer's experts) runs before any of it
+    changes."""
     for i, layer in enumerate(model.model.layers):
-        if not hasattr(layer.self_attn, "encoded"):
-            raise ECF8Error(f"layer {i} holds no compressed blocks")
+        if not hasattr(layer.self_attn, "encoded") or not all(
+                hasattr(ex, "encoded") for ex in layer.mlp.experts):
+            raise ECF8Error(f"layer {i} holds blocks that are not compressed")
+    cache = {}
+    untiled = []
+    for i, layer in enumerate(model.model.layers):
         key = i % len(drawn) if drawn is not None else None
-        install(layer.self_attn, ATTN_LINEARS,
-                encode(None if key is None else (key, "attn"), layer.self_attn, ATTN_LINEARS),
-                f"layer {i} attention")
+        got = tiled.tile_block(layer.self_attn, ATTN_LINEARS, cache,
+                               None if key is None else (key, "attn"), n_threads)
+        if isinstance(got, str):
+            untiled.append((f"model.layers.{i}.self_attn", got))
+        else:
+            tiled.install_tiles(layer.self_attn, ATTN_LINEARS, *got)
+        experts, refused = [], None
         for e, ex in enumerate(layer.mlp.experts):
-            install(ex, EXPERT_LINEARS,
-                    encode(None if key is None else (key, e), ex, EXPERT_LINEARS),
-                    f"layer {i} expert {e}")
+            got = tiled.tile_block(ex, EXPERT_LINEARS, cache,
+                                   None if key is None else (key, e), n_threads)
+            if isinstance(got, str):
+                refused = (f"model.layers.{i}.mlp.experts.{e}", got)
+                break
+            experts.append(got)
+        if refused is not None:
+            untiled.append((f"model.layers.{i}.mlp.experts",
+                            f"{refused[0]}: {refused[1]}; one grouped launch serves the layer's "
+                            "experts, so all of them stay on the routed decode"))
+            continue
+        for ex, got in zip(layer.mlp.experts, experts):
+            tiled.install_tiles(ex, EXPERT_LINEARS, *got)
+    tiled.report_untiled(untiled)
+    model.__dict__["_ecf8_untiled"] = untiled
     return model

@@ -26,7 +26,8 @@ import torch
 from ._lib import ECF8Error, check, lib
 
 __all__ = ["code_from_luts", "tile_encode", "TiledOperand", "tile_decode", "TileLinearPlan",
-           "linear_waves", "TileMoePlan", "TileDecodeBatch", "SEG_SYMBOLS"]
+           "linear_waves", "TileMoePlan", "TileDecodeBatch", "SEG_SYMBOLS", "tile_block",
+           "install_tiles", "report_untiled"]
 
 SEG_SYMBOLS = 2048
 _GROUP = 128
@@ -288,3 +289,74 @@ class TileDecodeBatch:
                 self.ops_dev.data_ptr(), self.tables_dev.data_ptr(), self.outs_dev.data_ptr(),
                 self.n_ops, self.n, self.k, torch.cuda.current_stream(self.device).cuda_stream),
                 "ecf8_tile_decode_batch")
+
+
+# ------------------------------------------------- re-tiling compressed blocks
+
+_BLOCK_KEYS = ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
+               "split_positions")
+
+
+def tile_block(mod, names, cache: dict | None = None, key=None, n_threads: int | None = None):
+    """Re-tile one compressed block (a module holding the reference-layout
+    buffers and ``weight_injection_modules``) without changing it.
+
+    Returns (encodings {Linear name: tile_encode result}, automaton table)
+    or, when the tiled layout cannot hold the block, the reason as a string:
+    LUTs with a 1-bit code (no automaton table), or a Linear whose 16x128
+    segment needs more than 64 chunks (over 3 bits per exponent).
+    ``cache`` / ``key``: blocks with equal contents share one encoding (or
+    one refusal)."""
+    from ._lib import ECF8_TABLE_DFA
+    from .decode import build_table, decode
+
+    table = build_table(mod.luts.contiguous())
+    if table.kind != ECF8_TABLE_DFA:
+        return "its LUTs hold a 1-bit code, which the tiled decode's automaton cannot take"
+    enc = cache.get(key) if cache is not None and key is not None else None
+    if enc is None:
+        flat = decode(mod.luts, mod.encoded, mod.packed_other_4bits, mod.output_positions,
+                      mod.gaps).cpu()
+        bits, vals = code_from_luts(mod.luts)
+        enc = {}
+        try:
+            for sub, part in zip(mod.weight_injection_modules,
+                                 torch.tensor_split(flat, mod.split_positions)):
+                name = next(n for n in names if mod.get_submodule(n) is sub)
+                enc[name] = tile_encode(part.view(sub.out_features, sub.in_features), bits, vals,
+                                        n_threads)
+        except ECF8Error as e:
+            enc = f"a Linear does not fit the tiled layout ({e})"
+        if cache is not None and key is not None:
+            cache[key] = enc
+    return enc if isinstance(enc, str) else (enc, table)
+
+
+def install_tiles(mod, names, enc: dict, table) -> None:
+    """Give a block its tiled Linears (from ``tile_block``) on its device
+    and drop its reference-layout buffers, decode hook and injected views.
+    The device copies are made before anything of the block changes."""
+    dev = mod.encoded.device
+    tiles = {}
+    for n in names:
+        sub = mod.get_submodule(n)
+        tiles[n] = TiledOperand(enc[n], sub.weight_scale_inv, sub.out_features, sub.in_features,
+                                dev)
+    mod._ecf8_tiles = tiles
+    mod._ecf8_tile_table = table
+    mod._forward_pre_hooks.clear()
+    for n in names:  # weight views a decode hook injected earlier
+        mod.get_submodule(n).__dict__.pop("weight", None)
+    for attr in _BLOCK_KEYS:
+        if attr in mod._buffers:
+            del mod._buffers[attr]
+    mod.__dict__.pop("_ecf8_state", None)
+    mod.__dict__.pop("_ecf8_launch", None)
+
+
+def report_untiled(untiled) -> None:
+    """One stderr line per block left on decode-then-GEMM."""
+    import sys
+
+    for name, reason in untiled:
+        print(f"[ecf8] {name} stays decode-then-GEMM: {reason}", file=sys.stderr)

@@ -15,6 +15,7 @@ from __future__ import annotations
 import math
 import sys
 
+import numpy as np
 import pytest
 import torch
 
@@ -647,3 +648,74 @@ def test_fused_attention_equals_the_unfused_pair(cuda_device, G):
         decode_attention(q, kc, vc, pos, attention_work(B, Hq, Lmax, dev), torch.empty_like(oqf),
                          torch.empty_like(osf), Hq, out_bf16=ob)
         assert torch.equal(obf, ob), p0
+
+
+def _skew_exponents(w, frac, exp, seed):
+    """e4m3fn weight with ``frac`` of its exponents set to ``exp`` (sign and
+    mantissa kept; exponent 15 with mantissa 7 avoided)."""
+    b = w.view(torch.uint8).clone()
+    rng = np.random.default_rng(seed)
+    hit = torch.from_numpy(rng.random(tuple(b.shape)) < frac)
+    b[hit] = (b[hit] & 0x87) | (exp << 3)
+    return b.view(FP8)
+
+
+def _spread_exponents(w, seed):
+    """e4m3fn weight with exponents drawn uniformly from 1..14 (about 3.8
+    bits each under any code), sign and mantissa kept."""
+    b = w.view(torch.uint8).clone()
+    rng = np.random.default_rng(seed)
+    e = torch.from_numpy(rng.integers(1, 15, tuple(b.shape), dtype=np.int64)).to(torch.uint8)
+    return ((b & 0x87) | (e << 3)).view(FP8)
+
+
+def test_retile_keeps_refused_layers_on_decode_then_gemm(cuda_device):
+    """Three layers: one the tiled layout holds, one whose LUTs have a
+    1-bit code (no automaton table) and one whose down projection needs
+    over 3 bits per exponent in its segments.  retile_layers re-tiles the
+    first, leaves the other two compressed with their decode hooks, and the
+    fused run gives the FP8 model's tokens and logits, eager and
+    graph-replayed."""
+    from dfloat.run.run import TensorManager
+    from ecf8_amd.llm import Qwen3Config, Qwen3Runner, compress_layers, random_model, \
+        retile_layers
+
+    cfg = Qwen3Config(**dict(SMALL, layers=3))
+    plain, drawn = random_model(cfg, cuda_device, seed=5)
+    for name in list(drawn[1]):
+        w, s = drawn[1][name]
+        drawn[1][name] = (_skew_exponents(w, 0.85, 11, seed=len(name)), s)
+    w, s = drawn[2]["mlp.down_proj"]
+    drawn[2]["mlp.down_proj"] = (_spread_exponents(w, seed=3), s)
+    for i, layer in enumerate(plain.model.layers):
+        for name, (w, _s) in drawn[i].items():
+            layer.get_submodule(name).weight.data.copy_(w.to(cuda_device))
+    comp, _ = random_model(cfg, cuda_device, seed=5)
+    compress_layers(comp, drawn)
+    retile_layers(comp, drawn)
+    untiled = dict(comp._ecf8_untiled)
+    assert sorted(untiled) == ["model.layers.1", "model.layers.2"], untiled
+    assert "1-bit code" in untiled["model.layers.1"]
+    assert "does not fit" in untiled["model.layers.2"]
+    l0, l1, l2 = comp.model.layers
+    assert hasattr(l0, "_ecf8_tiles") and not hasattr(l0, "encoded")
+    for lay in (l1, l2):
+        assert hasattr(lay, "encoded") and not hasattr(lay, "_ecf8_tiles")
+        assert len(lay._forward_pre_hooks) == 1
+    B, T, new = 2, 16, 6
+    prompt = _prompt(cfg, B, T)
+    results = {}
+    for name, model in (("fp8", plain), ("fused", comp)):
+        for graph in (False, True):
+            _say(f"[llm] partial retile {name} graph={graph}")
+            TensorManager.clear_device()
+            r = Qwen3Runner(model, B, T, T + new, cuda_device)
+            if graph:
+                r.capture()
+            toks = r.generate(prompt, new).cpu()
+            results[(name, graph)] = (toks, r.logits.float().cpu())
+            del r
+    base_t, base_l = results[("fp8", False)]
+    for key, (t, l) in results.items():
+        assert torch.equal(t, base_t), key
+        assert torch.equal(l, base_l), key

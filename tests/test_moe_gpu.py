@@ -287,12 +287,16 @@ def test_moe_with_a_multi_symbol_expert_matches_uncompressed(cuda_device):
     """An expert whose exponents are dominated by one value gets a 1-bit
     code, so its block needs the multi-symbol table and stays outside the
     batched launch: the routed decode still covers it, and the compressed
-    model gives the FP8 model's tokens and logits, eager and graph-replayed."""
+    model gives the FP8 model's tokens and logits, eager and graph-replayed.
+    Re-tiled, that expert's layer keeps all its experts on the routed decode
+    (one grouped launch serves a layer's experts) while its attention block
+    and the other layer are tiled, with the same tokens and logits."""
     from dfloat.run.run import TensorManager
     from ecf8_amd.decode import build_table
-    from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, random_moe_model
+    from ecf8_amd.moe import Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers, \
+        random_moe_model, retile_moe_layers
 
-    cfg = Qwen3MoeConfig(**dict(SMALL_MOE, layers=1))
+    cfg = Qwen3MoeConfig(**dict(SMALL_MOE, layers=2))
     plain, drawn = random_moe_model(cfg, cuda_device, seed=6)
     comp, _ = random_moe_model(cfg, cuda_device, seed=6)
     rng = np.random.default_rng(0)
@@ -308,7 +312,8 @@ def test_moe_with_a_multi_symbol_expert_matches_uncompressed(cuda_device):
     B, T, new = 4, 24, 5
     prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(4))
     results = {}
-    for name, model in (("fp8", plain), ("ecf8", comp)):
+
+    def run(name, model):
         for graph in (False, True):
             print(f"[moe multi] {name} graph={graph}", flush=True)
             TensorManager.clear_device()
@@ -317,6 +322,19 @@ def test_moe_with_a_multi_symbol_expert_matches_uncompressed(cuda_device):
                 r.capture()
             toks = r.generate(prompt, new).cpu()
             results[(name, graph)] = (toks, r.logits.float().cpu())
+            del r
+
+    run("fp8", plain)
+    run("ecf8", comp)
+    retile_moe_layers(comp, drawn)
+    untiled = dict(comp._ecf8_untiled)
+    assert list(untiled) == ["model.layers.0.mlp.experts"], untiled
+    assert "experts.3" in untiled["model.layers.0.mlp.experts"]
+    l0, l1 = comp.model.layers
+    assert hasattr(l0.self_attn, "_ecf8_tiles") and hasattr(l1.self_attn, "_ecf8_tiles")
+    assert all(hasattr(e, "encoded") and not hasattr(e, "_ecf8_tiles") for e in l0.mlp.experts)
+    assert all(hasattr(e, "_ecf8_tiles") and not hasattr(e, "encoded") for e in l1.mlp.experts)
+    run("fused", comp)
     base_t, base_l = results[("fp8", False)]
     for key, (t, l) in results.items():
         assert torch.equal(t, base_t), key

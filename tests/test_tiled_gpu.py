@@ -137,3 +137,50 @@ def test_tile_linear_refusals(layer, cuda_device):
         TileLinearPlan([ops["self_attn.k_proj"], ops["mlp.down_proj"]], table, out)  # K differs
     with pytest.raises(ECF8Error):
         TileLinearPlan([ops["self_attn.k_proj"]], table, out[:, :512])  # too few columns
+
+
+def test_tile_kernels_turn_a_non_automaton_table_into_nans(layer, cuda_device):
+    """The tile entry points cannot see on the host what kind of table a
+    device-built table is.  Handed a multi-symbol table (a block whose code
+    has a 1-bit symbol), the kernels read its kind word with the entries and
+    write NaNs over every output they own -- bf16 0x7FC0 from the linear,
+    e4m3fn 0x7F from the decode -- and nothing outside it."""
+    import ctypes
+
+    from ecf8_amd._lib import lib
+    from ecf8_amd.decode import build_table
+    from ecf8_amd.tiled import linear_waves
+
+    ops, _dense, _table = layer
+    # LUTs of a 1-bit code: exponent 11 for 80 % of the symbols
+    from dfloat.compress import compress_flat
+
+    rng = np.random.default_rng(1)
+    b = rng.integers(0, 256, 1 << 16, dtype=np.int64).astype(np.uint8)
+    hit = rng.random(b.size) < 0.8
+    b[hit] = (b[hit] & 0x87) | (11 << 3)
+    b[(b & 0x7F) == 0x7F] = 0x7E
+    res = compress_flat(torch.from_numpy(b).view(FP8))
+    multi = build_table(res["luts"].contiguous().to(cuda_device))
+    assert multi.kind == 0
+    stream = torch.cuda.current_stream(cuda_device).cuda_stream
+    op = ops["self_attn.o_proj"]
+    M = 5
+    aq, as_ = _activations(M, op.k, 2, cuda_device)
+    out = torch.zeros(M + 1, op.n + 128, dtype=torch.bfloat16, device=cuda_device)
+    s = op.c_struct(64)
+    rc = lib().ecf8_tile_linear(aq.data_ptr(), as_.data_ptr(), M, op.k, ctypes.byref(s), 1,
+                                multi.data.data_ptr(), out.data_ptr(), out.shape[1],
+                                linear_waves(op.n, op.k, cuda_device), stream)
+    assert rc == 0
+    got = out.view(torch.int16).cpu()
+    assert bool((got[:M, 64:64 + op.n] == 0x7FC0).all())
+    assert bool((got[:M, :64] == 0).all()) and bool((got[:M, 64 + op.n:] == 0).all())
+    assert bool((got[M] == 0).all())
+    dec = torch.zeros(op.n * op.k + 256, dtype=torch.uint8, device=cuda_device)
+    s0 = op.c_struct()
+    rc = lib().ecf8_tile_decode(ctypes.byref(s0), op.k, multi.data.data_ptr(), dec.data_ptr(),
+                                stream)
+    assert rc == 0
+    d = dec.cpu()
+    assert bool((d[: op.n * op.k] == 0x7F).all()) and bool((d[op.n * op.k:] == 0).all())
