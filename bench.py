@@ -179,6 +179,25 @@ def _qwen3_layer_workload(args, dev):
                               d["encoded"].numel(), n, max_block, min_bits,
                               d["table"].data.data_ptr(), d["table"].kind, 512, 8, hstream))
              for d in sets]
+    if args.call_form == "reference":
+        # each step as the reference's callers launch the kernel
+        # (dfloat/run/run.py:104-119): dfloat.run._decode, which checks its
+        # cached table against the LUTs on the device before the decode
+        from dfloat.run.run import _decode
+
+        def ref_call(d):
+            kw = dict(grid=(-(-d["encoded"].numel() // 4096),), block=(512,),
+                      shared_mem=512 * 4 + 4 + max_block,
+                      args=[d["luts"].data_ptr(), d["encoded"].data_ptr(),
+                            d["packed_other_4bits"].data_ptr(), d["output_positions"].data_ptr(),
+                            d["gaps"].data_ptr(), d["out"].data_ptr(), n_luts,
+                            d["encoded"].numel(), n])
+            return lambda: (_decode(**kw), 0)[1]
+
+        calls = [(ref_call(d), ()) for d in sets]
+        for fn, _ in calls:  # each set's table cache filled before timing
+            fn()
+        torch.cuda.synchronize()
 
     def verify():
         # every rotated set: each decoded the timed launches' bytes
@@ -196,6 +215,10 @@ def _qwen3_layer_workload(args, dev):
         "bytes_per_thread": 8,
         "table_kind": "dfa" if sets[0]["table"].kind == 1 else "multi",
     }
+    if args.call_form == "reference":
+        config["workload"] = "qwen3-8b-layer-decode-reference-call-form"
+        config["call_form"] = ("dfloat.run._decode(grid=, block=, shared_mem=, args=[...]): "
+                               "table-cache check kernel + decode kernel per step")
     return calls, verify, alg, n, config, (block, n, flat)
 
 
@@ -755,6 +778,9 @@ def main():
     ap.add_argument("--single-launches", type=int, default=10,
                     help="launches timed one by one (an event pair each) for the per-launch "
                          "kernel duration")
+    ap.add_argument("--call-form", choices=("abi", "reference"), default="abi",
+                    help="qwen3-8b-layer: 'reference' launches each step through "
+                         "dfloat.run._decode, the reference's RawKernel call form")
     ap.add_argument("--mode", choices=("decode", "copy"), default="decode",
                     help="copy: time a plain 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()

@@ -28,7 +28,7 @@ import torch
 import torch.nn as nn
 
 from ecf8_amd import decode as _dev
-from ecf8_amd._lib import ECF8_TABLE_ANY, ECF8_TABLE_BYTES, ECF8Error, check, lib
+from ecf8_amd._lib import ECF8_TABLE_ANY, ECF8_TABLE_CACHE_BYTES, ECF8Error, check, lib
 from ecf8_amd.hf_fp8 import bind_fp8_linears
 
 __all__ = [
@@ -51,13 +51,43 @@ class _DecodeLauncher:
     kernel's: luts, encoded, packed_other_4bits, output_positions, gaps,
     outputs (device addresses), n_luts, n_bytes, n_elements
     (decode.cu:16-26).  Like the reference's launch it is asynchronous on the
-    current stream: each call builds the derived table for the given LUTs on
-    the device (one workgroup, into a table buffer from torch's allocator on
-    that stream), then launches the decode, which reads the table's kind on
-    the device.  Nothing returns to the host, so the call can be captured in
-    a HIP graph, and a LUT buffer whose contents change between calls is
-    always decoded with its current contents.  The hook path builds each
-    module's table once instead."""
+    current stream.
+
+    The decode reads a derived table of the LUTs.  Each (device, stream, LUT
+    address, n_luts) keeps one table cache (``ecf8_build_table_cached``):
+    before every decode a one-workgroup kernel compares the LUT bytes with
+    the ones the cached table was built from and rebuilds it only if they
+    changed, so a LUT buffer rewritten between calls is always decoded with
+    its current contents, and an unchanged one costs a compare instead of a
+    rebuild.  The decode reads the table's kind on the device.  Nothing
+    returns to the host, so calls can be captured in a HIP graph.  At most
+    ``max_cached`` caches are kept (least recently used dropped first;
+    ECF8_TABLE_CACHE_BYTES each); ``clear()`` drops them all."""
+
+    max_cached = 512
+
+    def __init__(self):
+        from collections import OrderedDict
+
+        self._caches = OrderedDict()
+
+    def clear(self):
+        self._caches.clear()
+
+    def _table_cache(self, dev: int, st, luts: int, n_luts: int) -> torch.Tensor:
+        key = (dev, st.cuda_stream, luts, n_luts)
+        cache = self._caches.get(key)
+        if cache is None:
+            with torch.cuda.stream(st):
+                # zero-filled: never matches a LUT stack (n_luts >= 2)
+                cache = torch.zeros(ECF8_TABLE_CACHE_BYTES // 8, dtype=torch.int64,
+                                    device=torch.device("cuda", dev))
+            self._caches[key] = cache
+            while len(self._caches) > self.max_cached:
+                self._caches.popitem(last=False)
+        else:
+            self._caches.move_to_end(key)
+        return cache
 
     def __call__(self, grid, block, args, shared_mem: int = 0, stream=None):
         luts, encoded, packed, op, gaps, outputs, n_luts, n_bytes, n_elements = args
@@ -70,18 +100,14 @@ class _DecodeLauncher:
             raise ECF8Error(f"grid {nblk} does not cover {n_bytes} bytes with {tpb} threads")
         dev = torch.cuda.current_device()
         st = torch.cuda.current_stream(dev) if stream is None else stream
-        with torch.cuda.stream(st):
-            table = torch.empty(ECF8_TABLE_BYTES // 4, dtype=torch.int32,
-                                device=torch.device("cuda", dev))
+        cache = self._table_cache(dev, st, int(luts), int(n_luts))
         s = st.cuda_stream
         L = lib()
-        check(L.ecf8_build_table(int(luts), int(n_luts), ECF8_TABLE_ANY, table.data_ptr(), None, s),
-              "ecf8_build_table")
+        check(L.ecf8_build_table_cached(int(luts), int(n_luts), ECF8_TABLE_ANY, cache.data_ptr(),
+                                        s), "ecf8_build_table_cached")
         check(L.ecf8_decode(int(luts), int(encoded), int(packed), int(op), int(gaps), int(outputs),
                             int(n_luts), int(n_bytes), int(n_elements), max_block, 0,
-                            table.data_ptr(), ECF8_TABLE_ANY, tpb, bpt, s), "ecf8_decode")
-        # the table is freed back to torch's allocator on this stream: a later
-        # allocation on the stream runs after this decode
+                            cache.data_ptr(), ECF8_TABLE_ANY, tpb, bpt, s), "ecf8_decode")
 
 
 _decode = _DecodeLauncher()

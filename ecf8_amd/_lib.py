@@ -18,6 +18,7 @@ from .build import LIB_PATH
 ECF8_OK = 0
 ECF8_TABLE_BYTES = 24624
 ECF8_MAX_LUTS = 18
+ECF8_TABLE_CACHE_BYTES = ECF8_TABLE_BYTES + 8 + ECF8_MAX_LUTS * 256
 ECF8_TABLE_ANY = -1
 ECF8_TABLE_MULTI = 0
 ECF8_TABLE_DFA = 1
@@ -38,6 +39,7 @@ _SIGNATURES = {
     "ecf8_decode_batched_select": ([_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i32, _vp], _i32),
     "ecf8_build_table_host": ([_vp, _i32, _i32, _vp, _vp], _i32),
     "ecf8_build_table": ([_vp, _i32, _i32, _vp, _vp, _vp], _i32),
+    "ecf8_build_table_cached": ([_vp, _i32, _i32, _vp, _vp], _i32),
     "ecf8_decode": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _i32, _i32,
                      _i32, _vp], _i32),
     "ecf8_decode_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp],

@@ -30,18 +30,37 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
   return v;
 }
 
+// snap (optional): [n_luts, want_kind, LUT bytes] the table in `table` was
+// built from.  When it matches the current LUTs the table is kept as it is;
+// otherwise it is rebuilt and snap rewritten (after the comparison, which
+// every lane finishes before the barrier that publishes its result).
 __global__ __launch_bounds__(kBuildThreads) void build_table_kernel(
-    const uint8_t *__restrict__ luts, int n_luts, int want_kind, uint32_t *__restrict__ table) {
+    const uint8_t *__restrict__ luts, int n_luts, int want_kind, uint32_t *__restrict__ table,
+    uint32_t *__restrict__ snap) {
   __shared__ TableScratch s;
   __shared__ int s_wave_total[kBuildThreads / 64];
   __shared__ int s_fail;
   const int tid = threadIdx.x;
   const uint32_t *l32 = reinterpret_cast<const uint32_t *>(luts);
   uint32_t *s32 = reinterpret_cast<uint32_t *>(s.luts);
-  for (int i = tid; i < n_luts * 64; i += kBuildThreads) s32[i] = l32[i];
+  int differs = 0;
+  for (int i = tid; i < n_luts * 64; i += kBuildThreads) {
+    const uint32_t v = l32[i];
+    s32[i] = v;
+    if (snap) differs |= snap[2 + i] != v;
+  }
   if (tid == 0) {
     s.n_luts = n_luts;
     s_fail = 0;
+    if (snap) differs |= snap[0] != (uint32_t)n_luts || snap[1] != (uint32_t)want_kind;
+  }
+  if (snap) {
+    if (!__syncthreads_or(differs)) return;  // uniform: the table is current
+    for (int i = tid; i < n_luts * 64; i += kBuildThreads) snap[2 + i] = s32[i];
+    if (tid == 0) {
+      snap[0] = (uint32_t)n_luts;
+      snap[1] = (uint32_t)want_kind;
+    }
   }
   __syncthreads();
 
@@ -134,7 +153,7 @@ extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, 
   if (((uintptr_t)luts & 3) || ((uintptr_t)table & 3)) return ECF8_ERR_MISALIGNED;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(build_table_kernel, dim3(1), dim3(kBuildThreads), 0, s, luts, n_luts,
-                     want_kind, table);
+                     want_kind, table, static_cast<uint32_t *>(nullptr));
   if (hipGetLastError() != hipSuccess) return ECF8_ERR_HIP;
   if (!table_kind) return ECF8_OK;
   uint32_t kind = 0;
@@ -145,4 +164,19 @@ extern "C" int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, 
   if (kind != ECF8_TABLE_DFA && kind != ECF8_TABLE_MULTI) return ECF8_ERR_FORMAT;
   *table_kind = (int)kind;
   return ECF8_OK;
+}
+
+extern "C" int ecf8_build_table_cached(const uint8_t *luts, int n_luts, int want_kind, void *cache,
+                                       void *stream) {
+  if (!luts || !cache) return ECF8_ERR_INVALID_ARG;
+  if (n_luts < 2 || n_luts > ECF8_MAX_LUTS) return ECF8_ERR_FORMAT;
+  // the kind is only known on the device here, so the automaton cannot be
+  // demanded (a refusal could not be reported)
+  if (want_kind != ECF8_TABLE_ANY && want_kind != ECF8_TABLE_MULTI) return ECF8_ERR_INVALID_ARG;
+  if (((uintptr_t)luts & 3) || ((uintptr_t)cache & 7)) return ECF8_ERR_MISALIGNED;
+  static_assert(ECF8_TABLE_BYTES % 8 == 0, "the snapshot follows the table 8-byte aligned");
+  auto *table = static_cast<uint32_t *>(cache);
+  hipLaunchKernelGGL(build_table_kernel, dim3(1), dim3(kBuildThreads), 0, (hipStream_t)stream,
+                     luts, n_luts, want_kind, table, table + ECF8_TABLE_BYTES / 4);
+  return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }

@@ -91,7 +91,11 @@ extern "C" int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *cod
   memset(code_bits, 0, 16);
   memset(code_vals, 0, 16 * sizeof(uint32_t));
   // the symbol every 16-bit window decodes to under the reference rule
-  // (dfloat/run/decode.cu:85-91)
+  // (dfloat/run/decode.cu:85-91); kNoSymbol for a window whose result has no
+  // code (length 0): the LUT builder fills the range of the EOF code with
+  // the symbol before it, or with 0 when the EOF code is the lowest key --
+  // such windows only occur in a stream's final padding
+  constexpr uint8_t kNoSymbol = 0xFF;
   std::vector<uint8_t> sym(65536);
   for (uint32_t w = 0; w < 65536; ++w) {
     int v = luts[w >> 8];
@@ -102,8 +106,8 @@ extern "C" int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *cod
     }
     if (v > 15) return ECF8_ERR_FORMAT;
     const int len = len_row[v];
-    if (len < 1 || len > 16) return ECF8_ERR_FORMAT;
-    sym[w] = (uint8_t)v;
+    if (len > 16) return ECF8_ERR_FORMAT;
+    sym[w] = len ? (uint8_t)v : kNoSymbol;
   }
   // A symbol's code of length L: the first aligned block of 2^(16-L)
   // windows that all decode to it.  The rule decodes every window of such a

@@ -317,16 +317,16 @@ def tile_block(mod, names, cache: dict | None = None, key=None, n_threads: int |
     if enc is None:
         flat = decode(mod.luts, mod.encoded, mod.packed_other_4bits, mod.output_positions,
                       mod.gaps).cpu()
-        bits, vals = code_from_luts(mod.luts)
         enc = {}
         try:
+            bits, vals = code_from_luts(mod.luts)
             for sub, part in zip(mod.weight_injection_modules,
                                  torch.tensor_split(flat, mod.split_positions)):
                 name = next(n for n in names if mod.get_submodule(n) is sub)
                 enc[name] = tile_encode(part.view(sub.out_features, sub.in_features), bits, vals,
                                         n_threads)
         except ECF8Error as e:
-            enc = f"a Linear does not fit the tiled layout ({e})"
+            enc = f"the tiled layout cannot hold a Linear of the block ({e})"
         if cache is not None and key is not None:
             cache[key] = enc
     return enc if isinstance(enc, str) else (enc, table)

@@ -79,6 +79,24 @@ int ecf8_build_table(const uint8_t *luts, int n_luts, int want_kind, uint32_t *t
                      int *table_kind, void *stream);
 
 /*
+ * The derived table of `luts`, kept in a caller-owned device buffer `cache`
+ * of ECF8_TABLE_CACHE_BYTES (8-byte aligned): the table (its first
+ * ECF8_TABLE_BYTES, the `table` argument of ecf8_decode), then the LUT
+ * bytes and want_kind it was built from.  One workgroup on `stream`
+ * compares the LUTs with that copy and rebuilds the table (as
+ * ecf8_build_table with a NULL table_kind) only when they differ; a
+ * zero-filled cache never matches.  Fully asynchronous and capturable.
+ * No reference counterpart: it makes the reference's per-call decode form
+ * (the RawKernel launch of dfloat/run/run.py:104-119, which a call-form
+ * stand-in must serve without knowing whether the LUTs changed since the
+ * last call) cost a compare of at most 4,608 bytes instead of a rebuild.
+ * Calls sharing one cache must not overlap (one stream per cache).
+ */
+#define ECF8_TABLE_CACHE_BYTES (ECF8_TABLE_BYTES + 8 + ECF8_MAX_LUTS * 256)
+int ecf8_build_table_cached(const uint8_t *luts, int n_luts, int want_kind, void *cache,
+                            void *stream);
+
+/*
  * Decode one compressed block into FP8 e4m3fn bytes.
  * Replaces the CUDA kernel `decode` (dfloat/run/decode.cu:15-26) as launched
  * by decode_hook (dfloat/run/run.py:97-119) and validate_cuda_decoding_fp8

@@ -437,6 +437,93 @@ def test_device_table_builder_writes_the_host_builders_bytes(cuda_device):
     assert n_dfa >= 20  # both kinds are exercised
 
 
+def test_cached_table_is_rebuilt_only_when_the_luts_change(cuda_device):
+    """ecf8_build_table_cached: a zero-filled cache gets the table
+    ecf8_build_table writes; a call with unchanged LUTs leaves the cached
+    table as it is (a word planted in it survives); a call after the LUT
+    bytes (or their row count) change rebuilds it for the new LUTs."""
+    from ecf8_amd._lib import ECF8_MAX_LUTS, ECF8_TABLE_BYTES, ECF8_TABLE_CACHE_BYTES, lib
+    from ecf8_amd.decode import build_table_host
+
+    stacks = _lut_stacks()[:40]
+    L = lib()
+    stream = torch.cuda.current_stream(cuda_device).cuda_stream
+    words = ECF8_TABLE_BYTES // 4
+    cache = torch.zeros(ECF8_TABLE_CACHE_BYTES // 8, dtype=torch.int64, device=cuda_device)
+    luts_buf = torch.zeros(ECF8_MAX_LUTS * 256, dtype=torch.uint8, device=cuda_device)
+    table_of = lambda: cache.view(torch.int32)[:words].cpu().numpy().view(np.uint32)  # noqa: E731
+    prev = None
+    for i, luts in enumerate(stacks):
+        n_luts = luts.shape[0]
+        luts_buf[: n_luts * 256].copy_(torch.from_numpy(np.ascontiguousarray(luts).reshape(-1)))
+        want, _ = build_table_host(luts, ANY)
+        assert L.ecf8_build_table_cached(luts_buf.data_ptr(), n_luts, ANY, cache.data_ptr(),
+                                         stream) == 0
+        assert np.array_equal(table_of(), want), i
+        if prev is not None and np.array_equal(prev, want):
+            continue
+        # unchanged LUTs: the planted word stays, nothing is rebuilt
+        cache.view(torch.int32)[7] = 0x1234567
+        assert L.ecf8_build_table_cached(luts_buf.data_ptr(), n_luts, ANY, cache.data_ptr(),
+                                         stream) == 0
+        got = table_of()
+        assert got[7] == 0x1234567 and np.array_equal(np.delete(got, 7), np.delete(want, 7)), i
+        prev = want
+    # the same bytes under another row count are other LUTs
+    n_luts = stacks[-1].shape[0]
+    if n_luts > 2:
+        cache.view(torch.int32)[7] = 0x1234567
+        assert L.ecf8_build_table_cached(luts_buf.data_ptr(), n_luts - 1, ANY, cache.data_ptr(),
+                                         stream) == 0
+        want, _ = build_table_host(np.ascontiguousarray(stacks[-1][: n_luts - 1]), ANY)
+        assert np.array_equal(table_of(), want)
+    # refusals on the host, before any launch
+    assert L.ecf8_build_table_cached(luts_buf.data_ptr(), 1, ANY, cache.data_ptr(), stream) != 0
+    assert L.ecf8_build_table_cached(luts_buf.data_ptr(), 3, DFA, cache.data_ptr(), stream) != 0
+    assert L.ecf8_build_table_cached(luts_buf.data_ptr(), 3, ANY, cache.data_ptr() + 4,
+                                     stream) != 0
+
+
+def test_reference_call_form_keeps_one_table_per_lut_buffer(cuda_device):
+    """Repeated _decode calls on one block reuse one table cache (no
+    allocation after the first call), and the cache count stays bounded."""
+    from dfloat.run.run import _decode
+
+    flat = _random_block(3)
+    d = _dev_block(_compress(flat), cuda_device)
+    n_bytes = d["encoded"].numel()
+    out = torch.empty(flat.size, dtype=torch.float8_e4m3fn, device=cuda_device)
+    call = dict(grid=(-(-n_bytes // 4096),), block=(512,), shared_mem=0,
+                args=[d["luts"].data_ptr(), d["encoded"].data_ptr(),
+                      d["packed_other_4bits"].data_ptr(), d["output_positions"].data_ptr(),
+                      d["gaps"].data_ptr(), out.data_ptr(), d["luts"].shape[0], n_bytes,
+                      flat.size])
+    _decode.clear()
+    _decode(**call)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(cuda_device)
+    for _ in range(5):
+        out.view(torch.uint8).zero_()
+        _decode(**call)
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(cuda_device) == before
+    assert len(_decode._caches) == 1
+    assert np.array_equal(out.view(torch.uint8).cpu().numpy(), flat)
+    old = _decode.max_cached
+    copies = [d["luts"].clone() for _ in range(6)]  # six LUT buffers: six cache keys
+    try:
+        _decode.max_cached = 3
+        for luts in copies:
+            out.view(torch.uint8).zero_()
+            _decode(**dict(call, args=[luts.data_ptr()] + call["args"][1:]))
+            assert len(_decode._caches) <= 3
+        torch.cuda.synchronize()
+        assert np.array_equal(out.view(torch.uint8).cpu().numpy(), flat)
+    finally:
+        _decode.max_cached = old
+        _decode.clear()
+
+
 @pytest.mark.parametrize("seed", [0, 1, 4, 6])
 def test_decode_with_the_kind_read_on_the_device(seed, cuda_device):
     """A table built asynchronously (kind ECF8_TABLE_ANY): the decode

@@ -696,7 +696,7 @@ def test_retile_keeps_refused_layers_on_decode_then_gemm(cuda_device):
     untiled = dict(comp._ecf8_untiled)
     assert sorted(untiled) == ["model.layers.1", "model.layers.2"], untiled
     assert "1-bit code" in untiled["model.layers.1"]
-    assert "does not fit" in untiled["model.layers.2"]
+    assert "cannot hold a Linear" in untiled["model.layers.2"]
     l0, l1, l2 = comp.model.layers
     assert hasattr(l0, "_ecf8_tiles") and not hasattr(l0, "encoded")
     for lay in (l1, l2):

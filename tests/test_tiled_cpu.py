@@ -228,3 +228,20 @@ def test_layout_refusals():
     uni_bits, uni_vals = np.full(16, 4, np.uint8), np.arange(16, dtype=np.uint32)
     with pytest.raises(ECF8Error, match="too small"):
         tile_encode(flat, uni_bits, uni_vals)
+
+
+def test_code_read_off_luts_whose_eof_code_is_the_lowest_key():
+    """A code whose EOF code is all zeros leaves the lowest LUT entries to
+    the builder's default symbol 0, here absent from the data (length 0):
+    those windows carry no symbol, and every present symbol's code is still
+    recovered."""
+    from ecf8_amd.tiled import code_from_luts
+
+    _, _, table = oc.get_nbit_codec({11: 900, 12: 150}, 16)
+    luts = oc.get_luts_from_huffman_table(table)
+    assert luts[-1][0] == 0 and oc.lut_decode_one(luts, 0)[0] == 0  # code-less windows
+    bits, vals = code_from_luts(luts)
+    for sym, (nb, val) in table.items():
+        if isinstance(sym, int):
+            assert (bits[sym], vals[sym]) == (nb, val), sym
+    assert {s for s in range(16) if bits[s]} == {11, 12}
