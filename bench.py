@@ -83,34 +83,44 @@ def cpu_baseline(block, n_elements, alg_bytes, repeats=3):
     }
 
 
-def cpu_encode(flat, sample: int = 1048576):
+def cpu_encode(flat, seed: int = 0):
     """CPU encode timings (the reference's CPU path is its encoder,
     dfloat/utils.py:373-499): the product's C++ encoder (ecf8_encode_exponents,
     one thread) over the whole layer, and the oracle's per-symbol Python
-    restatement of the reference loop over the first `sample` elements."""
+    restatement of the reference loop over the 4096x4096 tensor the
+    reference's CPU case names (seeded N(0, 0.02), 128x128 block scales),
+    whose output the C decoder then checks against the original bytes."""
+    import numpy as np
     import torch
 
     from dfloat.compress import compress_flat
+    from ecf8_amd.synth import synthetic_fp8
     from oracle import codec as oc
+    from oracle import native
 
     n = flat.numel()
     t0 = time.perf_counter()
     compress_flat(flat)  # split + counts + codebook + LUTs + C++ bitstream encoder
     full = time.perf_counter() - t0
-    part = flat[:sample].view(torch.uint8).numpy()
+    w, _ = synthetic_fp8(4096, 4096, 0.02, seed=seed)
+    part = w.reshape(-1).view(torch.uint8).numpy()
     t0 = time.perf_counter()
-    oc.compress_block(part)
+    blk = oc.compress_block(part)
     py = time.perf_counter() - t0
+    back = native.decode(*(blk[k] for k in ("luts", "encoded", "packed_other_4bits",
+                                            "output_positions", "gaps")))
     return {
         "product_cpp": {"value": round(n / full / 1e6, 2), "unit": "M elements/s",
                         "cores": torch.get_num_threads(),
                         "sample": f"whole layer ({n} elements): split and counts (torch, "
                                   f"{torch.get_num_threads()} threads), codebook, LUTs, bitstream "
                                   f"(C++ encoder, 1 thread), {full:.2f} s"},
-        "reference_loop_python": {"value": round(sample / py / 1e6, 4), "unit": "M elements/s",
+        "reference_loop_python": {"value": round(part.size / py / 1e6, 4), "unit": "M elements/s",
                                   "cores": 1, "kind": "port",
-                                  "sample": f"first {sample} elements, per-symbol Python "
-                                            f"restatement of dfloat/utils.py:373-499, {py:.2f} s"},
+                                  "sample": f"4096x4096 seeded N(0, 0.02) tensor ({part.size} "
+                                            f"elements), per-symbol Python restatement of "
+                                            f"dfloat/utils.py:373-499, {py:.2f} s",
+                                  "round_trip_bit_exact": bool(np.array_equal(back, part))},
     }
 
 
@@ -441,6 +451,10 @@ def e2e_generate(args):
         if mode == "ecf8_fused":
             r["weights_mib"] += sum(op.nbytes() for layer in model.model.layers
                                     for op in layer._ecf8_tiles.values()) / 2**20
+        if mode in ("fp8", "ecf8_fused"):
+            r["linears"] = runner.time_linears()
+            print(f"[bench] {mode}: decode-step linears per layer {r['linears']}",
+                  file=sys.stderr, flush=True)
         results[mode] = r
         del runner
     ecf8_modes = ("ecf8", "ecf8_prefetch", "ecf8_fused")
@@ -478,8 +492,23 @@ def e2e_generate(args):
         "ecf8_modes": {m: summary(results[m]) for m in ecf8_modes},
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,
+        "linears_per_layer_step": {m: _linear_summary(results[m]["linears"])
+                                   for m in ("fp8", "ecf8_fused")},
     }
     return line
+
+
+def _linear_summary(lin: dict) -> dict:
+    """Per-layer decode-step linear times with their weight bytes as a rate
+    and a fraction of the HBM peak."""
+    total_us = sum(v["us"] for v in lin.values())
+    total_b = sum(v["bytes"] for v in lin.values())
+    out = {k: {"us": v["us"], "tb_per_s": round(v["bytes"] / (v["us"] * 1e-6) / 1e12, 3)}
+           for k, v in lin.items()}
+    out["layer"] = {"us": round(total_us, 2), "bytes": total_b,
+                    "tb_per_s": round(total_b / (total_us * 1e-6) / 1e12, 3),
+                    "hbm_frac": round(total_b / (total_us * 1e-6) / (HBM_PEAK_GBPS * 1e9), 4)}
+    return out
 
 
 def moe_generate(args):
@@ -709,34 +738,76 @@ def dit_generate(args):
         sys.exit(1)
 
 
-def e2e_child(workload: str, seed: int, timeout_s: float):
-    """Run an end-to-end workload of this script in a child process (its own
-    HIP context, so its kernels stay out of this process's profile and its
-    memory is returned when it ends) and return the summary of its JSON
-    line, or the reason it has none."""
+def _child_line(extra_args, timeout_s: float):
+    """Run this script with ``extra_args`` in a child process (its own HIP
+    context, so its kernels stay out of this process's profile and its
+    memory is returned when it ends); returns (JSON line, wall seconds) or
+    ({"error": reason}, wall seconds)."""
     import subprocess
 
-    cmd = [sys.executable, os.path.abspath(__file__), "--workload", workload, "--seed", str(seed)]
+    cmd = [sys.executable, os.path.abspath(__file__), *extra_args]
     t0 = time.perf_counter()
-    print(f"[bench] e2e child: {' '.join(cmd[1:])}", file=sys.stderr, flush=True)
+    print(f"[bench] child: {' '.join(cmd[1:])}", file=sys.stderr, flush=True)
     try:
         res = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
     except subprocess.TimeoutExpired:
-        return {"error": f"timed out after {timeout_s:.0f} s"}
+        return {"error": f"timed out after {timeout_s:.0f} s"}, time.perf_counter() - t0
     sys.stderr.write(res.stderr)
     lines = [ln for ln in res.stdout.splitlines() if ln.startswith("{")]
     if not lines:
-        return {"error": f"exit status {res.returncode}, no result line"}
-    full = json.loads(lines[-1])
+        return ({"error": f"exit status {res.returncode}, no result line"},
+                time.perf_counter() - t0)
+    return json.loads(lines[-1]), time.perf_counter() - t0
+
+
+def e2e_child(workload: str, seed: int, timeout_s: float):
+    """Summary of an end-to-end generate workload run in a child process
+    (see _child_line), or the reason it has none."""
+    full, wall = _child_line(["--workload", workload, "--seed", str(seed)], timeout_s)
+    if "error" in full:
+        return full
     keep = ("uncompressed_fp8", "ecf8", "ecf8_mode", "ecf8_modes", "ratio_vs_uncompressed",
-            "identical_tokens", "experts_routed_last_step")
+            "identical_tokens", "experts_routed_last_step", "linears_per_layer_step")
     out = {"workload": full["config"]["workload"], "unit": full["unit"],
            "batch": full["config"]["batch"], "prompt_len": full["config"]["prompt_len"],
            "new_tokens": full["config"]["new_tokens"],
            "ecf8_decode": full["config"]["ecf8_decode"]}
     out.update({k: full[k] for k in keep if k in full})
-    out["wall_s"] = round(time.perf_counter() - t0, 1)
+    out["wall_s"] = round(wall, 1)
     return out
+
+
+def dit_child(seed: int, timeout_s: float):
+    """Summary of the FLUX.1-dev-shaped DiT image (28 steps, every decode
+    mode) run in a child process."""
+    full, wall = _child_line(["--workload", "flux-dit-generate", "--seed", str(seed)], timeout_s)
+    if "error" in full:
+        return full
+    cfg = full["config"]
+    out = {"workload": cfg["workload"], "unit": full["unit"], "steps": cfg["steps"],
+           "image_tokens": cfg["image_tokens"], "text_tokens": cfg["text_tokens"],
+           "batch": cfg["batch"], "ecf8_decode": cfg["ecf8_decode"]}
+    out.update({k: full[k] for k in ("uncompressed_fp8", "ecf8", "ecf8_mode", "ecf8_modes",
+                                     "ratio_vs_uncompressed", "weights_bit_exact",
+                                     "identical_latents") if k in full})
+    out["wall_s"] = round(wall, 1)
+    return out
+
+
+def batched_child(seed: int, steps: int, warmup: int, timeout_s: float):
+    """The batched MoE-layer decode line (one Qwen3-30B-A3B-shaped layer,
+    attention + 128 experts in one launch) run in a child process with the
+    same step counts as this line."""
+    full, wall = _child_line(["--workload", "qwen3-moe-layer", "--seed", str(seed), "--steps",
+                              str(steps), "--warmup", str(warmup)], timeout_s)
+    if "error" in full:
+        return full
+    cfg = full["config"]
+    return {"workload": cfg["workload"], "blocks": cfg["blocks"], "elements": cfg["elements"],
+            "algorithmic_bytes": cfg["algorithmic_bytes"], "value": full["value"],
+            "unit": full["unit"], "steps": full["steps"], "warmup": full["warmup"],
+            "ms_per_step": full["ms_per_step"], "roofline": full["roofline"],
+            "bit_exact": full["bit_exact"], "wall_s": round(wall, 1)}
 
 
 def main():
@@ -772,9 +843,10 @@ def main():
     ap.add_argument("--distinct-layers", type=int, default=2,
                     help="generate: layers drawn independently (the rest copy them)")
     ap.add_argument("--e2e", choices=("all", "dense", "none"), default="all",
-                    help="qwen3-8b-layer: also run the end-to-end generate workloads (dense "
-                         "Qwen3-8B bs16, and the MoE) in child processes and report them in "
-                         "the line's e2e object")
+                    help="qwen3-8b-layer: also run the end-to-end workloads in child processes "
+                         "and report them in the line's e2e object (dense Qwen3-8B bs16; with "
+                         "'all' also the MoE, the FLUX DiT image, and the batched MoE-layer "
+                         "decode in the line's batched object)")
     ap.add_argument("--single-launches", type=int, default=10,
                     help="launches timed one by one (an event pair each) for the per-launch "
                          "kernel duration")
@@ -867,14 +939,16 @@ def main():
     cpu = enc = None
     if not args.no_cpu_baseline and cpu_case is not None:
         cpu = cpu_baseline(cpu_case[0], cpu_case[1], alg)
-        enc = cpu_encode(cpu_case[2])
-    e2e = None
-    if args.workload == "qwen3-8b-layer" and args.e2e != "none":
+        enc = cpu_encode(cpu_case[2], args.seed)
+    e2e = batched = None
+    if args.workload == "qwen3-8b-layer" and args.e2e != "none" and args.call_form == "abi":
         del calls, cpu_case
         torch.cuda.empty_cache()
         e2e = {"qwen3_8b_bs16": e2e_child("qwen3-8b-generate", args.seed, 420)}
         if args.e2e == "all":
             e2e["qwen3_30b_a3b_bs16"] = e2e_child("qwen3-moe-generate", args.seed, 480)
+            e2e["flux_dit_1024"] = dit_child(args.seed, 420)
+            batched = batched_child(args.seed, args.steps, args.warmup, 300)
     line = {
         "metric": "ECF8 decode GB/s + % HBM roofline; e2e tokens/s, Qwen3-8B-shape bs16",
         "value": round(gbps, 1),
@@ -901,6 +975,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_encode": enc,
         "e2e": e2e,
+        "batched": batched,
         "wall_s_timed": round(wall, 4),
         "bit_exact": ok,
     }

@@ -113,36 +113,49 @@ class _DecodeLauncher:
 _decode = _DecodeLauncher()
 
 
+def _device_key(device) -> torch.device:
+    """``device`` with its index filled in ("cuda" -> "cuda:<current>"), so
+    one device never holds two decode buffers."""
+    d = torch.device(device)
+    if d.type == "cuda" and d.index is None:
+        d = torch.device("cuda", torch.cuda.current_device())
+    return d
+
+
 class TensorManager:
-    """One grow-only e4m3fn decode buffer per device, shared by every
-    compressed block on it (dfloat/run/run.py:36-81)."""
+    """The decode buffer of each device, shared by every compressed block on
+    it (the reference keeps one per device, dfloat/run/run.py:36-81).
+
+    ``get_tensor`` hands out the first ``n_elements`` of the device's buffer.
+    The buffer only grows: when a block needs more (or another dtype), the
+    old buffer is released before the larger one is taken, so the two never
+    hold memory at once.  Blocks decode one after another on a device, so
+    sharing the buffer is safe; a caller that keeps a view past the next
+    decode on that device sees the next block's weights."""
 
     _tensors: Dict[torch.device, torch.Tensor] = {}
 
-    @staticmethod
-    def get_tensor(device, n_elements: int, dtype=torch.float8_e4m3fn) -> torch.Tensor:
-        if isinstance(device, str):
-            device = torch.device(device)
-        cur = TensorManager._tensors.get(device)
-        if cur is not None:
-            if cur.numel() >= n_elements:
-                return cur[:n_elements]
-            del TensorManager._tensors[device]
-            del cur
+    @classmethod
+    def get_tensor(cls, device, n_elements: int, dtype=torch.float8_e4m3fn) -> torch.Tensor:
+        key = _device_key(device)
+        buf = cls._tensors.get(key)
+        if buf is not None and buf.numel() >= n_elements and buf.dtype == dtype:
+            return buf[:n_elements]
+        if buf is not None:
+            del cls._tensors[key], buf
             torch.cuda.empty_cache()
-        new = torch.empty(n_elements, dtype=dtype, device=device)
-        print(f"Allocated {n_elements} {dtype} on device {device}", file=stderr)
-        TensorManager._tensors[device] = new
-        return new
+        buf = torch.empty(n_elements, dtype=dtype, device=key)
+        cls._tensors[key] = buf
+        print(f"[dfloat] decode buffer on {key}: {n_elements} elements of {dtype}", file=stderr)
+        return buf
 
-    @staticmethod
-    def clear_device(device=None):
+    @classmethod
+    def clear_device(cls, device=None):
+        """Release the buffer of ``device``, or of every device."""
         if device is None:
-            TensorManager._tensors.clear()
+            cls._tensors.clear()
         else:
-            if isinstance(device, str):
-                device = torch.device(device)
-            TensorManager._tensors.pop(device, None)
+            cls._tensors.pop(_device_key(device), None)
         torch.cuda.empty_cache()
 
 
@@ -251,39 +264,47 @@ def _shared_mem_size(module, threads_per_block: int) -> int:
 
 def _process_compressed_tensor(module, attr_name, tensor_value, tensor_name, pattern_dict,
                                threads_per_block, bytes_per_thread):
-    """Register one compressed tensor of a block (dfloat/run/run.py:406-458):
-    ``split_positions`` becomes a list attribute, everything else a buffer;
-    ``encoded`` also installs the decode hook and removes the dense weights
-    the block replaces; ``output_positions`` also records shared_mem_size."""
+    """Attach one tensor of a compressed block to its module, as the
+    reference's loader does (dfloat/run/run.py:406-458).
+
+    ``split_positions`` is kept as a list of ints; every other tensor becomes
+    a buffer.  Two tensors trigger more: ``output_positions`` fixes the
+    block's ``shared_mem_size``, and ``encoded`` -- the block itself -- gets
+    the decode hook and gives up the dense weights it replaces
+    (``_take_dense_weights``)."""
     if attr_name == "split_positions":
-        module.split_positions = tensor_value.tolist()
-    else:
-        module.register_buffer(attr_name, tensor_value)
-    if attr_name == "encoded":
-        module.register_forward_pre_hook(get_hook(threads_per_block, bytes_per_thread))
-        module_path = ".".join(tensor_name.split(".")[:-1])
-        for pattern, attr_names in pattern_dict.items():
-            if not re.fullmatch(pattern, module_path):
-                continue
-            if isinstance(module, (nn.Embedding, nn.Linear)):
-                tmp = module.weight
-                delattr(module, "weight")
-                del tmp
-            else:
-                module.weight_injection_modules = []
-                for attr_path in attr_names:
-                    target = module
-                    for p in attr_path.split("."):
-                        target = getattr(target, p)
-                    if not hasattr(target, "weight"):
-                        raise ValueError(f"Weight not found for {attr_path}")
-                    tmp = target.weight
-                    delattr(target, "weight")
-                    del tmp
-                    module.weight_injection_modules.append(target)
-            break
-    elif attr_name == "output_positions":
+        module.split_positions = [int(v) for v in tensor_value.tolist()]
+        return
+    module.register_buffer(attr_name, tensor_value)
+    if attr_name == "output_positions":
         module.shared_mem_size = _shared_mem_size(module, threads_per_block)
+    elif attr_name == "encoded":
+        module.register_forward_pre_hook(get_hook(threads_per_block, bytes_per_thread))
+        _take_dense_weights(module, tensor_name.rpartition(".")[0], pattern_dict)
+
+
+def _take_dense_weights(module, module_path: str, pattern_dict: dict) -> None:
+    """Drop the dense weights a compressed block replaces.  The first
+    pattern of ``pattern_dict`` that matches the block's path decides: a
+    block that is itself a Linear or Embedding loses its own ``weight``;
+    any other block loses the weights of the layers the pattern lists, and
+    those layers, in that order, become its ``weight_injection_modules``
+    (the hook's views of the decoded block go to them)."""
+    layer_paths = next((paths for pattern, paths in pattern_dict.items()
+                        if re.fullmatch(pattern, module_path)), None)
+    if layer_paths is None:
+        return
+    if isinstance(module, (nn.Linear, nn.Embedding)):
+        delattr(module, "weight")
+        return
+    targets = []
+    for path in layer_paths:
+        target = module.get_submodule(path)
+        if not hasattr(target, "weight"):
+            raise ValueError(f"{module_path}.{path} has no weight for the decoded block to replace")
+        delattr(target, "weight")
+        targets.append(target)
+    module.weight_injection_modules = targets
 
 
 def _process_file(model, path, pattern_dict, tpb, bpt, state_names, params, bufs, cache):

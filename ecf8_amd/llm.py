@@ -321,6 +321,59 @@ class Qwen3Runner(_GreedyRunner):
             self._tile_bufs[name] = buf
         return buf[:numel]
 
+    LINEARS = (("qkv", ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"), "qkv", "H"),
+               ("o", ("self_attn.o_proj",), "o", "A"),
+               ("gate_up", ("mlp.gate_proj", "mlp.up_proj"), "gu", "H"),
+               ("down", ("mlp.down_proj",), "down", "I"))
+
+    def time_linears(self, reps: int = 3) -> dict:
+        """Decode-step (M = batch) time of each linear of a layer: the
+        linear of every layer launched back to back between one event pair,
+        so the layers' weights stream from HBM as in a decode step (36
+        Qwen3-8B layers hold 5.8-6.9 GB, far above the 256 MB MALL); the
+        best of ``reps`` rounds, divided by the layer count.  Returns
+        {linear: {"us": ..., "bytes": weight bytes read per layer}}.  Runs
+        the FP8 linears of resident weights or the tiled linears of
+        re-tiled layers; layers decoded by their hooks share one buffer and
+        are not timed this way."""
+        cfg, M = self.cfg, self.B
+        layers = list(self.model.model.layers)
+        widths = {"H": cfg.hidden, "A": cfg.heads * cfg.head_dim, "I": cfg.intermediate}
+        dev = self.dev
+        res = {}
+        for which, names, out_name, kin in self.LINEARS:
+            K_in = widths[kin]
+            out = getattr(self, out_name)
+            plans, nbytes = [], 0
+            for i, layer in enumerate(layers):
+                tiles = getattr(layer, "_ecf8_tiles", None)
+                if tiles is None and hasattr(layer, "encoded"):
+                    raise ECF8Error("layers decoded by their hooks share one buffer")
+                plans.append(self._linear(layer, i, which, names, out, M))
+                if i == 0:
+                    nbytes = (sum(tiles[n].nbytes() + tiles[n].weight_scale.numel() * 4
+                                  for n in names) if tiles is not None else
+                              sum(layer.get_submodule(n).weight.numel() +
+                                  layer.get_submodule(n).weight_scale_inv.numel() * 4
+                                  for n in names))
+            aq, as_ = self.aq[K_in], self.as_[K_in]
+            for p in plans:  # warm-up round
+                p(aq, as_, M)
+            best = None
+            stream = torch.cuda.current_stream(dev)
+            for _ in range(reps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize(dev)
+                a.record(stream)
+                for p in plans:
+                    p(aq, as_, M)
+                b.record(stream)
+                torch.cuda.synchronize(dev)
+                ms = a.elapsed_time(b) / len(plans)
+                best = ms if best is None else min(best, ms)
+            res[which] = {"us": round(best * 1e3, 2), "bytes": int(nbytes)}
+        return res
+
     def layer(self, layer: DecoderLayer, index: int, x_prev, prefill: bool):
         cfg = self.cfg
         B, T = self.B, (self.T if prefill else 1)

@@ -48,8 +48,10 @@ extern "C" {
  * and code_vals[s] = the block's L-bit prefix; code_bits[s] = 0 when no
  * such block exists.  Every code so recovered decodes to its symbol under
  * the rule (the compressor's own code, except where code-less windows of an
- * incomplete code form an earlier such block).  ECF8_ERR_FORMAT when a
- * window decodes to no symbol.
+ * incomplete code form an earlier such block).  A window whose rule result
+ * has code length 0 (the EOF code's range filled with an absent symbol)
+ * carries no symbol; ECF8_ERR_FORMAT when a window leaves the LUT stack or
+ * yields a value above 15 or a length above 16.
  */
 int ecf8_code_from_luts(const uint8_t *luts, int n_luts, uint8_t *code_bits, uint32_t *code_vals);
 
