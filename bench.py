@@ -124,6 +124,88 @@ def cpu_encode(flat, seed: int = 0):
     }
 
 
+CEILING_SIZES = {  # bytes streamed by one launch, named for the decode path's launches
+    "o_proj 4096x4096": 4096 * 4096,
+    "qkv 6144x4096": 6144 * 4096,
+    "down 4096x12288": 4096 * 12288,
+    "gate_up 24576x4096": 24576 * 4096,
+    "qwen3-8b layer": 192937984,
+}
+
+
+def stream_ceiling(steps, warmup):
+    """What one launch of a plain streaming kernel reaches on this GPU, per
+    size the decode path streams: a read-only sweep and a copy
+    (ecf8_stream_probe) over every grid (1, 2, 4, 8 workgroups per CU),
+    workgroup size (256, 512, 1024 lanes), loads in flight per lane (1, 2,
+    4, 8) and load/store hint (plain, non-temporal); each size rotates over
+    enough buffers (>= 2 GiB) that the 256 MB MALL cannot serve a launch
+    from an earlier one.  Prints the best configuration per size and op."""
+    import torch
+
+    from ecf8_amd._lib import check, lib
+
+    dev = torch.device("cuda", 0)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    L = lib()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    hs = torch.cuda.current_stream(dev).cuda_stream
+    results, every = {}, []
+    for name, nbytes in CEILING_SIZES.items():
+        n_buf = max(2, -(-(2 << 30) // nbytes))
+        srcs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_buf)]
+        dsts = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_buf)]
+        for t in srcs:
+            t.random_(0, 256)
+        per_op = {}
+        for op, op_name in ((0, "read"), (1, "copy")):
+            best = None
+            for wpc in (1, 2, 4, 8):
+                for block in (256, 512, 1024):
+                    for depth in (1, 2, 4, 8):
+                        for nt in (0, 1):
+                            grid = cus * wpc
+
+                            def launch(i):
+                                check(L.ecf8_stream_probe(op, srcs[i % n_buf].data_ptr(),
+                                                          dsts[i % n_buf].data_ptr(), nbytes,
+                                                          grid, block, depth, nt,
+                                                          sink.data_ptr(), hs),
+                                      "ecf8_stream_probe")
+
+                            for i in range(warmup):
+                                launch(i)
+                            a = torch.cuda.Event(enable_timing=True)
+                            b = torch.cuda.Event(enable_timing=True)
+                            torch.cuda.synchronize()
+                            a.record()
+                            for i in range(steps):
+                                launch(warmup + i)
+                            b.record()
+                            torch.cuda.synchronize()
+                            us = a.elapsed_time(b) / steps * 1e3
+                            moved = nbytes * (1 if op == 0 else 2)
+                            cand = {"us": round(us, 2), "tb_per_s": round(moved / us / 1e6, 3),
+                                    "workgroups_per_cu": wpc, "block": block,
+                                    "loads_in_flight_per_lane": depth,
+                                    "nontemporal": bool(nt)}
+                            if best is None or us < best["us"]:
+                                best = cand
+                            every.append([op_name, name, wpc, block, depth, nt, round(us, 2)])
+            per_op[op_name] = best
+            print(f"[ceiling] {name}: {op_name} best {best}", file=sys.stderr, flush=True)
+        results[name] = {"bytes": nbytes, **per_op}
+        del srcs, dsts
+        torch.cuda.empty_cache()
+    line = {"metric": "one-launch streaming ceiling per size (read-only sweep and copy)",
+            "unit": "us per launch", "steps": steps, "warmup": warmup, "cus": cus,
+            "ceiling": results,
+            "sweep_columns": ["op", "size", "workgroups_per_cu", "block",
+                              "loads_in_flight_per_lane", "nontemporal", "us"],
+            "sweep": every}
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration(steps, warmup):
     """A plain device-to-device copy of known size (1 GiB read + 1 GiB
     written per launch): the reference point for scaling the HBM counters
@@ -853,8 +935,9 @@ def main():
     ap.add_argument("--call-form", choices=("abi", "reference"), default="abi",
                     help="qwen3-8b-layer: 'reference' launches each step through "
                          "dfloat.run._decode, the reference's RawKernel call form")
-    ap.add_argument("--mode", choices=("decode", "copy"), default="decode",
-                    help="copy: time a plain 1 GiB device copy (HBM counter calibration)")
+    ap.add_argument("--mode", choices=("decode", "copy", "ceiling"), default="decode",
+                    help="copy: time a plain 1 GiB device copy (HBM counter calibration); "
+                         "ceiling: sweep the streaming probe kernels per size")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -862,6 +945,8 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         return copy_calibration(args.steps, args.warmup)
+    if args.mode == "ceiling":
+        return stream_ceiling(args.steps, args.warmup)
     if args.workload in ("qwen3-8b-generate", "qwen3-moe-generate"):
         if args.workload == "qwen3-8b-generate":
             if args.new_tokens is None:

@@ -55,6 +55,7 @@ _SIGNATURES = {
         [_vp, _i32, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, ctypes.c_char_p, ctypes.c_size_t],
         _i32,
     ),
+    "ecf8_stream_probe": ([_i32, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp], _i32),
     # include/ecf8_tile.h: the tiled execution layout
     "ecf8_code_from_luts": ([_vp, _i32, _vp, _vp], _i32),
     "ecf8_tile_sizes": ([_vp, _i64, _i64, _vp, _vp, _vp], _i32),
@@ -79,8 +80,8 @@ _SIGNATURES = {
                                      _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp], _i32),
     "ecf8_moe_route": ([_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "ecf8_moe_group": ([_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
-    "ecf8_moe_linear": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _vp, _i64,
-                         _vp], _i32),
+    "ecf8_moe_linear": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i32, _vp,
+                         _i64, _vp], _i32),
     "ecf8_moe_combine": ([_vp, _i64, _vp, _vp, _i64, _i32, _i64, _vp, _vp], _i32),
 }
 

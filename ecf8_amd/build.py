@@ -16,6 +16,7 @@ REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libecf8.so")
 SOURCES = [os.path.join(HERE, "csrc", f)
            for f in ("ecf8_decode.hip", "ecf8_table_kernel.hip", "ecf8_llm.hip", "ecf8_tile.hip",
+                     "ecf8_stream.hip",
                      "ecf8_tables.cpp", "ecf8_host.cpp", "ecf8_tile_host.cpp")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

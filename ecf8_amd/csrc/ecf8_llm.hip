@@ -32,6 +32,26 @@ constexpr int kAttnChunk = 256;      // positions per attention workgroup
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Tile layout of FP8 operands (activations always, weights optionally; see
+// ecf8_llm.h): per 16 rows and 128-column group one 2 KB block in the
+// order the MFMA lanes take their operands -- lane l = 16 g + r holds row
+// r's bytes [16 g, +16) at byte 16 l and [64 + 16 g, +16) at 1024 + 16 l,
+// so each 16-byte load of a wave covers 1 KB contiguous.
+// Byte offset of row m's lane-part (g = 0) of group kg:
+__device__ __forceinline__ size_t tile_row_off(int m, int kg, int kgroups) {
+  return ((size_t)(m >> 4) * kgroups + kg) * 2048 + (size_t)(m & 15) * 16;
+}
+// ... and of the 16 bytes [16 c, +16) of the group (c = 0..7):
+__device__ __forceinline__ size_t tile_chunk_off(int m, int kg, int kgroups, int c) {
+  return tile_row_off(m, kg, kgroups) + (size_t)(c >> 2) * 1024 + (size_t)(c & 3) * 256;
+}
+// Per-lane base of row m's operand bytes (lane part g), to which a group
+// adds kg * 2048 and the second half 1024 more.
+__device__ __forceinline__ const uint8_t *tile_lane_base(const uint8_t *p, int m, int kgroups,
+                                                         int g) {
+  return p + tile_row_off(m, 0, kgroups) + (size_t)g * 256;
+}
+
 // 16-byte streaming load (weights are read once per launch)
 __device__ __forceinline__ uint4 load_stream16(const uint8_t *p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
@@ -119,7 +139,21 @@ struct LinearSegs {
   const float *ws[ECF8_LINEAR_MAX_SEGS];
   int n_end[ECF8_LINEAR_MAX_SEGS];  // cumulative output columns
   int col[ECF8_LINEAR_MAX_SEGS];    // first output column of the segment
+  int tiled[ECF8_LINEAR_MAX_SEGS];  // weight in the tile layout (else row-major)
   int count;
+};
+
+// A 16-row panel's weight operand for the lane (r, g): the lane's base
+// address, the step between 128-column groups and the offset of the
+// group's second half, in either weight layout.
+struct WeightLane {
+  const uint8_t *base;
+  int step, half;
+  __device__ __forceinline__ WeightLane(const uint8_t *w, bool tiled, int n0, int r, int g, int K)
+      : base(tiled ? tile_lane_base(w, n0 + r, K / kGroup, g) : w + (size_t)(n0 + r) * K + 16 * g),
+        step(tiled ? 2048 : kGroup),
+        half(tiled ? 1024 : 64) {}
+  __device__ __forceinline__ const uint8_t *at(int kg) const { return base + (size_t)kg * step; }
 };
 
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * w[n,k]) * as[m,g] * ws[n/128, g]
@@ -143,13 +177,14 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
   int n0 = blockIdx.x * 16;
   const uint8_t *w = segs.w[0];
   const float *ws = segs.ws[0];
-  int col = segs.col[0], seg_start = 0;
+  int col = segs.col[0], seg_start = 0, wt = segs.tiled[0];
 #pragma unroll
   for (int s = 1; s < ECF8_LINEAR_MAX_SEGS; ++s) {
     if (s < segs.count && n0 >= segs.n_end[s - 1]) {
       w = segs.w[s];
       ws = segs.ws[s];
       col = segs.col[s];
+      wt = segs.tiled[s];
       seg_start = segs.n_end[s - 1];
     }
   }
@@ -157,7 +192,7 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
 
   const int r = lane & 15, g = lane >> 4;
   const int m0 = blockIdx.y * 16 * MT;
-  const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+  const WeightLane wl(w, wt != 0, n0, r, g, K);
   const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
 
   float acc[MT][4];
@@ -174,8 +209,8 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
     for (int u = 0; u < kUnroll; ++u) {
       const int kg = kb + 8 * u;
       if (kg < kgroups) {
-        wv[u][0] = load_stream16(wrow + kg * kGroup);
-        wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+        wv[u][0] = load_stream16(wl.at(kg));
+        wv[u][1] = load_stream16(wl.at(kg) + wl.half);
         wsv[u] = wsrow[kg];
       }
     }
@@ -188,9 +223,9 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
         const int m = m0 + t * 16 + r;
         uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0;
         if (m < M) {
-          const uint8_t *ap = aq + (size_t)m * K + kg * kGroup + 16 * g;
+          const uint8_t *ap = tile_lane_base(aq, m, kgroups, g) + (size_t)kg * 2048;
           a0 = *reinterpret_cast<const uint4 *>(ap);
-          a1 = *reinterpret_cast<const uint4 *>(ap + 64);
+          a1 = *reinterpret_cast<const uint4 *>(ap + 1024);
         }
         v4f d = {0.f, 0.f, 0.f, 0.f};
         d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
@@ -241,23 +276,25 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
   int n0 = blockIdx.x * 16;
   const uint8_t *w = segs.w[0];
   const float *ws = segs.ws[0];
-  int col = segs.col[0], seg_start = 0;
+  int col = segs.col[0], seg_start = 0, wt = segs.tiled[0];
 #pragma unroll
   for (int s = 1; s < ECF8_LINEAR_MAX_SEGS; ++s) {
     if (s < segs.count && n0 >= segs.n_end[s - 1]) {
       w = segs.w[s];
       ws = segs.ws[s];
       col = segs.col[s];
+      wt = segs.tiled[s];
       seg_start = segs.n_end[s - 1];
     }
   }
   n0 -= seg_start;
 
   const int r = lane & 15, g = lane >> 4;
-  const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+  const WeightLane wl(w, wt != 0, n0, r, g, K);
   const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
   const bool row_ok = r < M;
-  const uint8_t *arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+  // rows past M (inside the padded 16-row tile) are zeroed after the load
+  const uint8_t *arow = tile_lane_base(aq, r, kgroups, g);
   bool srow_ok[4];
   const float *srow[4];
 #pragma unroll
@@ -275,12 +312,11 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
     for (int u = 0; u < kU; ++u) {
       const int kg = kb + WAVES * u;
       if (kg < kgroups) {
-        wv[u][0] = load_stream16(wrow + kg * kGroup);
-        wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+        wv[u][0] = load_stream16(wl.at(kg));
+        wv[u][1] = load_stream16(wl.at(kg) + wl.half);
         wsv[u] = wsrow[kg];
-        // rows past M read row 0 (always valid) and are zeroed after the load
-        av[u][0] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
-        av[u][1] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+        av[u][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048);
+        av[u][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048 + 1024);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sav[u][i] = srow[i][kg];
       }
@@ -342,12 +378,12 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
   uint4 av[kU][2];
   float sav[kU][4];
   {
-    const uint8_t *arow = aq + (size_t)(row_ok ? r : 0) * K + 16 * g;
+    const uint8_t *arow = tile_lane_base(aq, r, kgroups, g);
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int kg = wave + WAVES * u;
-      av[u][0] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
-      av[u][1] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+      av[u][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048);
+      av[u][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048 + 1024);
       if (!row_ok) av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -358,11 +394,13 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
     }
   }
 
-  auto tile_base = [&](int tile, const uint8_t *&w, const float *&ws, int &col, int &n0) {
+  auto tile_base = [&](int tile, const uint8_t *&w, const float *&ws, int &col, int &n0,
+                       int &wt) {
     n0 = tile * 16;
     w = segs.w[0];
     ws = segs.ws[0];
     col = segs.col[0];
+    wt = segs.tiled[0];
     int seg_start = 0;
 #pragma unroll
     for (int s2 = 1; s2 < ECF8_LINEAR_MAX_SEGS; ++s2) {
@@ -370,6 +408,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
         w = segs.w[s2];
         ws = segs.ws[s2];
         col = segs.col[s2];
+        wt = segs.tiled[s2];
         seg_start = segs.n_end[s2 - 1];
       }
     }
@@ -378,15 +417,15 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
   auto load_w = [&](int tile, uint4 (&wv)[kU][2], float (&wsv)[kU]) {
     const uint8_t *w;
     const float *ws;
-    int col, n0;
-    tile_base(tile, w, ws, col, n0);
-    const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+    int col, n0, wt;
+    tile_base(tile, w, ws, col, n0, wt);
+    const WeightLane wl(w, wt != 0, n0, r, g, K);
     const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int kg = wave + WAVES * u;
-      wv[u][0] = load_stream16(wrow + kg * kGroup);
-      wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+      wv[u][0] = load_stream16(wl.at(kg));
+      wv[u][1] = load_stream16(wl.at(kg) + wl.half);
       wsv[u] = wsrow[kg];
     }
   };
@@ -430,8 +469,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
       const int m = 4 * (l >> 4) + i;
       const uint8_t *w;
       const float *ws;
-      int col, n0;
-      tile_base(tile, w, ws, col, n0);
+      int col, n0, wt;
+      tile_base(tile, w, ws, col, n0, wt);
       if (m < M) out[(size_t)m * ldo + col + n0 + (l & 15)] = (uint16_t)f32_bf16(sum);
     }
     if (!more) break;
@@ -512,10 +551,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t *__res
         r[2 * i] = bf16_f32(p[i] & 0xffffu);
         r[2 * i + 1] = bf16_f32(p[i] >> 16);
       }
-      quant16(r, oq + base, os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
+      quant16(r, oq + tile_chunk_off(m, t >> 3, K / kGroup, t & 7),
+              os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
     }
   } else {
-    quant16(v, oq + base, os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
+    quant16(v, oq + tile_chunk_off(m, t >> 3, K / kGroup, t & 7),
+            os + (size_t)m * (K / kGroup) + (t >> 3), (t & 7) == 0);
   }
 }
 
@@ -532,8 +573,8 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t *__r
   load16_bf16(gu + (size_t)m * 2 * I + I + e, u);
 #pragma unroll
   for (int i = 0; i < 16; ++i) g[i] = g[i] / (1.f + expf(-g[i])) * u[i];
-  quant16(g, oq + (size_t)m * I + e, os + (size_t)m * (I / kGroup) + (e >> 7),
-          (threadIdx.x & 7) == 0);
+  quant16(g, oq + tile_chunk_off(m, e >> 7, I / kGroup, (e >> 4) & 7),
+          os + (size_t)m * (I / kGroup) + (e >> 7), (threadIdx.x & 7) == 0);
 }
 
 // plain bf16 -> e4m3fn per 1x128 group; grid (ceil(K / 4096), M), K a
@@ -545,8 +586,8 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restri
   if (e >= K) return;
   float v[16];
   load16_bf16(x + (size_t)m * K + e, v);
-  quant16(v, oq + (size_t)m * K + e, os + (size_t)m * (K / kGroup) + (e >> 7),
-          (threadIdx.x & 7) == 0);
+  quant16(v, oq + tile_chunk_off(m, e >> 7, K / kGroup, (e >> 4) & 7),
+          os + (size_t)m * (K / kGroup) + (e >> 7), (threadIdx.x & 7) == 0);
 }
 
 // --------------------------------------------- per-head norm + rotary + KV
@@ -617,8 +658,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 __device__ __forceinline__ void combine_head(const float *__restrict__ wm,
                                              const float *__restrict__ wl,
                                              const float *__restrict__ wacc, size_t bh, int S,
-                                             int used, int lane, uint8_t *__restrict__ oq,
-                                             float *__restrict__ os, uint16_t *__restrict__ ob) {
+                                             int used, int lane, int Hq,
+                                             uint8_t *__restrict__ oq, float *__restrict__ os,
+                                             uint16_t *__restrict__ ob) {
   float mx = -INFINITY;
   for (int s = 0; s < used; ++s) mx = fmaxf(mx, wm[bh * S + s]);
   float l = 0.f, a0 = 0.f, a1 = 0.f;
@@ -635,7 +677,10 @@ __device__ __forceinline__ void combine_head(const float *__restrict__ wm,
   float amax = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
   const float sc = amax > 0.f ? amax / kFp8Max : 1.f;
   const uint32_t q2 = f32_e4m3(a0 / sc) | (f32_e4m3(a1 / sc) << 8);
-  reinterpret_cast<uint16_t *>(oq)[bh * 64 + lane] = (uint16_t)q2;
+  // row b = bh / Hq, group = head: bytes 2 lane, 2 lane + 1 of the group
+  const int b = (int)(bh / (size_t)Hq), head = (int)(bh % (size_t)Hq);
+  *reinterpret_cast<uint16_t *>(oq + tile_chunk_off(b, head, Hq, lane >> 3) + 2 * (lane & 7)) =
+      (uint16_t)q2;
   if (lane == 0) os[bh] = sc;
 }
 
@@ -827,13 +872,13 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
                                                           const float *__restrict__ wl,
                                                           const float *__restrict__ wacc,
                                                           const int *__restrict__ pos, int Lmax,
-                                                          int S, uint8_t *__restrict__ oq,
+                                                          int S, int Hq, uint8_t *__restrict__ oq,
                                                           float *__restrict__ os,
                                                           uint16_t *__restrict__ ob) {
   int L = pos[0] + 1;
   L = L < 1 ? 1 : (L > Lmax ? Lmax : L);
   const int used = (L + kAttnChunk - 1) / kAttnChunk;
-  combine_head(wm, wl, wacc, blockIdx.x, S, used, threadIdx.x, oq, os, ob);
+  combine_head(wm, wl, wacc, blockIdx.x, S, used, threadIdx.x, Hq, oq, os, ob);
 }
 
 // ---------------------------------------------------- FP8 block dequantize
@@ -1104,6 +1149,7 @@ struct MoeLinear {
   const uint64_t *ws;  // [E * n_segs] scale addresses
   uint16_t *out;
   int n_segs, seg_n, K, ldo;
+  int wtiled;  // expert weights in the tile layout (else row-major)
 };
 
 template <int WAVES, int kU>
@@ -1121,14 +1167,14 @@ __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
   const int K = a.K, kgroups = K / kGroup;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const uint8_t *wrow = w + (size_t)(n0 + r) * K + 16 * g;
+  const WeightLane wl(w, a.wtiled != 0, n0, r, g, K);
   const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
 
   for (int rc = 0; rc < rows; rc += 16) {
     const int mrows = min(16, rows - rc);
     const bool row_ok = r < mrows;
     const int q = r0 + rc + (row_ok ? r : 0);
-    const uint8_t *arow = a.aq + (size_t)(a.row_of ? a.row_of[q] : q) * K + 16 * g;
+    const uint8_t *arow = tile_lane_base(a.aq, a.row_of ? a.row_of[q] : q, kgroups, g);
     bool srow_ok[4];
     const float *srow[4];
 #pragma unroll
@@ -1145,11 +1191,11 @@ __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
       for (int u = 0; u < kU; ++u) {
         const int kg = kb + WAVES * u;
         if (kg < kgroups) {
-          wv[u][0] = load_stream16(wrow + kg * kGroup);
-          wv[u][1] = load_stream16(wrow + kg * kGroup + 64);
+          wv[u][0] = load_stream16(wl.at(kg));
+          wv[u][1] = load_stream16(wl.at(kg) + wl.half);
           wsv[u] = wsrow[kg];
-          av[u][0] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup);
-          av[u][1] = *reinterpret_cast<const uint4 *>(arow + kg * kGroup + 64);
+          av[u][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048);
+          av[u][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048 + 1024);
 #pragma unroll
           for (int i = 0; i < 4; ++i) sav[u][i] = srow[i][kg];
         }
@@ -1242,6 +1288,8 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
   for (int i = 0; i < n_segs; ++i) {
     const ecf8_linear_seg &g = segs[i];
     if (!g.weight || !g.weight_scale || g.n <= 0 || g.out_col < 0) return ECF8_ERR_INVALID_ARG;
+    if (g.weight_layout != ECF8_WEIGHT_ROWS && g.weight_layout != ECF8_WEIGHT_TILES)
+      return ECF8_ERR_INVALID_ARG;
     if (g.n % kGroup) return ECF8_ERR_UNSUPPORTED;
     if (!aligned(g.weight, 16) || !aligned(g.weight_scale, 4)) return ECF8_ERR_MISALIGNED;
     if (g.out_col + g.n > ldo) return ECF8_ERR_CAPACITY;
@@ -1250,6 +1298,7 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
     s.ws[i] = g.weight_scale;
     s.n_end[i] = (int)n_total;
     s.col[i] = (int)g.out_col;
+    s.tiled[i] = g.weight_layout == ECF8_WEIGHT_TILES;
   }
   if (n_total > (1 << 24)) return ECF8_ERR_UNSUPPORTED;
   s.count = n_segs;
@@ -1388,7 +1437,7 @@ extern "C" int ecf8_decode_attention(const void *q, const void *k_cache, const v
     attn_split_kernel<8, false><<<grid, 256, 0, as_stream(stream)>>>(
         qp, kp, vp, pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc, none);
   attn_combine_kernel<<<(unsigned)(B * Hq), 64, 0, as_stream(stream)>>>(
-      wm, wl, wacc, pos, (int)Lmax, (int)S, static_cast<uint8_t *>(out_q), out_scale,
+      wm, wl, wacc, pos, (int)Lmax, (int)S, Hq, static_cast<uint8_t *>(out_q), out_scale,
       static_cast<uint16_t *>(out_bf16));
   return launched();
 }
@@ -1423,7 +1472,7 @@ extern "C" int ecf8_decode_attention_fused(const void *qkv, int64_t B, int Hq, i
     attn_split_kernel<8, true><<<grid, 256, 0, as_stream(stream)>>>(
         nullptr, kp, vp, pos, Hkv, (int)Lmax, (int)S, wm, wl, wacc, fu);
   attn_combine_kernel<<<(unsigned)(B * Hq), 64, 0, as_stream(stream)>>>(
-      wm, wl, wacc, pos, (int)Lmax, (int)S, static_cast<uint8_t *>(out_q), out_scale,
+      wm, wl, wacc, pos, (int)Lmax, (int)S, Hq, static_cast<uint8_t *>(out_q), out_scale,
       static_cast<uint16_t *>(out_bf16));
   return launched();
 }
@@ -1465,9 +1514,11 @@ extern "C" int ecf8_moe_linear(const void *aq, const float *as, const int *row_o
                                const int *offsets, const int *active, const int *n_active,
                                int n_experts, const void *const *weights,
                                const float *const *weight_scales, int n_segs, int64_t seg_n,
-                               int64_t K, void *out, int64_t ldo, void *stream) {
+                               int64_t K, int weight_layout, void *out, int64_t ldo,
+                               void *stream) {
   if (!aq || !as || !offsets || !active || !n_active || !weights || !weight_scales || !out ||
-      n_experts <= 0 || n_segs < 1 || n_segs > ECF8_LINEAR_MAX_SEGS || seg_n <= 0 || K <= 0)
+      n_experts <= 0 || n_segs < 1 || n_segs > ECF8_LINEAR_MAX_SEGS || seg_n <= 0 || K <= 0 ||
+      (weight_layout != ECF8_WEIGHT_ROWS && weight_layout != ECF8_WEIGHT_TILES))
     return ECF8_ERR_INVALID_ARG;
   if (seg_n % kGroup || K % kGroup || K > (1 << 20) || n_segs * seg_n > (1 << 20) ||
       n_experts > 65535)
@@ -1479,7 +1530,7 @@ extern "C" int ecf8_moe_linear(const void *aq, const float *as, const int *row_o
   MoeLinear a{static_cast<const uint8_t *>(aq), as, row_of, offsets, active, n_active,
               reinterpret_cast<const uint64_t *>(weights),
               reinterpret_cast<const uint64_t *>(weight_scales), static_cast<uint16_t *>(out),
-              n_segs, (int)seg_n, (int)K, (int)ldo};
+              n_segs, (int)seg_n, (int)K, (int)ldo, weight_layout == ECF8_WEIGHT_TILES};
   const dim3 grid((unsigned)(n_segs * seg_n / 16), (unsigned)n_experts);
   // each wave's share of the K groups in one batch of loads where it fits
   const int64_t kg = K / kGroup;

@@ -614,7 +614,11 @@ void tile_linear16_kernel(
     return (uint32_t)q;
   };
   const int r = lane & 15, g = lane >> 4;
-  const uint8_t *const arow = a.aq + (size_t)a_row(r) * K + 16 * g;
+  // activations in the tile layout (include/ecf8_llm.h): row R's lane part
+  // g of group kg at ((R / 16) * kgroups + kg) * 2048 + (R % 16) * 16 + 256 g
+  const uint32_t arow_r = a_row(r);
+  const uint8_t *const arow =
+      a.aq + (size_t)(arow_r >> 4) * kgroups * 2048 + (arow_r & 15u) * 16u + 256u * (uint32_t)g;
   uint32_t srow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
@@ -777,8 +781,8 @@ void tile_linear16_kernel(
       if constexpr (kOthNow)
         on[j] = seg_other(sc[j].op, (uint32_t)sc[j].p * (uint32_t)kgroups + (uint32_t)sc[j].kg,
                           lane);
-      av[j][0] = *reinterpret_cast<const uint4 *>(arow + sc[j].kg * kGroup);
-      av[j][1] = *reinterpret_cast<const uint4 *>(arow + sc[j].kg * kGroup + 64);
+      av[j][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)sc[j].kg * 2048);
+      av[j][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)sc[j].kg * 2048 + 1024);
 #pragma unroll
       for (int i = 0; i < 4; ++i) sav[j][i] = as[srow[i] + (uint32_t)sc[j].kg];
     }

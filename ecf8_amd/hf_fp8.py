@@ -62,7 +62,7 @@ def engine_fp8_linear(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Te
         return x.new_empty(*lead, n)
     xb = x2.to(torch.bfloat16).contiguous()
     dev = x.device
-    aq = torch.empty(m, k, dtype=torch.float8_e4m3fn, device=dev)
+    aq = torch.empty(K.pad16(m), k, dtype=torch.float8_e4m3fn, device=dev)  # tile layout
     a_scale = torch.empty(m, k // K.GROUP, dtype=torch.float32, device=dev)
     K.act_quant(xb, m, aq, a_scale)
     out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)

@@ -63,7 +63,9 @@ class Qwen3Config:
 
 class FP8Linear(nn.Module):
     """e4m3fn weight [out, in] with fp32 scale_inv per 128x128 block (the
-    FP8 checkpoint layout); ``weight`` may be replaced by an injected view."""
+    FP8 checkpoint layout); ``weight`` may be replaced by an injected view.
+    ``weight_layout``: K.WEIGHT_ROWS (row-major, as loaded or injected) or
+    K.WEIGHT_TILES (re-laid out by ``tile_resident_weights``)."""
 
     def __init__(self, in_features: int, out_features: int):
         super().__init__()
@@ -72,6 +74,33 @@ class FP8Linear(nn.Module):
                                    requires_grad=False)
         self.register_buffer("weight_scale_inv", torch.ones(
             math.ceil(out_features / 128), math.ceil(in_features / 128), dtype=torch.float32))
+        self.weight_layout = K.WEIGHT_ROWS
+
+
+def weight_layout(lin) -> int:
+    """The layout of a Linear's current ``weight`` (row-major unless
+    ``tile_resident_weights`` re-laid it out)."""
+    return getattr(lin, "weight_layout", K.WEIGHT_ROWS)
+
+
+def tile_resident_weights(model: nn.Module) -> int:
+    """Re-lay every resident FP8 Linear weight of ``model`` out in the tile
+    layout of include/ecf8_llm.h (in place: one copy, the same bytes
+    reordered), which the FP8 linears read with 1 KB-contiguous loads;
+    returns the number of Linears changed.  Compressed blocks (weights
+    injected row-major by their decode hooks) are not touched."""
+    count = 0
+    for mod in model.modules():
+        if isinstance(mod, FP8Linear) and "weight" in mod._parameters \
+                and weight_layout(mod) == K.WEIGHT_ROWS:
+            w = mod.weight
+            if w.shape[0] % 16 or w.shape[1] % 128:
+                continue
+            with torch.no_grad():
+                mod.weight = nn.Parameter(K.to_tiles(w.data), requires_grad=False)
+            mod.weight_layout = K.WEIGHT_TILES
+            count += 1
+    return count
 
 
 class RMSNorm(nn.Module):
@@ -141,9 +170,9 @@ class _GreedyRunner:
 
     def _plan(self, layer, index, which, weights, out):
         """Linear argument blocks are cached per (layer, which, weight
-        addresses): injected views of the decode buffer keep their
-        addresses from call to call."""
-        key = (index, which, tuple(w.data_ptr() for w, _ in weights))
+        addresses and layouts): injected views of the decode buffer keep
+        their addresses from call to call."""
+        key = (index, which, tuple((e[0].data_ptr(),) + tuple(e[2:]) for e in weights))
         p = self._plans.get(key)
         if p is None:
             p = K.LinearPlan(weights, out)
@@ -266,7 +295,8 @@ class Qwen3Runner(_GreedyRunner):
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.step = torch.zeros(1, dtype=torch.int64, device=dev)
         self.res = torch.empty(M, cfg.hidden, dtype=torch.float32, device=dev)
-        self.aq = {k: torch.empty(M, k, dtype=torch.float8_e4m3fn, device=dev)
+        # quantized activations in the tile layout: rows padded to 16
+        self.aq = {k: torch.empty(K.pad16(M), k, dtype=torch.float8_e4m3fn, device=dev)
                    for k in sorted({cfg.hidden, cfg.intermediate, Hq * D})}
         self.as_ = {k: torch.empty(M, k // 128, dtype=torch.float32, device=dev) for k in self.aq}
         self.qkv = torch.empty(M, (Hq + 2 * Hkv) * D, **bf)
@@ -293,8 +323,8 @@ class Qwen3Runner(_GreedyRunner):
         tiles = getattr(layer, "_ecf8_tiles", None)
         if tiles is None:
             mods = [layer.get_submodule(n) for n in names]
-            return self._plan(layer, index, which, [(x.weight, x.weight_scale_inv) for x in mods],
-                              out)
+            return self._plan(layer, index, which,
+                              [(x.weight, x.weight_scale_inv, weight_layout(x)) for x in mods], out)
         if M <= 16:
             key = (index, which, "tiled")
             p = self._plans.get(key)
@@ -328,8 +358,9 @@ class Qwen3Runner(_GreedyRunner):
 
     def time_linears(self, reps: int = 3) -> dict:
         """Decode-step (M = batch) time of each linear of a layer: the
-        linear of every layer launched back to back between one event pair,
-        so the layers' weights stream from HBM as in a decode step (36
+        linear of every layer launched back to back (one HIP graph replayed
+        between one event pair), so the layers' weights stream from HBM as
+        in a decode step (36
         Qwen3-8B layers hold 5.8-6.9 GB, far above the 256 MB MALL); the
         best of ``reps`` rounds, divided by the layer count.  Returns
         {linear: {"us": ..., "bytes": weight bytes read per layer}}.  Runs
@@ -359,18 +390,27 @@ class Qwen3Runner(_GreedyRunner):
             aq, as_ = self.aq[K_in], self.as_[K_in]
             for p in plans:  # warm-up round
                 p(aq, as_, M)
+            torch.cuda.synchronize(dev)
+            # one graph of the launches, so host launch time cannot starve
+            # the GPU between these short kernels (a decode step replays a
+            # graph too)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for p in plans:
+                    p(aq, as_, M)
+            graph.replay()
             best = None
             stream = torch.cuda.current_stream(dev)
             for _ in range(reps):
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 torch.cuda.synchronize(dev)
                 a.record(stream)
-                for p in plans:
-                    p(aq, as_, M)
+                graph.replay()
                 b.record(stream)
                 torch.cuda.synchronize(dev)
                 ms = a.elapsed_time(b) / len(plans)
                 best = ms if best is None else min(best, ms)
+            del graph
             res[which] = {"us": round(best * 1e3, 2), "bytes": int(nbytes)}
         return res
 
@@ -466,7 +506,9 @@ def compress_layers(model: Qwen3ForCausalLM, drawn=None, threads_per_block: int 
                     "split_positions": torch.tensor(split, dtype=torch.int64)}
             if drawn is not None:
                 cache[key] = comp
-        dev = layer.self_attn.q_proj.weight.device
+        dev = layer.self_attn.q_proj.weight_scale_inv.device
+        for n in LINEAR_NAMES:  # the hook injects row-major views of the decoded block
+            layer.get_submodule(n).weight_layout = K.WEIGHT_ROWS
         for attr in ("luts", "encoded", "packed_other_4bits", "output_positions", "gaps",
                      "split_positions"):
             value = comp[attr] if attr == "split_positions" else comp[attr].to(dev).clone()

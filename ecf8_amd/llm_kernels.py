@@ -14,11 +14,49 @@ from ._lib import ECF8Error, check, lib
 
 GROUP = 128
 MAX_SEGS = 3
+WEIGHT_ROWS, WEIGHT_TILES = 0, 1  # ECF8_WEIGHT_ROWS / ECF8_WEIGHT_TILES
 
 
 class _Seg(ctypes.Structure):
     _fields_ = [("weight", ctypes.c_void_p), ("weight_scale", ctypes.c_void_p),
-                ("n", ctypes.c_int64), ("out_col", ctypes.c_int64)]
+                ("n", ctypes.c_int64), ("out_col", ctypes.c_int64),
+                ("weight_layout", ctypes.c_int64)]
+
+
+def pad16(rows: int) -> int:
+    """Rows of a tile-layout buffer holding ``rows`` rows."""
+    return (int(rows) + 15) // 16 * 16
+
+
+def to_tiles(x: torch.Tensor) -> torch.Tensor:
+    """[R, K] e4m3fn/uint8 row-major -> the tile layout of include/ecf8_llm.h
+    as a [pad16(R), K] tensor of the same dtype (pad rows zero): per 16
+    rows and 128 columns a 2 KB block, lane l = 16 g + r holding row r's
+    bytes [16 g, +16) at 16 l and [64 + 16 g, +16) at 1024 + 16 l."""
+    R, K = x.shape
+    if K % GROUP:
+        raise ECF8Error("the tile layout needs K a multiple of 128")
+    b = x.view(torch.uint8)
+    Rp = pad16(R)
+    if Rp != R:
+        b = torch.cat([b, b.new_zeros(Rp - R, K)])
+    t = b.reshape(Rp // 16, 16, K // GROUP, 2, 4, 16).permute(0, 2, 3, 4, 1, 5)
+    return t.contiguous().view(Rp, K).view(x.dtype)
+
+
+def from_tiles(t: torch.Tensor, R: int, K: int) -> torch.Tensor:
+    """The first R rows of a tile-layout buffer, row-major [R, K]."""
+    Rp = pad16(R)
+    b = t.reshape(-1).view(torch.uint8)[: Rp * K]
+    x = b.view(Rp // 16, K // GROUP, 2, 4, 16, 16).permute(0, 4, 1, 2, 3, 5)
+    return x.contiguous().view(Rp, K)[:R].view(t.dtype)
+
+
+def _act_rows(M, K, t, name):
+    """A tile-layout activation buffer ``t`` holds M rows of K columns."""
+    if t is not None and (t.dim() != 2 or t.shape[1] != K or t.shape[0] < pad16(M)):
+        raise ECF8Error(f"{name} {tuple(t.shape)} is not a tile-layout [>= {pad16(M)}, {K}] "
+                        "buffer (rows padded to 16)")
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -53,7 +91,9 @@ class LinearPlan:
 
     def __init__(self, weights, out: torch.Tensor):
         """``weights``: list of (weight e4m3fn [n, K], weight_scale_inv f32
-        [n/128, K/128]); outputs are written side by side into ``out``
+        [n/128, K/128]) or (weight, scale, layout) with layout WEIGHT_ROWS
+        (row-major, the default) or WEIGHT_TILES (the tile layout, e.g.
+        from ``to_tiles``); outputs are written side by side into ``out``
         columns in that order."""
         if not 1 <= len(weights) <= MAX_SEGS:
             raise ECF8Error(f"1..{MAX_SEGS} weight segments per linear")
@@ -62,7 +102,11 @@ class LinearPlan:
         K = weights[0][0].shape[1]
         segs = (_Seg * len(weights))()
         col = 0
-        for i, (w, s) in enumerate(weights):
+        for i, entry in enumerate(weights):
+            w, s = entry[0], entry[1]
+            layout = entry[2] if len(entry) > 2 else WEIGHT_ROWS
+            if layout not in (WEIGHT_ROWS, WEIGHT_TILES):
+                raise ECF8Error(f"unknown weight layout {layout}")
             _need(w, torch.float8_e4m3fn, "weight", dev)
             _need(s, torch.float32, "weight_scale_inv", dev)
             n, k = w.shape
@@ -70,19 +114,21 @@ class LinearPlan:
                 raise ECF8Error(f"weight {tuple(w.shape)} does not fit K={K} in 128-multiples")
             if tuple(s.shape) != (n // GROUP, K // GROUP):
                 raise ECF8Error(f"weight_scale_inv {tuple(s.shape)} for weight {tuple(w.shape)}")
-            segs[i] = _Seg(w.data_ptr(), s.data_ptr(), n, col)
+            segs[i] = _Seg(w.data_ptr(), s.data_ptr(), n, col, layout)
             col += n
         if out.shape[-1] < col:
             raise ECF8Error(f"out has {out.shape[-1]} columns, {col} needed")
         self.segs, self.count, self.K, self.N, self.out, self.ldo = segs, len(weights), K, col, out, out.shape[-1]
-        self._keep = [t for pair in weights for t in pair]
+        self._keep = [t for entry in weights for t in entry[:2]]
 
     def __call__(self, aq: torch.Tensor, a_scale: torch.Tensor, M: int):
+        """``aq``: quantized activations in the tile layout ([>= pad16(M), K])."""
         _need(aq, torch.float8_e4m3fn, "aq", self.out.device)
         _need(a_scale, torch.float32, "a_scale", self.out.device)
-        if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < M
+        if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < pad16(M)
                 or tuple(a_scale.shape[1:]) != (self.K // GROUP,) or a_scale.shape[0] < M):
-            raise ECF8Error("activation shape does not match the linear")
+            raise ECF8Error("activation shape does not match the linear (tile-layout aq has "
+                            "rows padded to 16)")
         if self.out.shape[0] < M:
             raise ECF8Error("out has fewer rows than M")
         check(lib().ecf8_fp8_linear(aq.data_ptr(), a_scale.data_ptr(), M, self.K, self.segs,
@@ -112,7 +158,8 @@ def rmsnorm(residual, weight, eps, M, x=None, out_q=None, out_scale=None, out_bf
     if out_q is not None:
         _need(out_q, torch.float8_e4m3fn, "out_q", dev)
         _need(out_scale, torch.float32, "out_scale", dev)
-    _rows(M, K, residual, x, out_q, out_bf16)
+    _rows(M, K, residual, x, out_bf16)
+    _act_rows(M, K, out_q, "out_q")
     _rows(M, K // GROUP, out_scale)
     if weight.numel() != K:
         raise ECF8Error("norm weight shape does not match the rows")
@@ -128,7 +175,7 @@ def silu_mul_quant(gate_up, M, out_q, out_scale):
     _need(out_scale, torch.float32, "out_scale", dev)
     inter = gate_up.shape[-1] // 2
     _rows(M, 2 * inter, gate_up)
-    _rows(M, inter, out_q)
+    _act_rows(M, inter, out_q, "out_q")
     _rows(M, inter // GROUP, out_scale)
     check(lib().ecf8_silu_mul_quant(gate_up.data_ptr(), M, inter, out_q.data_ptr(),
                                     out_scale.data_ptr(), _stream(gate_up)), "ecf8_silu_mul_quant")
@@ -139,7 +186,8 @@ def act_quant(x, M, out_q, out_scale):
     _need(x, torch.bfloat16, "x", dev)
     _need(out_q, torch.float8_e4m3fn, "out_q", dev)
     _need(out_scale, torch.float32, "out_scale", dev)
-    _rows(M, x.shape[-1], x, out_q)
+    _rows(M, x.shape[-1], x)
+    _act_rows(M, x.shape[-1], out_q, "out_q")
     _rows(M, x.shape[-1] // GROUP, out_scale)
     check(lib().ecf8_act_quant(x.data_ptr(), M, x.shape[-1], out_q.data_ptr(), out_scale.data_ptr(),
                                _stream(x)), "ecf8_act_quant")
@@ -195,9 +243,9 @@ def decode_attention(q, k_cache, v_cache, pos, work, out_q, out_scale, Hq, out_b
         _need(out_bf16, torch.bfloat16, "out_bf16", dev)
     if D != 128 or v_cache.shape != k_cache.shape:
         raise ECF8Error("caches must be [B, Hkv, Lmax, 128]")
-    if (out_q.numel() < B * Hq * 128 or out_scale.numel() < B * Hq
+    if (out_q.numel() < pad16(B) * Hq * 128 or out_scale.numel() < B * Hq
             or (out_bf16 is not None and out_bf16.numel() < B * Hq * 128)):
-        raise ECF8Error("outputs too small")
+        raise ECF8Error("outputs too small (out_q: tile layout, rows padded to 16)")
     check(lib().ecf8_decode_attention(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                       pos.data_ptr(), B, Hq, Hkv, Lmax, work.data_ptr(),
                                       work.numel(), out_q.data_ptr(), out_scale.data_ptr(),
@@ -229,9 +277,9 @@ def decode_attention_fused(qkv, B, Hq, Hkv, q_norm, k_norm, eps, cos_t, sin_t, p
     if (pos.numel() < 1 or q_norm.numel() != 128 or k_norm.numel() != 128
             or qkv.numel() < B * (Hq + 2 * Hkv) * 128):
         raise ECF8Error("pos, q_norm / k_norm [128] or qkv does not fit")
-    if (out_q.numel() < B * Hq * 128 or out_scale.numel() < B * Hq
+    if (out_q.numel() < pad16(B) * Hq * 128 or out_scale.numel() < B * Hq
             or (out_bf16 is not None and out_bf16.numel() < B * Hq * 128)):
-        raise ECF8Error("outputs too small")
+        raise ECF8Error("outputs too small (out_q: tile layout, rows padded to 16)")
     check(lib().ecf8_decode_attention_fused(
         qkv.data_ptr(), B, Hq, Hkv, q_norm.data_ptr(), k_norm.data_ptr(), float(eps),
         cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), Lmax, k_cache.data_ptr(),
@@ -311,9 +359,11 @@ class MoeLinearPlan:
     """Device address tables of one grouped expert linear: ``experts`` is a
     list (one per expert) of 1..3 segments (weight e4m3fn [seg_n, K],
     weight_scale_inv f32 [seg_n/128, K/128]), e.g. (gate, up) or (down,).
-    Segment s of every expert writes output columns [s*seg_n, +seg_n)."""
+    Segment s of every expert writes output columns [s*seg_n, +seg_n).
+    ``weight_layout``: WEIGHT_ROWS (row-major) or WEIGHT_TILES, for every
+    expert weight."""
 
-    def __init__(self, experts, out: torch.Tensor):
+    def __init__(self, experts, out: torch.Tensor, weight_layout: int = WEIGHT_ROWS):
         dev = out.device
         _need(out, torch.bfloat16, "out", dev)
         n_segs = len(experts[0])
@@ -332,16 +382,19 @@ class MoeLinearPlan:
                 ss.append(s.data_ptr())
         if seg_n % GROUP or K % GROUP or out.shape[-1] < n_segs * seg_n:
             raise ECF8Error("seg_n and K must be multiples of 128 and fit out")
+        if weight_layout not in (WEIGHT_ROWS, WEIGHT_TILES):
+            raise ECF8Error(f"unknown weight layout {weight_layout}")
         self.w_table = torch.tensor(ws, dtype=torch.int64).to(dev)
         self.s_table = torch.tensor(ss, dtype=torch.int64).to(dev)
         self.E, self.n_segs, self.seg_n, self.K, self.out = len(experts), n_segs, seg_n, K, out
+        self.weight_layout = int(weight_layout)
         self._keep = [t for segs in experts for pair in segs for t in pair]
 
     def __call__(self, aq, a_scale, r: MoeRouting, gather: bool, M: int | None = None):
-        """``gather``: activation rows are tokens (aq [>= M, K], row of a
-        sorted pair = its token); otherwise aq has one row per sorted pair
-        ([>= M * top_k, K]).  M: the tokens routed into ``r`` (default: its
-        capacity)."""
+        """``gather``: activation rows are tokens (aq: tile layout,
+        [>= pad16(M), K], row of a sorted pair = its token); otherwise aq
+        has one row per sorted pair ([>= pad16(M * top_k), K]).  M: the
+        tokens routed into ``r`` (default: its capacity)."""
         dev = self.out.device
         _need(aq, torch.float8_e4m3fn, "aq", dev)
         _need(a_scale, torch.float32, "a_scale", dev)
@@ -350,7 +403,7 @@ class MoeLinearPlan:
             raise ECF8Error(f"1 <= M <= {r.M}")
         P = r.M * r.top_k
         rows = M if gather else M * r.top_k
-        if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < rows
+        if (aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < pad16(rows)
                 or tuple(a_scale.shape[1:]) != (self.K // GROUP,) or a_scale.shape[0] < rows
                 or self.out.shape[0] < P or r.E != self.E):
             raise ECF8Error("activation / output shape does not match the grouped linear")
@@ -358,8 +411,9 @@ class MoeLinearPlan:
                                     r.pair_tok.data_ptr() if gather else None,
                                     r.offsets.data_ptr(), r.active.data_ptr(), r.n_active.data_ptr(),
                                     self.E, self.w_table.data_ptr(), self.s_table.data_ptr(),
-                                    self.n_segs, self.seg_n, self.K, self.out.data_ptr(),
-                                    self.out.shape[-1], _stream(aq)), "ecf8_moe_linear")
+                                    self.n_segs, self.seg_n, self.K, self.weight_layout,
+                                    self.out.data_ptr(), self.out.shape[-1], _stream(aq)),
+              "ecf8_moe_linear")
         return self.out
 
 

@@ -33,7 +33,7 @@ from . import decode as _dev
 from . import llm_kernels as K
 from . import tiled
 from ._lib import ECF8Error
-from .llm import FP8Linear, RMSNorm, _GreedyRunner, _rotary_tables
+from .llm import FP8Linear, RMSNorm, _GreedyRunner, _rotary_tables, weight_layout
 from .synth import QWEN3_MOE_ATTN, QWEN3_MOE_EXPERT
 
 ATTN_LINEARS = ("k_proj", "o_proj", "q_proj", "v_proj")   # sorted
@@ -143,6 +143,7 @@ class _LayerExperts:
         self.compressed = hasattr(experts[0], "encoded")
         self.tiled = hasattr(experts[0], "_ecf8_tiles")
         weights = []
+        layout = K.WEIGHT_ROWS  # decoded experts land row-major in the expert buffer
         if self.tiled:
             n_e = sum(lin.out_features * lin.in_features
                       for lin in (experts[0].gate_proj, experts[0].up_proj, experts[0].down_proj))
@@ -198,8 +199,13 @@ class _LayerExperts:
             for ex in experts:
                 weights.append(tuple((lin.weight, lin.weight_scale_inv)
                                      for lin in (ex.gate_proj, ex.up_proj, ex.down_proj)))
-        self.gu = K.MoeLinearPlan([[g, u] for g, u, _ in weights], gu_out)
-        self.down = K.MoeLinearPlan([[d] for _, _, d in weights], down_out)
+            layouts = {weight_layout(lin) for ex in experts
+                       for lin in (ex.gate_proj, ex.up_proj, ex.down_proj)}
+            if len(layouts) != 1:
+                raise ECF8Error("a layer's experts must share one weight layout")
+            layout = layouts.pop()
+        self.gu = K.MoeLinearPlan([[g, u] for g, u, _ in weights], gu_out, layout)
+        self.down = K.MoeLinearPlan([[d] for _, _, d in weights], down_out, layout)
 
     def decode_routed(self, flags):
         self.select(flags)
@@ -214,7 +220,8 @@ class _LayerExperts:
 
 class Qwen3MoeRunner(_GreedyRunner):
     """Prefill + greedy decode of a fixed batch on one device.  The prompt's
-    MoE runs in chunks of ``prefill_chunk`` tokens (at most 8192 (token,
+    MoE runs in chunks of ``prefill_chunk`` tokens (rounded down to a
+    multiple of 16, the activation tile height; at most 8192 (token,
     expert) pairs per routing step)."""
 
     def __init__(self, model: Qwen3MoeForCausalLM, batch: int, prompt_len: int, max_len: int,
@@ -226,8 +233,9 @@ class Qwen3MoeRunner(_GreedyRunner):
             raise ECF8Error("query heads must be 4 or 8 per KV head")
         if cfg.moe_intermediate % 128 or cfg.experts > 256:
             raise ECF8Error("expert intermediate must be a multiple of 128; at most 256 experts")
-        chunk = min(prefill_chunk, 8192 // cfg.top_k)
-        if batch * cfg.top_k > 8192 or chunk < 1:
+        # chunks start on 16-row boundaries of the tile-layout activations
+        chunk = min(prefill_chunk, 8192 // cfg.top_k) // 16 * 16
+        if batch * cfg.top_k > 8192 or chunk < 16:
             raise ECF8Error("a decode step routes at most 8192 (token, expert) pairs")
         self.model, self.cfg = model, cfg
         self.dev = torch.device(device) if device is not None else model.lm_head.weight.device
@@ -243,9 +251,10 @@ class Qwen3MoeRunner(_GreedyRunner):
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.step = torch.zeros(1, dtype=torch.int64, device=dev)
         self.res = torch.empty(M, H, dtype=torch.float32, device=dev)
-        self.aqH = torch.empty(M, H, dtype=torch.float8_e4m3fn, device=dev)
+        # quantized activations in the tile layout: rows padded to 16
+        self.aqH = torch.empty(K.pad16(M), H, dtype=torch.float8_e4m3fn, device=dev)
         self.asH = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
-        self.aqA = torch.empty(M, Hq * D, dtype=torch.float8_e4m3fn, device=dev)
+        self.aqA = torch.empty(K.pad16(M), Hq * D, dtype=torch.float8_e4m3fn, device=dev)
         self.asA = torch.empty(M, Hq * D // 128, dtype=torch.float32, device=dev)
         self.qkv = torch.empty(M, (Hq + 2 * Hkv) * D, **bf)
         self.q = torch.empty(B * Hq * prompt_len * D, **bf)
@@ -259,7 +268,7 @@ class Qwen3MoeRunner(_GreedyRunner):
         P = Mr * cfg.top_k
         self.route = K.MoeRouting(Mr, cfg.top_k, E, dev)
         self.gu = torch.empty(P, 2 * I, **bf)
-        self.hq = torch.empty(P, I, dtype=torch.float8_e4m3fn, device=dev)
+        self.hq = torch.empty(K.pad16(P), I, dtype=torch.float8_e4m3fn, device=dev)
         self.hs = torch.empty(P, I // 128, dtype=torch.float32, device=dev)
         self.down = torch.empty(P, H, **bf)
         layers = list(model.model.layers)
@@ -284,7 +293,8 @@ class Qwen3MoeRunner(_GreedyRunner):
         tiles = getattr(a, "_ecf8_tiles", None)
         if tiles is None:
             mods = [a.get_submodule(n) for n in names]
-            return self._plan(a, index, which, [(x.weight, x.weight_scale_inv) for x in mods], out)
+            return self._plan(a, index, which,
+                              [(x.weight, x.weight_scale_inv, weight_layout(x)) for x in mods], out)
         if M <= 16:
             key = (index, which, "tiled")
             p = self._plans.get(key)
@@ -345,7 +355,9 @@ class Qwen3MoeRunner(_GreedyRunner):
             if ex.compressed and not prefill:
                 ex.decode_routed(r.select)
             gu, down = (ex.tiled_gu, ex.tiled_down) if fused else (ex.gu, ex.down)
-            gu(self.aqH[c0:c0 + m], self.asH[c0:c0 + m], r, gather=True, M=m)
+            # c0 is a multiple of 16: the chunk's rows are whole activation
+            # tiles, the same bytes as the row range of a [rows, H] view
+            gu(self.aqH[c0:c0 + K.pad16(m)], self.asH[c0:c0 + m], r, gather=True, M=m)
             K.silu_mul_quant(self.gu, m * cfg.top_k, self.hq, self.hs)
             down(self.hq, self.hs, r, gather=False, M=m)
             K.moe_combine(self.down, r, m, self.y[c0:c0 + m])
@@ -431,6 +443,8 @@ def compress_moe_layers(model: Qwen3MoeForCausalLM, drawn=None, threads_per_bloc
 
     def register(mod, path, pattern, comp):
         dev = mod.get_submodule(pattern[next(iter(pattern))][0]).weight_scale_inv.device
+        for n in pattern[next(iter(pattern))]:  # the hooks inject row-major views
+            mod.get_submodule(n).weight_layout = K.WEIGHT_ROWS
         for attr in (*_KEYS, "split_positions"):
             value = comp[attr] if attr == "split_positions" else comp[attr].to(dev).clone()
             _process_compressed_tensor(mod, attr, value, f"{path}.{attr}", pattern,

@@ -181,10 +181,11 @@ class TileLinearPlan:
     def __call__(self, aq: torch.Tensor, a_scale: torch.Tensor, M: int):
         dev = self.out.device
         if (aq.dtype != torch.float8_e4m3fn or a_scale.dtype != torch.float32 or aq.device != dev
-                or aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < M
+                or aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < 16
                 or tuple(a_scale.shape[1:]) != (self.K // _GROUP,) or a_scale.shape[0] < M
                 or not aq.is_contiguous() or not a_scale.is_contiguous()):
-            raise ECF8Error("activation shape does not match the linear")
+            raise ECF8Error("activation shape does not match the linear (aq: tile layout, "
+                            "16 rows)")
         if not 1 <= M <= 16 or self.out.shape[0] < M:
             raise ECF8Error("the tiled linear runs 1..16 rows")
         check(lib().ecf8_tile_linear(aq.data_ptr(), a_scale.data_ptr(), M, self.K, self.arr,
@@ -244,7 +245,7 @@ class TileMoePlan:
             raise ECF8Error("the tiled grouped linear runs 1..16 routed tokens")
         rows = M if gather else M * r.top_k
         if (aq.dtype != torch.float8_e4m3fn or a_scale.dtype != torch.float32 or aq.device != dev
-                or aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < rows
+                or aq.dim() != 2 or aq.shape[1] != self.K or aq.shape[0] < (rows + 15) // 16 * 16
                 or tuple(a_scale.shape[1:]) != (self.K // _GROUP,) or a_scale.shape[0] < rows
                 or not aq.is_contiguous() or not a_scale.is_contiguous()
                 or self.out.shape[0] < r.M * r.top_k or r.E != self.E):

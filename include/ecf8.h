@@ -256,6 +256,21 @@ int ecf8_decode_bf16(const uint8_t *luts, const uint8_t *encoded,
                      int table_kind, const ecf8_scaled_part *parts, int n_parts,
                      int threads_per_block, int bytes_per_thread, void *stream);
 
+/* --------------------------------------------------------- measurement */
+
+/*
+ * Streaming probe for the bandwidth a one-launch kernel reaches on this
+ * GPU (bench.py --mode ceiling): op 0 reads `bytes` of src (16-byte
+ * aligned, a multiple of 16), op 1 copies them to dst; `grid` workgroups
+ * of `block` (64..1024, a power of two) lanes sweep the buffer
+ * grid-stride, each lane keeping `depth` (1, 2, 4 or 8) 16-byte loads in
+ * flight, with non-temporal loads and stores if `nontemporal`.  `sink`: one
+ * device u32 the read sweep may write.  No reference counterpart; the
+ * decode path never calls it.
+ */
+int ecf8_stream_probe(int op, const void *src, void *dst, int64_t bytes, int grid, int block,
+                      int depth, int nontemporal, uint32_t *sink, void *stream);
+
 /* ------------------------------------------------------------------ host */
 
 /*

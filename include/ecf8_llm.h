@@ -27,22 +27,41 @@ extern "C" {
 
 #define ECF8_LINEAR_MAX_SEGS 3
 
+/*
+ * FP8 operand layouts.  Quantized activations (every aq / out_q below) are
+ * always in the tile layout; weights may be in either:
+ *   ECF8_WEIGHT_ROWS   e4m3fn [rows, K] row-major (the checkpoint's layout,
+ *                      and the decoder's output);
+ *   ECF8_WEIGHT_TILES  the tile layout.
+ * Tile layout of an [R, K] e4m3fn matrix (K a multiple of 128, rows padded
+ * to a multiple of 16): for each 16-row tile t and 128-column group kg one
+ * 2048-byte block at ((t * K/128) + kg) * 2048, in the order the lanes of
+ * v_mfma_f32_16x16x32_fp8_fp8 take their operands -- lane l = 16 g + r
+ * holds bytes [16 g, +16) of the tile's row r at block byte 16 l, and bytes
+ * [64 + 16 g, +16) at 1024 + 16 l -- so each 16-byte load of a wave reads
+ * 1 KB contiguous.  The pad rows of the last tile are never read into a
+ * stored output.  Activation scales stay row-major fp32 [M, K/128].
+ */
+#define ECF8_WEIGHT_ROWS 0
+#define ECF8_WEIGHT_TILES 1
+
 /* One weight matrix of a (possibly fused) linear: weight e4m3fn [n, K]
- * row-major (16-byte aligned), weight_scale fp32 [n/128, K/128]; its
- * outputs go to columns [out_col, out_col + n) of the output. */
+ * (16-byte aligned) in weight_layout, weight_scale fp32 [n/128, K/128];
+ * its outputs go to columns [out_col, out_col + n) of the output. */
 typedef struct ecf8_linear_seg {
   const void *weight;
   const float *weight_scale;
   int64_t n;
   int64_t out_col;
+  int64_t weight_layout; /* ECF8_WEIGHT_ROWS or ECF8_WEIGHT_TILES */
 } ecf8_linear_seg;
 
 /*
  * out[m, seg.out_col + j] (bf16, row stride ldo) =
  *   sum_g (sum_{k in g} aq[m, k] * w[j, k]) * as[m, g] * ws[j/128, g]
  * for each of n_segs (1..3) segments, e.g. q/k/v or gate/up in one launch.
- * aq: e4m3fn [M, K] (16-byte aligned), as: fp32 [M, K/128].  K and every
- * seg.n must be multiples of 128.
+ * aq: e4m3fn [M, K] in the tile layout (16-byte aligned, ceil(M/16) * 16
+ * rows), as: fp32 [M, K/128].  K and every seg.n must be multiples of 128.
  */
 int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64_t K,
                     const ecf8_linear_seg *segs, int n_segs, void *out, int64_t ldo,
@@ -53,21 +72,23 @@ int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64_t K,
  *   residual[m] += x[m]  (x bf16 [M, K], or NULL for no add; residual fp32)
  *   y = residual[m] * rsqrt(mean(residual[m]^2) + eps) * weight  (bf16 weight)
  * y goes to out_bf16 (bf16 [M, K]) and/or, quantized, to out_q (e4m3fn
- * [M, K]) + out_scale (fp32 [M, K/128]); with both, the quantized form is
+ * [M, K], tile layout) + out_scale (fp32 [M, K/128]); with both, the
+ * quantized form is
  * that of the bf16-rounded y (what ecf8_act_quant of out_bf16 gives).
  */
 int ecf8_rmsnorm(const void *x, float *residual, const void *weight, float eps, int64_t M,
                  int64_t K, void *out_q, float *out_scale, void *out_bf16, void *stream);
 
 /* h = silu(gate) * up for gate_up bf16 [M, 2I] (gate in columns [0, I)),
- * quantized to out_q e4m3fn [M, I] + out_scale fp32 [M, I/128].
+ * quantized to out_q e4m3fn [M, I] (tile layout) + out_scale fp32
+ * [M, I/128].
  * I must be a multiple of 128. */
 int ecf8_silu_mul_quant(const void *gate_up, int64_t M, int64_t I, void *out_q,
                         float *out_scale, void *stream);
 
-/* bf16 [M, K] -> e4m3fn + fp32 scale per 1x128 group (scale = amax/448,
- * 1 for an all-zero group; q = round_nearest_even(x / scale)).
- * K must be a multiple of 128. */
+/* bf16 [M, K] -> e4m3fn (tile layout) + fp32 scale per 1x128 group
+ * (scale = amax/448, 1 for an all-zero group; q =
+ * round_nearest_even(x / scale)).  K must be a multiple of 128. */
 int ecf8_act_quant(const void *x, int64_t M, int64_t K, void *out_q, float *out_scale,
                    void *stream);
 
@@ -102,7 +123,7 @@ int64_t ecf8_attention_work_floats(int64_t B, int Hq, int64_t Lmax);
  * 1/sqrt(128)) over cached positions [0, pos[0]] (pos: device int32, the
  * new token's position, already written to the caches), grouped-query with
  * Hq = 4 * Hkv or 8 * Hkv.  The result per (b, head) is quantized as one 128-group:
- * out_q e4m3fn [B, Hq*128], out_scale fp32 [B, Hq]; out_bf16 (optional,
+ * out_q e4m3fn [B, Hq*128] (tile layout), out_scale fp32 [B, Hq]; out_bf16 (optional,
  * bf16 [B, Hq*128]) receives the unquantized result.
  */
 int ecf8_decode_attention(const void *q, const void *k_cache, const void *v_cache, const int *pos,
@@ -159,15 +180,16 @@ int ecf8_moe_group(const int *topk_idx, const float *topk_w, int64_t M, int top_
  *   out[q, s * seg_n + j] = linear(aq[row(q)], weights[e * n_segs + s])[j]
  * for every sorted position q of expert e, with the block-scaled math of
  * ecf8_fp8_linear; row(q) = row_of[q] (e.g. pair_tok: gather the token's
- * activation row) or q when row_of is NULL.  weights / weight_scales are
- * device arrays of n_experts * n_segs addresses (e4m3fn [seg_n, K] and
- * fp32 [seg_n/128, K/128]); active entries must be < n_experts.  The grid
- * covers every expert and idle slots exit, so the launch can be captured
- * in a graph. */
+ * activation row) or q when row_of is NULL (aq in the tile layout).
+ * weights / weight_scales are device arrays of n_experts * n_segs
+ * addresses (e4m3fn [seg_n, K] in weight_layout, and fp32 [seg_n/128,
+ * K/128]); active entries must be < n_experts.  The grid covers every
+ * expert and idle slots exit, so the launch can be captured in a graph. */
 int ecf8_moe_linear(const void *aq, const float *as, const int *row_of, const int *offsets,
                     const int *active, const int *n_active, int n_experts,
                     const void *const *weights, const float *const *weight_scales, int n_segs,
-                    int64_t seg_n, int64_t K, void *out, int64_t ldo, void *stream);
+                    int64_t seg_n, int64_t K, int weight_layout, void *out, int64_t ldo,
+                    void *stream);
 
 /* out bf16 [M, H] = sum_k pair_w[q] * down[q, :] (down bf16, row stride
  * ldd) over q = pair_pos[m * top_k + k], k in order, accumulated in fp32. */

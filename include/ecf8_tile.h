@@ -95,7 +95,8 @@ typedef struct ecf8_tile_operand {
  * ecf8_fp8_linear uses for the same shape -- 16 when K/128 >= 64 or when
  * K = 4096 has more than 2 x CUs 16-column tiles, else 8 -- and the result
  * is then bit-identical to decoding W and calling ecf8_fp8_linear.
- * aq: 16-byte aligned; out: bf16, ldo elements per row.
+ * aq: the tile layout of ecf8_llm.h (16-byte aligned, rows padded to 16);
+ * out: bf16, ldo elements per row.
  */
 int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int64_t K,
                      const ecf8_tile_operand *ops, int n_ops, const uint32_t *table, void *out,

@@ -156,6 +156,8 @@ def test_consumer_kernels_reject_before_launch():
     assert L.ecf8_fp8_linear(fake, fake, 16, 4096, seg, 1, fake, 64, None) == 6    # ldo too small
     bad_n = (_Seg * 1)(_Seg(fake, fake, 100, 0))
     assert L.ecf8_fp8_linear(fake, fake, 16, 4096, bad_n, 1, fake, 128, None) == 2
+    bad_layout = (_Seg * 1)(_Seg(fake, fake, 128, 0, 2))
+    assert L.ecf8_fp8_linear(fake, fake, 16, 4096, bad_layout, 1, fake, 128, None) == 1
     assert L.ecf8_rmsnorm(None, None, fake, ctypes.c_float(1e-6), 4, 4096, fake, fake, None, None) == 1
     assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 4096, None, fake, None, None) == 1
     assert L.ecf8_rmsnorm(None, fake, fake, ctypes.c_float(1e-6), 4, 4096, fake, None, fake, None) == 1
@@ -214,14 +216,16 @@ def test_moe_kernels_reject_before_launch():
     assert g(None, fake, 16, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 1
     assert g(fake, fake, 1100, 8, 128, fake, fake, fake, fake, fake, fake, None, None) == 2  # P > 8192
     lin = L.ecf8_moe_linear
-    assert lin(None, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1536,
+    assert lin(None, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, 0, fake, 1536,
                None) == 1
-    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 700, 2048, fake, 1536,
+    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 700, 2048, 0, fake, 1536,
                None) == 2   # seg_n % 128
-    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1000,
+    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, 0, fake, 1000,
                None) == 6   # ldo < n_segs * seg_n
-    assert lin(fake + 4, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, fake, 1536,
-               None) == 3
+    assert lin(fake + 4, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, 0, fake,
+               1536, None) == 3
+    assert lin(fake, fake, None, fake, fake, fake, 128, fake, fake, 2, 768, 2048, 2, fake, 1536,
+               None) == 1   # unknown weight layout
     c = L.ecf8_moe_combine
     assert c(fake, 1024, fake, fake, 16, 8, 2048, fake, None) == 1   # ldd < H
     assert c(fake, 2052, fake, fake, 16, 8, 2052, fake, None) == 2   # H % 8

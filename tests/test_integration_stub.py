@@ -183,10 +183,10 @@ def test_tiled_block_matches_the_fp8_linear_on_the_gpu(monkeypatch, cuda_device)
     a_s = torch.empty(16, 32, dtype=torch.float32, device=dev)
     act_quant(x, 16, aq, a_s)
     for M in (1, 7, 16):
-        got = ns["tiled_linear"](res["luts"], w, s.to(dev), aq[:M].contiguous(),
-                                 a_s[:M].contiguous(), linear_waves(1024, 4096, dev))
+        got = ns["tiled_linear"](res["luts"], w, s.to(dev), aq, a_s, M,
+                                 linear_waves(1024, 4096, dev))
         want = torch.empty(M, 1024, dtype=torch.bfloat16, device=dev)
-        fp8_linear(aq[:M].contiguous(), a_s[:M].contiguous(), [(w.to(dev), s.to(dev))], want, M)
+        fp8_linear(aq, a_s, [(w.to(dev), s.to(dev))], want, M)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), M
     # LUTs with a 1-bit code: refused, nothing launched
@@ -195,5 +195,4 @@ def test_tiled_block_matches_the_fp8_linear_on_the_gpu(monkeypatch, cuda_device)
     b[::7] = (b[::7] & 0x87) | (12 << 3)
     skew = compress_flat(b.view(torch.float8_e4m3fn).reshape(-1))
     with pytest.raises(RuntimeError, match="no automaton"):
-        ns["tiled_linear"](skew["luts"], b.view(torch.float8_e4m3fn), s.to(dev), aq[:1].contiguous(),
-                           a_s[:1].contiguous(), 8)
+        ns["tiled_linear"](skew["luts"], b.view(torch.float8_e4m3fn), s.to(dev), aq, a_s, 1, 8)

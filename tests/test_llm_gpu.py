@@ -24,6 +24,22 @@ pytestmark = pytest.mark.gpu
 FP8 = torch.float8_e4m3fn
 
 
+def pad16(m):
+    return (m + 15) // 16 * 16
+
+
+def to_tiles(x):
+    from ecf8_amd.llm_kernels import to_tiles as t
+
+    return t(x)
+
+
+def from_tiles(t, R, K):
+    from ecf8_amd.llm_kernels import from_tiles as f
+
+    return f(t, R, K)
+
+
 def _say(msg):
     print(msg, flush=True)
     sys.stdout.flush()
@@ -76,31 +92,34 @@ def test_act_quant_matches_torch_cast(cuda_device):
     x[2, 128:256] = 0.0   # an all-zero group gets scale 1
     x[3, :5] = torch.tensor([448.0, -1e-8, 3e-3, 2 ** -10, -(2 ** -7)])
     x = x.to(torch.bfloat16)
-    q = torch.empty(M, Kd, dtype=FP8, device=cuda_device)
+    q = torch.empty(pad16(M), Kd, dtype=FP8, device=cuda_device)  # tile layout
     s = torch.empty(M, Kd // 128, device=cuda_device)
     act_quant(x.to(cuda_device), M, q, s)
     qr, sr = _ref_quant(x)
     assert torch.equal(s.cpu(), sr)
-    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+    assert torch.equal(from_tiles(q, M, Kd).cpu().view(torch.uint8), qr.view(torch.uint8))
 
 
 @pytest.mark.parametrize("Kd", [768, 2048, 4096 + 640])
 def test_act_quant_rows_of_any_group_multiple(cuda_device, Kd):
     """Rows that are not a multiple of 4096 (the MoE shapes): the workgroup
-    covering a row's tail writes nothing past the row."""
+    covering a row's tail writes nothing past the row -- neither the pad
+    rows of the 16-row tile nor past the buffer."""
     from ecf8_amd.llm_kernels import act_quant
 
     gen = torch.Generator().manual_seed(Kd)
     M = 5
     x = (torch.randn(M, Kd, generator=gen) * 3).to(torch.bfloat16)
-    flat = torch.full((M * Kd + 4096,), 0x11, dtype=torch.uint8, device=cuda_device)
-    q = flat[: M * Kd].view(FP8).view(M, Kd)
+    flat = torch.full((16 * Kd + 4096,), 0x11, dtype=torch.uint8, device=cuda_device)
+    q = flat[: 16 * Kd].view(FP8).view(16, Kd)
     s = torch.empty(M, Kd // 128, device=cuda_device)
     act_quant(x.to(cuda_device), M, q, s)
     qr, sr = _ref_quant(x)
     assert torch.equal(s.cpu(), sr)
-    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
-    assert bool((flat[M * Kd:].cpu() == 0x11).all())
+    rows = from_tiles(q, 16, Kd).cpu().view(torch.uint8)
+    assert torch.equal(rows[:M], qr.view(torch.uint8))
+    assert bool((rows[M:] == 0x11).all())
+    assert bool((flat[16 * Kd:].cpu() == 0x11).all())
 
 
 # ------------------------------------------------------------ FP8 linear
@@ -120,11 +139,13 @@ def _linear_ref(aq, a_s, segs):
     return torch.cat(outs, dim=1)
 
 
+@pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("M,Kd", [(1, 1024), (5, 1024), (16, 1024), (16, 8192), (3, 12288),
                                   (17, 1024), (64, 1024), (130, 1024)])
-def test_fp8_linear_matches_fp64(cuda_device, M, Kd):
+def test_fp8_linear_matches_fp64(cuda_device, M, Kd, layout):
     """M <= 16 runs the one-tile kernel (8 waves, or 16 from K = 8192 on);
-    larger M the 64-row tile kernel."""
+    larger M the 64-row tile kernel.  Weights row-major (layout 0) or in
+    the tile layout (1); activations always in the tile layout."""
     from ecf8_amd.llm_kernels import LinearPlan
 
     _say(f"[llm] fp8_linear M={M} K={Kd}")
@@ -139,7 +160,8 @@ def test_fp8_linear_matches_fp64(cuda_device, M, Kd):
         segs.append((w, ws))
     ldo = sum(shapes) + 64
     out = torch.full((M, ldo), 7.0, dtype=torch.bfloat16, device=cuda_device)
-    LinearPlan(segs, out)(aq, a_s, M)
+    plan_w = [(to_tiles(w), ws, 1) if layout else (w, ws) for w, ws in segs]
+    LinearPlan(plan_w, out)(to_tiles(aq), a_s, M)
     ref = _linear_ref(aq, a_s, segs)
     got = out[:, : sum(shapes)].double().cpu()
     tol = 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()
@@ -162,10 +184,14 @@ def test_fp8_linear_persistent_path_matches_fp64(cuda_device):
     w = _rand_fp8((n, Kd), gen, cuda_device)
     ws = (torch.rand(n // 128, Kd // 128, generator=gen) * 1e-3 + 1e-5).to(cuda_device)
     out = torch.empty(M, n, dtype=torch.bfloat16, device=cuda_device)
-    LinearPlan([(w, ws)], out)(aq, a_s, M)
     ref = _linear_ref(aq, a_s, [(w, ws)])
+    LinearPlan([(w, ws)], out)(to_tiles(aq), a_s, M)
     got = out.double().cpu()
     assert bool(((got - ref).abs() <= 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()).all())
+    rows_out = out.clone()
+    # the same product from tile-layout weights, bit for bit
+    LinearPlan([(to_tiles(w), ws, 1)], out)(to_tiles(aq), a_s, M)
+    assert torch.equal(out.view(torch.int16), rows_out.view(torch.int16))
 
 
 def test_fp8_linear_is_deterministic(cuda_device):
@@ -178,9 +204,10 @@ def test_fp8_linear_is_deterministic(cuda_device):
     ws = torch.rand(4, 32, generator=gen).to(cuda_device)
     out = torch.empty(16, 512, dtype=torch.bfloat16, device=cuda_device)
     p = LinearPlan([(w, ws)], out)
-    first = p(aq, a_s, 16).clone()
+    aqt = to_tiles(aq)
+    first = p(aqt, a_s, 16).clone()
     for _ in range(3):
-        assert torch.equal(p(aq, a_s, 16), first)
+        assert torch.equal(p(aqt, a_s, 16), first)
 
 
 # ------------------------------------------------------------ row kernels
@@ -212,21 +239,21 @@ def test_rmsnorm_residual_and_outputs(cuda_device, with_x, Kd):
     assert torch.allclose(ob.float().cpu(), y_ref, rtol=2 ** -7, atol=1e-6)
     # fp8 output
     rd = r.to(dev)
-    q = torch.empty(M, Kd, dtype=FP8, device=dev)
+    q = torch.empty(pad16(M), Kd, dtype=FP8, device=dev)
     s = torch.empty(M, Kd // 128, device=dev)
     rmsnorm(rd, w.to(dev), 1e-6, M, x=None if x is None else x.to(dev), out_q=q, out_scale=s)
-    _assert_fp8_close(q, s, y_ref)
+    _assert_fp8_close(from_tiles(q, M, Kd), s, y_ref)
     # both outputs: the fp8 form is act_quant of the bf16 form, bit for bit
     rd = r.to(dev)
     ob2 = torch.empty(M, Kd, dtype=torch.bfloat16, device=dev)
-    q2 = torch.empty(M, Kd, dtype=FP8, device=dev)
+    q2 = torch.empty(pad16(M), Kd, dtype=FP8, device=dev)
     s2 = torch.empty(M, Kd // 128, device=dev)
     rmsnorm(rd, w.to(dev), 1e-6, M, x=None if x is None else x.to(dev), out_q=q2, out_scale=s2,
             out_bf16=ob2)
     assert torch.equal(ob2, ob)
     qr, sr = _ref_quant(ob2)
     assert torch.equal(s2.cpu(), sr)
-    assert torch.equal(q2.cpu().view(torch.uint8), qr.view(torch.uint8))
+    assert torch.equal(from_tiles(q2, M, Kd).cpu().view(torch.uint8), qr.view(torch.uint8))
 
 
 @pytest.mark.parametrize("I", [8192, 768])
@@ -238,10 +265,10 @@ def test_silu_mul_quant(cuda_device, I):
     gu = (torch.randn(M, 2 * I, generator=gen) * 4).to(torch.bfloat16)
     g, u = gu.float()[:, :I], gu.float()[:, I:]
     ref = g * torch.sigmoid(g) * u
-    q = torch.empty(M, I, dtype=FP8, device=cuda_device)
+    q = torch.empty(pad16(M), I, dtype=FP8, device=cuda_device)
     s = torch.empty(M, I // 128, device=cuda_device)
     silu_mul_quant(gu.to(cuda_device), M, q, s)
-    _assert_fp8_close(q, s, ref)
+    _assert_fp8_close(from_tiles(q, M, I), s, ref)
 
 
 # ------------------------------------------------------ rotary + caches
@@ -311,7 +338,7 @@ def test_decode_attention_matches_fp32(cuda_device, pos0, G):
     vc = torch.randn(B, Hkv, Lmax, 128, generator=gen).to(torch.bfloat16)
     pos = torch.tensor([pos0], dtype=torch.int32, device=dev)
     work = attention_work(B, Hq, Lmax, dev)
-    oq = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+    oq = torch.empty(pad16(B), Hq * 128, dtype=FP8, device=dev)
     os_ = torch.empty(B, Hq, device=dev)
     ob = torch.empty(B, Hq * 128, dtype=torch.bfloat16, device=dev)
     decode_attention(q.to(dev), kc.to(dev), vc.to(dev), pos, work, oq, os_, Hq, out_bf16=ob)
@@ -321,7 +348,7 @@ def test_decode_attention_matches_fp32(cuda_device, pos0, G):
     sc = torch.matmul(q.float()[:, :, None], k.transpose(-1, -2).contiguous())[:, :, 0] / math.sqrt(128)
     ref = torch.matmul(torch.softmax(sc, -1)[:, :, None], v)[:, :, 0].reshape(B, Hq * 128)
     assert torch.allclose(ob.float().cpu(), ref, rtol=2 ** -7, atol=1e-4)
-    _assert_fp8_close(oq, os_, ref, rel=2 ** -4 + 5e-3)
+    _assert_fp8_close(from_tiles(oq, B, Hq * 128), os_, ref, rel=2 ** -4 + 5e-3)
 
 
 def test_wrappers_reject_bad_arguments_before_launch(cuda_device):
@@ -337,7 +364,10 @@ def test_wrappers_reject_bad_arguments_before_launch(cuda_device):
     res = torch.zeros(2, 4096, device=dev)
     with pytest.raises(ECF8Error, match="out_bf16, or out_q"):
         rmsnorm(res, torch.ones(4096, **bf), 1e-6, 2)
-    q8 = torch.empty(2, 4096, dtype=FP8, device=dev)
+    q8 = torch.empty(16, 4096, dtype=FP8, device=dev)  # tile layout: rows padded to 16
+    with pytest.raises(ECF8Error, match="tile-layout"):
+        rmsnorm(res, torch.ones(4096, **bf), 1e-6, 2, out_q=q8[:2],
+                out_scale=torch.empty(2, 32, device=dev))
     for short in (torch.empty(1, 32, device=dev), torch.empty(32, device=dev)):
         with pytest.raises(ECF8Error, match="is not"):
             rmsnorm(res, torch.ones(4096, **bf), 1e-6, 2, out_q=q8, out_scale=short)
@@ -359,7 +389,7 @@ def test_wrappers_reject_bad_arguments_before_launch(cuda_device):
         qk_norm_rope(qkv, B, T, Hq, Hkv, torch.ones(128, **bf), torch.ones(128, **bf), 1e-6, cos,
                      cos, pos[:0], q_out, kc, vc)
     work = attention_work(B, Hq, Lmax, dev)
-    oq = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+    oq = torch.empty(pad16(B), Hq * 128, dtype=FP8, device=dev)
     with pytest.raises(ECF8Error, match="pos"):
         decode_attention(q_out, kc, vc, pos[:0], work, oq, torch.empty(B, Hq, device=dev), Hq)
 
@@ -602,7 +632,7 @@ def test_fused_attention_equals_the_unfused_pair(cuda_device, G):
         q = torch.empty(B * Hq * 128, dtype=torch.bfloat16, device=dev)
         qk_norm_rope(qkv, B, 1, Hq, Hkv, qn, kn, 1e-6, cos, sin, pos, q, kc, vc)
         work = attention_work(B, Hq, Lmax, dev)
-        oq = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+        oq = torch.empty(pad16(B), Hq * 128, dtype=FP8, device=dev)
         os_ = torch.empty(B, Hq, device=dev)
         ob = torch.empty(B, Hq * 128, dtype=torch.bfloat16, device=dev)
         decode_attention(q, kc, vc, pos, work, oq, os_, Hq, out_bf16=ob)
@@ -619,12 +649,13 @@ def test_fused_attention_equals_the_unfused_pair(cuda_device, G):
             assert torch.equal(kf, kc) and torch.equal(vf, vc)
             assert torch.equal(obf, ob)
             assert torch.equal(osf, os_)
-            assert torch.equal(oqf.view(torch.uint8), oq.view(torch.uint8))
+            assert torch.equal(from_tiles(oqf, B, Hq * 128).view(torch.uint8),
+                               from_tiles(oq, B, Hq * 128).view(torch.uint8))
     # graph replays with a moving position
     pos = torch.tensor([300], dtype=torch.int32, device=dev)
     kf, vf = kc0.clone(), vc0.clone()
     workf = attention_work(B, Hq, Lmax, dev)
-    oqf = torch.empty(B, Hq * 128, dtype=FP8, device=dev)
+    oqf = torch.empty(pad16(B), Hq * 128, dtype=FP8, device=dev)
     osf = torch.empty(B, Hq, device=dev)
     obf = torch.empty(B, Hq * 128, dtype=torch.bfloat16, device=dev)
     s = torch.cuda.Stream(dev)

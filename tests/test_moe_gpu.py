@@ -101,11 +101,14 @@ def _pair_linear_ref(a_rows, a_s_rows, w, ws):
     return (part * scale).sum(-1)
 
 
+@pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("gather", [True, False])
-def test_grouped_expert_linear_matches_fp64(cuda_device, gather):
+def test_grouped_expert_linear_matches_fp64(cuda_device, gather, layout):
     """gate/up form (gather the token rows, two segments) and down form (one
-    row per sorted pair, one segment, K below 16 groups)."""
-    from ecf8_amd.llm_kernels import MoeLinearPlan, MoeRouting, moe_group
+    row per sorted pair, one segment, K below 16 groups); expert weights
+    row-major (layout 0) or in the tile layout (1), activations in the tile
+    layout."""
+    from ecf8_amd.llm_kernels import MoeLinearPlan, MoeRouting, moe_group, to_tiles
 
     dev = cuda_device
     gen = torch.Generator().manual_seed(11 if gather else 12)
@@ -132,7 +135,9 @@ def test_grouped_expert_linear_matches_fp64(cuda_device, gather):
         experts.append(segs)
     ldo = n_segs * seg_n + 32
     out = torch.full((P, ldo), 7.0, dtype=torch.bfloat16, device=dev)
-    MoeLinearPlan(experts, out)(aq, a_s, r, gather=gather)
+    plan_experts = [[(to_tiles(w), ws) for w, ws in segs] for segs in experts] if layout \
+        else experts
+    MoeLinearPlan(plan_experts, out, layout)(to_tiles(aq), a_s, r, gather=gather)
     offsets, active, _ = _groups_ref(idx, E)
     tok = r.pair_tok.cpu().long()
     got = out.double().cpu()
@@ -199,10 +204,10 @@ def test_compressed_moe_matches_uncompressed_exactly(small_moe_models, cuda_devi
         for graph in (False, True):
             print(f"[moe] e2e {name} graph={graph}", flush=True)
             TensorManager.clear_device()
-            # the prompt's MoE in 24-token chunks (eager) or one chunk (graph):
+            # the prompt's MoE in 16-token chunks (eager) or one chunk (graph):
             # per-token results do not depend on the chunking
             r = Qwen3MoeRunner(model, B, T, T + new, cuda_device,
-                               prefill_chunk=512 if graph else 24)
+                               prefill_chunk=512 if graph else 16)
             if graph:
                 r.capture()
             for rep in range(2):

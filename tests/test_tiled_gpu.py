@@ -116,7 +116,9 @@ def test_tile_linear_follows_an_fp64_restatement(layer, cuda_device):
     TileLinearPlan([ops["self_attn.k_proj"]], table, out)(aq, as_, M)
     w, s = dense["self_attn.k_proj"]
     wd = w.double().cpu() * s.double().cpu().repeat_interleave(128, 0).repeat_interleave(128, 1)
-    xd = (aq[:M].double().cpu().view(M, K // 128, 128)
+    from ecf8_amd.llm_kernels import from_tiles
+
+    xd = (from_tiles(aq, M, K).double().cpu().view(M, K // 128, 128)
           * as_[:M].double().cpu()[..., None]).view(M, K)
     ref = xd @ wd.T
     got = out[:M].double().cpu()

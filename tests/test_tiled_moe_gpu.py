@@ -89,7 +89,7 @@ def _acts(rows, K, seed, dev):
 
     g = torch.Generator().manual_seed(seed)
     x = (torch.randn(rows, K, generator=g) * 0.5).to(torch.bfloat16).to(dev)
-    aq = torch.empty(rows, K, dtype=torch.float8_e4m3fn, device=dev)
+    aq = torch.empty((rows + 15) // 16 * 16, K, dtype=torch.float8_e4m3fn, device=dev)  # tiles
     as_ = torch.empty(rows, K // 128, dtype=torch.float32, device=dev)
     act_quant(x, rows, aq, as_)
     return aq, as_
@@ -221,7 +221,7 @@ def test_retiled_moe_model_matches_fp8_exactly(cuda_device):
             _say(f"[tiled-moe] e2e {name} graph={graph}")
             TensorManager.clear_device()
             r = Qwen3MoeRunner(model, B, T, T + new, cuda_device,
-                               prefill_chunk=512 if graph else 24)
+                               prefill_chunk=512 if graph else 16)
             if graph:
                 r.capture()
             for rep in range(2):
