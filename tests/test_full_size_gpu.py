@@ -137,8 +137,11 @@ def test_qwen3_8b_model_bs16_matches_fp8(cuda_device):
         del r
         torch.cuda.empty_cache()
 
-    for graph in (False, True):
-        run("fp8", graph)
+    run("fp8", False)
+    from ecf8_amd.llm import tile_resident_weights
+
+    assert tile_resident_weights(model) == 7 * cfg.layers  # FP8 weights re-laid out in tiles
+    run("fp8", True)
     _say("[full] Qwen3-8B: compressing")
     compress_layers(model, drawn)
     # every layer's hook injects its original weights
@@ -199,8 +202,11 @@ def test_qwen3_moe_model_bs16_matches_fp8(cuda_device):
         del r
         torch.cuda.empty_cache()
 
-    for graph in (False, True):
-        run("fp8", graph)
+    run("fp8", False)
+    from ecf8_amd.llm import tile_resident_weights
+
+    assert tile_resident_weights(model) == cfg.layers * (4 + 3 * cfg.experts)
+    run("fp8", True)
     _say("[full] Qwen3-30B-A3B: compressing 6,192 blocks")
     compress_moe_layers(model, drawn)
     n_blocks = sum(1 for m in model.modules() if "encoded" in m._buffers)
