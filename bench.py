@@ -584,6 +584,70 @@ def e2e_generate(args):
     return line
 
 
+def linears_workload(args):
+    """The four decode-step linears of the Qwen3-8B-shaped model alone
+    (M = --batch rows; each linear launched for all 36 layers back to back,
+    so the weights stream from HBM as in a decode step): first over FP8
+    weights resident in the tile layout, then over the same layers
+    ECF8-compressed and re-tiled (the fused decode-into-MFMA linears).  The
+    activations are one seeded random batch quantized per 1x128 group; the
+    last layer's outputs of the two modes must be identical.  Starts no
+    child process, so a counter profile of it sees only these kernels."""
+    import torch
+
+    from ecf8_amd import llm_kernels as K
+    from ecf8_amd.llm import (Qwen3Config, Qwen3Runner, compress_layers, random_model,
+                              retile_layers, tile_resident_weights)
+
+    dev = torch.device("cuda", 0)
+    cfg = Qwen3Config()
+    B = args.batch
+    if B > 16:
+        raise SystemExit("--batch: the decode-step linears take at most 16 rows")
+    model, drawn = random_model(cfg, dev, distinct_layers=args.distinct_layers, seed=args.seed)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 11)
+    results, outs = {}, {}
+    for mode in ("fp8", "ecf8_fused"):
+        if mode == "fp8":
+            tile_resident_weights(model)
+        else:
+            compress_layers(model, drawn)
+            retile_layers(model, drawn)
+        runner = Qwen3Runner(model, B, 1, 2, dev)
+        if mode == "fp8":
+            acts = {k: torch.randn(B, k, generator=g, device=dev).to(torch.bfloat16)
+                    for k in runner.aq}
+        for k, x in acts.items():
+            K.act_quant(x, B, runner.aq[k], runner.as_[k])
+        results[mode] = runner.time_linears(reps=args.steps)
+        torch.cuda.synchronize()
+        outs[mode] = {out: getattr(runner, out)[:B].clone() for _, _, out, _ in runner.LINEARS}
+        print(f"[bench] {mode}: decode-step linears per layer {results[mode]}", file=sys.stderr,
+              flush=True)
+        del runner
+    same = all(torch.equal(outs["fp8"][o], outs["ecf8_fused"][o]) for o in outs["fp8"])
+    fp8, fused = _linear_summary(results["fp8"]), _linear_summary(results["ecf8_fused"])
+    line = {
+        "metric": "decode-step linear time per Qwen3-8B-shape layer (q/k/v, o, gate/up, down)",
+        "value": fused["layer"]["us"],
+        "unit": "us",
+        "n_gpus": 1,
+        "higher_is_better": False,
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (random-init weights, random activations)",
+        "config": {"workload": "qwen3-8b-decode-step-linears", "layers": cfg.layers, "rows": B,
+                   "reps": args.steps, "timing": "best of reps; one graph replay of the 36 "
+                                                 "layers' launches per linear"},
+        "fp8": fp8,
+        "ecf8_fused": fused,
+        "ratio_fp8_over_fused": round(fp8["layer"]["us"] / fused["layer"]["us"], 4),
+        "identical_outputs": same,
+    }
+    print(json.dumps(line), flush=True)
+    sys.exit(0 if same else 1)
+
+
 def _linear_summary(lin: dict) -> dict:
     """Per-layer decode-step linear times with their weight bytes as a rate
     and a fraction of the HBM peak."""
@@ -909,14 +973,15 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "flux-block-bf16",
                                            "qwen3-8b-generate", "qwen3-moe-generate",
-                                           "flux-dit-generate"),
+                                           "flux-dit-generate", "qwen3-8b-linears"),
                     default="qwen3-8b-layer",
                     help="qwen3-moe-layer: attention + 128 experts in one batched launch; "
                          "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8; "
                          "qwen3-moe-generate: the same for the 30B-A3B-shaped MoE; "
                          "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8; "
                          "flux-block-bf16: one FLUX double block decoded straight into bf16 "
-                         "weights")
+                         "weights; qwen3-8b-linears: the decode-step linears alone, FP8 vs "
+                         "fused ECF8 (--steps = timing rounds)")
     ap.add_argument("--dit-steps", type=int, default=28)
     ap.add_argument("--routed-tokens", type=int, default=0,
                     help="qwen3-moe-layer: decode only the experts a top-k router picks for "
@@ -965,6 +1030,8 @@ def main():
         sys.exit(0 if line["identical_tokens"] else 1)
     if args.workload == "flux-dit-generate":
         return dit_generate(args)
+    if args.workload == "qwen3-8b-linears":
+        return linears_workload(args)
 
     import torch
 
