@@ -143,17 +143,51 @@ struct LinearSegs {
   int count;
 };
 
-// A 16-row panel's weight operand for the lane (r, g): the lane's base
-// address, the step between 128-column groups and the offset of the
-// group's second half, in either weight layout.
+// Buffer resources: a wave-uniform base and extent in scalar registers, so
+// a load's address is that base + a scalar offset + one VGPR of 32-bit
+// lane offset (a 64-bit address per lane per load would cost the registers
+// of a whole batch of loads).  Raw buffer (stride 0); lane offsets at or
+// past `bytes` read zero instead of faulting.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+// 16 bytes at lane offset voff + scalar offset soff (kNt: streamed,
+// non-temporal -- data read once per launch)
+template <bool kNt>
+__device__ __forceinline__ uint4 buf_load16(Rsrc r, uint32_t voff, uint32_t soff) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNt ? 2 : 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float buf_load_f32(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+// A 16-row panel's weight operand for the lane (r, g), in either weight
+// layout: the panel's first byte (wave-uniform: n0 is a multiple of 16),
+// the lane's 32-bit offset from it (r K + 16 g row-major, 16 l in the tile
+// layout), the step between 128-column groups and the offset of the
+// group's second half.  A uniform base and a 32-bit lane offset let each
+// load take its address from scalar registers plus one VGPR.
 struct WeightLane {
   const uint8_t *base;
+  uint32_t lane;
   int step, half;
   __device__ __forceinline__ WeightLane(const uint8_t *w, bool tiled, int n0, int r, int g, int K)
-      : base(tiled ? tile_lane_base(w, n0 + r, K / kGroup, g) : w + (size_t)(n0 + r) * K + 16 * g),
+      : base(tiled ? w + (size_t)(n0 >> 4) * (size_t)(K / kGroup) * 2048 : w + (size_t)n0 * K),
+        lane(tiled ? 16u * (uint32_t)(16 * g + r) : (uint32_t)r * (uint32_t)K + 16u * (uint32_t)g),
         step(tiled ? 2048 : kGroup),
         half(tiled ? 1024 : 64) {}
-  __device__ __forceinline__ const uint8_t *at(int kg) const { return base + (size_t)kg * step; }
+  __device__ __forceinline__ const uint8_t *at(int kg) const {
+    return base + (size_t)kg * step + lane;
+  }
+  // the panel as a buffer: 16 rows x K bytes in either layout
+  __device__ __forceinline__ Rsrc rsrc(int K) const { return make_rsrc(base, 16u * (uint32_t)K); }
+  // group kg's two 16-byte halves (kg wave-uniform), streamed
+  __device__ __forceinline__ void load(Rsrc r, int kg, uint4 &lo, uint4 &hi) const {
+    lo = buf_load16<true>(r, lane, (uint32_t)kg * (uint32_t)step);
+    hi = buf_load16<true>(r, lane, (uint32_t)kg * (uint32_t)step + (uint32_t)half);
+  }
 };
 
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * w[n,k]) * as[m,g] * ws[n/128, g]
@@ -261,16 +295,19 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
   }
 }
 
-// Small-M form (M <= 16, the decode step): one 16-row MFMA tile, WAVES
-// waves splitting K round-robin in batches of 4 groups.  Every load a batch
-// needs (weights from HBM, activations and both scales from L2) is issued
-// before its first MFMA, so a batch costs one memory round trip.
+// Small-M form (M <= 16, the decode step): one 16-row MFMA tile per
+// workgroup of WAVES waves, wave w taking the K groups w, w + WAVES, ... in
+// batches of 4.  Every load a batch needs (weights from HBM, activations
+// and both scales from L2) is issued before its first MFMA, so a batch
+// costs one memory round trip; the loads are buffer loads from scalar
+// bases (96 VGPRs for a batch, no spills).
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
     const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, LinearSegs segs,
     uint16_t *__restrict__ out, int ldo) {
   __shared__ float red[WAVES][4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kgroups = K / kGroup;
 
   int n0 = blockIdx.x * 16;
@@ -292,16 +329,20 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
   const int r = lane & 15, g = lane >> 4;
   const WeightLane wl(w, wt != 0, n0, r, g, K);
   const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
-  const bool row_ok = r < M;
-  // rows past M (inside the padded 16-row tile) are zeroed after the load
-  const uint8_t *arow = tile_lane_base(aq, r, kgroups, g);
-  bool srow_ok[4];
-  const float *srow[4];
+  // An MFMA output row depends on its own A row and scale only, and rows
+  // past M are never stored: the pad rows of the tile-layout activations
+  // are multiplied as they are, and output rows past M take row M-1's
+  // scale (an in-bounds read).
+  // buffers: the panel's weights, the first 16-row tile of the
+  // activations, their scales (M rows); lane offsets: the lane's activation
+  // bytes in a group block, the scale rows it applies
+  const Rsrc wr = wl.rsrc(K);
+  const Rsrc ar = make_rsrc(aq, (uint32_t)kgroups * 2048u);
+  const Rsrc sr = make_rsrc(as, 4u * (uint32_t)M * (uint32_t)kgroups);
+  const uint32_t alane = 16u * (uint32_t)lane;
+  uint32_t srow[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    srow_ok[i] = 4 * g + i < M;
-    srow[i] = as + (size_t)(srow_ok[i] ? 4 * g + i : 0) * kgroups;
-  }
+  for (int i = 0; i < 4; ++i) srow[i] = 4u * (uint32_t)min(4 * g + i, M - 1) * (uint32_t)kgroups;
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   constexpr int kU = 4;
@@ -312,22 +353,18 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
     for (int u = 0; u < kU; ++u) {
       const int kg = kb + WAVES * u;
       if (kg < kgroups) {
-        wv[u][0] = load_stream16(wl.at(kg));
-        wv[u][1] = load_stream16(wl.at(kg) + wl.half);
+        wl.load(wr, kg, wv[u][0], wv[u][1]);
         wsv[u] = wsrow[kg];
-        av[u][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048);
-        av[u][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048 + 1024);
+        av[u][0] = buf_load16<false>(ar, alane, (uint32_t)kg * 2048u);
+        av[u][1] = buf_load16<false>(ar, alane, (uint32_t)kg * 2048u + 1024u);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sav[u][i] = srow[i][kg];
+        for (int i = 0; i < 4; ++i) sav[u][i] = buf_load_f32(sr, srow[i], 4u * (uint32_t)kg);
       }
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int kg = kb + WAVES * u;
       if (kg >= kgroups) break;
-      if (!row_ok) av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sav[u][i] = srow_ok[i] ? sav[u][i] : 0.f;
       v4f d = {0.f, 0.f, 0.f, 0.f};
       d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
           (long)(((uint64_t)av[u][0].y << 32) | av[u][0].x),
@@ -370,7 +407,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
     uint16_t *__restrict__ out, int ldo, int n_tiles) {
   constexpr int K = 4096, kgroups = K / kGroup, kU = kgroups / WAVES;
   __shared__ float red[WAVES][4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const bool row_ok = r < M;
 
@@ -420,12 +458,12 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
     int col, n0, wt;
     tile_base(tile, w, ws, col, n0, wt);
     const WeightLane wl(w, wt != 0, n0, r, g, K);
+    const Rsrc wr = wl.rsrc(K);
     const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int kg = wave + WAVES * u;
-      wv[u][0] = load_stream16(wl.at(kg));
-      wv[u][1] = load_stream16(wl.at(kg) + wl.half);
+      wl.load(wr, kg, wv[u][0], wv[u][1]);
       wsv[u] = wsrow[kg];
     }
   };
@@ -1165,9 +1203,11 @@ __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
   const float *ws = reinterpret_cast<const float *>(a.ws[(size_t)e * a.n_segs + seg]);
   const int col = seg * a.seg_n;
   const int K = a.K, kgroups = K / kGroup;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const WeightLane wl(w, a.wtiled != 0, n0, r, g, K);
+  const Rsrc wr = wl.rsrc(K);
   const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
 
   for (int rc = 0; rc < rows; rc += 16) {
@@ -1191,8 +1231,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
       for (int u = 0; u < kU; ++u) {
         const int kg = kb + WAVES * u;
         if (kg < kgroups) {
-          wv[u][0] = load_stream16(wl.at(kg));
-          wv[u][1] = load_stream16(wl.at(kg) + wl.half);
+          wl.load(wr, kg, wv[u][0], wv[u][1]);
           wsv[u] = wsrow[kg];
           av[u][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048);
           av[u][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)kg * 2048 + 1024);
@@ -1317,11 +1356,11 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
     }
     // long K: 16 waves, so each wave's share stays within two batches
     if (K / kGroup >= 64)
-      fp8_linear16_kernel<16><<<(unsigned)(n_total / 16), 1024, 0, as_stream(stream)>>>(
-          a, as, (int)M, (int)K, s, o, (int)ldo);
+      fp8_linear16_kernel<16><<<n_tiles, 1024, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s,
+                                                                       o, (int)ldo);
     else
-      fp8_linear16_kernel<8><<<(unsigned)(n_total / 16), 512, 0, as_stream(stream)>>>(
-          a, as, (int)M, (int)K, s, o, (int)ldo);
+      fp8_linear16_kernel<8><<<n_tiles, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o,
+                                                                     (int)ldo);
   } else {
     dim3 grid((unsigned)(n_total / 16), (unsigned)((M + 63) / 64));
     fp8_linear_kernel<4><<<grid, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o, (int)ldo);
