@@ -64,6 +64,15 @@ struct TileSegs {
 
 __device__ __forceinline__ float bf16_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
 
+// Raw buffer resources: a wave-uniform base in scalar registers and a
+// 32-bit lane offset per load (instead of a 64-bit address per lane and
+// load), extent unbounded (the offsets come from the layout's own
+// indices).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc rsrc_at(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, -1, 0x00020000);
+}
+
 // fp32 -> bf16, round to nearest even (as the FP8 linear does)
 __device__ __forceinline__ uint32_t f32_bf16(float f) {
   uint32_t u = __float_as_uint(f);
@@ -98,20 +107,21 @@ __device__ __forceinline__ SegLoad seg_window(const TileOperand &t, uint32_t s, 
   SegLoad r;
   r.n_chunks = (int)((end - off + kTileChunkBytes - 1) / kTileChunkBytes);
   // lanes past the segment's chunks re-read its first one (in bounds; unused)
-  const uint32_t b = off + (lane < r.n_chunks ? (uint32_t)(kTileChunkBytes * lane) : 0u);
-  const u32x4_a4 v = *reinterpret_cast<const u32x4_a4 *>(t.stream + b);
+  const uint32_t b = lane < r.n_chunks ? (uint32_t)(kTileChunkBytes * lane) : 0u;
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc_at(t.stream + off), b, 0, 0);
   r.d0 = v.x;
   r.d1 = v.y;
   r.d2 = v.z;
   r.d3 = v.w;
-  r.gapw = t.gaps[(size_t)s * kTileGapWords + (lane >> 3)];
+  r.gapw = __builtin_amdgcn_raw_buffer_load_b32(rsrc_at(t.gaps + (size_t)s * kTileGapWords),
+                                                4u * (uint32_t)(lane >> 3), 0, 0);
   return r;
 }
 
 // The lane's 32 sign/mantissa nibbles of segment s (read once: streamed).
 __device__ __forceinline__ u32x4 seg_other(const TileOperand &t, uint32_t s, int lane) {
-  return __builtin_nontemporal_load(
-      reinterpret_cast<const u32x4 *>(t.other + (size_t)s * kTileOtherBytes + 16 * lane));
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc_at(t.other + (size_t)s * kTileOtherBytes),
+                                               16u * (uint32_t)lane, 0, 2 /* nt */);
 }
 
 // Byte i (0..15) of the lane's chunk window, shifted into a table offset
@@ -617,11 +627,13 @@ void tile_linear16_kernel(
   // activations in the tile layout (include/ecf8_llm.h): row R's lane part
   // g of group kg at ((R / 16) * kgroups + kg) * 2048 + (R % 16) * 16 + 256 g
   const uint32_t arow_r = a_row(r);
-  const uint8_t *const arow =
-      a.aq + (size_t)(arow_r >> 4) * kgroups * 2048 + (arow_r & 15u) * 16u + 256u * (uint32_t)g;
+  const uint32_t aoff = (arow_r >> 4) * (uint32_t)kgroups * 2048u + (arow_r & 15u) * 16u +
+                        256u * (uint32_t)g;
+  const Rsrc ar = rsrc_at(a.aq), sr = rsrc_at(a.as);
+  // byte offsets of the lane's four scale rows
   uint32_t srow[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) srow[i] = a_row(4 * g + i) * (uint32_t)kgroups;
+  for (int i = 0; i < 4; ++i) srow[i] = 4u * a_row(4 * g + i) * (uint32_t)kgroups;
   const int ng = (kgroups + WAVES - 1) / WAVES;
   // steps per panel of each hardware wave, and (packed) step q's FP8 wave
   // and its step in that wave: position hwave * spw + q of the FP8 waves'
@@ -781,10 +793,15 @@ void tile_linear16_kernel(
       if constexpr (kOthNow)
         on[j] = seg_other(sc[j].op, (uint32_t)sc[j].p * (uint32_t)kgroups + (uint32_t)sc[j].kg,
                           lane);
-      av[j][0] = *reinterpret_cast<const uint4 *>(arow + (size_t)sc[j].kg * 2048);
-      av[j][1] = *reinterpret_cast<const uint4 *>(arow + (size_t)sc[j].kg * 2048 + 1024);
+      const uint32_t akg = (uint32_t)sc[j].kg * 2048u;
+      const u32x4 a0 = __builtin_amdgcn_raw_buffer_load_b128(ar, aoff, akg, 0);
+      const u32x4 a1 = __builtin_amdgcn_raw_buffer_load_b128(ar, aoff, akg + 1024u, 0);
+      av[j][0] = make_uint4(a0.x, a0.y, a0.z, a0.w);
+      av[j][1] = make_uint4(a1.x, a1.y, a1.z, a1.w);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sav[j][i] = as[srow[i] + (uint32_t)sc[j].kg];
+      for (int i = 0; i < 4; ++i)
+        sav[j][i] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(sr, srow[i], 4u * (uint32_t)sc[j].kg, 0));
     }
     issue_order();
 #pragma unroll
