@@ -192,23 +192,90 @@ struct WeightLane {
 
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * w[n,k]) * as[m,g] * ws[n/128, g]
 //
-// One workgroup = 8 waves = one 16-column tile (times MT 16-row tiles),
-// the K groups split round-robin over the waves and summed through LDS in
-// wave order.  A wave runs v_mfma_f32_16x16x32_fp8_fp8: lane l holds row
-// l%16 of both operands and bytes [16*(l/16), +16) and [64 + 16*(l/16), +16)
-// of each 128-byte group, i.e. each 16-byte load feeds two MFMAs.  The K
-// order inside a group is a permutation shared by both operands, so the
-// dot product is unchanged.
-template <int MT>
-__global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restrict__ aq,
-                                                         const float *__restrict__ as, int M, int K,
-                                                         LinearSegs segs, uint16_t *__restrict__ out,
-                                                         int ldo) {
-  __shared__ float red[8][MT * 4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// ------------------------------------------------ prompt-size GEMM (M > 16)
+//
+// out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * w[n,k]) * as[m,g] * ws[n/128, g]
+// for M > 16: 128 x 128 output tiles per 256-lane workgroup (2 x 2 waves of
+// 64 x 64), one 128-column K group per step through a two-stage LDS ring.
+//
+// Every operand block -- 16 rows x one K group, 2 KB -- lands in LDS in
+// the tile layout of ecf8_llm.h straight from global memory
+// (global_load_lds_dwordx4: each lane's 16 bytes to LDS at 16 x lane, no
+// register staging): the tile-layout activations and weights block by
+// block, row-major weights gathered into the same order.  The MFMA is
+// gfx950's v_mfma_f32_16x16x128_f8f6f4 (one instruction per 16 x 16 tile
+// and K group): lane l = 16 g + r feeds it the 32 bytes of row r at block
+// bytes 16 l and 1024 + 16 l of both operands -- the same K positions for
+// both, so the dot product is that of the group -- and each LDS read is 16
+// consecutive bytes per lane (conflict-free).  Each group's product is
+// scaled by as[m, g] * ws[n/128, g] and added to the fp32 accumulators in
+// group order.  Rows past M read the last valid 16-row block and are never
+// stored.  Workgroups are ordered so each XCD (blockIdx.x mod 8) takes a
+// contiguous run of tiles, column block by column block: the weight block
+// a tile column reads stays in that XCD's L2 across its row blocks.
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void lds_load16(const uint8_t *g, void *lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(const void *g, void *lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
+}
+// Workgroup barrier without a memory fence (a fence on LDS would also wait
+// for every stage's loads in flight: they write LDS and are counted by
+// vmcnt).  Each wave waits for its own loads of the stage it is about to
+// read with an explicit vmcnt first; the empty asm keeps the compiler from
+// moving memory operations across the barrier.
+__device__ __forceinline__ void gemm_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes of LDS at byte offset `off` + the immediate O of a stage, read
+// by inline asm: the compiler cannot see that it reads LDS, so it does not
+// wait for the loads still filling the other stages (the caller waits for
+// lgkmcnt before using the result).
+template <int O>
+__device__ __forceinline__ uint4 lds_read16(uint32_t off) {
+  uint4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(off), "i"(O));
+  return r;
+}
+
+#ifndef ECF8_GEMM_BM
+#define ECF8_GEMM_BM 256
+#endif
+constexpr int kGemmBM = ECF8_GEMM_BM;        // tile rows: 2 x 64 per wave row pair
+constexpr int kGemmBN = 128;                 // tile columns
+constexpr int kGemmWaves = kGemmBM / 32;     // (BM / 64) x 2 waves of 64 x 64
+constexpr int kGemmABlocks = kGemmBM / 16, kGemmBBlocks = kGemmBN / 16;
+constexpr int kGemmStages = 3;
+// loads per wave and stage: A and B block halves, and one of scales
+constexpr int kGemmLoads = 2 * (kGemmABlocks + kGemmBBlocks) / kGemmWaves + 1;
+// one stage: A blocks, B blocks, A scales
+constexpr int kGemmStageBytes = (kGemmABlocks + kGemmBBlocks) * 2048 + kGemmBM * 4;
+static_assert(kGemmABlocks % kGemmWaves == 0 && kGemmBBlocks % kGemmWaves == 0,
+              "blocks deal evenly to the waves");
+static_assert(kGemmLoads < 64, "vmcnt immediate");
+
+__global__ __launch_bounds__(kGemmWaves * 64) void fp8_gemm_kernel(
+    const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, LinearSegs segs,
+    uint16_t *__restrict__ out, int ldo, int n_mb, int n_tiles) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_ring[kGemmStages * kGemmStageBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
   const int kgroups = K / kGroup;
 
-  int n0 = blockIdx.x * 16;
+  // tile order: XCD x = blockIdx.x % 8 takes tiles [x * per, (x + 1) * per)
+  int tile = blockIdx.x;
+  const int per = n_tiles / 8;
+  if (tile < 8 * per) tile = (tile % 8) * per + tile / 8;
+  const int mb = tile % n_mb, nb = tile / n_mb;
+  const int m0 = mb * kGemmBM;
+
+  int n0 = nb * kGemmBN;
   const uint8_t *w = segs.w[0];
   const float *ws = segs.ws[0];
   int col = segs.col[0], seg_start = 0, wt = segs.tiled[0];
@@ -223,84 +290,149 @@ __global__ __launch_bounds__(512) void fp8_linear_kernel(const uint8_t *__restri
     }
   }
   n0 -= seg_start;
+  typedef const __attribute__((address_space(4))) float ConstF;  // scalar loads
+  ConstF *const wsrow = (ConstF *)(ws + (size_t)(n0 / kGroup) * kgroups);
+  const int last_rb = (M + 15) / 16 - 1;  // the last 16-row block of aq
+  const uint32_t ring = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)s_ring;
 
-  const int r = lane & 15, g = lane >> 4;
-  const int m0 = blockIdx.y * 16 * MT;
-  const WeightLane wl(w, wt != 0, n0, r, g, K);
-  const float *wsrow = ws + (size_t)(n0 / kGroup) * kgroups;
-
-  float acc[MT][4];
+  // loads of group kg into stage st: wave v fills A blocks v A/W.. and B
+  // blocks v B/W.. (A/W, B/W blocks per wave) and the scales of rows 32 v ..
+  // 32 v + 31 (lanes 0..31)
+  auto issue = [&](int st, int kg) {
+    uint8_t *const sa = s_ring + st * kGemmStageBytes;
+    uint8_t *const sb = sa + kGemmABlocks * 2048;
+    float *const ss = reinterpret_cast<float *>(sb + kGemmBBlocks * 2048);
+    constexpr int na = kGemmABlocks / kGemmWaves, nbk = kGemmBBlocks / kGemmWaves;
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[t][i] = 0.f;
-
-  constexpr int kUnroll = 4;
-  for (int kb = wave; kb < kgroups; kb += 8 * kUnroll) {
-    uint4 wv[kUnroll][2];
-    float wsv[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int kg = kb + 8 * u;
-      if (kg < kgroups) {
-        wv[u][0] = load_stream16(wl.at(kg));
-        wv[u][1] = load_stream16(wl.at(kg) + wl.half);
-        wsv[u] = wsrow[kg];
-      }
+    for (int h = 0; h < na; ++h) {
+      const int t = na * wave + h;
+      const int rb = min(m0 / 16 + t, last_rb);
+      const uint8_t *ab = aq + ((size_t)rb * kgroups + kg) * 2048;
+      lds_load16(ab + 16 * lane, sa + t * 2048);
+      lds_load16(ab + 1024 + 16 * lane, sa + t * 2048 + 1024);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int kg = kb + 8 * u;
-      if (kg >= kgroups) break;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int m = m0 + t * 16 + r;
-        uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0;
-        if (m < M) {
-          const uint8_t *ap = tile_lane_base(aq, m, kgroups, g) + (size_t)kg * 2048;
-          a0 = *reinterpret_cast<const uint4 *>(ap);
-          a1 = *reinterpret_cast<const uint4 *>(ap + 1024);
-        }
-        v4f d = {0.f, 0.f, 0.f, 0.f};
-        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-            (long)(((uint64_t)a0.y << 32) | a0.x), (long)(((uint64_t)wv[u][0].y << 32) | wv[u][0].x), d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-            (long)(((uint64_t)a0.w << 32) | a0.z), (long)(((uint64_t)wv[u][0].w << 32) | wv[u][0].z), d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-            (long)(((uint64_t)a1.y << 32) | a1.x), (long)(((uint64_t)wv[u][1].y << 32) | wv[u][1].x), d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
-            (long)(((uint64_t)a1.w << 32) | a1.z), (long)(((uint64_t)wv[u][1].w << 32) | wv[u][1].z), d, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int mi = m0 + t * 16 + 4 * g + i;
-          const float sa = mi < M ? as[(size_t)mi * kgroups + kg] : 0.f;
-          acc[t][i] = fmaf(d[i], sa * wsv[u], acc[t][i]);
-        }
+    for (int h = 0; h < nbk; ++h) {
+      const int t = nbk * wave + h;
+      const uint8_t *b0, *b1;
+      if (wt) {
+        const uint8_t *bb = w + ((size_t)(n0 / 16 + t) * kgroups + kg) * 2048;
+        b0 = bb + 16 * lane;
+        b1 = bb + 1024 + 16 * lane;
+      } else {
+        b0 = w + (size_t)(n0 + 16 * t + (lane & 15)) * K + kg * kGroup + 16 * (lane >> 4);
+        b1 = b0 + 64;
       }
+      lds_load16(b0, sb + t * 2048);
+      lds_load16(b1, sb + t * 2048 + 1024);
     }
+    if (lane < 32) {
+      const int row = min(m0 + 32 * wave + lane, M - 1);
+      lds_load4(as + (size_t)row * kgroups + kg, ss + 32 * wave);
+    }
+  };
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // the lane's LDS offsets in a stage: its A, B and scale reads
+  const uint32_t a_off = (uint32_t)(4 * wm) * 2048u + 16u * (uint32_t)lane;
+  const uint32_t b_off = (uint32_t)(kGemmABlocks + 4 * wn) * 2048u + 16u * (uint32_t)lane;
+  const uint32_t s_off =
+      (uint32_t)(kGemmABlocks + kGemmBBlocks) * 2048u + 4u * (64u * wm + 4u * (lane >> 4));
+
+  issue(0, 0);
+  if (kgroups > 1) issue(1, 1);
+  for (int kg = 0; kg < kgroups; ++kg) {
+    const int st = kg % kGemmStages;
+    // this stage's loads are done unless it is the last: the next one's
+    // kGemmLoads may stay in flight
+    if (kg + 1 < kgroups)
+      __builtin_amdgcn_s_waitcnt((kGemmLoads & 15) | ((kGemmLoads >> 4) << 14) | (0x7 << 4) |
+                                 (0xF << 8));
+    else
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0)
+    // every wave's loads of stage st are in LDS, and every wave is done
+    // reading the stage refilled below (read in the previous step)
+    gemm_barrier();
+    const uint32_t base = ring + (uint32_t)st * kGemmStageBytes;
+    uint4 al[4], ah[4], bl[4], bh[4], sv[4];
+    al[0] = lds_read16<0>(base + a_off);
+    ah[0] = lds_read16<1024>(base + a_off);
+    al[1] = lds_read16<2048>(base + a_off);
+    ah[1] = lds_read16<3072>(base + a_off);
+    al[2] = lds_read16<4096>(base + a_off);
+    ah[2] = lds_read16<5120>(base + a_off);
+    al[3] = lds_read16<6144>(base + a_off);
+    ah[3] = lds_read16<7168>(base + a_off);
+    bl[0] = lds_read16<0>(base + b_off);
+    bh[0] = lds_read16<1024>(base + b_off);
+    bl[1] = lds_read16<2048>(base + b_off);
+    bh[1] = lds_read16<3072>(base + b_off);
+    bl[2] = lds_read16<4096>(base + b_off);
+    bh[2] = lds_read16<5120>(base + b_off);
+    bl[3] = lds_read16<6144>(base + b_off);
+    bh[3] = lds_read16<7168>(base + b_off);
+    sv[0] = lds_read16<0>(base + s_off);
+    sv[1] = lds_read16<64>(base + s_off);
+    sv[2] = lds_read16<128>(base + s_off);
+    sv[3] = lds_read16<192>(base + s_off);
+    const float sw = wsrow[kg];
+    __builtin_amdgcn_s_waitcnt((0x3F & 15) | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));  // lgkmcnt(0)
+    // the stage read in the previous step is free: group kg + 2 goes there
+    if (kg + 2 < kgroups) issue((kg + 2) % kGemmStages, kg + 2);
+    v8i a[4], b[4];
+    v4f c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = v8i{(int)al[i].x, (int)al[i].y, (int)al[i].z, (int)al[i].w,
+                 (int)ah[i].x, (int)ah[i].y, (int)ah[i].z, (int)ah[i].w};
+      b[i] = v8i{(int)bl[i].x, (int)bl[i].y, (int)bl[i].z, (int)bl[i].w,
+                 (int)bh[i].x, (int)bh[i].y, (int)bh[i].z, (int)bh[i].w};
+      c[i] = v4f{__uint_as_float(sv[i].x) * sw, __uint_as_float(sv[i].y) * sw,
+                 __uint_as_float(sv[i].z) * sw, __uint_as_float(sv[i].w) * sw};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4f z = {0.f, 0.f, 0.f, 0.f};
+        // scale operands 0: the unscaled e4m3 x e4m3 form
+        const v4f d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[i], b[j], z, 0, 0, 0, 0,
+                                                                        0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(d[q], c[i][q], acc[i][j][q]);
+      }
   }
 
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][t * 4 + i][lane] = acc[t][i];
-  __syncthreads();
-  for (int v = threadIdx.x; v < MT * 4 * 64; v += 512) {
-    const int ti = v >> 6, l = v & 63;
-    float sum = 0.f;
+    for (int q = 0; q < 4; ++q) {
+      const int m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + q;
+      if (m < M) {
+        uint16_t *o = out + (size_t)m * ldo + col + n0 + 64 * wn + (lane & 15);
 #pragma unroll
-    for (int wv = 0; wv < 8; ++wv) sum += red[wv][ti][l];
-    const int m = m0 + (ti >> 2) * 16 + 4 * (l >> 4) + (ti & 3);
-    if (m < M) out[(size_t)m * ldo + col + n0 + (l & 15)] = (uint16_t)f32_bf16(sum);
-  }
+        for (int j = 0; j < 4; ++j) o[16 * j] = (uint16_t)f32_bf16(acc[i][j][q]);
+      }
+    }
 }
 
 // Small-M form (M <= 16, the decode step): one 16-row MFMA tile per
 // workgroup of WAVES waves, wave w taking the K groups w, w + WAVES, ... in
-// batches of 4.  Every load a batch needs (weights from HBM, activations
-// and both scales from L2) is issued before its first MFMA, so a batch
-// costs one memory round trip; the loads are buffer loads from scalar
-// bases (96 VGPRs for a batch, no spills).
+// batches of 4 and summing each group with four v_mfma_f32_16x16x32_fp8_fp8:
+// lane l = 16 g + r holds row r of both operands, bytes [16 g, +16) and
+// [64 + 16 g, +16) of the group -- the 16-byte halves at block bytes 16 l
+// and 1024 + 16 l of the tile layout -- so each 16-byte load feeds two
+// MFMAs; the K order inside a group is a permutation shared by both
+// operands, so the dot product is unchanged.  Every load a batch needs
+// (weights from HBM, activations and both scales from L2) is issued before
+// its first MFMA, so a batch costs one memory round trip; the loads are
+// buffer loads from scalar bases (96 VGPRs for a batch, no spills).  The
+// waves' sums meet in LDS and are added in wave order.
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
     const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, LinearSegs segs,
@@ -1362,8 +1494,11 @@ extern "C" int ecf8_fp8_linear(const void *aq, const float *as, int64_t M, int64
       fp8_linear16_kernel<8><<<n_tiles, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o,
                                                                      (int)ldo);
   } else {
-    dim3 grid((unsigned)(n_total / 16), (unsigned)((M + 63) / 64));
-    fp8_linear_kernel<4><<<grid, 512, 0, as_stream(stream)>>>(a, as, (int)M, (int)K, s, o, (int)ldo);
+    const int n_mb = (int)((M + kGemmBM - 1) / kGemmBM);
+    const int64_t n_tiles = (n_total / kGemmBN) * n_mb;
+    if (n_tiles > INT32_MAX) return ECF8_ERR_UNSUPPORTED;
+    fp8_gemm_kernel<<<(unsigned)n_tiles, kGemmWaves * 64, 0, as_stream(stream)>>>(
+        a, as, (int)M, (int)K, s, o, (int)ldo, n_mb, (int)n_tiles);
   }
   return launched();
 }

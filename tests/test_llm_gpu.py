@@ -141,11 +141,12 @@ def _linear_ref(aq, a_s, segs):
 
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("M,Kd", [(1, 1024), (5, 1024), (16, 1024), (16, 8192), (3, 12288),
-                                  (17, 1024), (64, 1024), (130, 1024)])
+                                  (17, 1024), (64, 1024), (130, 1024), (300, 4096), (513, 2048)])
 def test_fp8_linear_matches_fp64(cuda_device, M, Kd, layout):
     """M <= 16 runs the one-tile kernel (8 waves, or 16 from K = 8192 on);
-    larger M the 64-row tile kernel.  Weights row-major (layout 0) or in
-    the tile layout (1); activations always in the tile layout."""
+    larger M the LDS-tiled GEMM (256 x 128 tiles, partial row tiles at M =
+    17..513).  Weights row-major (layout 0) or in the tile layout (1);
+    activations always in the tile layout."""
     from ecf8_amd.llm_kernels import LinearPlan
 
     _say(f"[llm] fp8_linear M={M} K={Kd}")
