@@ -34,6 +34,7 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 REPO = os.path.dirname(os.path.abspath(__file__))
 
 
@@ -540,6 +541,10 @@ def e2e_generate(args):
             r["linears"] = runner.time_linears()
             print(f"[bench] {mode}: decode-step linears per layer {r['linears']}",
                   file=sys.stderr, flush=True)
+        if mode == "fp8":
+            # the prompt's GEMMs (every mode runs the same kernel on the same bytes)
+            r["prefill"] = runner.time_linears(prompt=True)
+            print(f"[bench] prompt GEMMs per layer {r['prefill']}", file=sys.stderr, flush=True)
         results[mode] = r
         del runner
     ecf8_modes = ("ecf8", "ecf8_prefetch", "ecf8_fused")
@@ -580,6 +585,7 @@ def e2e_generate(args):
         "identical_tokens": same,
         "linears_per_layer_step": {m: _linear_summary(results[m]["linears"])
                                    for m in ("fp8", "ecf8_fused")},
+        "prompt_gemms_per_layer": _gemm_summary(results["fp8"]["prefill"]),
     }
     return line
 
@@ -591,8 +597,10 @@ def linears_workload(args):
     weights resident in the tile layout, then over the same layers
     ECF8-compressed and re-tiled (the fused decode-into-MFMA linears).  The
     activations are one seeded random batch quantized per 1x128 group; the
-    last layer's outputs of the two modes must be identical.  Starts no
-    child process, so a counter profile of it sees only these kernels."""
+    last layer's outputs of the two modes must be identical.  Also times
+    the prompt's GEMMs (M = batch x --prompt-len rows, FP8 weights) as
+    TFLOP/s.  Starts no child process, so a counter profile of it sees only
+    these kernels."""
     import torch
 
     from ecf8_amd import llm_kernels as K
@@ -613,13 +621,16 @@ def linears_workload(args):
         else:
             compress_layers(model, drawn)
             retile_layers(model, drawn)
-        runner = Qwen3Runner(model, B, 1, 2, dev)
+        T = args.prompt_len if mode == "fp8" else 1
+        runner = Qwen3Runner(model, B, T, T + 1, dev)
         if mode == "fp8":
-            acts = {k: torch.randn(B, k, generator=g, device=dev).to(torch.bfloat16)
+            acts = {k: torch.randn(B * T, k, generator=g, device=dev).to(torch.bfloat16)
                     for k in runner.aq}
         for k, x in acts.items():
-            K.act_quant(x, B, runner.aq[k], runner.as_[k])
+            K.act_quant(x[: B * T], B * T, runner.aq[k], runner.as_[k])
         results[mode] = runner.time_linears(reps=args.steps)
+        if mode == "fp8":
+            prompt = runner.time_linears(reps=args.steps, prompt=True)
         torch.cuda.synchronize()
         outs[mode] = {out: getattr(runner, out)[:B].clone() for _, _, out, _ in runner.LINEARS}
         print(f"[bench] {mode}: decode-step linears per layer {results[mode]}", file=sys.stderr,
@@ -643,9 +654,24 @@ def linears_workload(args):
         "ecf8_fused": fused,
         "ratio_fp8_over_fused": round(fp8["layer"]["us"] / fused["layer"]["us"], 4),
         "identical_outputs": same,
+        "prompt_gemms_per_layer": dict(_gemm_summary(prompt), rows=B * args.prompt_len),
     }
     print(json.dumps(line), flush=True)
     sys.exit(0 if same else 1)
+
+
+def _gemm_summary(lin: dict) -> dict:
+    """Per-layer prompt GEMM times as TFLOP/s and a fraction of MI355X's
+    dense FP8 MFMA peak."""
+    out = {k: {"us": v["us"], "tflop_s": round(v["flops"] / (v["us"] * 1e-6) / 1e12, 1),
+               "fp8_peak_frac": round(v["flops"] / (v["us"] * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+           for k, v in lin.items()}
+    us = sum(v["us"] for v in lin.values())
+    fl = sum(v["flops"] for v in lin.values())
+    out["layer"] = {"us": round(us, 2), "gflop": round(fl / 1e9, 1),
+                    "tflop_s": round(fl / (us * 1e-6) / 1e12, 1),
+                    "fp8_peak_frac": round(fl / (us * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+    return out
 
 
 def _linear_summary(lin: dict) -> dict:

@@ -356,18 +356,20 @@ class Qwen3Runner(_GreedyRunner):
                ("gate_up", ("mlp.gate_proj", "mlp.up_proj"), "gu", "H"),
                ("down", ("mlp.down_proj",), "down", "I"))
 
-    def time_linears(self, reps: int = 3) -> dict:
+    def time_linears(self, reps: int = 3, prompt: bool = False) -> dict:
         """Decode-step (M = batch) time of each linear of a layer: the
         linear of every layer launched back to back (one HIP graph replayed
         between one event pair), so the layers' weights stream from HBM as
         in a decode step (36
         Qwen3-8B layers hold 5.8-6.9 GB, far above the 256 MB MALL); the
         best of ``reps`` rounds, divided by the layer count.  Returns
-        {linear: {"us": ..., "bytes": weight bytes read per layer}}.  Runs
-        the FP8 linears of resident weights or the tiled linears of
-        re-tiled layers; layers decoded by their hooks share one buffer and
-        are not timed this way."""
-        cfg, M = self.cfg, self.B
+        {linear: {"us": ..., "bytes": weight bytes read per layer,
+        "flops": per layer}}.  Runs the FP8 linears of resident weights or
+        the tiled linears of re-tiled layers; layers decoded by their hooks
+        share one buffer and are not timed this way.  ``prompt``: the
+        prompt's GEMMs instead (M = batch x prompt length, resident FP8
+        weights only)."""
+        cfg, M = self.cfg, (self.B * self.T if prompt else self.B)
         layers = list(self.model.model.layers)
         widths = {"H": cfg.hidden, "A": cfg.heads * cfg.head_dim, "I": cfg.intermediate}
         dev = self.dev
@@ -380,6 +382,8 @@ class Qwen3Runner(_GreedyRunner):
                 tiles = getattr(layer, "_ecf8_tiles", None)
                 if tiles is None and hasattr(layer, "encoded"):
                     raise ECF8Error("layers decoded by their hooks share one buffer")
+                if tiles is not None and M > 16:
+                    raise ECF8Error("the prompt's GEMMs of re-tiled layers read decoded scratch")
                 plans.append(self._linear(layer, i, which, names, out, M))
                 if i == 0:
                     nbytes = (sum(tiles[n].nbytes() + tiles[n].weight_scale.numel() * 4
@@ -411,7 +415,10 @@ class Qwen3Runner(_GreedyRunner):
                 ms = a.elapsed_time(b) / len(plans)
                 best = ms if best is None else min(best, ms)
             del graph
-            res[which] = {"us": round(best * 1e3, 2), "bytes": int(nbytes)}
+            n_out = sum(layers[0].get_submodule(n).weight.shape[0] if tiles is None else tiles[n].n
+                        for n in names)
+            res[which] = {"us": round(best * 1e3, 2), "bytes": int(nbytes),
+                          "flops": 2 * M * n_out * K_in}
         return res
 
     def layer(self, layer: DecoderLayer, index: int, x_prev, prefill: bool):
