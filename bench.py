@@ -973,12 +973,20 @@ def dit_child(seed: int, timeout_s: float):
     return out
 
 
+BATCHED_MIN_STEPS = 200
+
+
 def batched_child(seed: int, steps: int, warmup: int, timeout_s: float):
     """The batched MoE-layer decode line (one Qwen3-30B-A3B-shaped layer,
-    attention + 128 experts in one launch) run in a child process with the
-    same step counts as this line."""
+    attention + 128 experts in one launch) run in a child process with this
+    line's warm-up and at least BATCHED_MIN_STEPS timed launches (~47 ms):
+    on MI355X the first ~15 ms of sustained decode load run up to 8 %
+    slower than the rest (launch times 235 -> 255 -> 235 us, with or
+    without a GPU-busy prime beforehand), so a 20-launch window after 5
+    warm-up launches would time that onset alone."""
     full, wall = _child_line(["--workload", "qwen3-moe-layer", "--seed", str(seed), "--steps",
-                              str(steps), "--warmup", str(warmup)], timeout_s)
+                              str(max(steps, BATCHED_MIN_STEPS)), "--warmup", str(warmup)],
+                             timeout_s)
     if "error" in full:
         return full
     cfg = full["config"]
