@@ -946,7 +946,8 @@ def e2e_child(workload: str, seed: int, timeout_s: float):
     if "error" in full:
         return full
     keep = ("uncompressed_fp8", "ecf8", "ecf8_mode", "ecf8_modes", "ratio_vs_uncompressed",
-            "identical_tokens", "experts_routed_last_step", "linears_per_layer_step")
+            "identical_tokens", "experts_routed_last_step", "linears_per_layer_step",
+            "prompt_gemms_per_layer")
     out = {"workload": full["config"]["workload"], "unit": full["unit"],
            "batch": full["config"]["batch"], "prompt_len": full["config"]["prompt_len"],
            "new_tokens": full["config"]["new_tokens"],
