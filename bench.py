@@ -629,10 +629,10 @@ def linears_workload(args):
         for k, x in acts.items():
             K.act_quant(x[: B * T], B * T, runner.aq[k], runner.as_[k])
         results[mode] = runner.time_linears(reps=args.steps)
-        if mode == "fp8":
-            prompt = runner.time_linears(reps=args.steps, prompt=True)
         torch.cuda.synchronize()
         outs[mode] = {out: getattr(runner, out)[:B].clone() for _, _, out, _ in runner.LINEARS}
+        if mode == "fp8":  # after the compared outputs: it rewrites the output buffers
+            prompt = runner.time_linears(reps=args.steps, prompt=True)
         print(f"[bench] {mode}: decode-step linears per layer {results[mode]}", file=sys.stderr,
               flush=True)
         del runner
