@@ -141,12 +141,14 @@ def tile_decode(op: TiledOperand, table, out: torch.Tensor | None = None) -> tor
 
 def linear_waves(n_total: int, k: int, device) -> int:
     """The wave count the FP8 linear uses for M <= 16 at this shape (16 for
-    K >= 64 groups or the persistent K = 4096 form, else 8): the tiled
-    linear must use the same one to sum in the same order."""
+    K >= 64 groups, for at most one 16-column tile per CU, or the
+    persistent K = 4096 form; else 8): the tiled linear must use the same
+    one to sum in the same order."""
     if k // _GROUP >= 64:
         return 16
     cus = torch.cuda.get_device_properties(device).multi_processor_count
-    if k == 4096 and n_total // 16 > 2 * cus:
+    tiles = n_total // 16
+    if tiles <= cus or (k == 4096 and tiles > 2 * cus):
         return 16
     return 8
 

@@ -92,8 +92,9 @@ typedef struct ecf8_tile_operand {
  *   out[m, out_col + n] = sum_g (sum_{k in g} aq[m,k] W[n,k]) as[m,g] ws[n/128,g]
  * `table`: the ECF8_TABLE_DFA table of the block's LUTs (all operands
  * share the block's code).  `waves` (8 or 16) must be the wave count
- * ecf8_fp8_linear uses for the same shape -- 16 when K/128 >= 64 or when
- * K = 4096 has more than 2 x CUs 16-column tiles, else 8 -- and the result
+ * ecf8_fp8_linear uses for the same shape -- 16 when K/128 >= 64, when
+ * there are at most as many 16-column tiles as CUs, or when K = 4096 has
+ * more than 2 x CUs tiles; else 8 -- and the result
  * is then bit-identical to decoding W and calling ecf8_fp8_linear.
  * aq: the tile layout of ecf8_llm.h (16-byte aligned, rows padded to 16);
  * out: bf16, ldo elements per row.

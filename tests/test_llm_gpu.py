@@ -143,7 +143,9 @@ def _linear_ref(aq, a_s, segs):
 @pytest.mark.parametrize("M,Kd", [(1, 1024), (5, 1024), (16, 1024), (16, 8192), (3, 12288),
                                   (17, 1024), (64, 1024), (130, 1024), (300, 4096), (513, 2048)])
 def test_fp8_linear_matches_fp64(cuda_device, M, Kd, layout):
-    """M <= 16 runs the one-tile kernel (8 waves, or 16 from K = 8192 on);
+    """M <= 16 runs the one-tile kernel (16 waves here: at most one
+    16-column tile per CU, or K >= 8192; the 8-wave shape is checked
+    below);
     larger M the LDS-tiled GEMM (256 x 128 tiles, partial row tiles at M =
     17..513).  Weights row-major (layout 0) or in the tile layout (1);
     activations always in the tile layout."""
@@ -168,6 +170,31 @@ def test_fp8_linear_matches_fp64(cuda_device, M, Kd, layout):
     tol = 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()
     assert bool(((got - ref).abs() <= tol).all())
     assert bool((out[:, sum(shapes):].cpu() == 7.0).all())  # columns past the segments untouched
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_fp8_linear_eight_wave_shape_matches_fp64(cuda_device, M):
+    """More 16-column tiles than CUs (but not the persistent K = 4096 form):
+    the eight-wave kernel, q/k/v-shaped segments."""
+    from ecf8_amd.llm_kernels import LinearPlan
+
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    Kd = 1024
+    shapes = [16 * cus, 512, 512]  # > cus tiles in all
+    gen = torch.Generator().manual_seed(91 + M)
+    aq = _rand_fp8((M, Kd), gen, cuda_device)
+    a_s = (torch.rand(M, Kd // 128, generator=gen) * 1e-2 + 1e-4).to(cuda_device)
+    segs = []
+    for n in shapes:
+        w = _rand_fp8((n, Kd), gen, cuda_device)
+        ws = (torch.rand(n // 128, Kd // 128, generator=gen) * 1e-3 + 1e-5).to(cuda_device)
+        segs.append((w, ws))
+    out = torch.full((M, sum(shapes)), 7.0, dtype=torch.bfloat16, device=cuda_device)
+    LinearPlan([(to_tiles(w), ws, 1) for w, ws in segs], out)(to_tiles(aq), a_s, M)
+    ref = _linear_ref(aq, a_s, segs)
+    got = out.double().cpu()
+    tol = 2 ** -7 * ref.abs() + 1e-4 * ref.abs().max()
+    assert bool(((got - ref).abs() <= tol).all())
 
 
 def test_fp8_linear_persistent_path_matches_fp64(cuda_device):
