@@ -660,6 +660,85 @@ def linears_workload(args):
     sys.exit(0 if same else 1)
 
 
+def moe_linears_workload(args):
+    """The decode-step linears of the Qwen3-30B-A3B-shaped MoE model alone
+    (M = --batch tokens): attention q/k/v and o, and the routed experts'
+    grouped gate/up and down, each launched for all 48 layers back to back
+    on one routing of seeded random activations through layer 0's router
+    (top-8 of 128 experts per token; every layer runs that routing, so each
+    reads the picked experts' weights, ~0.4 GB per layer), first over FP8
+    weights resident in the tile layout, then over the same blocks
+    ECF8-compressed and re-tiled.  The last layer's outputs of the two
+    modes must be identical.  Starts no child process."""
+    import torch
+
+    from ecf8_amd import llm_kernels as K
+    from ecf8_amd.llm import tile_resident_weights
+    from ecf8_amd.moe import (Qwen3MoeConfig, Qwen3MoeRunner, compress_moe_layers,
+                              random_moe_model, retile_moe_layers)
+
+    dev = torch.device("cuda", 0)
+    cfg = Qwen3MoeConfig()
+    B = args.batch
+    if B > 16:
+        raise SystemExit("--batch: the decode-step linears take at most 16 rows")
+    model, drawn = random_moe_model(cfg, dev, distinct_layers=args.distinct_layers, seed=args.seed)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 11)
+    P, I, A = B * cfg.top_k, cfg.moe_intermediate, cfg.heads * cfg.head_dim
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    x_h = torch.randn(B, cfg.hidden, generator=g, device=dev).to(torch.bfloat16)
+    x_a = torch.randn(B, A, generator=g, device=dev).to(torch.bfloat16)
+    x_gu = torch.randn(P, 2 * I, generator=g, device=dev).to(torch.bfloat16)
+    results, outs, n_active = {}, {}, {}
+    for mode in ("fp8", "ecf8_fused"):
+        if mode == "fp8":
+            tile_resident_weights(model)
+        else:
+            compress_moe_layers(model, drawn)
+            retile_moe_layers(model, drawn)
+        runner = Qwen3MoeRunner(model, B, 1, 2, dev)
+        layer0 = model.model.layers[0]
+        runner.hb[:B].copy_(x_h)
+        K.act_quant(runner.hb, B, runner.aqH, runner.asH)
+        K.act_quant(x_a, B, runner.aqA, runner.asA)
+        K.moe_route(runner.hb[:B], layer0.mlp.gate.weight, B, runner.route)
+        K.moe_group(runner.route, B)
+        runner.gu[:P].copy_(x_gu)
+        K.silu_mul_quant(runner.gu, P, runner.hq, runner.hs)
+        n_active[mode] = int(runner.route.n_active.item())
+        results[mode] = runner.time_linears(reps=args.steps)
+        torch.cuda.synchronize()
+        outs[mode] = {"qkv": runner.qkv[:B].clone(), "o": runner.o[:B].clone(),
+                      "gate_up": runner.gu[:P].clone(), "down": runner.down[:P].clone()}
+        print(f"[bench] {mode}: decode-step linears per layer {results[mode]}", file=sys.stderr,
+              flush=True)
+        del runner
+    same = all(torch.equal(outs["fp8"][o], outs["ecf8_fused"][o]) for o in outs["fp8"])
+    fp8, fused = _linear_summary(results["fp8"]), _linear_summary(results["ecf8_fused"])
+    line = {
+        "metric": "decode-step linear time per Qwen3-30B-A3B-shape MoE layer (q/k/v, o, routed "
+                  "gate/up, routed down)",
+        "value": fused["layer"]["us"],
+        "unit": "us",
+        "n_gpus": 1,
+        "higher_is_better": False,
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (random-init weights, random activations)",
+        "config": {"workload": "qwen3-moe-decode-step-linears", "layers": cfg.layers,
+                   "tokens": B, "experts": cfg.experts, "top_k": cfg.top_k,
+                   "experts_routed": n_active["fp8"], "reps": args.steps,
+                   "timing": "best of reps; one graph replay of the 48 layers' launches per "
+                             "linear"},
+        "fp8": fp8,
+        "ecf8_fused": fused,
+        "ratio_fp8_over_fused": round(fp8["layer"]["us"] / fused["layer"]["us"], 4),
+        "identical_outputs": same and n_active["fp8"] == n_active["ecf8_fused"],
+    }
+    print(json.dumps(line), flush=True)
+    sys.exit(0 if line["identical_outputs"] else 1)
+
+
 def _gemm_summary(lin: dict) -> dict:
     """Per-layer prompt GEMM times as TFLOP/s and a fraction of MI355X's
     dense FP8 MFMA peak."""
@@ -755,6 +834,11 @@ def moe_generate(args):
         r = timed_generate(runner, prompt, new)
         # experts the last step's router picked, in the last layer
         r["experts_routed_last_step"] = int(runner.route.n_active.item())
+        if mode in ("fp8", "ecf8_fused"):
+            # on the last step's routing and inputs
+            r["linears"] = runner.time_linears()
+            print(f"[bench] {mode}: decode-step linears per layer {r['linears']}",
+                  file=sys.stderr, flush=True)
         print(f"[bench] {mode}: {r['tokens_per_s']:.1f} tokens/s, latency {r['latency_s']:.3f}s, "
               f"peak {r['peak_mib']:.0f} MiB", file=sys.stderr, flush=True)
         r["weights_mib"] = sum(t.numel() * t.element_size() for t in
@@ -805,6 +889,8 @@ def moe_generate(args):
         "experts_routed_last_step": ecf8["experts_routed_last_step"],
         "ratio_vs_uncompressed": round(ecf8["tokens_per_s"] / fp8["tokens_per_s"], 4),
         "identical_tokens": same,
+        "linears_per_layer_step": {m: _linear_summary(results[m]["linears"])
+                                   for m in ("fp8", "ecf8_fused")},
     }
     return line
 
@@ -1008,7 +1094,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("qwen3-8b-layer", "qwen3-moe-layer", "flux-block-bf16",
                                            "qwen3-8b-generate", "qwen3-moe-generate",
-                                           "flux-dit-generate", "qwen3-8b-linears"),
+                                           "flux-dit-generate", "qwen3-8b-linears",
+                                           "qwen3-moe-linears"),
                     default="qwen3-8b-layer",
                     help="qwen3-moe-layer: attention + 128 experts in one batched launch; "
                          "qwen3-8b-generate: end-to-end greedy generation, FP8 vs ECF8; "
@@ -1016,7 +1103,8 @@ def main():
                          "flux-dit-generate: one 1024x1024 DiT image, FP8 vs ECF8; "
                          "flux-block-bf16: one FLUX double block decoded straight into bf16 "
                          "weights; qwen3-8b-linears: the decode-step linears alone, FP8 vs "
-                         "fused ECF8 (--steps = timing rounds)")
+                         "fused ECF8 (--steps = timing rounds); qwen3-moe-linears: the same for "
+                         "the MoE's attention and routed expert linears")
     ap.add_argument("--dit-steps", type=int, default=28)
     ap.add_argument("--routed-tokens", type=int, default=0,
                     help="qwen3-moe-layer: decode only the experts a top-k router picks for "
@@ -1067,6 +1155,8 @@ def main():
         return dit_generate(args)
     if args.workload == "qwen3-8b-linears":
         return linears_workload(args)
+    if args.workload == "qwen3-moe-linears":
+        return moe_linears_workload(args)
 
     import torch
 

@@ -83,13 +83,16 @@ __device__ __forceinline__ uint32_t f32_bf16(float f) {
 
 // 8 FP8 bytes -- operand elements 8r..8r+7 of a lane, as two dwords of 4
 // -- from its staged exponent dword E (elements 0..3 in the even nibbles,
-// 4..7 in the odd ones) and nibble dword O (byte j = o_j << 4 | o_{j+4},
-// o = sign << 3 | mantissa): the run order of the layout needs no byte
-// interleave.
+// 4..7 in the odd ones) and nibble dword O, whose byte q holds element q's
+// mantissa (bits 0..2) and sign (bit 7) where its FP8 byte has them, and
+// element q + 4's mantissa in bits 4..6 and sign one byte up, in bit 3 of
+// byte (q + 1) % 4: rotated right by 4 bits, O holds elements 4..7 in
+// place.  Five VALU ops per 8 bytes; the run order of the layout needs no
+// byte interleave.
 __device__ __forceinline__ uint2 merge8_runs(uint32_t e, uint32_t o) {
   uint2 r;
-  r.x = bfi<0x80808080u>(o, bfi<0x78787878u>(e << 3, o >> 4));
-  r.y = bfi<0x80808080u>(o << 4, bfi<0x78787878u>(e >> 1, o));
+  r.x = bfi<0x78787878u>(e << 3, o);
+  r.y = bfi<0x78787878u>(e >> 1, __builtin_amdgcn_alignbit(o, o, 4u));
   return r;
 }
 

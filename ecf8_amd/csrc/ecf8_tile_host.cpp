@@ -31,7 +31,23 @@ inline void tile_element(int64_t p, int64_t kg, int i, int64_t *row, int64_t *co
 }
 
 inline int exponent_of(uint8_t b) { return (b >> 3) & 0xF; }
-inline int other_of(uint8_t b) { return ((b >> 4) & 0x8) | (b & 0x7); }
+
+// Sign and mantissa of symbol i into the segment's nibble plane: each run
+// of 8 symbols (operand elements q and q + 4 at symbols 2q and 2q + 1) owns
+// 4 bytes; byte q holds element q's mantissa in bits 0..2 and sign in bit
+// 7, element q + 4's mantissa in bits 4..6, and in bit 3 the sign of
+// element ((q + 3) % 4) + 4 -- so that a 4-bit rotation of the run's dword
+// puts every high element's sign and mantissa where its FP8 byte has them.
+inline void put_sign_mantissa(uint8_t *other, int i, uint8_t b) {
+  uint8_t *const run = other + (i >> 3) * 4;
+  const int q = (i & 7) >> 1, sign = b >> 7, mant = b & 7;
+  if (!(i & 1)) {
+    run[q] |= (uint8_t)(mant | sign << 7);
+  } else {
+    run[q] |= (uint8_t)(mant << 4);
+    run[(q + 1) & 3] |= (uint8_t)(sign << 3);
+  }
+}
 
 // Bits of one segment under the code lengths.
 int64_t segment_bits(const uint8_t *w, int64_t k, int64_t p, int64_t kg, const uint8_t *code_bits,
@@ -56,6 +72,7 @@ void write_segment(const uint8_t *w, int64_t k, int64_t p, int64_t kg, const uin
   int64_t nbyte = 0, pos = 0;
   int next_chunk = 0;  // first chunk whose gap is not yet recorded
   memset(gaps, 0, kTileGapWords * 4);
+  memset(other, 0, kTileOtherBytes);
   for (int i = 0; i < kTileSegSymbols; ++i) {
     int64_t row, col;
     tile_element(p, kg, i, &row, &col);
@@ -74,9 +91,7 @@ void write_segment(const uint8_t *w, int64_t k, int64_t p, int64_t kg, const uin
       out[nbyte++] = (uint8_t)(acc >> (nacc - 8));
       nacc -= 8;
     }
-    const int o = other_of(b);
-    uint8_t &ob = other[i >> 1];
-    ob = (uint8_t)((i & 1) ? (ob | o) : (o << 4));
+    put_sign_mantissa(other, i, b);
   }
   if (nacc) out[nbyte++] = (uint8_t)(acc << (8 - nacc));
 }

@@ -179,6 +179,41 @@ class _GreedyRunner:
             self._plans[key] = p
         return p
 
+    def _time_launches(self, launches, reps: int, warm_ms: float = 40.0) -> float:
+        """Best time in ms per launch of ``launches`` (callables, each one
+        kernel launch on the current stream) over ``reps`` replays of one
+        HIP graph holding them all: a graph, so host launch time cannot
+        starve the GPU between these short kernels (a decode step replays a
+        graph too).  Before timing, one eager round and back-to-back
+        replays for about ``warm_ms`` of sustained load: on MI355X the
+        first ~15 ms of such load run up to 8 % slower, and a generation
+        runs its steps back to back."""
+        dev = self.dev
+        for f in launches:
+            f()
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for f in launches:
+                f()
+        stream = torch.cuda.current_stream(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize(dev)
+        for _ in range(min(1000, int(warm_ms / max(a.elapsed_time(b), 1e-3)))):
+            graph.replay()
+        # the timed replays follow on without a host round trip in between
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        marks[0].record(stream)
+        for i in range(reps):
+            graph.replay()
+            marks[i + 1].record(stream)
+        torch.cuda.synchronize(dev)
+        del graph
+        return min(marks[i].elapsed_time(marks[i + 1]) for i in range(reps)) / len(launches)
+
     def _prefill_attention(self, index: int, T: int):
         """Causal attention of the prompt in fp32 (torch), positions 0..T-1."""
         cfg = self.cfg
@@ -372,7 +407,6 @@ class Qwen3Runner(_GreedyRunner):
         cfg, M = self.cfg, (self.B * self.T if prompt else self.B)
         layers = list(self.model.model.layers)
         widths = {"H": cfg.hidden, "A": cfg.heads * cfg.head_dim, "I": cfg.intermediate}
-        dev = self.dev
         res = {}
         for which, names, out_name, kin in self.LINEARS:
             K_in = widths[kin]
@@ -392,29 +426,7 @@ class Qwen3Runner(_GreedyRunner):
                                   layer.get_submodule(n).weight_scale_inv.numel() * 4
                                   for n in names))
             aq, as_ = self.aq[K_in], self.as_[K_in]
-            for p in plans:  # warm-up round
-                p(aq, as_, M)
-            torch.cuda.synchronize(dev)
-            # one graph of the launches, so host launch time cannot starve
-            # the GPU between these short kernels (a decode step replays a
-            # graph too)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for p in plans:
-                    p(aq, as_, M)
-            graph.replay()
-            best = None
-            stream = torch.cuda.current_stream(dev)
-            for _ in range(reps):
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                torch.cuda.synchronize(dev)
-                a.record(stream)
-                graph.replay()
-                b.record(stream)
-                torch.cuda.synchronize(dev)
-                ms = a.elapsed_time(b) / len(plans)
-                best = ms if best is None else min(best, ms)
-            del graph
+            best = self._time_launches([lambda p=p: p(aq, as_, M) for p in plans], reps)
             n_out = sum(layers[0].get_submodule(n).weight.shape[0] if tiles is None else tiles[n].n
                         for n in names)
             res[which] = {"us": round(best * 1e3, 2), "bytes": int(nbytes),

@@ -362,6 +362,67 @@ class Qwen3MoeRunner(_GreedyRunner):
             down(self.hq, self.hs, r, gather=False, M=m)
             K.moe_combine(self.down, r, m, self.y[c0:c0 + m])
 
+    def time_linears(self, reps: int = 3) -> dict:
+        """Decode-step (M = batch) time of each linear of a layer, on the
+        inputs and the routing in the runner's buffers (those of the last
+        decode step's last layer, or set by the caller: aqH/asH, aqA/asA,
+        hq/hs and ``route``): the linear of every layer launched back to
+        back (one HIP graph replayed between one event pair), the best of
+        ``reps`` rounds divided by the layer count.
+        The grouped expert linears of every layer run the same routing, so
+        each reads the weights of the experts that step picked (~88 of 128
+        at 16 tokens, ~0.4 GB per layer: the 48 layers stream from HBM as in
+        a decode step).  Returns {linear: {"us", "bytes" (weights and scales
+        read per layer), "flops"}} for qkv, o, gate_up and down.  FP8
+        resident or re-tiled blocks only: blocks decoded by their hooks
+        share one buffer."""
+        cfg, M, r = self.cfg, self.B, self.route
+        layers = list(self.model.model.layers)
+        n_active = int(r.n_active.item())
+        if n_active <= 0:
+            raise ECF8Error("time_linears needs a routed decode step first")
+        Hq, D, I = cfg.heads, cfg.head_dim, cfg.moe_intermediate
+
+        def weight_bytes(mod, names):
+            tiles = getattr(mod, "_ecf8_tiles", None)
+            if tiles is not None:
+                return sum(tiles[n].nbytes() + tiles[n].weight_scale.numel() * 4 for n in names)
+            return sum(mod.get_submodule(n).weight.numel() +
+                       mod.get_submodule(n).weight_scale_inv.numel() * 4 for n in names)
+
+        res = {}
+        for which, names, out, aq, as_, k_in in (
+                ("qkv", ("q_proj", "k_proj", "v_proj"), self.qkv, self.aqH, self.asH, cfg.hidden),
+                ("o", ("o_proj",), self.o, self.aqA, self.asA, Hq * D)):
+            calls = []
+            for i, layer in enumerate(layers):
+                a = layer.self_attn
+                if getattr(a, "_ecf8_tiles", None) is None and hasattr(a, "encoded"):
+                    raise ECF8Error("blocks decoded by their hooks share one buffer")
+                p = self._attn_linear(a, i, which, names, out, M)
+                calls.append(lambda p=p: p(aq, as_, M))
+            n_out = sum(layers[0].self_attn.get_submodule(n).out_features for n in names)
+            res[which] = {"us": round(self._time_launches(calls, reps) * 1e3, 2),
+                          "bytes": int(weight_bytes(layers[0].self_attn, names)),
+                          "flops": 2 * M * n_out * k_in}
+        gu_calls, down_calls = [], []
+        for i in range(len(layers)):
+            ex = self.experts[i]
+            if ex.compressed and not ex.tiled:
+                raise ECF8Error("experts decoded per step share one buffer")
+            gu, down = (ex.tiled_gu, ex.tiled_down) if ex.tiled else (ex.gu, ex.down)
+            gu_calls.append(lambda gu=gu: gu(self.aqH[:K.pad16(M)], self.asH[:M], r, gather=True,
+                                             M=M))
+            down_calls.append(lambda down=down: down(self.hq, self.hs, r, gather=False, M=M))
+        ex0 = layers[0].mlp.experts[0]
+        pairs = M * cfg.top_k
+        for which, calls, names, flops in (
+                ("gate_up", gu_calls, ("gate_proj", "up_proj"), 2 * pairs * 2 * I * cfg.hidden),
+                ("down", down_calls, ("down_proj",), 2 * pairs * cfg.hidden * I)):
+            res[which] = {"us": round(self._time_launches(calls, reps) * 1e3, 2),
+                          "bytes": int(n_active * weight_bytes(ex0, names)), "flops": flops}
+        return res
+
     def layer(self, layer: MoeDecoderLayer, index: int, x_prev, prefill: bool):
         cfg = self.cfg
         M = self.B * (self.T if prefill else 1)

@@ -22,8 +22,12 @@
  *   seg_off  u32[S+1] segment byte offsets; seg_off[S] = end of the codes
  *   gaps     u32[8 S] bit offset of the first code in each 12-byte chunk
  *                     (4 bits per chunk, chunk c in bits 4(c%8) of word c/8)
- *   other    u8[1024 S] sign/mantissa nibbles in symbol order, even
- *                     symbol high (the reference's packed_other_4bits rule)
+ *   other    u8[1024 S] signs and mantissas, 4 bytes per run of 8
+ *                     symbols: byte q of a run holds element q's mantissa
+ *                     in bits 0..2 and sign in bit 7, element q + 4's
+ *                     mantissa in bits 4..6, and in bit 3 the sign of
+ *                     element ((q + 3) % 4) + 4 (FP8 bit positions, the
+ *                     high elements' a 4-bit rotation of the dword away)
  * A segment holds at most 64 chunks (768 bytes).
  */
 #ifndef ECF8_TILE_H

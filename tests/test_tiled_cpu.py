@@ -34,6 +34,27 @@ def _element(p, kg, i):
     return p * ROWS + r, col
 
 
+def _rotl32(x, n):
+    return ((x << n) | (x >> (32 - n))) & 0xFFFFFFFF
+
+
+def _run_dword(fp8):
+    """The nibble-plane dword of one run of 8 symbols from its operand
+    elements' FP8 bytes (fp8[m], m = 0..7): elements 0..3's sign and
+    mantissa bits (mask 0x87 of each byte) where their bytes have them, OR
+    elements 4..7's rotated left by 4 bits."""
+    lo = sum((fp8[q] & 0x87) << (8 * q) for q in range(4))
+    hi = sum((fp8[q + 4] & 0x87) << (8 * q) for q in range(4))
+    return lo | _rotl32(hi, 4)
+
+
+def _sign_mantissa(run_dword, m):
+    """Bits 0x87 of operand element m's FP8 byte, read back from its run's
+    dword (elements 4..7 after a 4-bit right rotation)."""
+    d = run_dword if m < 4 else _rotl32(run_dword, 28)
+    return (d >> (8 * (m % 4))) & 0x87
+
+
 def _py_encode(w: np.ndarray, table: dict):
     """Independent restatement of the layout, symbol by symbol."""
     n, k = w.shape
@@ -44,14 +65,17 @@ def _py_encode(w: np.ndarray, table: dict):
             seg_off.append(len(stream))
             bits, starts = "", []
             seg_other = bytearray(1024)
+            run = [0] * 8
             for i in range(2048):
                 r, c = _element(p, kg, i)
                 b = int(w[r, c])
-                e, o = (b >> 3) & 15, ((b >> 4) & 8) | (b & 7)
+                e = (b >> 3) & 15
                 starts.append(len(bits))
                 nb, val = table[e]
                 bits += format(val, f"0{nb}b")
-                seg_other[i // 2] |= (o << 4) if i % 2 == 0 else o
+                run[_RUN[i % 8]] = b
+                if i % 8 == 7:
+                    seg_other[i // 2 - 3:i // 2 + 1] = _run_dword(run).to_bytes(4, "little")
             nbytes = (len(bits) + 7) // 8
             bits += "0" * (8 * nbytes - len(bits))
             seg = bytes(int(bits[8 * t:8 * t + 8], 2) for t in range(nbytes))
@@ -163,10 +187,10 @@ def _check_segments(w, compressed):
             w16 = (w16 >> (8 - (pos & 7))) & 0xFFFF
             sym, ln = oc.lut_decode_one(luts, w16)
             starts.append(pos)
-            o_byte = int(other[s * 1024 + i // 2])
-            o = (o_byte >> 4) if i % 2 == 0 else (o_byte & 15)
+            at = s * 1024 + (i // 8) * 4
+            d = int.from_bytes(other[at:at + 4].tobytes(), "little")
             r, c = _element(p, kg, i)
-            assert ((o & 8) << 4 | sym << 3 | (o & 7)) == wb[r, c], (s, i)
+            assert (_sign_mantissa(d, _RUN[i % 8]) | sym << 3) == wb[r, c], (s, i)
             pos += ln
         for c in range(n_chunks):
             g = (int(gaps[s * 8 + c // 8]) >> (4 * (c % 8))) & 15
