@@ -296,11 +296,19 @@ __device__ __forceinline__ void panel_of(const TileSegs &segs, int panel, TileOp
   p = (n0 - start) / 16;
 }
 
-// The panels of a dense linear's workgroup walk: its fused operands.
+// The panels of a dense linear's workgroup walk: its fused operands, as one
+// run of panels (a wave's steps may cross from one operand to the next).
 struct DenseWalk {
   const TileSegs *segs;  // the kernel argument itself: indexed in place, never copied
   __device__ __forceinline__ void at(int panel, TileOperand &op, int &p, int &col) const {
     panel_of(*segs, panel, op, p, col);
+  }
+  // output column of panel `panel`
+  __device__ __forceinline__ int out_col(int panel) const {
+    TileOperand op;
+    int p, col;
+    panel_of(*segs, panel, op, p, col);
+    return col + p * 16;
   }
 };
 
@@ -318,39 +326,24 @@ __device__ __forceinline__ const T *uniform(const T *p) {
   return (const T *)(GlobalT *)(((uint64_t)hi << 32) | lo);
 }
 
-// The panels of one expert of a grouped linear: its n_segs (<= 3) operands
-// of seg_n columns each (e.g. gate, up), operand k at output column
-// k seg_n.  The operands are read once, into scalar registers.
+// The panels of one operand of one expert of a grouped linear (e.g. its
+// gate or its up projection, seg_n columns at output column k seg_n): a
+// wave's steps never leave its operand, whose addresses are read once into
+// scalar registers.
 struct ExpertWalk {
-  TileOperand op[ECF8_LINEAR_MAX_SEGS];
-  int tiles_per_seg, seg_n, n_segs;
-  __device__ __forceinline__ void load(const ecf8_tile_operand *ops, int n, int sn) {
-    static_assert(ECF8_LINEAR_MAX_SEGS == 3, "three operands per expert");
-    n_segs = n;
-    seg_n = sn;
-    tiles_per_seg = sn / 16;
-#pragma unroll
-    for (int k = 0; k < ECF8_LINEAR_MAX_SEGS; ++k) {
-      const ecf8_tile_operand &t = ops[k < n ? k : 0];
-      op[k] = TileOperand{uniform(static_cast<const uint8_t *>(t.stream)), uniform(t.seg_off),
-                          uniform(t.gaps), uniform(static_cast<const uint8_t *>(t.other)),
-                          uniform(t.weight_scale)};
-    }
-  }
-  template <class T>
-  static __device__ __forceinline__ T pick(bool c, T x, T y) {  // by value: a select, not an address
-    return c ? x : y;
-  }
-  __device__ __forceinline__ void at(int panel, TileOperand &o, int &p, int &col) const {
-    const bool k1 = panel >= tiles_per_seg, k2 = n_segs > 2 && panel >= 2 * tiles_per_seg;
-    o.stream = pick(k2, op[2].stream, pick(k1, op[1].stream, op[0].stream));
-    o.seg_off = pick(k2, op[2].seg_off, pick(k1, op[1].seg_off, op[0].seg_off));
-    o.gaps = pick(k2, op[2].gaps, pick(k1, op[1].gaps, op[0].gaps));
-    o.other = pick(k2, op[2].other, pick(k1, op[1].other, op[0].other));
-    o.ws = pick(k2, op[2].ws, pick(k1, op[1].ws, op[0].ws));
-    const int k = (k1 ? 1 : 0) + (k2 ? 1 : 0);
-    p = panel - k * tiles_per_seg;
+  TileOperand op;
+  int col;
+  __device__ __forceinline__ void load(const ecf8_tile_operand *ops, int k, int seg_n) {
+    const ecf8_tile_operand &t = ops[k];
+    op = TileOperand{uniform(static_cast<const uint8_t *>(t.stream)), uniform(t.seg_off),
+                     uniform(t.gaps), uniform(static_cast<const uint8_t *>(t.other)),
+                     uniform(t.weight_scale)};
     col = k * seg_n;
+  }
+  __device__ __forceinline__ void at(int panel, TileOperand &o, int &p, int &c) const {
+    o = op;
+    p = panel;
+    c = col;
   }
 };
 
@@ -591,8 +584,14 @@ void tile_linear16_kernel(
   const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = hw / HWW, hwave = hw % HWW;
   const int K = a.K, kgroups = K / kGroup;
-  // the workgroup's rows, operands and table (uniform)
-  int M, row0 = 0, n_panels;
+  // The groups of the grid (vgrid of them) are dealt to the operand lanes
+  // in equal runs: a grouped linear's operands (e.g. gate, up) one lane
+  // each, the host making vgrid a multiple of their count; a dense
+  // linear's fused operands one lane.  Group vw takes panels j, j + gpo,
+  // ... (j = vw % gpo) of lane vw / gpo, whose tps panels it shares with
+  // the lane's other gpo groups.
+  const int vgrid = (int)gridDim.x * G, vwg0 = (int)blockIdx.x * G, vwg = vwg0 + group;
+  int M, row0 = 0, tps, gpo;
   const uint32_t *table;
   Walk walk;
   if constexpr (kMoe) {
@@ -603,18 +602,49 @@ void tile_linear16_kernel(
     // an expert holds at most one pair per routed token: <= 16 rows
     M = min(uniform(a.offsets[e + 1]) - row0, 16);
     table = uniform(a.tables[e]);
-    walk.load(a.ops + (size_t)e * a.n_segs, a.n_segs, a.seg_n);
-    n_panels = a.n_segs * (a.seg_n / 16);
+    gpo = vgrid / a.n_segs;
+    tps = a.seg_n / 16;
+    walk.load(a.ops + (size_t)e * a.n_segs, uniform(vwg / gpo), a.seg_n);  // this wave's lane
   } else {
     M = a.M;
     table = a.table;
     walk = DenseWalk{&a.segs};
-    n_panels = a.n_panels;
+    gpo = vgrid;
+    tps = a.n_panels;
   }
-  // this group's panels: vwg, vwg + vgrid, ...
-  const int vwg = (int)blockIdx.x * G + group, vgrid = (int)gridDim.x * G;
-  const int vwg0 = (int)blockIdx.x * G;  // the workgroup's first group: the most panels
-  if (M <= 0 || vwg0 >= n_panels) return;  // uniform, before any barrier
+  // group vwg0 + gg's lane and first lane panel, from the workgroup's first
+  // group's (one division, in scalars; a dense linear has one lane, gpo =
+  // vgrid > every group)
+  const int first0 = kMoe ? uniform(vwg0 % gpo) : vwg0, lane0 = kMoe ? uniform(vwg0 / gpo) : 0;
+  auto group_start = [&](int gg, int &lane_no) {
+    int j = first0 + gg;
+    lane_no = lane0;
+    if constexpr (kMoe) {
+      while (j >= gpo) {  // at most G times
+        j -= gpo;
+        ++lane_no;
+      }
+    }
+    return j;
+  };
+  // the workgroup's groups walk in lockstep, as many steps as the one with
+  // the most panels
+  int most = 0;
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg) {
+    int ln;
+    const int j = group_start(gg, ln);
+    if (j < tps) most = max(most, (tps - 1 - j) / gpo + 1);
+  }
+  if (M <= 0 || most == 0) return;  // uniform, before any barrier
+  // output column of the o-th panel of group gg, -1 past its last
+  auto panel_col = [&](int gg, int o) {
+    int ln;
+    const int j = group_start(gg, ln) + o * gpo;
+    if (j >= tps) return -1;
+    if constexpr (kMoe) return ln * a.seg_n + j * 16;
+    else return walk.out_col(j);
+  };
   uint32_t *const stage = s_stage[hw];
   const float *const as = a.as;
 
@@ -661,7 +691,7 @@ void tile_linear16_kernel(
       pvc[q] = pu[q] == n_v - 1;
     }
   }
-  const int n_real = ((n_panels - 1 - vwg0) / vgrid + 1) * spw;  // the first group's steps
+  const int n_real = most * spw;
   // a multiple of NB passes of S steps (trailing ones past the last panel
   // compute nothing), so the unrolled loop's back edge always follows its
   // last copy
@@ -669,20 +699,21 @@ void tile_linear16_kernel(
 
   // passes t .. t+MD (S steps each): sc[0..S-1] is the pass being computed
   Step sc[(MD + 1) * S];
-  int pan = vwg, q = 0;  // cursor of the step after the last in sc
+  int lane_no;
+  int pan = group_start(group, lane_no), q = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
     const bool last = q == spw - 1;
     Step st;
     if constexpr (kPacked) {
       const bool q1 = q > 0;  // spw <= 2
-      st = step_at(walk, pan, q1 ? pv[1] : pv[0], q1 ? pu[1] : pu[0], WAVES, kgroups, n_panels,
+      st = step_at(walk, pan, q1 ? pv[1] : pv[0], q1 ? pu[1] : pu[0], WAVES, kgroups, tps,
                    q1 ? pvc[1] : pvc[0], last);
     } else {
-      st = step_at(walk, pan, hwave, q, WAVES, kgroups, n_panels, last, last);
+      st = step_at(walk, pan, hwave, q, WAVES, kgroups, tps, last, last);
     }
     if (++q == spw) {
       q = 0;
-      pan += vgrid;
+      pan += gpo;
     }
     return st;
   };
@@ -728,12 +759,11 @@ void tile_linear16_kernel(
     // on the device): every output this group owns becomes a bf16 NaN
     // instead of a product of misread weights.  Uniform, after the last
     // barrier the workgroup passes.
-    for (int pnl = vwg; pnl < n_panels; pnl += vgrid) {
-      TileOperand op;
-      int p, col;
-      walk.at(pnl, op, p, col);
+    for (int o = 0;; ++o) {
+      const int c = panel_col(group, o);
+      if (c < 0) break;
       for (int i = hwave * 64 + lane; i < 16 * M; i += HWW * 64)
-        a.out[(size_t)(row0 + (i >> 4)) * a.ldo + col + p * 16 + (i & 15)] = kBf16Nan;
+        a.out[(size_t)(row0 + (i >> 4)) * a.ldo + c + (i & 15)] = kBf16Nan;
     }
     return;
   }
@@ -755,17 +785,13 @@ void tile_linear16_kernel(
       const int jw = hw + k * HW;
       if (jw >= G * per_group) break;
       const int gg = jw / per_group, j = (jw % per_group) >> 2, i = jw & 3, l = lane;
-      const int panel = vwg0 + gg + (first_pending + j) * vgrid;
-      if (panel >= n_panels) continue;  // a group out of panels
+      const int c = panel_col(gg, first_pending + j);
+      if (c < 0) continue;  // a group out of panels
       float sum = 0.f;
 #pragma unroll
       for (int wv = 0; wv < WAVES; ++wv) sum += s_part[j][gg][wv][i * 64 + l];
-      TileOperand op;
-      int p, col;
-      walk.at(panel, op, p, col);
       const int mm = 4 * (l >> 4) + i;
-      if (mm < M)
-        a.out[(size_t)(row0 + mm) * a.ldo + col + p * 16 + (l & 15)] = (uint16_t)f32_bf16(sum);
+      if (mm < M) a.out[(size_t)(row0 + mm) * a.ldo + c + (l & 15)] = (uint16_t)f32_bf16(sum);
     }
     lds_barrier();
     first_pending += pending;
@@ -1072,7 +1098,7 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
                          (int)seg_n};
   const int64_t n_tiles = n_segs * seg_n / 16;
   // the FP8 grouped linear's wave count for this K (it sums in that order)
-  const bool eight = K / kGroup > 8;
+  const bool eight = K / kGroup > ECF8_MOE_FOUR_WAVE_GROUPS;
   // groups: G FP8 workgroups per workgroup (splits counts FP8 workgroups)
   auto launch = [&](auto kernel, int threads, int groups) {
     int64_t g = splits;
@@ -1083,7 +1109,9 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
       g = (slots * groups * 10 + 7 * n_experts - 1) / (7 * n_experts);
     }
     g = g < 1 ? 1 : g > n_tiles ? n_tiles : g;
-    const int64_t wgs = (g + groups - 1) / groups;
+    int64_t wgs = (g + groups - 1) / groups;
+    // the kernel deals the groups to the operands in equal runs
+    while ((wgs * groups) % n_segs) ++wgs;
     kernel<<<dim3((unsigned)wgs, (unsigned)n_experts), threads, 0, as_stream(stream)>>>(args);
     return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
   };
@@ -1094,6 +1122,11 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
   if (ECF8_TILE_MOE_PACK && packs(4, 3, (int)(K / kGroup)))
     return launch(tile_linear16_kernel<4, 3, kMoe4PGroups, kMoeRed, true>, 192 * kMoe4PGroups,
                   kMoe4PGroups);
+  // four FP8 waves of three or four steps (e.g. K = 2048): sixteen waves per
+  // workgroup (73 KB of LDS, two per CU).  On MI355X, Qwen3-30B-A3B expert
+  // gate/up at 16 tokens: 58.5 us per layer against 58.9 at eight FP8 waves
+  if (K / kGroup > 8)
+    return launch(tile_linear16_kernel<4, 4, 4, kMoeRed, true>, 1024, 4);
   return launch(tile_linear16_kernel<4, 4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
                 kMoe4Groups);
 }

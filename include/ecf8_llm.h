@@ -184,7 +184,11 @@ int ecf8_moe_group(const int *topk_idx, const float *topk_w, int64_t M, int top_
  * weights / weight_scales are device arrays of n_experts * n_segs
  * addresses (e4m3fn [seg_n, K] in weight_layout, and fp32 [seg_n/128,
  * K/128]); active entries must be < n_experts.  The grid covers every
- * expert and idle slots exit, so the launch can be captured in a graph. */
+ * expert and idle slots exit, so the launch can be captured in a graph.
+ * Each output sums its K groups over four waves when K/128 <=
+ * ECF8_MOE_FOUR_WAVE_GROUPS, else over eight (wave w takes groups w,
+ * w + waves, ...), then the waves in order. */
+#define ECF8_MOE_FOUR_WAVE_GROUPS 16
 int ecf8_moe_linear(const void *aq, const float *as, const int *row_of, const int *offsets,
                     const int *active, const int *n_active, int n_experts,
                     const void *const *weights, const float *const *weight_scales, int n_segs,

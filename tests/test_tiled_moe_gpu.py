@@ -6,9 +6,10 @@ compressed as its own block and re-tiled under its own code:
 * ecf8_tile_decode_batch writes every expert's original FP8 bytes;
 * ecf8_tile_moe_linear -- routed experts decoding their weight operands on
   the fly -- is bit-identical to ecf8_moe_linear over the decoded experts,
-  for gate/up (token rows gathered, 8 waves) and down (one row per sorted
-  pair, 4 waves: packed on three hardware waves at K = 768, unpacked at
-  K = 1024), 1, 5 and 16 routed tokens, any workgroup split;
+  for gate/up (token rows gathered, 4 waves of 4 groups) and down (one row
+  per sorted pair, 4 waves: packed on three hardware waves at K = 768,
+  unpacked at K = 1024), 1, 5 and 16 routed tokens, any workgroup split;
+  eight waves at K = 4096, with three operands per expert;
 * a re-tiled small MoE model generates the FP8 model's tokens and logits,
   eager and graph-replayed;
 * it refuses what it cannot run.
@@ -173,6 +174,59 @@ def test_unpacked_four_wave_down_projection_is_bit_identical(wide_experts, cuda_
     rows = M * top_k
     assert torch.equal(got[:rows], ref[:rows])
     assert bool((got[rows:] == 7.0).all()) and bool((got[:, H:] == 7.0).all())
+    assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
+
+
+@pytest.fixture(scope="module")
+def deep_experts(cuda_device):
+    """Six experts of three [256, 4096] operands each: K = 4096 gives the
+    FP8 grouped linear eight waves, and three operands deal the workgroups
+    to three runs."""
+    from dfloat.compress import compress_flat
+    from ecf8_amd.decode import build_table
+    from ecf8_amd.synth import flat_block, synthetic_block
+    from ecf8_amd.tiled import TiledOperand, code_from_luts, tile_encode
+
+    names = ("a_proj", "b_proj", "c_proj")
+    dense, ops, tables = [], [], []
+    for e in range(6):
+        w = synthetic_block({n: (256, 4096, 0.02) for n in names}, seed=800 + e)
+        res = compress_flat(flat_block(w)[0])
+        tables.append(build_table(res["luts"].contiguous().to(cuda_device)))
+        bits, vals = code_from_luts(res["luts"])
+        ops.append([TiledOperand(tile_encode(w[n][0], bits, vals), w[n][1], 256, 4096,
+                                 cuda_device) for n in names])
+        dense.append([(w[n][0].to(cuda_device), w[n][1].to(cuda_device)) for n in names])
+    return dense, ops, tables
+
+
+@pytest.mark.parametrize("splits", [0, 1, 4])
+@pytest.mark.parametrize("M", [1, 16])
+def test_eight_wave_three_operand_grouped_linear_is_bit_identical(deep_experts, cuda_device, M,
+                                                                 splits):
+    from ecf8_amd import llm_kernels as K
+    from ecf8_amd.llm_kernels import MoeLinearPlan
+    from ecf8_amd.tiled import TileMoePlan
+
+    dense, ops, tables = deep_experts
+    n_exp, top_k, N = len(ops), 2, 3 * 256
+    g = torch.Generator().manual_seed(120 + M)
+    r = K.MoeRouting(16, top_k, n_exp, cuda_device)
+    r.topk_idx[:M] = torch.stack([torch.randperm(n_exp, generator=g)[:top_k]
+                                  for _ in range(M)]).to(torch.int32).to(cuda_device)
+    r.topk_w[:M] = torch.rand(M, top_k, generator=g).to(cuda_device)
+    K.moe_group(r, M)
+    aq, as_ = _acts(16, 4096, 60 + M, cuda_device)
+    P = 16 * top_k
+    ref = torch.full((P, N + 8), 7.0, dtype=torch.bfloat16, device=cuda_device)
+    got = ref.clone()
+    MoeLinearPlan(dense, ref)(aq, as_, r, True, M=M)
+    _say(f"[tiled-moe] eight-wave three-operand K=4096 M={M} splits={splits}")
+    TileMoePlan(ops, tables, got, splits=splits)(aq, as_, r, True, M=M)
+    torch.cuda.synchronize()
+    rows = M * top_k
+    assert torch.equal(got[:rows], ref[:rows])
+    assert bool((got[rows:] == 7.0).all()) and bool((got[:, N:] == 7.0).all())
     assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
 
 
