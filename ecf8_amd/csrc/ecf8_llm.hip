@@ -437,6 +437,7 @@ template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void fp8_linear16_kernel(
     const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, int K, LinearSegs segs,
     uint16_t *__restrict__ out, int ldo) {
+  static_assert(WAVES >= 4, "the final sums take one thread each of the first 256");
   __shared__ float red[WAVES][4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -538,6 +539,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_linear16p_kernel(
     const uint8_t *__restrict__ aq, const float *__restrict__ as, int M, LinearSegs segs,
     uint16_t *__restrict__ out, int ldo, int n_tiles) {
   constexpr int K = 4096, kgroups = K / kGroup, kU = kgroups / WAVES;
+  static_assert(WAVES >= 4, "the final sums take one thread each of the first 256");
   __shared__ float red[WAVES][4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1398,8 +1400,9 @@ __global__ __launch_bounds__(WAVES * 64) void moe_linear16_kernel(MoeLinear a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
     __syncthreads();
-    if (threadIdx.x < 256) {
-      const int i = threadIdx.x >> 6, l = threadIdx.x & 63;
+    // the 256 sums (4 accumulators x 64 lanes), over the threads
+    for (int t = threadIdx.x; t < 256; t += WAVES * 64) {
+      const int i = t >> 6, l = t & 63;
       float sum = 0.f;
 #pragma unroll
       for (int wv2 = 0; wv2 < WAVES; ++wv2) sum += red[wv2][i][l];
@@ -1713,12 +1716,15 @@ extern "C" int ecf8_moe_linear(const void *aq, const float *as, const int *row_o
               n_segs, (int)seg_n, (int)K, (int)ldo, weight_layout == ECF8_WEIGHT_TILES};
   const dim3 grid((unsigned)(n_segs * seg_n / 16), (unsigned)n_experts);
   // each wave's share of the K groups in one batch of loads where it fits.
-  // Four waves up to 16 groups: on MI355X, Qwen3-30B-A3B expert gate/up (K =
-  // 2048) at 16 tokens, 48.5 us per layer against 53.4 with eight waves of
-  // two groups (48 layers back to back)
+  // On MI355X, Qwen3-30B-A3B experts at 16 tokens (48 layers back to back):
+  // gate/up (K = 2048) 48.5 us per layer at four waves of four groups
+  // against 53.4 at eight of two; down (K = 768) 23.7 us at three waves of
+  // two groups against 26.9 at four (two, two, one, one)
   const int64_t kg = K / kGroup;
   static_assert(ECF8_MOE_FOUR_WAVE_GROUPS == 16, "four waves of at most four groups");
-  if (kg <= 8)
+  if (kg == 6)
+    moe_linear16_kernel<3, 2><<<grid, 192, 0, as_stream(stream)>>>(a);
+  else if (kg <= 8)
     moe_linear16_kernel<4, 2><<<grid, 256, 0, as_stream(stream)>>>(a);
   else if (kg <= ECF8_MOE_FOUR_WAVE_GROUPS)
     moe_linear16_kernel<4, 4><<<grid, 256, 0, as_stream(stream)>>>(a);

@@ -432,21 +432,9 @@ __device__ __forceinline__ uint32_t step_meta(const Step &st, int kgroups, int l
 #ifndef ECF8_TILE_MOE4_GROUPS
 #define ECF8_TILE_MOE4_GROUPS 2
 #endif
-// Packed four-wave shape (three hardware waves per FP8 workgroup): G = 4,
-// twelve waves -- a multiple of the CU's four SIMDs.  On MI355X,
-// Qwen3-30B-A3B down projection at 16 tokens: 49.1 us packed at G = 4
-// against 52.9 unpacked; 71.4 at G = 2 and 74.9 at G = 3 (six and nine
-// waves per workgroup load the SIMDs unevenly).
-// ECF8_TILE_MOE_PACK 0 runs K = 768 unpacked instead (four hardware waves
-// per FP8 workgroup): at G = 4, sixteen waves and eight per SIMD, the same
-// down projection took 48.6-53.8 us against 43.9-44.8 packed.
-#ifndef ECF8_TILE_MOE_PACK
-#define ECF8_TILE_MOE_PACK 1
-#endif
-#ifndef ECF8_TILE_MOE4P_GROUPS
-#define ECF8_TILE_MOE4P_GROUPS 4
-#endif
-constexpr int kDense16Red = ECF8_TILE_DENSE16_RED, kMoe4PGroups = ECF8_TILE_MOE4P_GROUPS;
+// Three-wave shape (K = 768: the FP8 grouped linear's three waves of two
+// groups each): G = 4, twelve waves -- a multiple of the CU's four SIMDs.
+constexpr int kDense16Red = ECF8_TILE_DENSE16_RED;
 constexpr int kDense8Red = ECF8_TILE_DENSE8_RED, kMoeRed = ECF8_TILE_MOE_RED;
 constexpr int kMoe8Groups = ECF8_TILE_MOE8_GROUPS, kMoe4Groups = ECF8_TILE_MOE4_GROUPS;
 constexpr int kDense8Groups = ECF8_TILE_DENSE8_GROUPS, kMoe8Red = ECF8_TILE_MOE8_RED;
@@ -502,22 +490,16 @@ constexpr bool kOthNow = ECF8_TILE_OTH_NOW;
 // out[m, col + n] = sum_g (sum_{k in g} aq[m,k] * W[n,k]) * as[m,g] * ws[n/128, g]
 // for M <= 16, persistent over the 16-column panels.
 //
-// A workgroup runs G groups of HWW hardware waves; group g is the FP8
+// A workgroup runs G groups of WAVES waves; group g is the FP8
 // linear's workgroup number blockIdx.x * G + g of a grid G times larger: it
 // takes those panels and sums each in the order of that workgroup's WAVES
 // waves, so the result does not depend on G (more waves per CU for shapes
 // whose FP8 workgroup is small).  The groups walk in lockstep (a group out
 // of panels walks empty steps), so every wave reaches the same barriers.
 //
-// HWW = WAVES: hardware wave w is the FP8 linear's wave w (groups w,
+// Hardware wave w of a group is the FP8 linear's wave w (groups w,
 // w + WAVES, ...; when WAVES does not divide the groups, the last step of
-// some waves is empty).  HWW < WAVES (packed): the FP8 waves' steps, wave
-// by wave, are dealt to the hardware waves in equal runs that never split
-// a wave's steps (the host checks), so a hardware wave may run several FP8
-// waves one after the other, each from a zero sum, parking each one's
-// partial sums in its own slot: the same products, sums and reduction --
-// e.g. K = 768, six groups over four FP8 waves (two, two, one, one) -- run
-// on three hardware waves of two steps each with no empty step.
+// some waves is empty).
 //
 // Each wave walks its steps (segments) as a software pipeline: while it
 // decodes step t, the code windows and nibbles of steps t+1..t+P (P =
@@ -562,8 +544,8 @@ struct TileMoeArgs {
 #ifndef ECF8_TILE_WPE
 #define ECF8_TILE_WPE 8
 #endif
-template <int WAVES, int HWW, int G, int RED, bool kMoe>
-__global__ __launch_bounds__(HWW * G * 64) __attribute__((amdgpu_waves_per_eu(ECF8_TILE_WPE)))
+template <int WAVES, int G, int RED, bool kMoe>
+__global__ __launch_bounds__(WAVES * G * 64) __attribute__((amdgpu_waves_per_eu(ECF8_TILE_WPE)))
 void tile_linear16_kernel(
     typename std::conditional<kMoe, TileMoeArgs, TileDenseArgs>::type a) {
   // P: passes ahead a window is loaded; MD: passes ahead its offsets are
@@ -573,9 +555,7 @@ void tile_linear16_kernel(
   // copies of the unrolled loop
   constexpr int P = kPrefetch, MD = kPrefetch + 1 > kMetaAhead ? kPrefetch + 1 : kMetaAhead;
   constexpr bool kLate = P == 0 && kLateWindow;
-  constexpr int NB = kLate ? 2 : MD, HW = HWW * G, S = kPair;
-  constexpr bool kPacked = HWW != WAVES;
-  static_assert(HWW <= WAVES, "at most one hardware wave per FP8 wave");
+  constexpr int HWW = WAVES, NB = kLate ? 2 : MD, HW = HWW * G, S = kPair;
   using Walk = typename std::conditional<kMoe, ExpertWalk, DenseWalk>::type;
   __shared__ uint32_t s_dfa[kDfaEntries + 1];  // + the table's kind word
   __shared__ __attribute__((aligned(16))) uint32_t s_stage[HW][S * kWaveStageDw];
@@ -668,29 +648,7 @@ void tile_linear16_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) srow[i] = 4u * a_row(4 * g + i) * (uint32_t)kgroups;
   const int ng = (kgroups + WAVES - 1) / WAVES;
-  // steps per panel of each hardware wave, and (packed) step q's FP8 wave
-  // and its step in that wave: position hwave * spw + q of the FP8 waves'
-  // steps listed wave by wave (the first `full` waves have ng steps, the
-  // others ng - 1)
-  const int spw = kPacked ? kgroups / HWW : ng;
-  constexpr int kMaxSpw = kPacked ? 2 : 1;
-  int pv[kMaxSpw], pu[kMaxSpw];
-  bool pvc[kMaxSpw];
-  if constexpr (kPacked) {
-    const int full = kgroups % WAVES ? kgroups % WAVES : WAVES;
-#pragma unroll
-    for (int q = 0; q < kMaxSpw; ++q) {
-      const int sp = hwave * spw + q;
-      const bool long_wave = sp < full * ng;
-      const int n_v = long_wave ? ng : ng - 1;
-      const int base = long_wave ? 0 : full * ng;
-      const int v0 = long_wave ? 0 : full;
-      const int d = n_v > 0 ? n_v : 1;
-      pv[q] = v0 + (sp - base) / d;
-      pu[q] = (sp - base) % d;
-      pvc[q] = pu[q] == n_v - 1;
-    }
-  }
+  const int spw = ng;  // steps per panel of each wave
   const int n_real = most * spw;
   // a multiple of NB passes of S steps (trailing ones past the last panel
   // compute nothing), so the unrolled loop's back edge always follows its
@@ -703,14 +661,7 @@ void tile_linear16_kernel(
   int pan = group_start(group, lane_no), q = 0;  // cursor of the step after the last in sc
   auto next_step = [&]() {
     const bool last = q == spw - 1;
-    Step st;
-    if constexpr (kPacked) {
-      const bool q1 = q > 0;  // spw <= 2
-      st = step_at(walk, pan, q1 ? pv[1] : pv[0], q1 ? pu[1] : pu[0], WAVES, kgroups, tps,
-                   q1 ? pvc[1] : pvc[0], last);
-    } else {
-      st = step_at(walk, pan, hwave, q, WAVES, kgroups, tps, last, last);
-    }
+    const Step st = step_at(walk, pan, hwave, q, WAVES, kgroups, tps, last, last);
     if (++q == spw) {
       q = 0;
       pan += gpo;
@@ -1000,24 +951,6 @@ int resident_grid(Kernel kernel, int threads, int64_t work, int *grid) {
   return ECF8_OK;
 }
 
-// Whether the steps of `waves` FP8 waves over `kgroups` groups (wave v
-// takes groups v, v + waves, ...), listed wave by wave, deal to `hw`
-// hardware waves in equal runs of at most two steps that split no wave's
-// steps, every wave having at least one.
-bool packs(int waves, int hw, int kgroups) {
-  if (hw <= 0 || kgroups < waves || kgroups % hw || kgroups / hw > 2) return false;
-  const int spw = kgroups / hw, ng = (kgroups + waves - 1) / waves;
-  const int full = kgroups % waves ? kgroups % waves : waves;
-  int first = 0;  // position of wave v's first step
-  for (int v = 0; v < waves; ++v) {
-    const int n_v = v < full ? ng : ng - 1;
-    for (int b = first + 1; b < first + n_v; ++b)
-      if (b % spw == 0) return false;  // a run would start inside wave v's steps
-    first += n_v;
-  }
-  return true;
-}
-
 int check_operand(const ecf8_tile_operand &t) {
   if (!t.stream || !t.seg_off || !t.gaps || !t.other || !t.weight_scale) return ECF8_ERR_INVALID_ARG;
   if (!aligned(t.stream, 4) || !aligned(t.seg_off, 4) || !aligned(t.gaps, 4) ||
@@ -1061,16 +994,16 @@ extern "C" int ecf8_tile_linear(const void *aq, const float *as, int64_t M, int6
   const TileDenseArgs args{a, as, (int)M, (int)K, s, table, o, (int)ldo, n_panels};
   int grid = 0, rc;
   if (waves == 16) {
-    rc = resident_grid(tile_linear16_kernel<16, 16, 1, kDense16Red, false>, 1024, n_panels, &grid);
+    rc = resident_grid(tile_linear16_kernel<16, 1, kDense16Red, false>, 1024, n_panels, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<16, 16, 1, kDense16Red, false><<<(unsigned)grid, 1024, 0,
+    tile_linear16_kernel<16, 1, kDense16Red, false><<<(unsigned)grid, 1024, 0,
                                                           as_stream(stream)>>>(args);
   } else {
     constexpr int G = kDense8Groups;
-    rc = resident_grid(tile_linear16_kernel<8, 8, G, kDense8Red, false>, 512 * G,
+    rc = resident_grid(tile_linear16_kernel<8, G, kDense8Red, false>, 512 * G,
                        (n_panels + G - 1) / G, &grid);
     if (rc != ECF8_OK) return rc;
-    tile_linear16_kernel<8, 8, G, kDense8Red, false><<<(unsigned)grid, 512 * G, 0,
+    tile_linear16_kernel<8, G, kDense8Red, false><<<(unsigned)grid, 512 * G, 0,
                                                        as_stream(stream)>>>(args);
   }
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
@@ -1116,18 +1049,16 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
     return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
   };
   if (eight)
-    return launch(tile_linear16_kernel<8, 8, kMoe8Groups, kMoe8Red, true>, 512 * kMoe8Groups,
+    return launch(tile_linear16_kernel<8, kMoe8Groups, kMoe8Red, true>, 512 * kMoe8Groups,
                   kMoe8Groups);
-  // four FP8 waves whose steps pack onto three hardware waves (K = 768)
-  if (ECF8_TILE_MOE_PACK && packs(4, 3, (int)(K / kGroup)))
-    return launch(tile_linear16_kernel<4, 3, kMoe4PGroups, kMoeRed, true>, 192 * kMoe4PGroups,
-                  kMoe4PGroups);
+  // three FP8 waves of two steps (K = 768)
+  if (K / kGroup == 6) return launch(tile_linear16_kernel<3, 4, kMoeRed, true>, 768, 4);
   // four FP8 waves of three or four steps (e.g. K = 2048): sixteen waves per
   // workgroup (73 KB of LDS, two per CU).  On MI355X, Qwen3-30B-A3B expert
   // gate/up at 16 tokens: 58.5 us per layer against 58.9 at eight FP8 waves
   if (K / kGroup > 8)
-    return launch(tile_linear16_kernel<4, 4, 4, kMoeRed, true>, 1024, 4);
-  return launch(tile_linear16_kernel<4, 4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
+    return launch(tile_linear16_kernel<4, 4, kMoeRed, true>, 1024, 4);
+  return launch(tile_linear16_kernel<4, kMoe4Groups, kMoeRed, true>, 256 * kMoe4Groups,
                 kMoe4Groups);
 }
 

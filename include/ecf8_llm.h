@@ -185,8 +185,8 @@ int ecf8_moe_group(const int *topk_idx, const float *topk_w, int64_t M, int top_
  * addresses (e4m3fn [seg_n, K] in weight_layout, and fp32 [seg_n/128,
  * K/128]); active entries must be < n_experts.  The grid covers every
  * expert and idle slots exit, so the launch can be captured in a graph.
- * Each output sums its K groups over four waves when K/128 <=
- * ECF8_MOE_FOUR_WAVE_GROUPS, else over eight (wave w takes groups w,
+ * Each output sums its K groups over three waves when K/128 = 6, four when
+ * K/128 <= ECF8_MOE_FOUR_WAVE_GROUPS, else eight (wave w takes groups w,
  * w + waves, ...), then the waves in order. */
 #define ECF8_MOE_FOUR_WAVE_GROUPS 16
 int ecf8_moe_linear(const void *aq, const float *as, const int *row_of, const int *offsets,

@@ -122,8 +122,9 @@ int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *tab
  * for every sorted position q of expert e.  ops: device array of
  * n_experts * n_segs operands (each [seg_n, K], its own out_col unused);
  * tables: device array of n_experts ECF8_TABLE_DFA tables (each expert's
- * block).  The wave count is ecf8_moe_linear's for this K (8 when K/128 >
- * ECF8_MOE_FOUR_WAVE_GROUPS, else 4), so the result is bit-identical to
+ * block).  The wave count is ecf8_moe_linear's for this K (3 when K/128 =
+ * 6, 8 when K/128 > ECF8_MOE_FOUR_WAVE_GROUPS, else 4), so the result is
+ * bit-identical to
  * decoding the experts and calling ecf8_moe_linear.  The splits FP8
  * workgroups per expert (rounded up so that every operand s gets an equal
  * run of them; splits = 0 picks about 1.4 resident workgroups per expert

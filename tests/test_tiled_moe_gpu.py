@@ -7,8 +7,8 @@ compressed as its own block and re-tiled under its own code:
 * ecf8_tile_moe_linear -- routed experts decoding their weight operands on
   the fly -- is bit-identical to ecf8_moe_linear over the decoded experts,
   for gate/up (token rows gathered, 4 waves of 4 groups) and down (one row
-  per sorted pair, 4 waves: packed on three hardware waves at K = 768,
-  unpacked at K = 1024), 1, 5 and 16 routed tokens, any workgroup split;
+  per sorted pair: 3 waves of 2 groups at K = 768, 4 at K = 1024), 1, 5
+  and 16 routed tokens, any workgroup split;
   eight waves at K = 4096, with three operands per expert;
 * a re-tiled small MoE model generates the FP8 model's tokens and logits,
   eager and graph-replayed;
@@ -128,8 +128,8 @@ def test_tile_moe_linear_is_bit_identical_to_the_fp8_grouped_linear(experts, cud
 @pytest.fixture(scope="module")
 def wide_experts(cuda_device):
     """Eight experts of intermediate 1024: the down projection's K = 1024
-    gives the FP8 grouped linear four waves of two groups each, which run
-    unpacked (K = 768's six groups run packed on three hardware waves)."""
+    gives the FP8 grouped linear four waves of two groups each (K = 768's
+    six groups take three waves)."""
     from dfloat.compress import compress_flat
     from ecf8_amd.decode import build_table
     from ecf8_amd.synth import flat_block, synthetic_block
@@ -150,7 +150,7 @@ def wide_experts(cuda_device):
 
 
 @pytest.mark.parametrize("M", [1, 16])
-def test_unpacked_four_wave_down_projection_is_bit_identical(wide_experts, cuda_device, M):
+def test_four_wave_down_projection_is_bit_identical(wide_experts, cuda_device, M):
     from ecf8_amd import llm_kernels as K
     from ecf8_amd.llm_kernels import MoeLinearPlan
     from ecf8_amd.tiled import TileMoePlan
@@ -168,7 +168,7 @@ def test_unpacked_four_wave_down_projection_is_bit_identical(wide_experts, cuda_
     ref = torch.full((P, H + 8), 7.0, dtype=torch.bfloat16, device=cuda_device)
     got = ref.clone()
     MoeLinearPlan([[d] for d in dense], ref)(aq, as_, r, False, M=M)
-    _say(f"[tiled-moe] unpacked down K={inter} M={M}")
+    _say(f"[tiled-moe] four-wave down K={inter} M={M}")
     TileMoePlan([[o] for o in ops], tables, got)(aq, as_, r, False, M=M)
     torch.cuda.synchronize()
     rows = M * top_k
