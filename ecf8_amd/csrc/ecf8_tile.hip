@@ -537,6 +537,10 @@ struct TileMoeArgs {
   const uint32_t *const *tables;  // [E]
   uint16_t *out;
   int K, ldo, n_segs, seg_n;
+  // workgroups per expert: wgs > 0 on a (wgs, experts) grid; wgs = 0 on a
+  // one-dimensional grid that the active experts share (gridDim.x /
+  // n_active each, a multiple of wgs_unit, at most wgs_cap)
+  int wgs, wgs_unit, wgs_cap;
 };
 
 // Waves per SIMD the register allocation targets: eight (64 VGPRs), so
@@ -570,12 +574,31 @@ void tile_linear16_kernel(
   // linear's fused operands one lane.  Group vw takes panels j, j + gpo,
   // ... (j = vw % gpo) of lane vw / gpo, whose tps panels it shares with
   // the lane's other gpo groups.
-  const int vgrid = (int)gridDim.x * G, vwg0 = (int)blockIdx.x * G, vwg = vwg0 + group;
+  int vgrid = (int)gridDim.x * G, vwg0 = (int)blockIdx.x * G;
   int M, row0 = 0, tps, gpo;
   const uint32_t *table;
   Walk walk;
+  int slot = 0;
   if constexpr (kMoe) {
-    const int slot = blockIdx.y;
+    // this workgroup's expert slot and its split of that expert's panels
+    const int n_act = uniform(a.n_active[0]);
+    int wgs = a.wgs, t = (int)blockIdx.x;
+    if (wgs > 0) {
+      t += (int)blockIdx.y * wgs;
+    } else {
+      // as many workgroups per routed expert as the resident grid holds, so
+      // that every routed expert's work runs in one round (a fixed split
+      // sized for the typical expert count spills a few workgroups into a
+      // second round when more experts are routed)
+      wgs = n_act > 0 ? (int)gridDim.x / n_act : 1;
+      wgs = min(max(wgs / a.wgs_unit, 1) * a.wgs_unit, a.wgs_cap);
+    }
+    slot = t / wgs;
+    vgrid = wgs * G;
+    vwg0 = (t - slot * wgs) * G;
+  }
+  const int vwg = vwg0 + group;
+  if constexpr (kMoe) {
     if (slot >= uniform(a.n_active[0])) return;  // uniform, before any barrier
     const int e = uniform(a.active[slot]);
     row0 = uniform(a.offsets[e]);
@@ -1026,26 +1049,36 @@ extern "C" int ecf8_tile_moe_linear(const void *aq, const float *as, const int *
   if (!aligned(aq, 16) || !aligned(as, 4) || !aligned(out, 4) || !aligned(ops, 8) ||
       !aligned(tables, 8))
     return ECF8_ERR_MISALIGNED;
-  const TileMoeArgs args{static_cast<const uint8_t *>(aq), as, row_of, offsets, active, n_active,
-                         ops, tables, static_cast<uint16_t *>(out), (int)K, (int)ldo, n_segs,
-                         (int)seg_n};
+  const TileMoeArgs args0{static_cast<const uint8_t *>(aq), as, row_of, offsets, active, n_active,
+                          ops, tables, static_cast<uint16_t *>(out), (int)K, (int)ldo, n_segs,
+                          (int)seg_n, 0, 1, 1};
   const int64_t n_tiles = n_segs * seg_n / 16;
   // the FP8 grouped linear's wave count for this K (it sums in that order)
   const bool eight = K / kGroup > ECF8_MOE_FOUR_WAVE_GROUPS;
   // groups: G FP8 workgroups per workgroup (splits counts FP8 workgroups)
   auto launch = [&](auto kernel, int threads, int groups) {
-    int64_t g = splits;
-    if (g == 0) {  // about 1.4 workgroups per slot for the experts' share
+    TileMoeArgs args = args0;
+    // the kernel deals an expert's groups to its operands in equal runs:
+    // workgroups per expert a multiple of `unit`
+    int unit = 1;
+    while ((unit * groups) % n_segs) ++unit;
+    const int64_t most = (n_tiles + groups - 1) / groups;  // one panel per group
+    args.wgs_unit = unit;
+    args.wgs_cap = (int)((most + unit - 1) / unit * unit);
+    if (splits > 0) {
+      const int64_t g = splits > n_tiles ? n_tiles : splits;
+      args.wgs = (int)(((g + groups - 1) / groups + unit - 1) / unit * unit);
+      kernel<<<dim3((unsigned)args.wgs, (unsigned)n_experts), threads, 0,
+               as_stream(stream)>>>(args);
+    } else {
+      // one workgroup per resident slot (at least `unit` per expert)
       int64_t slots = 0;
       const int rc = resident_slots(kernel, threads, &slots);
       if (rc != ECF8_OK) return rc;
-      g = (slots * groups * 10 + 7 * n_experts - 1) / (7 * n_experts);
+      const int64_t grid = slots > (int64_t)unit * n_experts ? slots : (int64_t)unit * n_experts;
+      args.wgs = 0;
+      kernel<<<dim3((unsigned)grid), threads, 0, as_stream(stream)>>>(args);
     }
-    g = g < 1 ? 1 : g > n_tiles ? n_tiles : g;
-    int64_t wgs = (g + groups - 1) / groups;
-    // the kernel deals the groups to the operands in equal runs
-    while ((wgs * groups) % n_segs) ++wgs;
-    kernel<<<dim3((unsigned)wgs, (unsigned)n_experts), threads, 0, as_stream(stream)>>>(args);
     return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
   };
   if (eight)

@@ -125,11 +125,13 @@ int ecf8_tile_decode(const ecf8_tile_operand *op, int64_t K, const uint32_t *tab
  * block).  The wave count is ecf8_moe_linear's for this K (3 when K/128 =
  * 6, 8 when K/128 > ECF8_MOE_FOUR_WAVE_GROUPS, else 4), so the result is
  * bit-identical to
- * decoding the experts and calling ecf8_moe_linear.  The splits FP8
- * workgroups per expert (rounded up so that every operand s gets an equal
- * run of them; splits = 0 picks about 1.4 resident workgroups per expert
- * slot) take the 16-column tiles of their operand in turn, so each wave
- * reads one operand's addresses only.  Idle slots exit, so
+ * decoding the experts and calling ecf8_moe_linear.  Each routed expert's
+ * 16-column tiles are dealt to its FP8 workgroups, every operand s getting
+ * an equal run of them (so each wave reads one operand's addresses only):
+ * splits > 0 FP8 workgroups per expert (rounded up for the runs), or,
+ * splits = 0, one launch of the resident workgroups that the routed
+ * experts share on the device (as many per expert as n_active leaves room
+ * for), so that any routing runs in one round.  Idle workgroups exit, so
  * the launch can be captured in a graph.  The device arrays are trusted:
  * their pointers must satisfy ecf8_tile_linear's alignment rules.
  */
