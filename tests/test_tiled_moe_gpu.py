@@ -125,6 +125,51 @@ def test_tile_moe_linear_is_bit_identical_to_the_fp8_grouped_linear(experts, cud
     assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
 
 
+@pytest.mark.parametrize("spread", ["all", "random"])
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_many_routed_experts_share_the_resident_grid(experts, cuda_device, which, spread):
+    """128 expert slots (the 16 experts' operands, each reused 8 times):
+    16 tokens routed to 128 distinct experts (the most a decode step can
+    route: four workgroups per expert on the resident grid) or to a random
+    ~90 (five): still bit-identical to the FP8 grouped linear."""
+    from ecf8_amd import llm_kernels as K
+    from ecf8_amd.llm_kernels import MoeLinearPlan
+    from ecf8_amd.tiled import TileMoePlan
+
+    dense, ops, tables = experts
+    n_slots = 128
+    names = ["gate_proj", "up_proj"] if which == "gate_up" else ["down_proj"]
+    gather = which == "gate_up"
+    Kd = H if gather else I
+    N = sum(ops[0][n].n for n in names)
+    M = 16
+    r = K.MoeRouting(16, TOP_K, n_slots, cuda_device)
+    if spread == "all":
+        idx = torch.arange(M * TOP_K).view(M, TOP_K)
+    else:
+        g = torch.Generator().manual_seed(77)
+        idx = torch.stack([torch.randperm(n_slots, generator=g)[:TOP_K] for _ in range(M)])
+    r.topk_idx[:M] = idx.to(torch.int32).to(cuda_device)
+    r.topk_w[:M] = torch.rand(M, TOP_K, generator=torch.Generator().manual_seed(5)).to(cuda_device)
+    K.moe_group(r, M)
+    n_active = int(r.n_active.item())
+    assert n_active == 128 if spread == "all" else 80 <= n_active < 128
+    P = 16 * TOP_K
+    aq, as_ = _acts(16 if gather else P, Kd, 9, cuda_device)
+    ref = torch.full((P, N + 8), 7.0, dtype=torch.bfloat16, device=cuda_device)
+    got = ref.clone()
+    MoeLinearPlan([[dense[e % E][n] for n in names] for e in range(n_slots)], ref)(
+        aq, as_, r, gather, M=M)
+    _say(f"[tiled-moe] {which}: {n_active} of {n_slots} experts routed")
+    TileMoePlan([[ops[e % E][n] for n in names] for e in range(n_slots)],
+                [tables[e % E] for e in range(n_slots)], got)(aq, as_, r, gather, M=M)
+    torch.cuda.synchronize()
+    rows = M * TOP_K
+    assert torch.equal(got[:rows], ref[:rows])
+    assert bool((got[:, N:] == 7.0).all())
+    assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
+
+
 @pytest.fixture(scope="module")
 def wide_experts(cuda_device):
     """Eight experts of intermediate 1024: the down projection's K = 1024
