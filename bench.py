@@ -1061,18 +1061,21 @@ def dit_child(seed: int, timeout_s: float):
 
 
 BATCHED_MIN_STEPS = 200
+BATCHED_MIN_WARMUP = 100
 
 
 def batched_child(seed: int, steps: int, warmup: int, timeout_s: float):
     """The batched MoE-layer decode line (one Qwen3-30B-A3B-shaped layer,
-    attention + 128 experts in one launch) run in a child process with this
-    line's warm-up and at least BATCHED_MIN_STEPS timed launches (~47 ms):
-    on MI355X the first ~15 ms of sustained decode load run up to 8 %
-    slower than the rest (launch times 235 -> 255 -> 235 us, with or
-    without a GPU-busy prime beforehand), so a 20-launch window after 5
-    warm-up launches would time that onset alone."""
+    attention + 128 experts in one launch) run in a child process with at
+    least BATCHED_MIN_WARMUP warm-up launches (~24 ms) and at least
+    BATCHED_MIN_STEPS timed ones (~47 ms): on MI355X the first ~15 ms of
+    sustained decode load run up to 8 % slower than the rest (launch times
+    235 -> 255 -> 235 us, with or without a GPU-busy prime beforehand), so a
+    window after 5 warm-up launches would time that onset, not the
+    layer-after-layer rate of a model's decode."""
     full, wall = _child_line(["--workload", "qwen3-moe-layer", "--seed", str(seed), "--steps",
-                              str(max(steps, BATCHED_MIN_STEPS)), "--warmup", str(warmup)],
+                              str(max(steps, BATCHED_MIN_STEPS)), "--warmup",
+                              str(max(warmup, BATCHED_MIN_WARMUP))],
                              timeout_s)
     if "error" in full:
         return full
