@@ -753,22 +753,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
                                           (int)blockIdx.x, (int)gridDim.x, n_fb);
 }
 
+// Launches over at most this many tensors (e.g. an MoE layer's attention
+// block and 128 experts) keep their task table in LDS: each workgroup
+// derives every tensor's first task itself (over the selected tensors, for
+// a routed launch) and finds a task's tensor there, instead of by a binary
+// search over the descriptors in memory (about eight dependent L2 round
+// trips per task) -- and a routed launch needs no compaction kernel first.
+constexpr int kLdsBlocks = 256;
+
 // Many tensors in one launch (e.g. the routed experts of an MoE layer): the
 // work is split into tasks of up to `blocks_per_task` format-blocks of one
 // tensor; desc[d].task_begin is the first task of tensor d.  Each workgroup
 // takes tasks blockIdx.x, + gridDim.x, ..., loading the task's table before
 // decoding it.
 //
-// dev_counts (optional): {count, n_tasks} read from device memory instead
-// of the arguments, as written by select_blocks_kernel.
+// select (optional, count <= kLdsBlocks): one flag per descriptor; only the
+// tensors whose flag is nonzero are decoded, their tasks numbered in
+// descriptor order (task_begin is then ignored).  sel_counts (optional,
+// with select): workgroup 0 writes {selected tensors, their tasks} there.
+// dev_counts (optional, with descriptors compacted by select_blocks_kernel):
+// {count, n_tasks} read from device memory instead of the arguments.
 template <int kThreads>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_batched_kernel(
     const ecf8_block_desc *__restrict__ descs, int count, int n_tasks, int blocks_per_task,
-    int stage_cap, const int *__restrict__ dev_counts) {
+    int stage_cap, const int *__restrict__ dev_counts, const int32_t *__restrict__ select,
+    int32_t *__restrict__ sel_counts) {
   constexpr int kWaves = kThreads / 64;
+  static_assert(kLdsBlocks == 4 * 64, "one 16-byte read of the task table per lane");
   __shared__ uint32_t s_dfa[kDfaEntries];
-  __shared__ int s_wave_sum[kWaves];
+  __shared__ int s_wave_sum[kWaves], s_wave_sel[kWaves];
   __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
+  __shared__ __attribute__((aligned(16))) int s_begin[kLdsBlocks];
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
 
   if (dev_counts) {  // never above the launch's bounds
@@ -776,8 +791,46 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     n_tasks = min(n_tasks, __builtin_amdgcn_readfirstlane(dev_counts[1]));
   }
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   if (tid < kEdgeDwords) s_edge[tid] = 0u;
   constexpr uint32_t kBlockBytes = (uint32_t)kThreads * kChunkBytes;
+  const bool lds_table = count <= kLdsBlocks;  // uniform
+  if (lds_table) {
+    // s_begin[b]: tensor b's first task (an exclusive prefix of the
+    // selected tensors' task counts, computed as the descriptors' task_begin
+    // is); past the last tensor INT32_MAX, so that the search below never
+    // picks those entries.  Both loads of a tensor are issued together.
+    int base = 0, n_sel = 0;
+    for (int c0 = 0; c0 < kLdsBlocks; c0 += kThreads) {  // one pass for >= 256 threads
+      const int b = c0 + tid;
+      int tasks = 0, flag = 0;
+      if (b < count) {
+        flag = select ? select[b] : 1;
+        const int64_t nb = min(max(descs[b].n_bytes, (int64_t)0), (int64_t)INT32_MAX);
+        const int fbs = (int)((nb + kBlockBytes - 1) / kBlockBytes);
+        tasks = flag != 0 ? (fbs + blocks_per_task - 1) / blocks_per_task : 0;
+      }
+      const int incl = wave_inclusive_scan(tasks);
+      const int wave_sel = __builtin_popcountll(__builtin_amdgcn_ballot_w64(flag != 0));
+      if (lane == 63) {
+        s_wave_sum[wave] = incl;
+        s_wave_sel[wave] = wave_sel;
+      }
+      __syncthreads();
+      int total = 0;
+      const int before = waves_before<kWaves>(s_wave_sum, lane, wave, &total);
+      if (b < kLdsBlocks) s_begin[b] = b < count ? base + before + incl - tasks : INT32_MAX;
+      if (sel_counts && tid == 0)
+        for (int w = 0; w < kWaves; ++w) n_sel += s_wave_sel[w];
+      base += total;
+      __syncthreads();  // s_wave_sum is written again by the next pass and the decode
+    }
+    n_tasks = min(n_tasks, base);
+    if (sel_counts && blockIdx.x == 0 && tid == 0) {
+      sel_counts[0] = n_sel;
+      sel_counts[1] = base;
+    }
+  }
   // Task order.  Several tensors: the workgroups of XCD x (workgroups are
   // dealt to the 8 XCDs round robin) take the x-th eighth of the task list,
   // strided over them, so a tensor's tasks share one XCD's L2 and its table
@@ -793,18 +846,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   }
   for (; task < task_end; task += task_step) {
     // the tensor of this task: the last descriptor whose first task is <= it
-    int lo = 0, hi = count - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (descs[mid].task_begin <= task) lo = mid;
-      else hi = mid - 1;
+    int lo = 0, first = 0;
+    if (lds_table) {
+      // first tasks ascend: those <= task are a prefix of the table, counted
+      // with one ballot per entry of each lane's four
+      const int4 v = reinterpret_cast<const int4 *>(s_begin)[lane];
+      const int n = __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.x <= task)) +
+                    __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.y <= task)) +
+                    __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.z <= task)) +
+                    __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.w <= task));
+      if (n == 0) continue;  // uniform; never for a task below n_tasks
+      lo = n - 1;
+      first = __builtin_amdgcn_readfirstlane(s_begin[lo]);
+    } else {
+      int hi = count - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (descs[mid].task_begin <= task) lo = mid;
+        else hi = mid - 1;
+      }
+      first = descs[lo].task_begin;
     }
     const ecf8_block_desc &d = descs[lo];
     // uniform; blocks too small for the clamped vector loads (fewer than 12
     // bitstream bytes or 16 elements) or too large for 32-bit positions are
     // not batched, nor is a task outside its block (malformed task_begin)
     if (d.n_bytes < 12 || d.n_elements < 16 || d.n_bytes > INT32_MAX - 64 ||
-        d.n_elements > INT32_MAX - 64 || task < d.task_begin)
+        d.n_elements > INT32_MAX - 64 || task < first)
       continue;
     const uint32_t n_bytes = (uint32_t)d.n_bytes;
     const int n_fb = (int)((n_bytes + kBlockBytes - 1) / kBlockBytes);
@@ -815,7 +883,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     // Qwen3-30B-A3B layer (two rotated sets): 245.5 us with contiguous runs
     // of blocks per task, 238.6 us interleaved.
     const int tasks = (n_fb + blocks_per_task - 1) / blocks_per_task;
-    const int r = task - d.task_begin;
+    const int r = task - first;
     if (r >= tasks) continue;
     // the previous task ended with a barrier: no wave still reads s_dfa.
     // The table loads in dfa_blocks, seven per lane in flight (two round
@@ -1272,7 +1340,8 @@ int launch_decode(DecodeArgs a, int64_t max_block_elements, int kind, int tpb_sl
 
 template <int kThreads>
 int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int blocks_per_task,
-                       int cap, hipStream_t stream, int slot, const int *dev_counts = nullptr) {
+                       int cap, hipStream_t stream, int slot, const int *dev_counts = nullptr,
+                       const int32_t *select = nullptr, int32_t *sel_counts = nullptr) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(cap) + kSpillDwords);
   const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
@@ -1282,7 +1351,7 @@ int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int
                                  slot, n_tasks, &grid);
   if (rc != ECF8_OK) return rc;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), dyn, stream, descs, count,
-                     n_tasks, blocks_per_task, cap, dev_counts);
+                     n_tasks, blocks_per_task, cap, dev_counts, select, sel_counts);
   return hipGetLastError() == hipSuccess ? ECF8_OK : ECF8_ERR_HIP;
 }
 
@@ -1350,13 +1419,31 @@ extern "C" int ecf8_decode_batched_select(const ecf8_block_desc *descs, int coun
                                                                         : (int)max_block_elements;
   if (cap < 16) cap = 16;
   hipStream_t s = (hipStream_t)stream;
+  // the task count is only known on the device: a full persistent grid,
+  // each workgroup stops at the selected task count
+  const int n_tasks_bound = INT32_MAX;
+  if (count <= kLdsBlocks) {
+    // one launch: every workgroup scans the flags itself (work_descs is not
+    // used; workgroup 0 writes work_counts)
+    switch (threads_per_block) {
+      case 128:
+        return launch_dfa_batched<128>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 16,
+                                       nullptr, select, work_counts);
+      case 256:
+        return launch_dfa_batched<256>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 17,
+                                       nullptr, select, work_counts);
+      case 512:
+        return launch_dfa_batched<512>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 18,
+                                       nullptr, select, work_counts);
+      default:
+        return launch_dfa_batched<1024>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 19,
+                                        nullptr, select, work_counts);
+    }
+  }
   const int64_t block_bytes = (int64_t)threads_per_block * kChunkBytes;
   hipLaunchKernelGGL(select_blocks_kernel, dim3(1), dim3(1024), 0, s, descs, count, select,
                      blocks_per_task, block_bytes, work_descs, work_counts);
   if (hipGetLastError() != hipSuccess) return ECF8_ERR_HIP;
-  // the task count is only known on the device: a full persistent grid,
-  // each workgroup stops at the selected task count
-  const int n_tasks_bound = INT32_MAX;
   switch (threads_per_block) {
     case 128:
       return launch_dfa_batched<128>(work_descs, count, n_tasks_bound, blocks_per_task, cap, s, 16,

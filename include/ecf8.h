@@ -197,13 +197,16 @@ int ecf8_decode_batched(const ecf8_block_desc *descs, int count, int n_tasks, in
  * Batched decode of the blocks whose select[d] (device int32, one per
  * descriptor) is nonzero, e.g. the attention block and the experts the
  * router picked for this step: the reference decodes only the experts whose
- * modules run (their hooks, dfloat/run/run.py:84-155).  A one-workgroup
- * kernel compacts the selected descriptors into work_descs (device,
- * `count` entries) with task_begin recomputed and writes {count, n_tasks}
- * to work_counts (device int32[2]); the batched kernel then reads them
- * there.  Nothing is read back to the host, so the call can be captured in
- * a HIP graph and replayed with new flags.  descs' task_begin fields are
- * ignored.  Unselected blocks' outputs are not touched.
+ * modules run (their hooks, dfloat/run/run.py:84-155).  Up to 256
+ * descriptors (e.g. an MoE layer's attention block and 128 experts), one
+ * launch: each workgroup of the batched kernel scans the flags itself and
+ * workgroup 0 writes {selected count, their tasks} to work_counts (device
+ * int32[2]); work_descs is not used.  More descriptors: a one-workgroup
+ * kernel first compacts the selected ones into work_descs (device, `count`
+ * entries) and writes the same two counts to work_counts, where the batched
+ * kernel reads them.  Nothing is read back to the host, so the call can be
+ * captured in a HIP graph and replayed with new flags.  descs' task_begin
+ * fields are ignored.  Unselected blocks' outputs are not touched.
  */
 int ecf8_decode_batched_select(const ecf8_block_desc *descs, int count, const int32_t *select,
                                ecf8_block_desc *work_descs, int32_t *work_counts,

@@ -776,6 +776,17 @@ def test_batched_select_decodes_only_the_selected_blocks(cuda_device):
         _check_selected(flats, bufs, flags)
         n_sel, n_tasks = sel.counts.cpu().tolist()
         assert n_sel == int(flags.sum())
+        assert n_tasks == _selected_tasks(sel.plan, flags)
+
+
+def _selected_tasks(plan, flags):
+    """Tasks of the selected descriptors (flags per descriptor)."""
+    from ecf8_amd.decode import BLOCK_DESC_DTYPE
+
+    n_bytes = np.frombuffer(plan.descs.cpu().numpy().tobytes(), dtype=BLOCK_DESC_DTYPE)["n_bytes"]
+    fb = -(-n_bytes // (plan.threads_per_block * 8))
+    tasks = -(-fb // plan.blocks_per_task)
+    return int(tasks[np.asarray(flags)[: plan.count] != 0].sum())
 
 
 def test_batched_select_replays_in_a_graph_with_new_flags(cuda_device):
@@ -862,3 +873,71 @@ def test_batched_select_with_blocks_outside_the_batched_kernel(cuda_device):
         g.replay()
         torch.cuda.synchronize()
         check(f)
+
+
+def _many_blocks(cuda_device, n):
+    """n small blocks (one or two 128 x 128 Linears: 2 or 3 format-blocks
+    each), all automaton tables, outputs filled with a sentinel."""
+    from ecf8_amd import synth
+
+    one = {"up_proj": (128, 128, 0.02)}
+    two = {"down_proj": (128, 128, 0.02), "up_proj": (128, 128, 0.02)}
+    flats = [synth.flat_block(synth.synthetic_block(two if e % 3 else one, 500 + e))[0]
+             .view(torch.uint8).numpy() for e in range(n)]
+    blocks = [_dev_block(_compress(f), cuda_device) for f in flats]
+    bufs = [torch.full((f.size + 32,), 0x3C, dtype=torch.uint8, device=cuda_device) for f in flats]
+    return flats, blocks, bufs
+
+
+@pytest.mark.parametrize("n_blocks", [256, 264])
+def test_batched_launch_on_either_side_of_the_lds_task_table(n_blocks, cuda_device):
+    """Up to 256 descriptors the batched kernel keeps the task table in LDS
+    (each workgroup scans the task counts, and for a routed launch the
+    flags, itself); above, it searches the descriptors in memory and a
+    routed launch compacts the selected ones first.  Every path bit-exact,
+    unselected outputs untouched, the counts written, eager and replayed in
+    a graph."""
+    from ecf8_amd.decode import BatchSelect, build_table, prepare_batch
+
+    _say(f"batched over {n_blocks} blocks")
+    flats, blocks, bufs = _many_blocks(cuda_device, n_blocks)
+    tables = [build_table(b["luts"]) for b in blocks]
+    assert all(t.kind == DFA for t in tables)
+    plan = prepare_batch(blocks, [b[: f.size] for b, f in zip(bufs, flats)], tables,
+                         blocks_per_task=2)
+    assert plan.count == n_blocks and not plan.singles
+    from ecf8_amd.decode import decode_batched
+
+    decode_batched(blocks, [b[: f.size] for b, f in zip(bufs, flats)], tables, blocks_per_task=2)
+    torch.cuda.synchronize()
+    _check_selected(flats, bufs, np.ones(n_blocks, np.int32))
+
+    sel = BatchSelect(plan)
+    flags_dev = torch.zeros(n_blocks, dtype=torch.int32, device=cuda_device)
+    rng = np.random.default_rng(n_blocks)
+    draws = [(rng.random(n_blocks) < p).astype(np.int32) for p in (0.5, 0.1, 0.9)]
+    for f in draws:
+        for b in bufs:
+            b.fill_(0x3C)
+        flags_dev.copy_(torch.from_numpy(f).to(cuda_device))
+        sel(flags_dev)
+        torch.cuda.synchronize()
+        _check_selected(flats, bufs, f)
+        assert sel.counts.cpu().tolist() == [int(f.sum()), _selected_tasks(plan, f)]
+    s = torch.cuda.Stream(cuda_device)
+    s.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(s):
+        sel(flags_dev)
+    torch.cuda.current_stream(cuda_device).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sel(flags_dev)
+    for f in draws[::-1]:
+        for b in bufs:
+            b.fill_(0x3C)
+        flags_dev.copy_(torch.from_numpy(f).to(cuda_device))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _check_selected(flats, bufs, f)
