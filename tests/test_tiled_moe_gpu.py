@@ -125,13 +125,15 @@ def test_tile_moe_linear_is_bit_identical_to_the_fp8_grouped_linear(experts, cud
     assert len(set(got[:rows].float().reshape(-1).tolist())) > 100
 
 
-@pytest.mark.parametrize("spread", ["all", "random"])
+@pytest.mark.parametrize("spread", ["all", "random", "same"])
 @pytest.mark.parametrize("which", ["gate_up", "down"])
 def test_many_routed_experts_share_the_resident_grid(experts, cuda_device, which, spread):
     """128 expert slots (the 16 experts' operands, each reused 8 times):
     16 tokens routed to 128 distinct experts (the most a decode step can
-    route: four workgroups per expert on the resident grid) or to a random
-    ~90 (five): still bit-identical to the FP8 grouped linear."""
+    route: four workgroups per expert on the resident grid), to a random
+    ~90 (five), or all to the same top-k (8 experts, each holding a full
+    16-row tile, their split capped at one panel per group): still
+    bit-identical to the FP8 grouped linear."""
     from ecf8_amd import llm_kernels as K
     from ecf8_amd.llm_kernels import MoeLinearPlan
     from ecf8_amd.tiled import TileMoePlan
@@ -146,6 +148,10 @@ def test_many_routed_experts_share_the_resident_grid(experts, cuda_device, which
     r = K.MoeRouting(16, TOP_K, n_slots, cuda_device)
     if spread == "all":
         idx = torch.arange(M * TOP_K).view(M, TOP_K)
+    elif spread == "same":
+        g = torch.Generator().manual_seed(78)
+        pick = torch.randperm(n_slots, generator=g)[:TOP_K]
+        idx = torch.stack([pick[torch.randperm(TOP_K, generator=g)] for _ in range(M)])
     else:
         g = torch.Generator().manual_seed(77)
         idx = torch.stack([torch.randperm(n_slots, generator=g)[:TOP_K] for _ in range(M)])
@@ -153,7 +159,12 @@ def test_many_routed_experts_share_the_resident_grid(experts, cuda_device, which
     r.topk_w[:M] = torch.rand(M, TOP_K, generator=torch.Generator().manual_seed(5)).to(cuda_device)
     K.moe_group(r, M)
     n_active = int(r.n_active.item())
-    assert n_active == 128 if spread == "all" else 80 <= n_active < 128
+    if spread == "all":
+        assert n_active == 128
+    elif spread == "same":
+        assert n_active == TOP_K
+    else:
+        assert 80 <= n_active < 128
     P = 16 * TOP_K
     aq, as_ = _acts(16 if gather else P, Kd, 9, cuda_device)
     ref = torch.full((P, N + 8), 7.0, dtype=torch.bfloat16, device=cuda_device)
