@@ -1,6 +1,6 @@
-"""The ctypes stub INTEGRATION.md gives a maintainer of the reference (the
-block between its ``stub:begin`` / ``stub:end`` markers), run exactly as
-written: the reference's callers pass integer device addresses
+"""The ctypes stub that the repository's integration guide gives a
+maintainer of the reference (the block between its ``stub:begin`` /
+``stub:end`` markers), run exactly as written: the reference's callers pass integer device addresses
 (dfloat/run/run.py:104-119, scripts/compress.py:109-124).
 
 CPU: against a stand-in library that records each call, the stub makes
