@@ -875,16 +875,17 @@ def test_batched_select_with_blocks_outside_the_batched_kernel(cuda_device):
         check(f)
 
 
-def _many_blocks(cuda_device, n):
+def _many_blocks(cuda_device, n, tpb=512):
     """n small blocks (one or two 128 x 128 Linears: 2 or 3 format-blocks
-    each), all automaton tables, outputs filled with a sentinel."""
+    each at 512 threads per block), all automaton tables, outputs filled
+    with a sentinel."""
     from ecf8_amd import synth
 
     one = {"up_proj": (128, 128, 0.02)}
     two = {"down_proj": (128, 128, 0.02), "up_proj": (128, 128, 0.02)}
     flats = [synth.flat_block(synth.synthetic_block(two if e % 3 else one, 500 + e))[0]
              .view(torch.uint8).numpy() for e in range(n)]
-    blocks = [_dev_block(_compress(f), cuda_device) for f in flats]
+    blocks = [_dev_block(_compress(f, tpb), cuda_device) for f in flats]
     bufs = [torch.full((f.size + 32,), 0x3C, dtype=torch.uint8, device=cuda_device) for f in flats]
     return flats, blocks, bufs
 
@@ -941,3 +942,33 @@ def test_batched_launch_on_either_side_of_the_lds_task_table(n_blocks, cuda_devi
         g.replay()
         torch.cuda.synchronize()
         _check_selected(flats, bufs, f)
+
+
+@pytest.mark.parametrize("tpb,n_blocks", [(128, 200), (256, 40), (1024, 40)])
+def test_batched_launch_at_every_block_size(tpb, n_blocks, cuda_device):
+    """The batched kernel at 128, 256 and 1024 threads per format-block (the
+    other format geometries; 128 threads scan the LDS task table in two
+    passes): whole and routed launches bit-exact, unselected outputs
+    untouched, the routed counts written."""
+    from ecf8_amd.decode import BatchSelect, build_table, decode_batched, prepare_batch
+
+    _say(f"batched at tpb={tpb} over {n_blocks} blocks")
+    flats, blocks, bufs = _many_blocks(cuda_device, n_blocks, tpb)
+    tables = [build_table(b["luts"]) for b in blocks]
+    assert all(t.kind == DFA for t in tables)
+    outs = [b[: f.size] for b, f in zip(bufs, flats)]
+    plan = prepare_batch(blocks, outs, tables, threads_per_block=tpb, blocks_per_task=2)
+    assert plan.count == n_blocks and not plan.singles
+    decode_batched(plan)
+    torch.cuda.synchronize()
+    _check_selected(flats, bufs, np.ones(n_blocks, np.int32))
+    sel = BatchSelect(plan)
+    rng = np.random.default_rng(tpb)
+    for p in (0.5, 0.2):
+        f = (rng.random(n_blocks) < p).astype(np.int32)
+        for b in bufs:
+            b.fill_(0x3C)
+        sel(torch.from_numpy(f).to(cuda_device))
+        torch.cuda.synchronize()
+        _check_selected(flats, bufs, f)
+        assert sel.counts.cpu().tolist() == [int(f.sum()), _selected_tasks(plan, f)]
