@@ -1083,7 +1083,8 @@ def batched_child(seed: int, steps: int, warmup: int, timeout_s: float):
     return {"workload": cfg["workload"], "blocks": cfg["blocks"], "elements": cfg["elements"],
             "algorithmic_bytes": cfg["algorithmic_bytes"], "value": full["value"],
             "unit": full["unit"], "steps": full["steps"], "warmup": full["warmup"],
-            "ms_per_step": full["ms_per_step"], "roofline": full["roofline"],
+            "ms_per_step": full["ms_per_step"], "warmup_ms_per_step": full["warmup_ms_per_step"],
+            "roofline": full["roofline"],
             "bit_exact": full["bit_exact"], "wall_s": round(wall, 1)}
 
 
@@ -1183,14 +1184,20 @@ def main():
     # are the timed launches' own): verifying in between left the GPU idle
     # for the host copy and compare, and the timed launches then paid its
     # return from idle clocks (measured on MI355X: 72.5-73.3 us per launch
-    # instead of 68).
+    # instead of 68).  An event pair around the warm-up launches (no
+    # synchronization) reports their own average too: the first ~15 ms of
+    # sustained decode load run slower on MI355X.
+    stream = torch.cuda.current_stream(dev)
+    w_start = torch.cuda.Event(enable_timing=True)
+    w_end = torch.cuda.Event(enable_timing=True)
+    w_start.record(stream)
     for i in range(args.warmup):
         step(i)
+    w_end.record(stream)
 
     # One event pair around the K back-to-back launches on the launch stream:
     # a step is exactly one decode kernel, so the average launch duration is
     # the timed span over K (events between launches would add their own gaps).
-    stream = torch.cuda.current_stream(dev)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -1202,6 +1209,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     total_ms = start.elapsed_time(end)
+    warmup_ms = w_start.elapsed_time(w_end) / args.warmup if args.warmup else None
     ms_per_step = total_ms / args.steps
     gbps = alg / (ms_per_step * 1e-3) / 1e9
     # Per-launch wall time: launches one at a time, each between its own
@@ -1245,6 +1253,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "kernel_ms_per_launch": round(avg_launch_ms, 5),
+        "warmup_ms_per_step": round(warmup_ms, 5) if warmup_ms is not None else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
