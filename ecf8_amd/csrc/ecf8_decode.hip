@@ -753,12 +753,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
                                           (int)blockIdx.x, (int)gridDim.x, n_fb);
 }
 
-// Launches over at most this many tensors (e.g. an MoE layer's attention
-// block and 128 experts) keep their task table in LDS: each workgroup
-// derives every tensor's first task itself (over the selected tensors, for
-// a routed launch) and finds a task's tensor there, instead of by a binary
-// search over the descriptors in memory (about eight dependent L2 round
-// trips per task) -- and a routed launch needs no compaction kernel first.
+// Routed launches over at most this many tensors (e.g. an MoE layer's
+// attention block and 128 experts) select on the device in the batched
+// kernel itself (kSelect): each workgroup scans the selected tensors' task
+// counts into an LDS task table and finds a task's tensor there, so no
+// compaction kernel runs first.  Whole launches keep the binary search over
+// the descriptors' task_begin, in their own instance: compiled into one
+// kernel, the table's code raised its register spills, and on MI355X a
+// whole Qwen3-30B-A3B layer then fetched ~17 MB more per launch beyond L2
+// and ran 0.3 % slower.
 constexpr int kLdsBlocks = 256;
 
 // Many tensors in one launch (e.g. the routed experts of an MoE layer): the
@@ -767,23 +770,25 @@ constexpr int kLdsBlocks = 256;
 // takes tasks blockIdx.x, + gridDim.x, ..., loading the task's table before
 // decoding it.
 //
-// select (optional, count <= kLdsBlocks): one flag per descriptor; only the
-// tensors whose flag is nonzero are decoded, their tasks numbered in
-// descriptor order (task_begin is then ignored).  sel_counts (optional,
-// with select): workgroup 0 writes {selected tensors, their tasks} there.
+// kSelect (count <= kLdsBlocks): select holds one flag per descriptor; only
+// the tensors whose flag is nonzero are decoded, their tasks numbered in
+// descriptor order (task_begin is then ignored), and workgroup 0 writes
+// {selected tensors, their tasks} to sel_counts (optional).
 // dev_counts (optional, with descriptors compacted by select_blocks_kernel):
 // {count, n_tasks} read from device memory instead of the arguments.
-template <int kThreads>
+template <int kThreads, bool kSelect>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgpu_waves_per_eu(8))) void decode_dfa_batched_kernel(
     const ecf8_block_desc *__restrict__ descs, int count, int n_tasks, int blocks_per_task,
     int stage_cap, const int *__restrict__ dev_counts, const int32_t *__restrict__ select,
     int32_t *__restrict__ sel_counts) {
   constexpr int kWaves = kThreads / 64;
   static_assert(kLdsBlocks == 4 * 64, "one 16-byte read of the task table per lane");
+  constexpr int kTable = kSelect ? kLdsBlocks : 4;  // the whole-launch instance keeps none
   __shared__ uint32_t s_dfa[kDfaEntries];
-  __shared__ int s_wave_sum[kWaves], s_wave_sel[kWaves];
+  __shared__ int s_wave_sum[kWaves];
   __shared__ __attribute__((aligned(16))) uint32_t s_edge[kEdgeDwords];
-  __shared__ __attribute__((aligned(16))) int s_begin[kLdsBlocks];
+  __shared__ __attribute__((aligned(16))) int s_begin[kTable];
+  __shared__ int s_wave_sel[kSelect ? kWaves : 1];
   extern __shared__ __attribute__((aligned(16))) uint32_t s_dyn[];
 
   if (dev_counts) {  // never above the launch's bounds
@@ -791,11 +796,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
     n_tasks = min(n_tasks, __builtin_amdgcn_readfirstlane(dev_counts[1]));
   }
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
   if (tid < kEdgeDwords) s_edge[tid] = 0u;
   constexpr uint32_t kBlockBytes = (uint32_t)kThreads * kChunkBytes;
-  const bool lds_table = count <= kLdsBlocks;  // uniform
-  if (lds_table) {
+  if constexpr (kSelect) {
+    const int lane = tid & 63, wave = tid >> 6;
     // s_begin[b]: tensor b's first task (an exclusive prefix of the
     // selected tensors' task counts, computed as the descriptors' task_begin
     // is); past the last tensor INT32_MAX, so that the search below never
@@ -805,7 +809,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
       const int b = c0 + tid;
       int tasks = 0, flag = 0;
       if (b < count) {
-        flag = select ? select[b] : 1;
+        flag = select[b];
         const int64_t nb = min(max(descs[b].n_bytes, (int64_t)0), (int64_t)INT32_MAX);
         const int fbs = (int)((nb + kBlockBytes - 1) / kBlockBytes);
         tasks = flag != 0 ? (fbs + blocks_per_task - 1) / blocks_per_task : 0;
@@ -830,6 +834,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
       sel_counts[0] = n_sel;
       sel_counts[1] = base;
     }
+  } else {
+    (void)select;
+    (void)sel_counts;
   }
   // Task order.  Several tensors: the workgroups of XCD x (workgroups are
   // dealt to the 8 XCDs round robin) take the x-th eighth of the task list,
@@ -847,10 +854,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80), amdgp
   for (; task < task_end; task += task_step) {
     // the tensor of this task: the last descriptor whose first task is <= it
     int lo = 0, first = 0;
-    if (lds_table) {
+    if constexpr (kSelect) {
       // first tasks ascend: those <= task are a prefix of the table, counted
       // with one ballot per entry of each lane's four
-      const int4 v = reinterpret_cast<const int4 *>(s_begin)[lane];
+      const int4 v = reinterpret_cast<const int4 *>(s_begin)[threadIdx.x & 63];
       const int n = __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.x <= task)) +
                     __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.y <= task)) +
                     __builtin_popcountll(__builtin_amdgcn_ballot_w64(v.z <= task)) +
@@ -1213,9 +1220,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_num_sgpr(80))) void
 // Per device: CU count, and per kernel variant the occupancy at the last
 // dynamic LDS size it was launched with.
 // {DFA, MULTI} x 4 block sizes x {unchecked, checked} (slots 0-15), batched
-// DFA x 4 (16-19), the device-kind variants of DFA and MULTI (20-35), then
-// the scaled-bf16 DFA kernel (36)
-constexpr int kVariants = 37;
+// DFA x 4 (16-19), the device-kind variants of DFA and MULTI (20-35), the
+// scaled-bf16 DFA kernel (36), then batched DFA selecting in the kernel x 4
+// (37-40)
+constexpr int kVariants = 41;
 struct LaunchCache {
   int device = -1;
   int cus = 0;
@@ -1338,14 +1346,14 @@ int launch_decode(DecodeArgs a, int64_t max_block_elements, int kind, int tpb_sl
                  : launch_multi<kThreads, false, true>(a, 28 + 2 * tpb_slot + c);
 }
 
-template <int kThreads>
+template <int kThreads, bool kSelect = false>
 int launch_dfa_batched(const ecf8_block_desc *descs, int count, int n_tasks, int blocks_per_task,
                        int cap, hipStream_t stream, int slot, const int *dev_counts = nullptr,
                        const int32_t *select = nullptr, int32_t *sel_counts = nullptr) {
   constexpr int kMaxSyms = kThreads * kChunkBits;
   const size_t dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(cap) + kSpillDwords);
   const size_t max_dyn = sizeof(uint32_t) * 2 * ((size_t)stage_dwords(kMaxSyms) + kSpillDwords);
-  auto kernel = decode_dfa_batched_kernel<kThreads>;
+  auto kernel = decode_dfa_batched_kernel<kThreads, kSelect>;
   int grid = 0;
   const int rc = persistent_grid(reinterpret_cast<const void *>(kernel), kThreads, dyn, max_dyn,
                                  slot, n_tasks, &grid);
@@ -1427,17 +1435,17 @@ extern "C" int ecf8_decode_batched_select(const ecf8_block_desc *descs, int coun
     // used; workgroup 0 writes work_counts)
     switch (threads_per_block) {
       case 128:
-        return launch_dfa_batched<128>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 16,
-                                       nullptr, select, work_counts);
+        return launch_dfa_batched<128, true>(descs, count, n_tasks_bound, blocks_per_task, cap, s,
+                                             37, nullptr, select, work_counts);
       case 256:
-        return launch_dfa_batched<256>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 17,
-                                       nullptr, select, work_counts);
+        return launch_dfa_batched<256, true>(descs, count, n_tasks_bound, blocks_per_task, cap, s,
+                                             38, nullptr, select, work_counts);
       case 512:
-        return launch_dfa_batched<512>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 18,
-                                       nullptr, select, work_counts);
+        return launch_dfa_batched<512, true>(descs, count, n_tasks_bound, blocks_per_task, cap, s,
+                                             39, nullptr, select, work_counts);
       default:
-        return launch_dfa_batched<1024>(descs, count, n_tasks_bound, blocks_per_task, cap, s, 19,
-                                        nullptr, select, work_counts);
+        return launch_dfa_batched<1024, true>(descs, count, n_tasks_bound, blocks_per_task, cap, s,
+                                              40, nullptr, select, work_counts);
     }
   }
   const int64_t block_bytes = (int64_t)threads_per_block * kChunkBytes;

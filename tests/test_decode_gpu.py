@@ -892,12 +892,11 @@ def _many_blocks(cuda_device, n, tpb=512):
 
 @pytest.mark.parametrize("n_blocks", [256, 264])
 def test_batched_launch_on_either_side_of_the_lds_task_table(n_blocks, cuda_device):
-    """Up to 256 descriptors the batched kernel keeps the task table in LDS
-    (each workgroup scans the task counts, and for a routed launch the
-    flags, itself); above, it searches the descriptors in memory and a
-    routed launch compacts the selected ones first.  Every path bit-exact,
-    unselected outputs untouched, the counts written, eager and replayed in
-    a graph."""
+    """A routed launch of up to 256 descriptors selects in the batched
+    kernel itself (each workgroup scans the flags and task counts into an
+    LDS task table); above, a compaction kernel runs first.  Whole launches
+    search the descriptors in memory.  Every path bit-exact, unselected
+    outputs untouched, the counts written, eager and replayed in a graph."""
     from ecf8_amd.decode import BatchSelect, build_table, prepare_batch
 
     _say(f"batched over {n_blocks} blocks")

@@ -61,7 +61,13 @@ def test_one_tensor_kernel_fits_eight_waves_per_simd(kernel_meta):
     assert m["group_segment_fixed_size"] <= 24_704, m
 
 
-def test_batched_kernel_stays_within_the_same_budget(kernel_meta):
-    m = _find(kernel_meta, "decode_dfa_batched_kernelILi512E")
+@pytest.mark.parametrize("select", ["Lb0E", "Lb1E"])
+def test_batched_kernel_stays_within_the_same_budget(kernel_meta, select):
+    """Both instances (whole launches; routed launches selecting in the
+    kernel) keep eight waves per SIMD and four workgroups per CU: 64 VGPRs,
+    80 SGPRs, and static LDS that leaves room for a staging buffer; the
+    whole-launch instance carries no task table."""
+    m = _find(kernel_meta, "decode_dfa_batched_kernelILi512E" + select)
     assert m["vgpr_count"] <= 64, m
     assert m["sgpr_count"] <= 80, m
+    assert m["group_segment_fixed_size"] <= (24_704 if select == "Lb0E" else 25_760), m
