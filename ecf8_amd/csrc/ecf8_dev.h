@@ -118,11 +118,15 @@ __device__ __forceinline__ T *as_global(T *p) {
 }
 
 // load_dfa_batched in rounds of kBatch loads per lane, from a table address
-// read out of memory (a descriptor): the global address space is restated
-// so the loads are global, not flat, loads.
+// read out of memory (a descriptor), as buffer loads: one lane offset for
+// every round, each round's base in its own buffer resource (scalar, and
+// dependent on the table, so a caller's task loop cannot hoist it).  As
+// global loads, each round above the first needed its own lane address,
+// which the batched kernel's task loop kept live and spilled to scratch,
+// reloading them for every task.
 template <int kThreads, int kBatch>
 __device__ __forceinline__ void load_dfa_rounds(uint32_t *s_dfa, const uint32_t *table, int tid) {
-  const uint32_t *const t = as_global(table);
+  const uint32_t lane_off = 4u * (uint32_t)tid;
   constexpr int kIters = (kDfaEntries + kThreads - 1) / kThreads;
 #pragma unroll
   for (int j0 = 0; j0 < kIters; j0 += kBatch) {
@@ -130,7 +134,11 @@ __device__ __forceinline__ void load_dfa_rounds(uint32_t *s_dfa, const uint32_t 
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int i = tid + (j0 + j) * kThreads;
-      v[j] = (j0 + j < kIters && i < kDfaEntries) ? t[i] : 0u;
+      const __amdgpu_buffer_rsrc_t t = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint32_t *>(table + (j0 + j) * kThreads), 0, -1, 0x00020000);
+      v[j] = (j0 + j < kIters && i < kDfaEntries)
+                 ? __builtin_amdgcn_raw_buffer_load_b32(t, lane_off, 0, 0)
+                 : 0u;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
